@@ -1,0 +1,224 @@
+"""Benchmark of the sparse-convolution hot path on one MI355X.
+
+Workload (the headline case): subm_conv3d k=3, fp16,
+C_in = C_out = 128, batch 1, 400k voxels on sphere shells in a 512^3 grid,
+Kaiming-normal weight, synthetic data (seeded).
+
+One step = one pass of the hot path over the batch, inputs resident in HBM:
+  1. kernel-map build: coordinate hash + submanifold relation (edges, CSR
+     views, dense out_in_map / row masks) + mask-sorted implicit-GEMM view;
+  2. the implicit-GEMM convolution on the matrix cores.
+Each phase is bracketed by HIP events on the stream the kernels run on.
+
+``value`` = effective TFLOP/s of the convolution, F / t_conv with
+F = 2 * E * C_in * C_out (E = active edges, useful MACs only).  The JSON line
+also carries Mvoxels/s (N_out / t_conv), the kernel-map build time, the
+roofline of the dominant kernel and the reference CPU route timed on the
+host on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / 'mlx-lattice_amd'):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=20)
+    p.add_argument('--warmup', type=int, default=5)
+    p.add_argument('--cpu-threads', type=int, default=16,
+                   help='host threads for the CPU baseline (capped by the '
+                        'machine)')
+    p.add_argument('--cpu-sample-rows', type=int, default=131072,
+                   help='output rows of the bounded CPU-baseline sample')
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    return p.parse_args()
+
+
+def make_workload():
+    import numpy as np
+
+    from mlx_lattice_amd.synthetic import (
+        config_rng,
+        kaiming_weight,
+        sphere_shell_cloud,
+    )
+
+    rng = config_rng(3)
+    coords = sphere_shell_cloud(400000, 512, rng=rng)
+    feats = rng.standard_normal((len(coords), 128)).astype(np.float16)
+    weight = kaiming_weight((128, 3, 3, 3, 128), rng=rng).astype(np.float16)
+    return coords, feats, weight
+
+
+def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int):
+    """Reference CPU route (oracle restatement, eval_typed with per-FMA fp16
+    rounding for 128->128) on the first ``sample_rows`` output rows, plus the
+    single-threaded relation build on the full cloud."""
+    import numpy as np
+
+    from oracle import oracle
+
+    t0 = time.perf_counter()
+    rel = oracle.kernel_relation(coords, kernel_size=3)
+    t_map = time.perf_counter() - t0
+    hw = oracle.hardware_concurrency()
+    threads = max(1, min(threads, hw))
+    n = min(sample_rows, len(coords))
+    # parallel_for (cpu/algorithms.cpp:30-67) spawns ceil(n / 4096) workers
+    # at most.
+    workers = max(1, min(threads, (n + 4095) // 4096))
+    sample = dict(rel)
+    sample['counts'] = np.array([rel['counts'][0], n], np.int32)
+    e_sample = int(rel['row_offsets'][n])
+    t0 = time.perf_counter()
+    oracle.conv_features(feats, weight, sample, out_capacity=n, threads=threads)
+    t_conv = time.perf_counter() - t0
+    flops = 2.0 * e_sample * 128 * 128
+    return {
+        'value': round(flops / t_conv / 1e12, 6),
+        'unit': 'TFLOP/s',
+        'cores': workers,
+        'kind': 'port',
+        'sample': (f'reference CPU route restated (oracle/lattice_oracle.cpp):'
+                   f' relation build on all {len(coords)} rows single-thread '
+                   f'({t_map * 1e3:.1f} ms), conv on the first {n} output '
+                   f'rows ({e_sample} edges, {t_conv:.2f} s, '
+                   f'{n / t_conv / 1e6:.4f} Mvoxels/s), host has {hw} '
+                   f'hardware threads'),
+        'map_build_ms': round(t_map * 1e3, 3),
+        'mvoxels_per_s': round(n / t_conv / 1e6, 6),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f'bench.py: --gpus {args.gpus} is not supported: this build '
+              'measures one MI355X; the path shards by batch index with no '
+              'exchange (see DESIGN.md), so run one process per GPU.',
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from mlx_lattice_amd._native import ext
+
+    coords_np, feats_np, weight_np = make_workload()
+    dev = torch.device('cuda:0')
+    coords = torch.as_tensor(coords_np).to(dev)
+    feats = torch.as_tensor(feats_np).to(dev)
+    weight = torch.as_tensor(weight_np).to(dev)
+    active = torch.tensor([coords.shape[0]], dtype=torch.int32, device=dev)
+    n_out = int(coords.shape[0])
+
+    def map_build():
+        native = ext.build_submanifold_kernel_relation_with_view(
+            coords, active, [3, 3, 3], [1, 1, 1], check_range=False)
+        return native
+
+    def sorted_view(native):
+        return ext.build_sorted_implicit_gemm_view(native[10], native[11])
+
+    def conv(native, view):
+        reorder, smap, kv, tiles = view
+        return ext.sparse_conv_features_sorted_implicit_gemm(
+            feats, weight, smap, kv, reorder, tiles, native[0], native[1],
+            native[2], native[5], native[3], native[6], native[7], native[8],
+            native[9], n_out, 27)
+
+    # One checked build validates the coordinate range once.
+    native = ext.build_submanifold_kernel_relation_with_view(
+        coords, active, [3, 3, 3], [1, 1, 1])
+    for _ in range(args.warmup):
+        native = map_build()
+        view = sorted_view(native)
+        out = conv(native, view)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        native = map_build()
+        ev[i][1].record(stream)
+        view = sorted_view(native)
+        ev[i][2].record(stream)
+        out = conv(native, view)
+        ev[i][3].record(stream)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+
+    rel_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    view_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    conv_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    edges = int(native[5][0].item())
+    flops = 2.0 * edges * 128 * 128
+    conv_tflops = flops / (conv_ms * 1e-3) / 1e12
+    map_ms = rel_ms + view_ms
+    del out
+
+    record = {
+        'metric': 'subm_conv3d effective TFLOP/s + Mvoxels/s; kernel-map '
+                  'build ms (1 MI355X)',
+        'value': round(conv_tflops, 4),
+        'unit': 'TFLOP/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(t_wall * 1e3 / args.steps, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f16',
+        'data': 'synthetic',
+        'config': {
+            'workload': 'config3: subm_conv3d k=3 fp16 C_in=C_out=128, '
+                        'batch 1, 400k voxels on 200 sphere shells in 512^3',
+            'voxels': n_out,
+            'edges': edges,
+            'kernel_volume': 27,
+            'c_in': 128,
+            'c_out': 128,
+        },
+        'mvoxels_per_s': round(n_out / (conv_ms * 1e-3) / 1e6, 3),
+        'kernel_map_build_ms': round(map_ms, 4),
+        'relation_ms': round(rel_ms, 4),
+        'sorted_view_ms': round(view_ms, 4),
+        'conv_ms': round(conv_ms, 4),
+        'roofline': {
+            'bound': 'mfma',
+            'achieved': round(conv_tflops, 4),
+            'peak': PEAK_FP16_TFLOPS,
+            'unit': 'TFLOP/s',
+            'frac': round(conv_tflops / PEAK_FP16_TFLOPS, 5),
+            'traffic': None,
+            'kernel': 'conv_igemm<_Float16,128,FloatB>',
+        },
+    }
+    if not args.no_cpu_baseline:
+        record['cpu_baseline'] = cpu_baseline(
+            coords_np, feats_np, weight_np, args.cpu_threads,
+            args.cpu_sample_rows)
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -1,0 +1,192 @@
+/*
+ * lattice_hip.h — C ABI of the MI355X (gfx950) sparse-convolution hot path.
+ *
+ * Plain pointers, sizes and an opaque stream handle only.  Every pointer
+ * named "device" is HIP device memory; "host" pointers are read on the host
+ * before the call returns.  All work is enqueued on `stream` (a hipStream_t
+ * passed as void*, NULL = the default stream) and stays asynchronous: no
+ * entry point synchronises the stream or reads device memory back.
+ * Entry points never allocate or free memory: outputs and scratch
+ * ("workspace") are provided by the caller, sized by the *_workspace_bytes
+ * queries.
+ *
+ * Return value: LATTICE_OK or an error code; lattice_hip_last_error() returns
+ * a message for the calling thread's last failure.  Argument errors mirror
+ * the reference's std::invalid_argument (mapped to ValueError by the Python
+ * bindings), unsupported-path and HIP errors its std::runtime_error.
+ *
+ * The entry points replace the following reference interfaces (paths are
+ * relative to the mlx-lattice source tree):
+ *   build_kernel_relation            native/features/coordinates/api.h:67-79,
+ *                                    relations.cpp:540-581, bindings/coords.cpp:414-449
+ *   build_submanifold_kernel_relation relations.cpp:583-597, bindings/coords.cpp:480-507
+ *   build_target_kernel_relation     relations.cpp:672-722, bindings/coords.cpp:550-589
+ *   build_relation_implicit_gemm_view relations.cpp:498-538, bindings/coords.cpp:590-626
+ *   sorted implicit-GEMM view        mlx_lattice/core/relations/views.py:467-510
+ *   sparse_conv_features             native/features/convolution/api.cpp:119-246,
+ *                                    bindings/convolution.cpp:90-146
+ *   sparse_conv_features_sorted_implicit_gemm
+ *                                    api.cpp:248-281, bindings/convolution.cpp:147-234
+ *   sparse_quantized_conv_features   convolution/quantized.cpp:198-268,
+ *                                    bindings/convolution.cpp:12-89
+ */
+#ifndef LATTICE_HIP_H_
+#define LATTICE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lattice_status {
+    LATTICE_OK = 0,
+    LATTICE_ERROR_INVALID_ARGUMENT = 1,
+    LATTICE_ERROR_UNSUPPORTED = 2,
+    LATTICE_ERROR_HIP = 3
+};
+
+enum lattice_dtype {
+    LATTICE_F32 = 0,
+    LATTICE_F16 = 1,
+    LATTICE_BF16 = 2
+};
+
+/* Weight layouts of the float conv (native/features/convolution/contract.h:19-22). */
+enum lattice_weight_layout {
+    LATTICE_WEIGHT_KERNEL_MAJOR = 0, /* (K, C_in, C_out) contiguous */
+    LATTICE_WEIGHT_DENSE_5D = 1      /* (C_out, Kx, Ky, Kz, C_in) contiguous */
+};
+
+/* Bits of the device status word written by the relation builders. */
+enum lattice_relation_flags {
+    LATTICE_STATUS_COORD_RANGE = 1 /* an active coordinate does not fit the packed key */
+};
+
+/* Packed-key coordinate range: batch in [0, LATTICE_MAX_BATCH], spatial
+ * axes in [LATTICE_MIN_COORD, LATTICE_MAX_COORD]. */
+#define LATTICE_MAX_BATCH 1022
+#define LATTICE_MIN_COORD (-131072)
+#define LATTICE_MAX_COORD 131071
+
+const char* lattice_hip_last_error(void);
+const char* lattice_hip_version(void);
+
+/* next_pow2(max(2*rows, 1)): relations.cpp:95-105. */
+int lattice_hip_coord_hash_capacity(int rows);
+
+/* Kernel offsets in the reference order (offsets.cpp:11-45): odd sizes
+ * -r..r, even sizes 0..k-1, x outer, z inner, times dilation.  Writes K*3
+ * ints to `out` (host) when non-NULL; returns K, or -1 on invalid input. */
+int lattice_hip_kernel_offsets(const int kernel_size[3], const int dilation[3],
+                               int32_t* out);
+
+/* Output buffers of a relation build.  Capacities follow the reference:
+ * forward: out_capacity = rows, edge_capacity = rows*K (relations.cpp:550-553);
+ * target:  out_capacity = target_rows, edge_capacity = target_rows*K.
+ * Only active prefixes are defined for in_rows/out_rows/kernel_ids/
+ * in_edge_ids/kernel_edge_ids (counts[0] entries); row_offsets, the CSR row
+ * offsets, counts, out_coords (zero tail), out_in_map (-1 tail) and
+ * row_masks (zero tail) are fully written. */
+typedef struct lattice_relation_outputs {
+    int32_t* in_rows;            /* device [edge_capacity] */
+    int32_t* out_rows;           /* device [edge_capacity] */
+    int32_t* kernel_ids;         /* device [edge_capacity] */
+    int32_t* row_offsets;        /* device [out_capacity + 1] */
+    int32_t* out_coords;         /* device [out_capacity, 4]; NULL for target relations */
+    int32_t* counts;             /* device [2] = [E, N_out] */
+    int32_t* in_row_offsets;     /* device [in_capacity + 1] */
+    int32_t* in_edge_ids;        /* device [edge_capacity] */
+    int32_t* kernel_row_offsets; /* device [K + 1] */
+    int32_t* kernel_edge_ids;    /* device [edge_capacity] */
+    int32_t* out_in_map;         /* device [out_capacity, K] (implicit-GEMM view) */
+    int32_t* row_masks;          /* device [out_capacity, ceil(K/32)] */
+    int32_t* status;             /* device [1]: lattice_relation_flags bits */
+} lattice_relation_outputs;
+
+size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kernel_count);
+size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows,
+                                                   int kernel_count);
+
+/* Forward relation: write_kernel_relation (cpu/relation_build_detail.h:3-41).
+ * stride (1,1,1) with padding (0,0,0) keeps input rows as output rows
+ * (submanifold); otherwise outputs are the first-seen floor-divided cells.
+ * coords: device int32 [rows, 4]; active_rows: device int32 [1]. */
+int lattice_hip_build_kernel_relation(
+    const int32_t* coords, int rows, const int32_t* active_rows,
+    const int kernel_size[3], const int stride[3], const int padding[3],
+    const int dilation[3], const lattice_relation_outputs* out,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Target relation: write_target_kernel_relation (relation_build_detail.h:43-80). */
+int lattice_hip_build_target_kernel_relation(
+    const int32_t* coords, int rows, const int32_t* active_rows,
+    const int32_t* target_coords, int target_rows,
+    const int32_t* target_active_rows, const int kernel_size[3],
+    const int stride[3], const int padding[3], const int dilation[3],
+    const lattice_relation_outputs* out, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* Dense out_in_map + row masks: write_relation_implicit_gemm_view
+ * (relation_views_detail.h:122-169).  offsets: device int32 [K, 3]. */
+size_t lattice_hip_implicit_gemm_view_workspace_bytes(int source_rows);
+int lattice_hip_build_relation_implicit_gemm_view(
+    const int32_t* source_coords, int source_rows,
+    const int32_t* source_active_rows, const int32_t* output_coords,
+    int output_rows, const int32_t* output_active_rows,
+    const int32_t* offsets, int kernel_count, const int stride[3],
+    const int padding[3], int32_t* out_in_map, int32_t* row_masks,
+    int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tile-sorted view (core/relations/views.py:467-510): reorder_rows = stable
+ * argsort of the single-word row masks; sorted_out_in_map [rows, K];
+ * sorted_kv_out_in_map [K, rows]; tile_masks [ceil(rows/64)*4] = OR of the
+ * masks of each 16-row quarter of each 64-row tile.  K <= 32. */
+size_t lattice_hip_sorted_view_workspace_bytes(int rows);
+int lattice_hip_build_sorted_implicit_gemm_view(
+    const int32_t* out_in_map, const int32_t* row_masks, int rows,
+    int kernel_count, int32_t* reorder_rows, int32_t* sorted_out_in_map,
+    int32_t* sorted_kv_out_in_map, int32_t* tile_masks, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* Float sparse conv over the output CSR (cpu/algorithms.cpp:180-302):
+ * out[o] = sum_{e in CSR(o)} feats[in_rows[e]] @ W[kernel_ids[e]] with an
+ * fp32 accumulator; rows >= counts[1] are zero.  feats [n_in, c_in];
+ * out [out_capacity, c_out], both in `dtype`. */
+int lattice_hip_sparse_conv_features(
+    int dtype, const void* feats, int n_in, int c_in, const void* weights,
+    int weight_layout, int kernel_count, int c_out, const int32_t* in_rows,
+    const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
+    const int32_t* row_offsets, int out_capacity, void* out, void* stream);
+
+/* Implicit-GEMM conv over the sorted view: tile row i of the sorted order
+ * gathers feats[sorted_out_in_map[i, k]] for every k and scatters its result
+ * to out[reorder_rows[i]] (row i itself when reorder_rows is NULL).  fp16/bf16 with c_in % 32 == 0 and
+ * c_out % 16 == 0 run on MFMA (fp32 accumulate); other shapes take the
+ * bandwidth path. */
+int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
+    int dtype, const void* feats, int n_in, int c_in, const void* weights,
+    int weight_layout, int kernel_count, int c_out,
+    const int32_t* sorted_out_in_map, const int32_t* reorder_rows,
+    int out_capacity, void* out, void* stream);
+
+/* Quantized conv (cpu/quantized.cpp:64-141): weights uint32
+ * [K, storage_c_in*bits/32, c_out] with codes LSB-first along C_in,
+ * scales/biases [K, storage_c_in/group_size, c_out] in the feature dtype,
+ * w = q*scale + bias, fp32 accumulator.  When sorted_kv_out_in_map and
+ * reorder_rows are non-NULL the MFMA route with the dequant fused into the
+ * B-operand load is used (fp16, c_in % 32 == 0); otherwise the CSR route. */
+int lattice_hip_sparse_quantized_conv_features(
+    int dtype, const void* feats, int n_in, int c_in, const uint32_t* weights,
+    const void* scales, const void* biases, int kernel_count, int c_out,
+    int storage_c_in, int group_size, int bits, const int32_t* in_rows,
+    const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
+    const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
+    const int32_t* reorder_rows, int out_capacity, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LATTICE_HIP_H_ */

@@ -1,0 +1,160 @@
+// Shared helpers of the gfx950 sparse-convolution library: error plumbing,
+// launch helpers, wavefront intrinsics, the packed 64-bit coordinate key and
+// the open-addressing hash probe.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "lattice_hip.h"
+
+namespace lattice {
+
+// ---------------------------------------------------------------- errors --
+
+void set_error(const std::string& message);
+
+#define LATTICE_REQUIRE(cond, msg)                                   \
+    do {                                                             \
+        if (!(cond)) {                                               \
+            ::lattice::set_error(msg);                               \
+            return LATTICE_ERROR_INVALID_ARGUMENT;                   \
+        }                                                            \
+    } while (0)
+
+#define LATTICE_HIP_TRY(expr)                                        \
+    do {                                                             \
+        hipError_t lattice_err_ = (expr);                            \
+        if (lattice_err_ != hipSuccess) {                            \
+            ::lattice::set_error(std::string("HIP error: ") +        \
+                                 hipGetErrorString(lattice_err_) +   \
+                                 " at " #expr);                      \
+            return LATTICE_ERROR_HIP;                                \
+        }                                                            \
+    } while (0)
+
+#define LATTICE_LAUNCH_CHECK() LATTICE_HIP_TRY(hipGetLastError())
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(long long work, int per_block, unsigned cap = 1u << 20) {
+    long long blocks = (work + per_block - 1) / per_block;
+    if (blocks < 1) blocks = 1;
+    if (blocks > cap) blocks = cap;
+    return static_cast<unsigned>(blocks);
+}
+
+// Bump allocator over a caller workspace; every carve is 256-byte aligned.
+struct Workspace {
+    char* base;
+    size_t size;
+    size_t used = 0;
+    template <typename T>
+    T* take(size_t count) {
+        size_t bytes = (count * sizeof(T) + 255) & ~size_t(255);
+        if (used + bytes > size) return nullptr;
+        T* out = reinterpret_cast<T*>(base + used);
+        used += bytes;
+        return out;
+    }
+};
+
+inline size_t aligned_bytes(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+
+// ------------------------------------------------------- wave intrinsics --
+
+constexpr int kWave = 64;
+
+__device__ inline int lane_id() {
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0));
+}
+
+// Number of set bits of `mask` held by lanes below the calling lane.
+__device__ inline int lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+__device__ inline uint64_t ballot(bool pred) { return __ballot(pred); }
+
+// ------------------------------------------------------ packed coord key --
+//
+// key = batch << 54 | (x + 2^17) << 36 | (y + 2^17) << 18 | (z + 2^17).
+// Injective over batch in [0, 1022] and x, y, z in [-2^17, 2^17); the
+// all-ones word (batch 1023) is never produced and marks an empty slot.
+
+constexpr uint64_t kEmptyKey = ~0ull;
+constexpr int64_t kAxisBias = 131072;     // 2^17
+constexpr int64_t kAxisSpan = 262144;     // 2^18
+
+__host__ __device__ inline bool pack_key(int64_t b, int64_t x, int64_t y, int64_t z,
+                                         uint64_t* key) {
+    uint64_t ux = static_cast<uint64_t>(x + kAxisBias);
+    uint64_t uy = static_cast<uint64_t>(y + kAxisBias);
+    uint64_t uz = static_cast<uint64_t>(z + kAxisBias);
+    bool ok = b >= 0 && b <= LATTICE_MAX_BATCH && ux < uint64_t(kAxisSpan) &&
+              uy < uint64_t(kAxisSpan) && uz < uint64_t(kAxisSpan);
+    *key = (static_cast<uint64_t>(b) << 54) | (ux << 36) | (uy << 18) | uz;
+    return ok;
+}
+
+// 64-bit finaliser (MurmurHash3 fmix64): spreads the structured key bits.
+__host__ __device__ inline uint64_t mix64(uint64_t k) {
+    k ^= k >> 33;
+    k *= 0xff51afd7ed558ccdull;
+    k ^= k >> 33;
+    k *= 0xc4ceb9fe1a85ec53ull;
+    k ^= k >> 33;
+    return k;
+}
+
+// Open-addressing table: `keys` (uint64) and `rows` (int32), power-of-two
+// capacity, linear probing.  A stored row is the minimum input row that
+// inserted the key, i.e. its first occurrence.
+struct CoordTable {
+    uint64_t* keys;
+    int32_t* rows;
+    uint32_t mask;  // capacity - 1
+
+    __device__ inline void insert(uint64_t key, int32_t row) const {
+        uint32_t slot = static_cast<uint32_t>(mix64(key)) & mask;
+        while (true) {
+            unsigned long long prev = atomicCAS(
+                reinterpret_cast<unsigned long long*>(keys + slot),
+                static_cast<unsigned long long>(kEmptyKey),
+                static_cast<unsigned long long>(key));
+            if (prev == kEmptyKey || prev == key) {
+                atomicMin(rows + slot, row);
+                return;
+            }
+            slot = (slot + 1) & mask;
+        }
+    }
+
+    __device__ inline int32_t find(uint64_t key) const {
+        uint32_t slot = static_cast<uint32_t>(mix64(key)) & mask;
+        while (true) {
+            uint64_t k = keys[slot];
+            if (k == key) return rows[slot];
+            if (k == kEmptyKey) return -1;
+            slot = (slot + 1) & mask;
+        }
+    }
+};
+
+// floor division for a positive divisor (quantization_detail.h:3-10).
+__host__ __device__ inline int64_t floor_div_pos(int64_t v, int64_t d) {
+    int64_t q = v / d;
+    int64_t r = v % d;
+    if (r != 0 && r < 0) --q;
+    return q;
+}
+
+struct Int3 {
+    int x, y, z;
+};
+
+}  // namespace lattice

@@ -1,0 +1,196 @@
+"""Relation builders: the Python side of mlx_lattice/core/coords/builders.py
+(:42-233, :393-444) over the native ``_ext`` module.
+
+Each builder validates, calls the gfx950 relation kernels through ``_ext`` and
+wraps the native 10-tuple (plus the implicit-GEMM view that the same map
+query produced) into a ``KernelRelation``.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from mlx_lattice_amd.core.coords.validation import validate_coords
+from mlx_lattice_amd.core.relations import (
+    KernelRelation,
+    KernelSpec,
+    RelationImplicitGemmView,
+)
+from mlx_lattice_amd.core.relations.views import RelationKind
+from mlx_lattice_amd.core.types import Triple, triple
+
+
+def _ext():
+    from mlx_lattice_amd._native import ext
+
+    return ext
+
+
+def kernel_offsets(kernel_size: int | Sequence[int],
+                   dilation: int | Sequence[int] = 1) -> tuple[Triple, ...]:
+    """Offsets of a dense 3D kernel footprint (builders.py:130-153,
+    offsets.cpp:11-45): odd extents ``-r..r``, even extents ``0..k-1``,
+    x outer / z inner, times dilation."""
+    kernel = triple(kernel_size, name='kernel_size')
+    rate = triple(dilation, name='dilation')
+    _require_positive(kernel, 'kernel_size')
+    _require_positive(rate, 'dilation')
+    axes = []
+    for size in kernel:
+        if size % 2 == 1:
+            radius = size // 2
+            axes.append(range(-radius, radius + 1))
+        else:
+            axes.append(range(size))
+    return tuple((int(x * rate[0]), int(y * rate[1]), int(z * rate[2]))
+                 for x in axes[0] for y in axes[1] for z in axes[2])
+
+
+def build_relation_implicit_gemm_view(
+        relation: KernelRelation) -> RelationImplicitGemmView:
+    """Dense output-to-input map for implicit-GEMM kernels
+    (builders.py:42-79)."""
+    contract = relation.contract
+    if contract.kind not in ('forward', 'target', 'submanifold'):
+        raise ValueError(
+            'implicit GEMM view currently supports forward, target, and '
+            'submanifold relations.')
+    if (contract.source_coords is None or contract.source_active_rows is None
+            or contract.out_coords is None):
+        raise ValueError(
+            'kernel relation is missing coordinate context for implicit GEMM.')
+    output_active = (contract.target_active_rows
+                     if contract.kind in ('target', 'submanifold')
+                     else contract.out_count)
+    if output_active is None:
+        raise ValueError(
+            'kernel relation is missing output activity for implicit GEMM.')
+    offsets = torch.tensor(contract.kernel_offsets, dtype=torch.int32,
+                           device=contract.source_coords.device).reshape(-1, 3)
+    out_in_map, row_masks = _ext().build_relation_implicit_gemm_view(
+        contract.source_coords, contract.source_active_rows,
+        contract.out_coords, output_active, offsets, list(contract.stride),
+        list(contract.padding))
+    return RelationImplicitGemmView(out_in_map, row_masks=row_masks)
+
+
+def build_kernel_relation(coords: torch.Tensor,
+                          active_rows: torch.Tensor | None = None,
+                          kernel_size: int | Sequence[int] = 3,
+                          stride: int | Sequence[int] = 1,
+                          padding: int | Sequence[int] = 0,
+                          dilation: int | Sequence[int] = 1) -> KernelRelation:
+    """Forward sparse convolution relation (builders.py:156-191)."""
+    validate_coords(coords)
+    spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
+                      dilation=dilation)
+    offsets = kernel_offsets(spec.size, spec.dilation)
+    source_active = _active_rows(active_rows, coords)
+    native = _ext().build_kernel_relation_with_view(
+        coords, source_active, list(spec.size), list(spec.stride),
+        list(spec.padding), list(spec.dilation))
+    return _kernel_relation_from_native(
+        native, offsets=offsets, in_capacity=int(coords.shape[0]),
+        source_coords=coords, source_active_rows=source_active,
+        stride=spec.stride, padding=spec.padding, kind='forward')
+
+
+def build_submanifold_kernel_relation(
+        coords: torch.Tensor, active_rows: torch.Tensor | None = None,
+        kernel_size: int | Sequence[int] = 3,
+        dilation: int | Sequence[int] = 1) -> KernelRelation:
+    """Submanifold relation whose output support is ``coords``
+    (builders.py:194-233)."""
+    validate_coords(coords)
+    spec = KernelSpec(size=kernel_size, stride=1, padding=0,
+                      dilation=dilation)
+    if not all(value % 2 == 1 for value in spec.size):
+        raise ValueError(
+            'submanifold relations require odd kernels, stride=1, '
+            'padding=0, and positive dilation.')
+    offsets = kernel_offsets(spec.size, spec.dilation)
+    source_active = _active_rows(active_rows, coords)
+    native = _ext().build_submanifold_kernel_relation_with_view(
+        coords, source_active, list(spec.size), list(spec.dilation))
+    return _kernel_relation_from_native(
+        native, offsets=offsets, in_capacity=int(coords.shape[0]),
+        out_coords=coords, source_coords=coords,
+        source_active_rows=source_active, target_coords=coords,
+        target_active_rows=source_active, stride=spec.stride,
+        padding=spec.padding, kind='submanifold')
+
+
+def build_target_kernel_relation(
+        coords: torch.Tensor, target_coords: torch.Tensor, *,
+        active_rows: torch.Tensor | None = None,
+        target_active_rows: torch.Tensor | None = None,
+        kernel_size: int | Sequence[int] = 3,
+        stride: int | Sequence[int] = 1,
+        padding: int | Sequence[int] = 0,
+        dilation: int | Sequence[int] = 1) -> KernelRelation:
+    """Relation from source coords to explicit target coords
+    (builders.py:82-127)."""
+    validate_coords(coords)
+    validate_coords(target_coords)
+    if coords.dtype != target_coords.dtype:
+        raise ValueError('coordinate arrays must have matching dtype.')
+    spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
+                      dilation=dilation)
+    offsets = kernel_offsets(spec.size, spec.dilation)
+    source_active = _active_rows(active_rows, coords)
+    target_active = _active_rows(target_active_rows, target_coords)
+    native = _ext().build_target_kernel_relation_with_view(
+        coords, source_active, target_coords, target_active,
+        list(spec.size), list(spec.stride), list(spec.padding),
+        list(spec.dilation))
+    return _kernel_relation_from_native(
+        native, offsets=offsets, in_capacity=int(coords.shape[0]),
+        source_coords=coords, source_active_rows=source_active,
+        target_coords=target_coords, target_active_rows=target_active,
+        stride=spec.stride, padding=spec.padding, kind='target')
+
+
+def _kernel_relation_from_native(
+        native, *, offsets: tuple[Triple, ...], in_capacity: int,
+        out_coords: torch.Tensor | None = None,
+        source_coords: torch.Tensor, source_active_rows: torch.Tensor,
+        target_coords: torch.Tensor | None = None,
+        target_active_rows: torch.Tensor | None = None,
+        stride: Triple = (1, 1, 1), padding: Triple = (0, 0, 0),
+        kind: RelationKind = 'forward') -> KernelRelation:
+    (in_rows, out_rows, kernel_ids, row_offsets, native_out_coords, counts,
+     in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids,
+     *view) = native
+    relation_out_coords = (native_out_coords if out_coords is None
+                           else out_coords)
+    implicit = (RelationImplicitGemmView(view[0], row_masks=view[1])
+                if len(view) == 2 else None)
+    return KernelRelation(
+        in_rows, out_rows, kernel_ids, row_offsets=row_offsets,
+        counts=counts, in_row_offsets=in_row_offsets,
+        in_edge_ids=in_edge_ids, kernel_row_offsets=kernel_row_offsets,
+        kernel_edge_ids=kernel_edge_ids, kernel_offsets=offsets,
+        out_coords=relation_out_coords, n_in_capacity=in_capacity,
+        n_out_capacity=int(relation_out_coords.shape[0]),
+        n_kernels=len(offsets), source_coords=source_coords,
+        source_active_rows=source_active_rows, target_coords=target_coords,
+        target_active_rows=target_active_rows, stride=stride,
+        padding=padding, kind=kind, implicit_gemm=implicit)
+
+
+def _require_positive(values: Triple, name: str) -> None:
+    if any(value <= 0 for value in values):
+        raise ValueError(f'{name} values must be positive.')
+
+
+def _active_rows(value: torch.Tensor | None,
+                 coords: torch.Tensor) -> torch.Tensor:
+    if value is not None:
+        if tuple(value.shape) != (1,) or value.dtype != torch.int32:
+            raise ValueError(
+                'active_rows must have shape (1,) and int32 dtype.')
+        return value
+    return torch.tensor([coords.shape[0]], dtype=torch.int32,
+                        device=coords.device)

@@ -1,0 +1,427 @@
+"""Kernel relation contract and its execution views over torch tensors.
+
+Mirrors mlx_lattice/core/relations/views.py (RelationEdges :19-45,
+RelationCSRView :48-62, RelationImplicitGemmView :68-101,
+RelationSortedImplicitGemmView :104-146, SparseRelationContract :149-236,
+KernelRelation :259-525).  Every array is an int32 torch tensor on the
+relation's device; counts stay on the device.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+
+from mlx_lattice_amd.core.types import Triple
+
+RelationKind = Literal['forward', 'target', 'submanifold', 'transposed',
+                       'generative']
+
+_INDEX_DTYPES = (torch.int32, torch.int64)
+
+
+@dataclass(frozen=True, slots=True)
+class RelationEdges:
+    """Edge arrays ``(in_row, out_row, kernel_id)`` at the same index."""
+
+    in_rows: torch.Tensor
+    out_rows: torch.Tensor
+    kernel_ids: torch.Tensor
+
+    def __post_init__(self) -> None:
+        _validate_row_array(self.in_rows, name='in_rows')
+        _validate_row_array(self.out_rows, name='out_rows')
+        _validate_row_array(self.kernel_ids, name='kernel_ids')
+        _require_same_rows(self.in_rows, self.out_rows, self.kernel_ids,
+                           names=('in_rows', 'out_rows', 'kernel_ids'))
+
+    @property
+    def capacity(self) -> int:
+        return int(self.in_rows.shape[0])
+
+
+@dataclass(frozen=True, slots=True)
+class RelationCSRView:
+    """CSR view: ``row_offsets`` ``(rows + 1,)`` int32 and optional
+    ``edge_ids`` remapping CSR order to the canonical edge arrays."""
+
+    row_offsets: torch.Tensor
+    edge_ids: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        _validate_row_offsets(self.row_offsets)
+        if self.edge_ids is not None:
+            _validate_row_array(self.edge_ids, name='edge_ids')
+
+
+RelationView = RelationCSRView
+
+
+@dataclass(frozen=True, slots=True)
+class RelationImplicitGemmView:
+    """Dense ``out_in_map[o, k]`` (input row or -1) plus ``row_masks``
+    (bit k%32 of word k/32 set when offset k contributes)."""
+
+    out_in_map: torch.Tensor
+    row_masks: torch.Tensor
+
+    def __post_init__(self) -> None:
+        if self.out_in_map.ndim != 2:
+            raise ValueError('out_in_map must have shape (Nout, K).')
+        if self.out_in_map.dtype not in _INDEX_DTYPES:
+            raise ValueError('out_in_map must be int32 or int64.')
+        if self.row_masks.ndim != 2:
+            raise ValueError('row_masks must have shape (Nout, M).')
+        if self.row_masks.dtype not in _INDEX_DTYPES:
+            raise ValueError('row_masks must be int32 or int64.')
+        if int(self.row_masks.shape[0]) != int(self.out_in_map.shape[0]):
+            raise ValueError('row_masks must have one row per out_in_map row.')
+        expected = (int(self.out_in_map.shape[1]) + 31) // 32
+        if int(self.row_masks.shape[1]) != expected:
+            raise ValueError(
+                'row_masks must have ceil(K / 32) words per output row.')
+
+
+@dataclass(frozen=True, slots=True)
+class RelationSortedImplicitGemmView:
+    """Mask-sorted implicit-GEMM view consumed by the matrix-core route."""
+
+    sorted_out_in_map: torch.Tensor
+    sorted_kv_out_in_map: torch.Tensor
+    reorder_rows: torch.Tensor
+    tile_masks: torch.Tensor
+
+    def __post_init__(self) -> None:
+        if self.sorted_out_in_map.ndim != 2:
+            raise ValueError('sorted_out_in_map must have shape (Nout, K).')
+        if self.sorted_kv_out_in_map.ndim != 2:
+            raise ValueError('sorted_kv_out_in_map must have shape (K, Nout).')
+        if (int(self.sorted_kv_out_in_map.shape[0])
+                != int(self.sorted_out_in_map.shape[1])
+                or int(self.sorted_kv_out_in_map.shape[1])
+                != int(self.sorted_out_in_map.shape[0])):
+            raise ValueError('sorted_kv_out_in_map must be the K-major view '
+                             'of sorted_out_in_map.')
+        _validate_row_array(self.reorder_rows, name='reorder_rows')
+        _validate_row_array(self.tile_masks, name='tile_masks')
+        if int(self.reorder_rows.shape[0]) != int(
+                self.sorted_out_in_map.shape[0]):
+            raise ValueError(
+                'reorder_rows must have one row per sorted_out_in_map row.')
+
+
+@dataclass(frozen=True, slots=True)
+class SparseRelationContract:
+    """Counts, capacities, coordinate context and geometry of a relation."""
+
+    counts: torch.Tensor
+    kernel_offsets: tuple[Triple, ...]
+    out_coords: torch.Tensor | None = None
+    n_in_capacity: int | None = None
+    n_out_capacity: int | None = None
+    n_kernels: int | None = None
+    source_coords: torch.Tensor | None = None
+    source_active_rows: torch.Tensor | None = None
+    target_coords: torch.Tensor | None = None
+    target_active_rows: torch.Tensor | None = None
+    stride: Triple = (1, 1, 1)
+    padding: Triple = (0, 0, 0)
+    kind: RelationKind = 'forward'
+
+    def __post_init__(self) -> None:
+        _validate_counts(self.counts)
+        for name in ('out_coords', 'source_coords', 'target_coords'):
+            value = getattr(self, name)
+            if value is not None:
+                _validate_coords(value, name=name)
+        for name in ('source_active_rows', 'target_active_rows'):
+            value = getattr(self, name)
+            if value is not None:
+                _validate_active_rows(value, name=name)
+        if self.kind not in ('forward', 'target', 'submanifold',
+                             'transposed', 'generative'):
+            raise ValueError(
+                "relation kind must be 'forward', 'target', "
+                "'submanifold', 'transposed', or 'generative'.")
+        offsets = tuple((int(x), int(y), int(z))
+                        for x, y, z in self.kernel_offsets)
+        object.__setattr__(self, 'kernel_offsets', offsets)
+        object.__setattr__(self, 'stride', tuple(int(v) for v in self.stride))
+        object.__setattr__(self, 'padding',
+                           tuple(int(v) for v in self.padding))
+        n_in = _optional_count(self.n_in_capacity, 'n_in_capacity')
+        n_out = _optional_count(self.n_out_capacity, 'n_out_capacity')
+        n_kernels = _optional_count(self.n_kernels, 'n_kernels')
+        if offsets:
+            if n_kernels is not None and n_kernels != len(offsets):
+                raise ValueError('n_kernels must match kernel_offsets.')
+            n_kernels = len(offsets)
+        if self.out_coords is not None:
+            out_capacity = int(self.out_coords.shape[0])
+            if n_out is not None and n_out != out_capacity:
+                raise ValueError(
+                    'n_out_capacity must match out_coords capacity.')
+            n_out = out_capacity
+        object.__setattr__(self, 'n_in_capacity', n_in)
+        object.__setattr__(self, 'n_out_capacity', n_out)
+        object.__setattr__(self, 'n_kernels', n_kernels)
+
+    @property
+    def edge_count(self) -> torch.Tensor:
+        return self.counts[:1]
+
+    @property
+    def out_count(self) -> torch.Tensor:
+        return self.counts[1:2]
+
+
+@dataclass(frozen=True, slots=True, init=False)
+class KernelRelation:
+    """Sparse kernel relation with edge, CSR and implicit-GEMM views."""
+
+    contract: SparseRelationContract
+    edges: RelationEdges
+    output_csr: RelationCSRView
+    input_csr: RelationCSRView
+    kernel_csr: RelationCSRView
+    implicit_gemm: RelationImplicitGemmView | None = None
+    sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
+
+    def __init__(
+        self,
+        in_rows: torch.Tensor,
+        out_rows: torch.Tensor,
+        kernel_ids: torch.Tensor,
+        *,
+        row_offsets: torch.Tensor | None = None,
+        counts: torch.Tensor | None = None,
+        in_row_offsets: torch.Tensor | None = None,
+        in_edge_ids: torch.Tensor | None = None,
+        kernel_row_offsets: torch.Tensor | None = None,
+        kernel_edge_ids: torch.Tensor | None = None,
+        kernel_offsets: tuple[Triple, ...] = (),
+        out_coords: torch.Tensor | None = None,
+        n_in_capacity: int | None = None,
+        n_out_capacity: int | None = None,
+        n_kernels: int | None = None,
+        source_coords: torch.Tensor | None = None,
+        source_active_rows: torch.Tensor | None = None,
+        target_coords: torch.Tensor | None = None,
+        target_active_rows: torch.Tensor | None = None,
+        stride: Triple = (1, 1, 1),
+        padding: Triple = (0, 0, 0),
+        kind: RelationKind = 'forward',
+        implicit_gemm: RelationImplicitGemmView | None = None,
+        sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None,
+    ) -> None:
+        device = in_rows.device
+        if counts is None:
+            counts = torch.tensor(
+                [in_rows.shape[0],
+                 0 if out_coords is None else out_coords.shape[0]],
+                dtype=torch.int32, device=device)
+        _validate_counts(counts)
+        contract = SparseRelationContract(
+            counts=counts, kernel_offsets=kernel_offsets,
+            out_coords=out_coords, n_in_capacity=n_in_capacity,
+            n_out_capacity=n_out_capacity, n_kernels=n_kernels,
+            source_coords=source_coords,
+            source_active_rows=source_active_rows,
+            target_coords=target_coords,
+            target_active_rows=target_active_rows, stride=stride,
+            padding=padding, kind=kind)
+        if row_offsets is None:
+            cap = int(contract.n_out_capacity or 0)
+            row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
+                                      device=device)
+        _validate_row_offsets(row_offsets)
+        edges = RelationEdges(in_rows, out_rows, kernel_ids)
+        if in_row_offsets is None:
+            cap = int(contract.n_in_capacity or 0)
+            in_row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
+                                         device=device)
+        if in_edge_ids is None:
+            in_edge_ids = torch.zeros(edges.capacity, dtype=torch.int32,
+                                      device=device)
+        if kernel_row_offsets is None:
+            cap = int(contract.n_kernels or 0)
+            kernel_row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
+                                             device=device)
+        if kernel_edge_ids is None:
+            kernel_edge_ids = torch.zeros(edges.capacity, dtype=torch.int32,
+                                          device=device)
+        if (contract.n_out_capacity is not None
+                and int(row_offsets.shape[0])
+                != int(contract.n_out_capacity) + 1):
+            raise ValueError(
+                'row_offsets must have length n_out_capacity + 1.')
+        object.__setattr__(self, 'contract', contract)
+        object.__setattr__(self, 'edges', edges)
+        object.__setattr__(self, 'output_csr', RelationCSRView(row_offsets))
+        object.__setattr__(self, 'input_csr',
+                           RelationCSRView(in_row_offsets, in_edge_ids))
+        object.__setattr__(self, 'kernel_csr',
+                           RelationCSRView(kernel_row_offsets,
+                                           kernel_edge_ids))
+        object.__setattr__(self, 'implicit_gemm', implicit_gemm)
+        object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
+
+    @property
+    def edge_capacity(self) -> int:
+        return self.edges.capacity
+
+    @property
+    def counts(self) -> torch.Tensor:
+        """Native counts array ``[edge_count, out_count]`` (device)."""
+        return self.contract.counts
+
+    @property
+    def edge_count(self) -> torch.Tensor:
+        return self.contract.edge_count
+
+    @property
+    def out_count(self) -> torch.Tensor:
+        return self.contract.out_count
+
+    @property
+    def kernel_offsets(self) -> tuple[Triple, ...]:
+        return self.contract.kernel_offsets
+
+    @property
+    def out_coords(self) -> torch.Tensor | None:
+        return self.contract.out_coords
+
+    @property
+    def n_in_capacity(self) -> int | None:
+        return self.contract.n_in_capacity
+
+    @property
+    def n_out_capacity(self) -> int | None:
+        return self.contract.n_out_capacity
+
+    @property
+    def n_kernels(self) -> int | None:
+        return self.contract.n_kernels
+
+    @property
+    def row_offsets(self) -> torch.Tensor:
+        return self.output_csr.row_offsets
+
+    @property
+    def in_row_offsets(self) -> torch.Tensor:
+        return self.input_csr.row_offsets
+
+    @property
+    def in_edge_ids(self) -> torch.Tensor:
+        if self.input_csr.edge_ids is None:
+            raise ValueError('input CSR view is missing edge ids.')
+        return self.input_csr.edge_ids
+
+    @property
+    def kernel_row_offsets(self) -> torch.Tensor:
+        return self.kernel_csr.row_offsets
+
+    @property
+    def kernel_edge_ids(self) -> torch.Tensor:
+        if self.kernel_csr.edge_ids is None:
+            raise ValueError('kernel CSR view is missing edge ids.')
+        return self.kernel_csr.edge_ids
+
+    @property
+    def out_view(self) -> RelationCSRView:
+        return self.output_csr
+
+    @property
+    def in_view(self) -> RelationCSRView:
+        return self.input_csr
+
+    @property
+    def kernel_view(self) -> RelationCSRView:
+        return self.kernel_csr
+
+    def require_implicit_gemm(self) -> RelationImplicitGemmView:
+        """Return or lazily build the implicit-GEMM view (views.py:452-465)."""
+        if self.implicit_gemm is not None:
+            return self.implicit_gemm
+        from mlx_lattice_amd.core.coords.builders import (
+            build_relation_implicit_gemm_view,
+        )
+
+        view = build_relation_implicit_gemm_view(self)
+        object.__setattr__(self, 'implicit_gemm', view)
+        return view
+
+    def require_sorted_implicit_gemm(self) -> RelationSortedImplicitGemmView:
+        """Return or lazily build the mask-sorted view (views.py:467-510):
+        ``reorder_rows`` is the stable argsort of the row masks, the maps are
+        gathered in that order and ``tile_masks`` ORs each 16-row quarter of
+        every 64-row tile."""
+        if self.sorted_implicit_gemm is not None:
+            return self.sorted_implicit_gemm
+        view = self.require_implicit_gemm()
+        if view.row_masks.shape[1] != 1:
+            raise ValueError(
+                'sorted implicit GEMM view currently supports K <= 32.')
+        from mlx_lattice_amd._native import ext
+
+        reorder, sorted_map, kv_map, tiles = ext.build_sorted_implicit_gemm_view(
+            view.out_in_map, view.row_masks)
+        sorted_view = RelationSortedImplicitGemmView(
+            sorted_out_in_map=sorted_map, sorted_kv_out_in_map=kv_map,
+            reorder_rows=reorder, tile_masks=tiles)
+        object.__setattr__(self, 'sorted_implicit_gemm', sorted_view)
+        return sorted_view
+
+
+# ---------------------------------------------------------------- helpers --
+
+
+def _validate_row_array(value: torch.Tensor, *, name: str) -> None:
+    if value.ndim != 1:
+        raise ValueError(f'{name} must have shape (E,).')
+    if value.dtype not in _INDEX_DTYPES:
+        raise ValueError(f'{name} must be int32 or int64.')
+
+
+def _validate_coords(value: torch.Tensor, *, name: str) -> None:
+    if value.ndim != 2 or value.shape[1] != 4:
+        raise ValueError(f'{name} must have shape (N, 4).')
+    if value.dtype not in _INDEX_DTYPES:
+        raise ValueError(f'{name} must be int32 or int64.')
+
+
+def _validate_counts(value: torch.Tensor) -> None:
+    if tuple(value.shape) != (2,) or value.dtype != torch.int32:
+        raise ValueError(
+            'relation counts must have shape (2,) and int32 dtype.')
+
+
+def _validate_active_rows(value: torch.Tensor, *, name: str) -> None:
+    if tuple(value.shape) != (1,) or value.dtype != torch.int32:
+        raise ValueError(f'{name} must have shape (1,) and int32 dtype.')
+
+
+def _validate_row_offsets(value: torch.Tensor) -> None:
+    if value.ndim != 1 or value.dtype != torch.int32:
+        raise ValueError(
+            'row_offsets must have shape (N + 1,) and int32 dtype.')
+
+
+def _require_same_rows(first: torch.Tensor, *rest: torch.Tensor,
+                       names: tuple[str, ...]) -> None:
+    rows = int(first.shape[0])
+    for name, value in zip(names[1:], rest, strict=True):
+        if int(value.shape[0]) != rows:
+            raise ValueError(
+                f'{names[0]} and {name} must have the same row count.')
+
+
+def _optional_count(value: int | None, name: str) -> int | None:
+    if value is None:
+        return None
+    normalized = int(value)
+    if normalized < 0:
+        raise ValueError(f'{name} must be non-negative.')
+    return normalized

@@ -1,0 +1,7 @@
+from mlx_lattice_amd.nn.conv import Conv3d, SubmConv3d
+from mlx_lattice_amd.nn.quantized_conv import (
+    QuantizedConv3d,
+    QuantizedSubmConv3d,
+)
+
+__all__ = ['Conv3d', 'QuantizedConv3d', 'QuantizedSubmConv3d', 'SubmConv3d']

@@ -1,0 +1,148 @@
+"""Dispatch of a prebuilt relation to the native conv kernels
+(mlx_lattice/ops/_relation_exec.py:19-250).
+
+Route policy (this build's, the reference routes by Metal capability):
+fp16/bf16 features with ``C_in % 32 == 0``, ``C_out`` in {16, 32, 64, 128,
+256} and at most 32 kernel offsets run the matrix-core implicit GEMM over the
+mask-sorted view; everything else (fp32, small or odd channel counts) runs
+the CSR bandwidth kernel.  Both routes compute the same sum with an fp32
+accumulator.
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from mlx_lattice_amd._native import ext
+from mlx_lattice_amd.core.quantized import QuantizedWeight
+from mlx_lattice_amd.core.relations import KernelRelation
+
+_MATRIX_CORE_C_OUT = (16, 32, 64, 128, 256)
+_WEIGHT_CACHE: dict[int, tuple[weakref.ReferenceType, tuple, torch.dtype,
+                               torch.Tensor]] = {}
+
+
+def _empty_i32(device) -> torch.Tensor:
+    return torch.empty(0, dtype=torch.int32, device=device)
+
+
+def _require_static(relation: KernelRelation) -> None:
+    if relation.n_out_capacity is None or relation.n_kernels is None:
+        raise ValueError('kernel relation is missing static shape metadata.')
+
+
+def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
+                          relation: KernelRelation) -> bool:
+    return (relation.contract.kind in ('forward', 'target', 'submanifold')
+            and dtype in (torch.float16, torch.bfloat16)
+            and c_in % 32 == 0 and c_out in _MATRIX_CORE_C_OUT
+            and relation.n_kernels is not None and relation.n_kernels <= 32)
+
+
+def sparse_conv_features_from_relation(feats: torch.Tensor,
+                                       weight: torch.Tensor,
+                                       relation: KernelRelation,
+                                       ) -> torch.Tensor:
+    """Execute sparse convolution over a prebuilt relation
+    (_relation_exec.py:84-116)."""
+    _require_static(relation)
+    c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
+    if feats.ndim == 2 and _matrix_core_eligible(
+            feats.dtype, int(feats.shape[1]), c_out, relation):
+        return sparse_conv_features_sorted_from_relation(feats, weight,
+                                                         relation)
+    input_csr = relation.input_csr
+    kernel_csr = relation.kernel_csr
+    if input_csr.edge_ids is None or kernel_csr.edge_ids is None:
+        raise ValueError('kernel relation is missing grouped CSR views.')
+    return ext.sparse_conv_features(
+        feats, weight, relation.edges.in_rows, relation.edges.out_rows,
+        relation.edges.kernel_ids, relation.counts,
+        relation.output_csr.row_offsets, input_csr.row_offsets,
+        input_csr.edge_ids, kernel_csr.row_offsets, kernel_csr.edge_ids,
+        relation.n_out_capacity, relation.n_kernels)
+
+
+def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
+                                              weight: torch.Tensor,
+                                              relation: KernelRelation, *,
+                                              store_sorted: bool = False,
+                                              ) -> torch.Tensor:
+    """Matrix-core implicit GEMM over the sorted view
+    (_relation_exec.py:119-156)."""
+    _require_static(relation)
+    c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
+    if not _matrix_core_eligible(feats.dtype, int(feats.shape[1]), c_out,
+                                 relation):
+        raise ValueError(
+            'sorted implicit GEMM is not supported for this relation, '
+            'feature tensor, or weight tensor.')
+    view = relation.require_sorted_implicit_gemm()
+    return ext.sparse_conv_features_sorted_implicit_gemm(
+        feats, _matrix_core_weight(weight), view.sorted_out_in_map,
+        view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
+        relation.edges.in_rows, relation.edges.out_rows,
+        relation.edges.kernel_ids, relation.counts,
+        relation.output_csr.row_offsets, relation.input_csr.row_offsets,
+        relation.in_edge_ids, relation.kernel_csr.row_offsets,
+        relation.kernel_edge_ids, relation.n_out_capacity,
+        relation.n_kernels, store_sorted=store_sorted)
+
+
+def sparse_quantized_conv_features_from_relation(
+        feats: torch.Tensor, weight: QuantizedWeight,
+        relation: KernelRelation) -> torch.Tensor:
+    """Quantized sparse convolution over a prebuilt relation
+    (_relation_exec.py:19-61); the sorted plan is passed when the matrix-core
+    route applies."""
+    _require_static(relation)
+    if relation.n_kernels != weight.weight.shape[0]:
+        raise ValueError('quantized weight kernel rows must match the relation.')
+    device = feats.device
+    kv = reorder = tiles = _empty_i32(device)
+    if _matrix_core_eligible(feats.dtype, weight.in_channels,
+                             weight.out_channels, relation):
+        view = relation.require_sorted_implicit_gemm()
+        kv = view.sorted_kv_out_in_map
+        reorder = view.reorder_rows
+        tiles = view.tile_masks
+    return ext.sparse_quantized_conv_features(
+        feats, weight.weight, weight.scales, weight.biases,
+        relation.edges.in_rows, relation.edges.out_rows,
+        relation.edges.kernel_ids, relation.counts,
+        relation.output_csr.row_offsets, kv, reorder, tiles,
+        relation.n_out_capacity, relation.n_kernels, weight.in_channels,
+        weight.out_channels, weight.storage_in_channels, weight.group_size,
+        weight.bits)
+
+
+def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:
+    """5D weights go to the kernels as they are (C_in contiguous per
+    (C_out, k)); a mapped ``(K, C_in, C_out)`` weight is transposed once to
+    ``(C_out, K, 1, 1, C_in)`` and cached by identity like the reference's
+    ``_mapped_weight`` (_relation_exec.py:217-250)."""
+    if weight.ndim == 5:
+        return weight
+    key = id(weight)
+    shape = tuple(weight.shape)
+    cached = _WEIGHT_CACHE.get(key)
+    if cached is not None:
+        ref, cached_shape, cached_dtype, value = cached
+        if (ref() is weight and cached_shape == shape
+                and cached_dtype == weight.dtype
+                and value._version_of_source == weight._version):
+            return value
+    k, c_in, c_out = shape
+    packed = weight.permute(2, 0, 1).contiguous().reshape(c_out, k, 1, 1, c_in)
+    packed._version_of_source = weight._version
+
+    def _drop(ref, key=key):
+        entry = _WEIGHT_CACHE.get(key)
+        if entry is not None and entry[0] is ref:
+            _WEIGHT_CACHE.pop(key, None)
+
+    _WEIGHT_CACHE[key] = (weakref.ref(weight, _drop), shape, weight.dtype,
+                          packed)
+    return packed

@@ -1,0 +1,155 @@
+// Python module `_ext`: the reference's native binding surface
+// (native/bindings/coords.cpp:414-626, convolution.cpp:12-274) over torch
+// device tensors.  Relation builders return the reference's 10-tuple
+// (coords.cpp:79-92); the *_with_view variants append the implicit-GEMM view
+// (out_in_map, row_masks) computed by the same pass.
+
+#include <torch/extension.h>
+
+#include <array>
+#include <vector>
+
+#include "features/convolution/api.h"
+#include "features/coordinates/relations.h"
+#include "lattice_hip.h"
+
+namespace ln = lattice_native;
+namespace py = pybind11;
+
+namespace {
+
+ln::Triple triple_from_values(const std::vector<int>& values, const char* name) {
+    if (values.size() == 1) return {values[0], values[0], values[0]};
+    if (values.size() != 3) throw std::invalid_argument(std::string(name) + " must be an int or a 3-tuple.");
+    return {values[0], values[1], values[2]};
+}
+
+py::tuple relation_tuple(const ln::NativeKernelRelation& r) {
+    return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
+                          r.in_row_offsets, r.in_edge_ids, r.kernel_row_offsets, r.kernel_edge_ids);
+}
+
+py::tuple relation_tuple_with_view(const ln::NativeKernelRelation& r) {
+    return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
+                          r.in_row_offsets, r.in_edge_ids, r.kernel_row_offsets, r.kernel_edge_ids, r.out_in_map,
+                          r.row_masks);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "MI355X-native sparse convolution hot path (gfx950 HIP kernels behind a C ABI).";
+    m.def("version", []() { return std::string(lattice_hip_version()); });
+    m.def("coord_hash_capacity", [](int rows) { return lattice_hip_coord_hash_capacity(rows); }, py::arg("rows"));
+    m.def(
+        "kernel_offsets",
+        [](const std::vector<int>& kernel_size, const std::vector<int>& dilation) {
+            return ln::kernel_offsets(triple_from_values(kernel_size, "kernel_size"),
+                                      triple_from_values(dilation, "dilation"));
+        },
+        py::arg("kernel_size"), py::arg("dilation"));
+
+    auto forward = [](bool with_view) {
+        return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,
+                           const std::vector<int>& kernel_size, const std::vector<int>& stride,
+                           const std::vector<int>& padding, const std::vector<int>& dilation, bool check_range) {
+            auto r = ln::make_kernel_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
+                                              triple_from_values(stride, "stride"),
+                                              triple_from_values(padding, "padding"),
+                                              triple_from_values(dilation, "dilation"), check_range);
+            return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
+        };
+    };
+    m.def("build_kernel_relation", forward(false), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
+          py::arg("check_range") = true, "Build a forward sparse kernel relation.");
+    m.def("build_kernel_relation_with_view", forward(true), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
+          py::arg("check_range") = true);
+
+    auto subm = [](bool with_view) {
+        return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,
+                           const std::vector<int>& kernel_size, const std::vector<int>& dilation, bool check_range) {
+            auto r = ln::make_submanifold_kernel_relation(coords, active_rows,
+                                                          triple_from_values(kernel_size, "kernel_size"),
+                                                          triple_from_values(dilation, "dilation"), check_range);
+            return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
+        };
+    };
+    m.def("build_submanifold_kernel_relation", subm(false), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true,
+          "Build a submanifold sparse kernel relation.");
+    m.def("build_submanifold_kernel_relation_with_view", subm(true), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+
+    auto target = [](bool with_view) {
+        return [with_view](const at::Tensor& coords, const at::Tensor& active_rows, const at::Tensor& target_coords,
+                           const at::Tensor& target_active_rows, const std::vector<int>& kernel_size,
+                           const std::vector<int>& stride, const std::vector<int>& padding,
+                           const std::vector<int>& dilation, bool check_range) {
+            auto r = ln::make_target_kernel_relation(
+                coords, active_rows, target_coords, target_active_rows,
+                triple_from_values(kernel_size, "kernel_size"), triple_from_values(stride, "stride"),
+                triple_from_values(padding, "padding"), triple_from_values(dilation, "dilation"), check_range);
+            return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
+        };
+    };
+    m.def("build_target_kernel_relation", target(false), py::arg("coords"), py::arg("active_rows"),
+          py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
+          py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true,
+          "Build a target-aligned sparse kernel relation.");
+    m.def("build_target_kernel_relation_with_view", target(true), py::arg("coords"), py::arg("active_rows"),
+          py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
+          py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+
+    m.def(
+        "build_relation_implicit_gemm_view",
+        [](const at::Tensor& source_coords, const at::Tensor& source_active_rows, const at::Tensor& output_coords,
+           const at::Tensor& output_active_rows, const at::Tensor& offsets, const std::vector<int>& stride,
+           const std::vector<int>& padding) {
+            auto r = ln::make_relation_implicit_gemm_view(source_coords, source_active_rows, output_coords,
+                                                          output_active_rows, offsets,
+                                                          triple_from_values(stride, "stride"),
+                                                          triple_from_values(padding, "padding"));
+            return py::make_tuple(std::get<0>(r), std::get<1>(r));
+        },
+        py::arg("source_coords"), py::arg("source_active_rows"), py::arg("output_coords"),
+        py::arg("output_active_rows"), py::arg("offsets"), py::arg("stride"), py::arg("padding"),
+        "Build the dense output-to-input implicit-GEMM map.");
+    m.def(
+        "build_sorted_implicit_gemm_view",
+        [](const at::Tensor& out_in_map, const at::Tensor& row_masks) {
+            auto r = ln::make_sorted_implicit_gemm_view(out_in_map, row_masks);
+            return py::make_tuple(std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r));
+        },
+        py::arg("out_in_map"), py::arg("row_masks"),
+        "Return (reorder_rows, sorted_out_in_map, sorted_kv_out_in_map, tile_masks).");
+
+    m.def("sparse_conv_features", &ln::sparse_conv_features, py::arg("feats"), py::arg("weights"),
+          py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
+          py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("kernel_row_offsets"),
+          py::arg("kernel_edge_ids"), py::arg("out_capacity"), py::arg("n_kernels"));
+    m.def(
+        "sparse_conv_features_sorted_implicit_gemm",
+        [](const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& sorted_out_in_map,
+           const at::Tensor& sorted_kv_out_in_map, const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
+           const at::Tensor& /*in_rows*/, const at::Tensor& /*out_rows*/, const at::Tensor& /*kernel_ids*/,
+           const at::Tensor& /*counts*/, const at::Tensor& /*row_offsets*/, const at::Tensor& /*in_row_offsets*/,
+           const at::Tensor& /*in_edge_ids*/, const at::Tensor& /*kernel_row_offsets*/,
+           const at::Tensor& /*kernel_edge_ids*/, int out_capacity, int n_kernels, bool store_sorted) {
+            return ln::sparse_conv_features_sorted_implicit_gemm(feats, weights, sorted_out_in_map,
+                                                                 sorted_kv_out_in_map, reorder_rows, tile_masks,
+                                                                 out_capacity, n_kernels, store_sorted);
+        },
+        py::arg("feats"), py::arg("weights"), py::arg("sorted_out_in_map"), py::arg("sorted_kv_out_in_map"),
+        py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("in_rows"), py::arg("out_rows"),
+        py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("in_row_offsets"),
+        py::arg("in_edge_ids"), py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("out_capacity"),
+        py::arg("n_kernels"), py::kw_only(), py::arg("store_sorted") = false);
+    m.def("sparse_quantized_conv_features", &ln::sparse_quantized_conv_features, py::arg("feats"),
+          py::arg("weights"), py::arg("scales"), py::arg("biases"), py::arg("in_rows"), py::arg("out_rows"),
+          py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("sorted_kv_out_in_map"),
+          py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("out_capacity"), py::arg("n_kernels"),
+          py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"), py::arg("group_size"),
+          py::arg("bits"));
+}

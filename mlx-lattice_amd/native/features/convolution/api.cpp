@@ -1,0 +1,237 @@
+#include "features/convolution/api.h"
+
+#include <stdexcept>
+#include <string>
+
+#include "foundation/runtime.h"
+
+namespace lattice_native {
+
+namespace {
+
+int dtype_code(const at::Tensor& t, const char* op) {
+    switch (t.scalar_type()) {
+    case at::kFloat: return LATTICE_F32;
+    case at::kHalf: return LATTICE_F16;
+    case at::kBFloat16: return LATTICE_BF16;
+    default:
+        throw std::invalid_argument(std::string(op) + " supports float32 and float16 feats.");
+    }
+}
+
+void require_i32_vector(const at::Tensor& t, const char* message) {
+    if (t.dim() != 1 || t.scalar_type() != at::kInt) throw std::invalid_argument(message);
+}
+
+void validate_weights(const at::Tensor& feats, const at::Tensor& weights, int n_kernels, const char* op) {
+    if (feats.dim() != 2) throw std::invalid_argument("feats must have shape (N, C_in).");
+    if (weights.dim() != 3 && weights.dim() != 5) {
+        throw std::invalid_argument("weights must have shape (K, C_in, C_out) or (C_out, Kx, Ky, Kz, C_in).");
+    }
+    dtype_code(feats, op);
+    if (weights.scalar_type() != feats.scalar_type()) {
+        throw std::invalid_argument(std::string(op) + " weights must match feats dtype.");
+    }
+    const int64_t w_in = weights.dim() == 3 ? weights.size(1) : weights.size(4);
+    if (feats.size(1) != w_in) throw std::invalid_argument("feats channels must match weights input channels.");
+    if (n_kernels <= 0) {
+        throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    if (weights.dim() == 3 && weights.size(0) != n_kernels) {
+        throw std::invalid_argument("weights kernel rows must match n_kernels.");
+    }
+    if (weights.dim() == 5 && weights.size(1) * weights.size(2) * weights.size(3) != n_kernels) {
+        throw std::invalid_argument("weights kernel rows must match n_kernels.");
+    }
+    require_device(feats, "feats");
+    require_device(weights, "weights");
+}
+
+int64_t out_channels_of(const at::Tensor& weights) { return weights.dim() == 3 ? weights.size(2) : weights.size(0); }
+
+}  // namespace
+
+at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& weights_in, const at::Tensor& in_rows,
+                                const at::Tensor& out_rows, const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                const at::Tensor& row_offsets, const at::Tensor& in_row_offsets,
+                                const at::Tensor& in_edge_ids, const at::Tensor& kernel_row_offsets,
+                                const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels) {
+    const char* op = "sparse_conv_features";
+    if (out_capacity < 0) {
+        throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    validate_weights(feats_in, weights_in, n_kernels, op);
+    if (in_rows.dim() != 1 || out_rows.dim() != 1 || kernel_ids.dim() != 1) {
+        throw std::invalid_argument("relation rows and kernel_ids must be one-dimensional.");
+    }
+    if (in_rows.scalar_type() != at::kInt || out_rows.scalar_type() != at::kInt ||
+        kernel_ids.scalar_type() != at::kInt) {
+        throw std::invalid_argument("relation rows and kernel_ids must use int32 dtype.");
+    }
+    if (in_rows.size(0) != out_rows.size(0) || in_rows.size(0) != kernel_ids.size(0)) {
+        throw std::invalid_argument("relation row arrays and kernel_ids must have equal capacity.");
+    }
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("counts must have shape (2,) and int32 dtype.");
+    }
+    require_i32_vector(row_offsets, "row_offsets must be a one-dimensional int32 array.");
+    if (in_row_offsets.dim() != 1 || in_row_offsets.scalar_type() != at::kInt || kernel_row_offsets.dim() != 1 ||
+        kernel_row_offsets.scalar_type() != at::kInt) {
+        throw std::invalid_argument("plan row_offsets must be one-dimensional int32 arrays.");
+    }
+    if (in_edge_ids.dim() != 1 || kernel_edge_ids.dim() != 1 || in_edge_ids.scalar_type() != at::kInt ||
+        kernel_edge_ids.scalar_type() != at::kInt) {
+        throw std::invalid_argument("plan edge_ids must be one-dimensional int32 arrays.");
+    }
+    if (row_offsets.size(0) != out_capacity + 1) {
+        throw std::invalid_argument("row_offsets length must match out_capacity + 1.");
+    }
+    if (in_row_offsets.size(0) != feats_in.size(0) + 1) {
+        throw std::invalid_argument("in_row_offsets length must match input capacity + 1.");
+    }
+    if (kernel_row_offsets.size(0) != n_kernels + 1) {
+        throw std::invalid_argument("kernel_row_offsets length must match n_kernels + 1.");
+    }
+    if (in_edge_ids.size(0) != in_rows.size(0) || kernel_edge_ids.size(0) != in_rows.size(0)) {
+        throw std::invalid_argument("plan edge_ids must match relation edge capacity.");
+    }
+    const at::Tensor feats = feats_in.contiguous();
+    const at::Tensor weights = weights_in.contiguous();
+    const int64_t c_out = out_channels_of(weights);
+    at::Tensor out = at::empty({out_capacity, c_out}, feats.options());
+    const int layout = weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D;
+    check_status(lattice_hip_sparse_conv_features(
+        dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
+        weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
+        ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(),
+        current_stream(feats)));
+    return out;
+}
+
+at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in, const at::Tensor& weights_in,
+                                                     const at::Tensor& sorted_out_in_map,
+                                                     const at::Tensor& sorted_kv_out_in_map,
+                                                     const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
+                                                     int out_capacity, int n_kernels, bool store_sorted) {
+    const char* op = "sparse_conv_features_sorted_implicit_gemm";
+    if (sorted_out_in_map.dim() != 2 || sorted_out_in_map.scalar_type() != at::kInt) {
+        throw std::invalid_argument("sorted_out_in_map must have shape (N_out, K) and int32 dtype.");
+    }
+    require_i32_vector(reorder_rows, "reorder_rows must have shape (N_out,) and int32 dtype.");
+    require_i32_vector(tile_masks, "tile_masks must have shape (ceil(N_out / 64) * 4,) and int32 dtype.");
+    if (sorted_out_in_map.size(0) != out_capacity || sorted_out_in_map.size(1) != n_kernels ||
+        reorder_rows.size(0) != out_capacity) {
+        throw std::invalid_argument("sorted convolution view shape must match out_capacity and n_kernels.");
+    }
+    if (tile_masks.size(0) != ((out_capacity + 63) / 64) * 4) {
+        throw std::invalid_argument("tile_masks length must match ceil(out_capacity / 64) * 4.");
+    }
+    if (sorted_kv_out_in_map.dim() != 2 || sorted_kv_out_in_map.scalar_type() != at::kInt ||
+        sorted_kv_out_in_map.size(0) != n_kernels || sorted_kv_out_in_map.size(1) != out_capacity) {
+        throw std::invalid_argument("sorted_kv_out_in_map shape must match out_capacity and n_kernels.");
+    }
+    if (out_capacity < 0) {
+        throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    validate_weights(feats_in, weights_in, n_kernels, op);
+    const at::Tensor feats = feats_in.contiguous();
+    // The matrix-core B operand wants C_in contiguous per (C_out, k): the
+    // dense 5D layout.  A mapped (K, C_in, C_out) weight is transposed once.
+    const at::Tensor weights =
+        weights_in.dim() == 5 ? weights_in.contiguous() : weights_in.permute({2, 0, 1}).contiguous();
+    const int64_t c_out = out_channels_of(weights_in);
+    at::Tensor out = at::empty({out_capacity, c_out}, feats.options());
+    const at::Tensor map = sorted_out_in_map.contiguous();
+    const at::Tensor order = reorder_rows.contiguous();
+    check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
+        dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
+        weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(map),
+        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), current_stream(feats)));
+    return out;
+}
+
+at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::Tensor& weights_in,
+                                          const at::Tensor& scales_in, const at::Tensor& biases_in,
+                                          const at::Tensor& in_rows, const at::Tensor& out_rows,
+                                          const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                          const at::Tensor& row_offsets, const at::Tensor& sorted_kv_out_in_map,
+                                          const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
+                                          int out_capacity, int n_kernels, int in_channels, int out_channels,
+                                          int storage_in_channels, int group_size, int bits) {
+    if (out_capacity < 0 || n_kernels <= 0) {
+        throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    if (feats_in.dim() != 2 || (feats_in.scalar_type() != at::kHalf && feats_in.scalar_type() != at::kFloat &&
+                                feats_in.scalar_type() != at::kBFloat16)) {
+        throw std::invalid_argument("quantized sparse convolution features must be a float16 or float32 matrix.");
+    }
+    if (weights_in.dim() != 3 || weights_in.scalar_type() != at::kUInt32) {
+        throw std::invalid_argument("packed weights must be a three-dimensional uint32 array.");
+    }
+    if (scales_in.dim() != 3 || biases_in.sizes() != scales_in.sizes() ||
+        scales_in.scalar_type() != feats_in.scalar_type() || biases_in.scalar_type() != feats_in.scalar_type()) {
+        throw std::invalid_argument(
+            "quantized scales and biases must have shape (K, C_out, G) and match the feature dtype.");
+    }
+    if (bits != 4 && bits != 8) throw std::invalid_argument("quantized convolution bits must be 4 or 8.");
+    if (group_size != 32 && group_size != 64 && group_size != 128) {
+        throw std::invalid_argument("quantized convolution group_size must be 32, 64, or 128.");
+    }
+    if (in_channels <= 0 || out_channels <= 0 || storage_in_channels < in_channels ||
+        storage_in_channels % group_size != 0) {
+        throw std::invalid_argument("quantized convolution channel metadata is invalid.");
+    }
+    const int64_t packed_words = static_cast<int64_t>(storage_in_channels) * bits / 32;
+    const int64_t groups = storage_in_channels / group_size;
+    if (weights_in.size(0) != n_kernels || weights_in.size(1) != packed_words || weights_in.size(2) != out_channels ||
+        scales_in.size(0) != n_kernels || scales_in.size(1) != groups || scales_in.size(2) != out_channels) {
+        throw std::invalid_argument("packed weight shape does not match quantized convolution metadata.");
+    }
+    if (feats_in.size(1) != in_channels) {
+        throw std::invalid_argument("feature shape does not match quantized convolution metadata.");
+    }
+    const bool has_plan = sorted_kv_out_in_map.numel() != 0 || reorder_rows.numel() != 0 || tile_masks.numel() != 0;
+    if (has_plan) {
+        if (sorted_kv_out_in_map.dim() != 2 || sorted_kv_out_in_map.size(0) != n_kernels ||
+            sorted_kv_out_in_map.size(1) != out_capacity || sorted_kv_out_in_map.scalar_type() != at::kInt ||
+            reorder_rows.dim() != 1 || reorder_rows.size(0) != out_capacity ||
+            reorder_rows.scalar_type() != at::kInt || tile_masks.dim() != 1 ||
+            tile_masks.size(0) != 4 * ((out_capacity + 63) / 64) || tile_masks.scalar_type() != at::kInt) {
+            throw std::invalid_argument("quantized convolution sorted plan shapes are invalid.");
+        }
+    }
+    if (in_rows.dim() != 1 || out_rows.dim() != 1 || kernel_ids.dim() != 1 || in_rows.scalar_type() != at::kInt ||
+        out_rows.scalar_type() != at::kInt || kernel_ids.scalar_type() != at::kInt ||
+        in_rows.sizes() != out_rows.sizes() || in_rows.sizes() != kernel_ids.sizes()) {
+        throw std::invalid_argument(
+            "quantized convolution relation edges must be equal-length one-dimensional int32 arrays.");
+    }
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("quantized convolution counts must have shape (2,) and int32 dtype.");
+    }
+    if (row_offsets.dim() != 1 || row_offsets.size(0) != out_capacity + 1 || row_offsets.scalar_type() != at::kInt) {
+        throw std::invalid_argument(
+            "quantized convolution row_offsets must have length out_capacity + 1 and int32 dtype.");
+    }
+    require_device(feats_in, "feats");
+    const at::Tensor feats = feats_in.contiguous();
+    const at::Tensor weights = weights_in.contiguous();
+    const at::Tensor scales = scales_in.contiguous();
+    const at::Tensor biases = biases_in.contiguous();
+    at::Tensor kv;
+    at::Tensor order;
+    if (has_plan) {
+        kv = sorted_kv_out_in_map.contiguous();
+        order = reorder_rows.contiguous();
+    }
+    at::Tensor out = at::empty({out_capacity, out_channels}, feats.options());
+    check_status(lattice_hip_sparse_quantized_conv_features(
+        dtype_code(feats, "quantized sparse convolution"), feats.data_ptr(), static_cast<int>(feats.size(0)),
+        in_channels, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(),
+        n_kernels, out_channels, storage_in_channels, group_size, bits, ci32(in_rows), ci32(kernel_ids),
+        ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), has_plan ? ci32(kv) : nullptr,
+        has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(), current_stream(feats)));
+    return out;
+}
+
+}  // namespace lattice_native

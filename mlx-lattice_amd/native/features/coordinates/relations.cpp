@@ -1,0 +1,222 @@
+#include "features/coordinates/relations.h"
+
+#include <stdexcept>
+#include <string>
+
+#include "foundation/runtime.h"
+
+namespace lattice_native {
+
+namespace {
+
+void validate_coords(const at::Tensor& coords, const char* name = "coords") {
+    if (coords.dim() != 2 || coords.size(1) != 4) {
+        throw std::invalid_argument(std::string(name) + " must have shape (N, 4).");
+    }
+    if (coords.scalar_type() != at::kInt && coords.scalar_type() != at::kLong) {
+        throw std::invalid_argument(std::string(name) + " must be int32 or int64.");
+    }
+    if (coords.scalar_type() != at::kInt) {
+        throw std::invalid_argument("GPU sparse relations require int32 coordinates.");
+    }
+    require_device(coords, name);
+}
+
+void validate_active_rows(const at::Tensor& active_rows) {
+    if (active_rows.dim() != 1 || active_rows.size(0) != 1 || active_rows.scalar_type() != at::kInt) {
+        throw std::invalid_argument("active_rows must have shape (1,) and int32 dtype.");
+    }
+    require_device(active_rows, "active_rows");
+}
+
+void validate_positive(const Triple& v, const char* name) {
+    for (int x : v) {
+        if (x <= 0) throw std::invalid_argument(std::string(name) + " values must be positive.");
+    }
+}
+
+void validate_nonnegative(const Triple& v, const char* name) {
+    for (int x : v) {
+        if (x < 0) throw std::invalid_argument(std::string(name) + " values must be non-negative.");
+    }
+}
+
+// Raises when a builder flagged an active coordinate that does not fit the
+// packed key (reads one device word; the only host wait of a build).
+void check_coordinate_range(const at::Tensor& status) {
+    if (status.item<int32_t>() & LATTICE_STATUS_COORD_RANGE) {
+        throw std::invalid_argument(
+            "coordinates exceed the GPU packed-key range: batch must lie in [0, 1022] and x, y, z in "
+            "[-131072, 131071].");
+    }
+}
+
+NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_capacity, int K, bool coords) {
+    const int64_t edges = static_cast<int64_t>(out_capacity) * K;
+    NativeKernelRelation r;
+    r.in_rows = empty_i32({edges}, like);
+    r.out_rows = empty_i32({edges}, like);
+    r.kernel_ids = empty_i32({edges}, like);
+    r.output_row_offsets = empty_i32({out_capacity + 1}, like);
+    if (coords) r.out_coords = empty_i32({out_capacity, 4}, like);
+    r.counts = empty_i32({2}, like);
+    r.in_row_offsets = empty_i32({in_capacity + 1}, like);
+    r.in_edge_ids = empty_i32({edges}, like);
+    r.kernel_row_offsets = empty_i32({K + 1}, like);
+    r.kernel_edge_ids = empty_i32({edges}, like);
+    r.out_in_map = empty_i32({out_capacity, K}, like);
+    r.row_masks = empty_i32({out_capacity, (K + 31) / 32}, like);
+    return r;
+}
+
+lattice_relation_outputs outputs_of(NativeKernelRelation& r, at::Tensor& status) {
+    lattice_relation_outputs o{};
+    o.in_rows = i32(r.in_rows);
+    o.out_rows = i32(r.out_rows);
+    o.kernel_ids = i32(r.kernel_ids);
+    o.row_offsets = i32(r.output_row_offsets);
+    o.out_coords = r.out_coords.defined() ? i32(r.out_coords) : nullptr;
+    o.counts = i32(r.counts);
+    o.in_row_offsets = i32(r.in_row_offsets);
+    o.in_edge_ids = i32(r.in_edge_ids);
+    o.kernel_row_offsets = i32(r.kernel_row_offsets);
+    o.kernel_edge_ids = i32(r.kernel_edge_ids);
+    o.out_in_map = i32(r.out_in_map);
+    o.row_masks = i32(r.row_masks);
+    o.status = i32(status);
+    return o;
+}
+
+}  // namespace
+
+std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation) {
+    validate_positive(kernel_size, "kernel_size");
+    validate_positive(dilation, "dilation");
+    const int K = lattice_hip_kernel_offsets(kernel_size.data(), dilation.data(), nullptr);
+    std::vector<int32_t> flat(static_cast<size_t>(K) * 3);
+    lattice_hip_kernel_offsets(kernel_size.data(), dilation.data(), flat.data());
+    std::vector<Triple> out(static_cast<size_t>(K));
+    for (int k = 0; k < K; ++k) out[k] = {flat[3 * k], flat[3 * k + 1], flat[3 * k + 2]};
+    return out;
+}
+
+NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
+                                          Triple kernel_size, Triple stride, Triple padding, Triple dilation,
+                                          bool check_range) {
+    validate_coords(coords_in);
+    validate_active_rows(active_rows);
+    validate_positive(kernel_size, "kernel_size");
+    validate_positive(stride, "stride");
+    validate_nonnegative(padding, "padding");
+    validate_positive(dilation, "dilation");
+    const at::Tensor coords = coords_in.contiguous();
+    const int rows = static_cast<int>(coords.size(0));
+    const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
+    NativeKernelRelation r = allocate(coords, rows, rows, K, true);
+    at::Tensor status = empty_i32({1}, coords);
+    lattice_relation_outputs o = outputs_of(r, status);
+    at::Tensor ws = workspace(lattice_hip_kernel_relation_workspace_bytes(rows, K), coords);
+    check_status(lattice_hip_build_kernel_relation(ci32(coords), rows, ci32(active_rows), kernel_size.data(),
+                                                   stride.data(), padding.data(), dilation.data(), &o,
+                                                   ws.data_ptr(), static_cast<size_t>(ws.numel()),
+                                                   current_stream(coords)));
+    if (check_range) check_coordinate_range(status);
+    return r;
+}
+
+NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
+                                                      Triple kernel_size, Triple dilation, bool check_range) {
+    return make_kernel_relation(coords, active_rows, kernel_size, {1, 1, 1}, {0, 0, 0}, dilation, check_range);
+}
+
+NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
+                                                 const at::Tensor& target_in, const at::Tensor& target_active_rows,
+                                                 Triple kernel_size, Triple stride, Triple padding,
+                                                 Triple dilation, bool check_range) {
+    validate_coords(coords_in);
+    validate_coords(target_in, "target_coords");
+    validate_active_rows(active_rows);
+    validate_active_rows(target_active_rows);
+    validate_positive(kernel_size, "kernel_size");
+    validate_positive(stride, "stride");
+    validate_nonnegative(padding, "padding");
+    validate_positive(dilation, "dilation");
+    const at::Tensor coords = coords_in.contiguous();
+    const at::Tensor target = target_in.contiguous();
+    const int rows = static_cast<int>(coords.size(0));
+    const int target_rows = static_cast<int>(target.size(0));
+    const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
+    NativeKernelRelation r = allocate(coords, target_rows, rows, K, false);
+    r.out_coords = target;
+    at::Tensor status = empty_i32({1}, coords);
+    lattice_relation_outputs o = outputs_of(r, status);
+    o.out_coords = nullptr;
+    at::Tensor ws = workspace(lattice_hip_target_relation_workspace_bytes(rows, target_rows, K), coords);
+    check_status(lattice_hip_build_target_kernel_relation(
+        ci32(coords), rows, ci32(active_rows), ci32(target), target_rows, ci32(target_active_rows),
+        kernel_size.data(), stride.data(), padding.data(), dilation.data(), &o, ws.data_ptr(),
+        static_cast<size_t>(ws.numel()), current_stream(coords)));
+    if (check_range) check_coordinate_range(status);
+    return r;
+}
+
+std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(
+    const at::Tensor& source_in, const at::Tensor& source_active_rows, const at::Tensor& output_in,
+    const at::Tensor& output_active_rows, const at::Tensor& offsets_in, Triple stride, Triple padding) {
+    validate_coords(source_in, "source_coords");
+    validate_coords(output_in, "output_coords");
+    validate_active_rows(source_active_rows);
+    validate_active_rows(output_active_rows);
+    if (offsets_in.dim() != 2 || offsets_in.size(1) != 3 || offsets_in.scalar_type() != at::kInt) {
+        throw std::invalid_argument("offsets must have shape (K, 3) and int32 dtype.");
+    }
+    validate_positive(stride, "stride");
+    validate_nonnegative(padding, "padding");
+    const at::Tensor source = source_in.contiguous();
+    const at::Tensor output = output_in.contiguous();
+    const at::Tensor offsets = offsets_in.to(source.device()).contiguous();
+    const int source_rows = static_cast<int>(source.size(0));
+    const int output_rows = static_cast<int>(output.size(0));
+    const int K = static_cast<int>(offsets.size(0));
+    if (K <= 0) throw std::invalid_argument("offsets must have shape (K, 3) with K > 0.");
+    at::Tensor out_in_map = empty_i32({output_rows, K}, source);
+    at::Tensor row_masks = empty_i32({output_rows, (K + 31) / 32}, source);
+    at::Tensor status = empty_i32({1}, source);
+    at::Tensor ws = workspace(lattice_hip_implicit_gemm_view_workspace_bytes(source_rows), source);
+    check_status(lattice_hip_build_relation_implicit_gemm_view(
+        ci32(source), source_rows, ci32(source_active_rows), ci32(output), output_rows,
+        ci32(output_active_rows), ci32(offsets), K, stride.data(), padding.data(), i32(out_in_map),
+        i32(row_masks), i32(status), ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream(source)));
+    check_coordinate_range(status);
+    return {out_in_map, row_masks};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_sorted_implicit_gemm_view(
+    const at::Tensor& out_in_map_in, const at::Tensor& row_masks_in) {
+    if (out_in_map_in.dim() != 2 || out_in_map_in.scalar_type() != at::kInt) {
+        throw std::invalid_argument("out_in_map must have shape (Nout, K) and int32 dtype.");
+    }
+    if (row_masks_in.dim() != 2 || row_masks_in.scalar_type() != at::kInt ||
+        row_masks_in.size(0) != out_in_map_in.size(0)) {
+        throw std::invalid_argument("row_masks must have one row per out_in_map row.");
+    }
+    if (row_masks_in.size(1) != 1) {
+        throw std::invalid_argument("sorted implicit GEMM view currently supports K <= 32.");
+    }
+    require_device(out_in_map_in, "out_in_map");
+    const at::Tensor map = out_in_map_in.contiguous();
+    const at::Tensor masks = row_masks_in.contiguous();
+    const int rows = static_cast<int>(map.size(0));
+    const int K = static_cast<int>(map.size(1));
+    at::Tensor reorder = empty_i32({rows}, map);
+    at::Tensor sorted = empty_i32({rows, K}, map);
+    at::Tensor kv = empty_i32({K, rows}, map);
+    at::Tensor tiles = empty_i32({((rows + 63) / 64) * 4}, map);
+    at::Tensor ws = workspace(lattice_hip_sorted_view_workspace_bytes(rows), map);
+    check_status(lattice_hip_build_sorted_implicit_gemm_view(ci32(map), ci32(masks), rows, K, i32(reorder),
+                                                             i32(sorted), i32(kv), i32(tiles), ws.data_ptr(),
+                                                             static_cast<size_t>(ws.numel()), current_stream(map)));
+    return {reorder, sorted, kv, tiles};
+}
+
+}  // namespace lattice_native

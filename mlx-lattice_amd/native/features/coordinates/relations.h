@@ -1,0 +1,58 @@
+// Relation builders over torch device tensors: validation, output and
+// workspace allocation on the caller's device and current stream, then the
+// C-ABI call.  Mirrors native/features/coordinates/api.h:67-136 of the
+// reference.
+#pragma once
+
+#include <torch/extension.h>
+
+#include <array>
+#include <tuple>
+
+namespace lattice_native {
+
+using Triple = std::array<int, 3>;
+
+struct NativeKernelRelation {
+    at::Tensor in_rows;
+    at::Tensor out_rows;
+    at::Tensor kernel_ids;
+    at::Tensor output_row_offsets;
+    at::Tensor out_coords;
+    at::Tensor counts;
+    at::Tensor in_row_offsets;
+    at::Tensor in_edge_ids;
+    at::Tensor kernel_row_offsets;
+    at::Tensor kernel_edge_ids;
+    // Dense implicit-GEMM view computed by the same query pass.
+    at::Tensor out_in_map;
+    at::Tensor row_masks;
+};
+
+std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation);
+
+// check_range: read the device status word after the build and raise when an
+// active coordinate does not fit the packed key (one host wait).
+NativeKernelRelation make_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
+                                          Triple kernel_size, Triple stride, Triple padding, Triple dilation,
+                                          bool check_range = true);
+
+NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
+                                                      Triple kernel_size, Triple dilation,
+                                                      bool check_range = true);
+
+NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
+                                                 const at::Tensor& target_coords,
+                                                 const at::Tensor& target_active_rows, Triple kernel_size,
+                                                 Triple stride, Triple padding, Triple dilation,
+                                                 bool check_range = true);
+
+std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(
+    const at::Tensor& source_coords, const at::Tensor& source_active_rows, const at::Tensor& output_coords,
+    const at::Tensor& output_active_rows, const at::Tensor& offsets, Triple stride, Triple padding);
+
+// (reorder_rows, sorted_out_in_map, sorted_kv_out_in_map, tile_masks)
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_sorted_implicit_gemm_view(
+    const at::Tensor& out_in_map, const at::Tensor& row_masks);
+
+}  // namespace lattice_native

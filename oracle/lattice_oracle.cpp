@@ -1,0 +1,480 @@
+// CPU oracle for the sparse-convolution hot path.
+//
+// TEST INFRASTRUCTURE ONLY.  This file is a plain-C++ (MLX-free) restatement
+// of the reference CPU route of utakotoba/mlx-lattice.  Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, as the
+// checker or as the timed CPU baseline; the product path never calls it.
+//
+// Each function names the reference lines it follows.  Coordinates are read
+// as int64 exactly as the reference does (common_detail.h:78-107), so
+// candidate coordinates never wrap.
+//
+// Build: see oracle/Makefile (g++ -O3 -mf16c -shared -fPIC).
+
+#include <immintrin.h>
+
+#include <algorithm>
+#include <array>
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+namespace {
+
+using Coord = std::array<int64_t, 4>;
+using Edge = std::array<int32_t, 3>;
+
+// FNV-1a over the four coordinate words, masked to 31 bits.  Follows
+// native/features/coordinates/cpu/common_detail.h:68-77.  The hash only
+// affects bucket placement; results do not depend on it.
+struct CoordHash {
+    size_t operator()(const Coord& c) const {
+        uint32_t h = 2166136261u;
+        for (int i = 0; i < 4; ++i) {
+            h = (h ^ static_cast<uint32_t>(c[i])) * 16777619u;
+        }
+        return static_cast<size_t>(h & 0x7fffffffu);
+    }
+};
+
+using RowMap = std::unordered_map<Coord, int32_t, CoordHash>;
+
+std::vector<Coord> read_coords(const int32_t* coords, int rows) {
+    std::vector<Coord> out(static_cast<size_t>(rows));
+    for (int r = 0; r < rows; ++r) {
+        for (int a = 0; a < 4; ++a) {
+            out[r][a] = coords[static_cast<size_t>(r) * 4 + a];
+        }
+    }
+    return out;
+}
+
+// first_row_map: quantization_detail.h:395-402 (emplace keeps the first row).
+RowMap first_row_map(const std::vector<Coord>& values) {
+    RowMap rows;
+    rows.reserve(values.size());
+    for (int r = 0; r < static_cast<int>(values.size()); ++r) {
+        rows.emplace(values[r], r);
+    }
+    return rows;
+}
+
+// floor_div: quantization_detail.h:3-10.
+int64_t floor_div(int64_t v, int64_t d) {
+    int64_t q = v / d;
+    int64_t r = v % d;
+    if (r != 0 && ((r < 0) != (d < 0))) {
+        --q;
+    }
+    return q;
+}
+
+// downsample_values: quantization_detail.h:12-31 (first-seen order).
+std::vector<Coord> downsample_values(const std::vector<Coord>& values,
+                                     const int* stride) {
+    std::vector<Coord> out;
+    std::unordered_set<Coord, CoordHash> seen;
+    seen.reserve(values.size());
+    for (const auto& c : values) {
+        Coord q = {c[0], floor_div(c[1], stride[0]), floor_div(c[2], stride[1]),
+                   floor_div(c[3], stride[2])};
+        if (seen.insert(q).second) {
+            out.push_back(q);
+        }
+    }
+    return out;
+}
+
+// kernel_input_coord: relation_views_detail.h:1-13.
+Coord kernel_input_coord(const Coord& o, const int* off, const int* stride,
+                         const int* pad) {
+    return {o[0], o[1] * stride[0] + off[0] - pad[0],
+            o[2] * stride[1] + off[1] - pad[1],
+            o[3] * stride[2] + off[2] - pad[2]};
+}
+
+// write_map_rows: relation_views_detail.h:15-50.  Tails are zero-filled as
+// write_i32 does (common_detail.h:121-125).
+void write_map_rows(const std::vector<Edge>& edges, int out_capacity,
+                    int edge_capacity, int32_t* in_rows, int32_t* out_rows,
+                    int32_t* kernel_ids, int32_t* row_offsets) {
+    std::fill(in_rows, in_rows + edge_capacity, 0);
+    std::fill(out_rows, out_rows + edge_capacity, 0);
+    std::fill(kernel_ids, kernel_ids + edge_capacity, 0);
+    int current = 0;
+    int n = 0;
+    for (const auto& e : edges) {
+        while (current <= e[1] && current < out_capacity) {
+            row_offsets[current++] = n;
+        }
+        in_rows[n] = e[0];
+        out_rows[n] = e[1];
+        kernel_ids[n] = e[2];
+        ++n;
+    }
+    while (current <= out_capacity) {
+        row_offsets[current++] = n;
+    }
+}
+
+void write_coords(const std::vector<Coord>& values, int capacity,
+                  int32_t* out) {
+    std::fill(out, out + static_cast<size_t>(capacity) * 4, 0);
+    for (size_t r = 0; r < values.size(); ++r) {
+        for (int a = 0; a < 4; ++a) {
+            out[r * 4 + a] = static_cast<int32_t>(values[r][a]);
+        }
+    }
+}
+
+inline float half_to_float(uint16_t h) { return _cvtsh_ss(h); }
+inline uint16_t float_to_half(float f) {
+    return _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT);
+}
+
+int hardware_threads(int requested) {
+    if (requested > 0) {
+        return requested;
+    }
+    auto hw = std::thread::hardware_concurrency();
+    return hw == 0 ? 1 : static_cast<int>(hw);
+}
+
+// parallel_for with the reference grain: cpu/algorithms.cpp:30-67.
+template <typename Fn>
+void parallel_for(int begin, int end, int threads, Fn fn) {
+    constexpr int kGrain = 4096;
+    int count = end - begin;
+    if (count <= kGrain || threads <= 1) {
+        for (int i = begin; i < end; ++i) fn(i);
+        return;
+    }
+    int workers = std::min(threads, std::max(1, (count + kGrain - 1) / kGrain));
+    int block = (count + workers - 1) / workers;
+    std::vector<std::thread> pool;
+    for (int w = 1; w < workers; ++w) {
+        int first = begin + w * block;
+        int last = std::min(end, first + block);
+        if (first >= last) continue;
+        pool.emplace_back([first, last, &fn]() {
+            for (int i = first; i < last; ++i) fn(i);
+        });
+    }
+    int first_last = std::min(end, begin + block);
+    for (int i = begin; i < first_last; ++i) fn(i);
+    for (auto& t : pool) t.join();
+}
+
+// parallel_rows: cpu/quantized.cpp:15-44.
+template <typename Fn>
+void parallel_rows(int rows, int threads, Fn fn) {
+    int workers = std::min(rows, threads);
+    if (workers <= 1 || rows < 1024) {
+        for (int r = 0; r < rows; ++r) fn(r);
+        return;
+    }
+    int block = (rows + workers - 1) / workers;
+    std::vector<std::thread> pool;
+    for (int w = 1; w < workers; ++w) {
+        int b = w * block;
+        int e = std::min(rows, b + block);
+        if (b < e) {
+            pool.emplace_back([b, e, &fn]() {
+                for (int r = b; r < e; ++r) fn(r);
+            });
+        }
+    }
+    for (int r = 0; r < std::min(rows, block); ++r) fn(r);
+    for (auto& t : pool) t.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+// kernel_offsets: native/features/coordinates/offsets.cpp:11-45.
+// Writes K*3 ints; returns K.
+int oracle_kernel_offsets(const int* size, const int* dilation, int32_t* out) {
+    std::vector<int> axes[3];
+    for (int a = 0; a < 3; ++a) {
+        if (size[a] % 2 == 1) {
+            for (int v = -(size[a] / 2); v <= size[a] / 2; ++v) axes[a].push_back(v);
+        } else {
+            for (int v = 0; v < size[a]; ++v) axes[a].push_back(v);
+        }
+    }
+    int k = 0;
+    for (int x : axes[0])
+        for (int y : axes[1])
+            for (int z : axes[2]) {
+                if (out) {
+                    out[k * 3 + 0] = x * dilation[0];
+                    out[k * 3 + 1] = y * dilation[1];
+                    out[k * 3 + 2] = z * dilation[2];
+                }
+                ++k;
+            }
+    return k;
+}
+
+// write_kernel_relation: relation_build_detail.h:3-41.  Output capacities as
+// make_kernel_relation sizes them (relations.cpp:540-553): out rows = rows,
+// edges = rows*K.  counts = [E, N_out].
+void oracle_kernel_relation(const int32_t* coords, int rows, int active_rows,
+                            const int32_t* offsets, int K, const int* stride,
+                            const int* padding, int32_t* in_rows,
+                            int32_t* out_rows, int32_t* kernel_ids,
+                            int32_t* row_offsets, int32_t* out_coords,
+                            int32_t* counts) {
+    auto values = read_coords(coords, rows);
+    values.resize(std::min(active_rows, rows));
+    auto map = first_row_map(values);
+    bool identity = stride[0] == 1 && stride[1] == 1 && stride[2] == 1 &&
+                    padding[0] == 0 && padding[1] == 0 && padding[2] == 0;
+    auto out_values = identity ? values : downsample_values(values, stride);
+    std::vector<Edge> edges;
+    edges.reserve(out_values.size() * K);
+    for (int o = 0; o < static_cast<int>(out_values.size()); ++o) {
+        for (int k = 0; k < K; ++k) {
+            auto cand = kernel_input_coord(out_values[o], offsets + 3 * k,
+                                           stride, padding);
+            auto it = map.find(cand);
+            if (it != map.end()) edges.push_back({it->second, o, k});
+        }
+    }
+    write_map_rows(edges, rows, rows * K, in_rows, out_rows, kernel_ids,
+                   row_offsets);
+    write_coords(out_values, rows, out_coords);
+    counts[0] = static_cast<int32_t>(edges.size());
+    counts[1] = static_cast<int32_t>(out_values.size());
+}
+
+// write_target_kernel_relation: relation_build_detail.h:43-80.  Out
+// capacity = target_rows, edges = target_rows*K.
+void oracle_target_kernel_relation(
+    const int32_t* coords, int rows, int active_rows,
+    const int32_t* target_coords, int target_rows, int target_active_rows,
+    const int32_t* offsets, int K, const int* stride, const int* padding,
+    int32_t* in_rows, int32_t* out_rows, int32_t* kernel_ids,
+    int32_t* row_offsets, int32_t* counts) {
+    auto values = read_coords(coords, rows);
+    values.resize(std::min(active_rows, rows));
+    auto targets = read_coords(target_coords, target_rows);
+    int t_active = std::min(target_active_rows, target_rows);
+    auto map = first_row_map(values);
+    std::vector<Edge> edges;
+    for (int o = 0; o < t_active; ++o) {
+        for (int k = 0; k < K; ++k) {
+            auto cand = kernel_input_coord(targets[o], offsets + 3 * k, stride,
+                                           padding);
+            auto it = map.find(cand);
+            if (it != map.end()) edges.push_back({it->second, o, k});
+        }
+    }
+    write_map_rows(edges, target_rows, target_rows * K, in_rows, out_rows,
+                   kernel_ids, row_offsets);
+    counts[0] = static_cast<int32_t>(edges.size());
+    counts[1] = t_active;
+}
+
+// write_relation_grouped_view: relation_views_detail.h:84-120.  Stable
+// counting sort of edge ids by group; edge_ids tail = -1.
+void oracle_grouped_view(const int32_t* group_ids, int edge_capacity,
+                         int edge_count, int group_count, int32_t* offsets,
+                         int32_t* edge_ids) {
+    int n = std::max(0, std::min(edge_count, edge_capacity));
+    std::fill(offsets, offsets + group_count + 1, 0);
+    for (int e = 0; e < n; ++e) {
+        int g = group_ids[e];
+        if (g >= 0 && g < group_count) ++offsets[g + 1];
+    }
+    for (int g = 0; g < group_count; ++g) offsets[g + 1] += offsets[g];
+    std::vector<int32_t> cursor(offsets, offsets + group_count);
+    std::fill(edge_ids, edge_ids + edge_capacity, -1);
+    for (int e = 0; e < n; ++e) {
+        int g = group_ids[e];
+        if (g >= 0 && g < group_count) edge_ids[cursor[g]++] = e;
+    }
+}
+
+// write_relation_implicit_gemm_view: relation_views_detail.h:122-169.
+void oracle_implicit_gemm_view(const int32_t* source_coords, int source_rows,
+                               int source_active, const int32_t* output_coords,
+                               int output_rows, int output_active,
+                               const int32_t* offsets, int K,
+                               const int* stride, const int* padding,
+                               int32_t* out_in_map, int32_t* row_masks) {
+    auto src = read_coords(source_coords, source_rows);
+    auto outs = read_coords(output_coords, output_rows);
+    int s_active = std::max(0, std::min(source_active, source_rows));
+    int o_active = std::max(0, std::min(output_active, output_rows));
+    auto map = first_row_map(src);
+    int words = (K + 31) / 32;
+    std::fill(out_in_map, out_in_map + static_cast<size_t>(output_rows) * K, -1);
+    std::fill(row_masks, row_masks + static_cast<size_t>(output_rows) * words, 0);
+    for (int o = 0; o < o_active; ++o) {
+        for (int k = 0; k < K; ++k) {
+            auto cand = kernel_input_coord(outs[o], offsets + 3 * k, stride,
+                                           padding);
+            auto it = map.find(cand);
+            if (it == map.end() || it->second >= s_active) continue;
+            out_in_map[static_cast<size_t>(o) * K + k] = it->second;
+            row_masks[static_cast<size_t>(o) * words + k / 32] |=
+                static_cast<int32_t>(1u << (k % 32));
+        }
+    }
+}
+
+// Float sparse conv, cpu/algorithms.cpp:180-302 + eval_route :484-508.
+// weights: layout 0 = mapped (K, C_in, C_out) contiguous, layout 1 = dense
+// 5d (C_out, Kx, Ky, Kz, C_in) contiguous.  dtype: 0 = fp32, 1 = fp16 (raw
+// uint16 bits).  Square C in {16,32,64} uses the fp32 accumulator with one
+// final rounding (eval_dense_channels_typed); all other channel pairs round
+// the running sum to the feature dtype after every multiply-add (eval_typed).
+// threads <= 0 means std::thread::hardware_concurrency().
+void oracle_conv_features(int dtype, const void* feats, const void* weights,
+                          int weight_layout, int n_in, int c_in, int c_out,
+                          int K, const int32_t* in_rows,
+                          const int32_t* kernel_ids, const int32_t* counts,
+                          int edge_capacity, const int32_t* row_offsets,
+                          int out_capacity, void* out, int threads) {
+    int edge_total = std::min(counts[0], edge_capacity);
+    int active_out = std::min(counts[1], out_capacity);
+    int nthreads = hardware_threads(threads);
+    bool dense_route = c_in == c_out && (c_in == 16 || c_in == 32 || c_in == 64);
+    (void)n_in;
+    auto widx = [&](int k, int ci, int co) -> size_t {
+        if (weight_layout == 0) {
+            return (static_cast<size_t>(k) * c_in + ci) * c_out + co;
+        }
+        return (static_cast<size_t>(co) * K + k) * c_in + ci;
+    };
+    auto body = [&](auto load, auto store, auto round) {
+        parallel_for(0, out_capacity, nthreads, [&](int o) {
+            std::vector<float> acc(static_cast<size_t>(c_out), 0.0f);
+            if (o < active_out) {
+                for (int e = row_offsets[o]; e < row_offsets[o + 1]; ++e) {
+                    if (e < 0 || e >= edge_total) continue;
+                    int in = in_rows[e];
+                    int k = kernel_ids[e];
+                    if (in < 0 || k < 0) continue;
+                    for (int ci = 0; ci < c_in; ++ci) {
+                        float v = load(feats, static_cast<size_t>(in) * c_in + ci);
+                        for (int co = 0; co < c_out; ++co) {
+                            float w = load(weights, widx(k, ci, co));
+                            if (dense_route) {
+                                acc[co] += v * w;
+                            } else {
+                                acc[co] = round(acc[co] + v * w);
+                            }
+                        }
+                    }
+                }
+            }
+            for (int co = 0; co < c_out; ++co) {
+                store(out, static_cast<size_t>(o) * c_out + co, acc[co]);
+            }
+        });
+    };
+    if (dtype == 0) {
+        body([](const void* p, size_t i) { return static_cast<const float*>(p)[i]; },
+             [](void* p, size_t i, float v) { static_cast<float*>(p)[i] = v; },
+             [](float v) { return v; });
+    } else {
+        body([](const void* p, size_t i) {
+                 return half_to_float(static_cast<const uint16_t*>(p)[i]);
+             },
+             [](void* p, size_t i, float v) {
+                 static_cast<uint16_t*>(p)[i] = float_to_half(v);
+             },
+             [](float v) { return half_to_float(float_to_half(v)); });
+    }
+}
+
+// Quantized sparse conv, cpu/quantized.cpp:54-141.  weights uint32
+// (K, storage_c_in*bits/32, C_out); scales/biases (K, storage_c_in/g, C_out)
+// in the feature dtype; fp32 accumulator, one rounding.
+void oracle_quantized_conv_features(
+    int dtype, const void* feats, const uint32_t* weights, const void* scales,
+    const void* biases, int c_in, int c_out, int storage_c_in, int group_size,
+    int bits, int K, const int32_t* in_rows, const int32_t* kernel_ids,
+    const int32_t* counts, int edge_capacity, const int32_t* row_offsets,
+    int out_capacity, void* out, int threads) {
+    int out_count = std::min(counts[1], out_capacity);
+    int edge_count = std::min(counts[0], edge_capacity);
+    int packed_words = storage_c_in * bits / 32;
+    int groups = storage_c_in / group_size;
+    uint32_t mask = (bits == 32) ? 0xffffffffu : ((1u << bits) - 1u);
+    auto ld = [dtype](const void* p, size_t i) -> float {
+        return dtype == 0 ? static_cast<const float*>(p)[i]
+                          : half_to_float(static_cast<const uint16_t*>(p)[i]);
+    };
+    auto st = [dtype](void* p, size_t i, float v) {
+        if (dtype == 0) static_cast<float*>(p)[i] = v;
+        else static_cast<uint16_t*>(p)[i] = float_to_half(v);
+    };
+    parallel_rows(out_capacity, hardware_threads(threads), [&](int o) {
+        size_t base = static_cast<size_t>(o) * c_out;
+        if (o >= out_count) {
+            for (int co = 0; co < c_out; ++co) st(out, base + co, 0.0f);
+            return;
+        }
+        for (int co = 0; co < c_out; ++co) {
+            float acc = 0.0f;
+            for (int e = row_offsets[o]; e < row_offsets[o + 1]; ++e) {
+                if (e < 0 || e >= edge_count) continue;
+                int in = in_rows[e];
+                int k = kernel_ids[e];
+                if (in < 0 || k < 0 || k >= K) continue;
+                int wrow = k * packed_words;
+                int qrow = k * groups;
+                for (int ci = 0; ci < c_in; ++ci) {
+                    int g = ci / group_size;
+                    int bit = ci * bits;
+                    uint32_t word = weights[static_cast<size_t>(wrow) * c_out +
+                                            static_cast<size_t>(bit >> 5) * c_out + co];
+                    uint32_t q = (word >> (bit & 31)) & mask;
+                    size_t sidx = static_cast<size_t>(qrow + g) * c_out + co;
+                    float w = static_cast<float>(q) * ld(scales, sidx) + ld(biases, sidx);
+                    acc += ld(feats, static_cast<size_t>(in) * c_in + ci) * w;
+                }
+            }
+            st(out, base + co, acc);
+        }
+    });
+}
+
+// Affine dequantization of the spatial packed layout (core/quantized.py:
+// 191-223 with the unpack rule of cpu/quantized.cpp:54-62).  Writes the
+// mapped (K, C_in, C_out) fp32 weight for logical channels c_in.
+void oracle_dequantize_mapped(const uint32_t* weights, const float* scales,
+                              const float* biases, int K, int c_in, int c_out,
+                              int storage_c_in, int group_size, int bits,
+                              float* out) {
+    int packed_words = storage_c_in * bits / 32;
+    int groups = storage_c_in / group_size;
+    uint32_t mask = (1u << bits) - 1u;
+    for (int k = 0; k < K; ++k)
+        for (int ci = 0; ci < c_in; ++ci)
+            for (int co = 0; co < c_out; ++co) {
+                int bit = ci * bits;
+                uint32_t word = weights[(static_cast<size_t>(k) * packed_words + (bit >> 5)) * c_out + co];
+                uint32_t q = (word >> (bit & 31)) & mask;
+                size_t s = (static_cast<size_t>(k) * groups + ci / group_size) * c_out + co;
+                out[(static_cast<size_t>(k) * c_in + ci) * c_out + co] =
+                    static_cast<float>(q) * scales[s] + biases[s];
+            }
+}
+
+// Round trip through IEEE binary16 with round-to-nearest-even.
+void oracle_round_half(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = float_to_half(in[i]);
+}
+
+int oracle_hardware_concurrency(void) { return hardware_threads(0); }
+
+}  // extern "C"

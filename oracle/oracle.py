@@ -1,0 +1,287 @@
+"""ctypes wrapper over the CPU oracle (``oracle/liblattice_oracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py``.  The product path never imports
+this module.
+
+Each function restates a reference CPU routine (file:line citations are in
+``lattice_oracle.cpp``) over numpy arrays.  Relation outputs follow the
+reference's static capacities; the relation-level checks compare only the
+active prefixes, as the reference's own parity tests do
+(tests/cases/coords_cases.py:60-78).
+
+Pinning (what checks each function besides this restatement):
+- kernel_offsets, kernel_relation, target_kernel_relation, grouped_view,
+  implicit_gemm_view: the reference's known-answer tests transcribed into
+  tests/golden/reference_known_answers.json, plus an independent numpy
+  brute-force (dict lookups) on seeded clouds in tests/test_oracle.py.
+- conv_features: known answers (tests/ops/test_conv.py:44-83, 326-398,
+  638-671) and the textbook identity with a dense 3D cross-correlation on a
+  fully occupied box, plus an fp64 edge-sum restatement.
+- quantized_conv_features: the dequantized contract (packed conv equals the
+  float conv of the dequantized weight) and the unpack formula on hand-built
+  words.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / 'liblattice_oracle.so'
+_lib = None
+
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags='C_CONTIGUOUS')
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags='C_CONTIGUOUS')
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags='C_CONTIGUOUS')
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags='C_CONTIGUOUS')
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+
+
+def build() -> Path:
+    """Compile the oracle with its Makefile (g++ only)."""
+    subprocess.run(['make', '-s', '-C', str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        handle = ctypes.CDLL(str(_LIB_PATH))
+        handle.oracle_kernel_offsets.argtypes = [_i32p, _i32p, _vp]
+        handle.oracle_kernel_offsets.restype = _int
+        handle.oracle_kernel_relation.argtypes = [
+            _i32p, _int, _int, _i32p, _int, _i32p, _i32p,
+            _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]
+        handle.oracle_target_kernel_relation.argtypes = [
+            _i32p, _int, _int, _i32p, _int, _int, _i32p, _int, _i32p, _i32p,
+            _i32p, _i32p, _i32p, _i32p, _i32p]
+        handle.oracle_grouped_view.argtypes = [
+            _i32p, _int, _int, _int, _i32p, _i32p]
+        handle.oracle_implicit_gemm_view.argtypes = [
+            _i32p, _int, _int, _i32p, _int, _int, _i32p, _int, _i32p, _i32p,
+            _i32p, _i32p]
+        handle.oracle_conv_features.argtypes = [
+            _int, _vp, _vp, _int, _int, _int, _int, _int, _i32p, _i32p,
+            _i32p, _int, _i32p, _int, _vp, _int]
+        handle.oracle_quantized_conv_features.argtypes = [
+            _int, _vp, _u32p, _vp, _vp, _int, _int, _int, _int, _int, _int,
+            _i32p, _i32p, _i32p, _int, _i32p, _int, _vp, _int]
+        handle.oracle_dequantize_mapped.argtypes = [
+            _u32p, _f32p, _f32p, _int, _int, _int, _int, _int, _int, _f32p]
+        handle.oracle_hardware_concurrency.restype = _int
+        _lib = handle
+    return _lib
+
+
+def hardware_concurrency() -> int:
+    return int(lib().oracle_hardware_concurrency())
+
+
+def _triple(v) -> np.ndarray:
+    if isinstance(v, int):
+        v = (v, v, v)
+    return np.ascontiguousarray(v, dtype=np.int32)
+
+
+def kernel_offsets(kernel_size, dilation=1) -> np.ndarray:
+    size = _triple(kernel_size)
+    dil = _triple(dilation)
+    k = lib().oracle_kernel_offsets(size, dil, None)
+    out = np.zeros((k, 3), dtype=np.int32)
+    lib().oracle_kernel_offsets(size, dil, out.ctypes.data)
+    return out
+
+
+def kernel_relation(coords: np.ndarray, active_rows: int | None = None,
+                    kernel_size=3, stride=1, padding=0, dilation=1) -> dict:
+    """Forward relation (identity out when stride=1, padding=0)."""
+    coords = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+    rows = coords.shape[0]
+    active = rows if active_rows is None else int(active_rows)
+    offs = kernel_offsets(kernel_size, dilation)
+    k = offs.shape[0]
+    out = dict(
+        in_rows=np.zeros(rows * k, np.int32),
+        out_rows=np.zeros(rows * k, np.int32),
+        kernel_ids=np.zeros(rows * k, np.int32),
+        row_offsets=np.zeros(rows + 1, np.int32),
+        out_coords=np.zeros((rows, 4), np.int32),
+        counts=np.zeros(2, np.int32),
+    )
+    lib().oracle_kernel_relation(
+        coords, rows, active, offs, k, _triple(stride), _triple(padding),
+        out['in_rows'], out['out_rows'], out['kernel_ids'],
+        out['row_offsets'], out['out_coords'], out['counts'])
+    _add_views(out, rows, k)
+    return out
+
+
+def target_kernel_relation(coords, target, active_rows=None,
+                           target_active_rows=None, kernel_size=3, stride=1,
+                           padding=0, dilation=1) -> dict:
+    coords = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+    target = np.ascontiguousarray(target, dtype=np.int32).reshape(-1, 4)
+    rows, trows = coords.shape[0], target.shape[0]
+    active = rows if active_rows is None else int(active_rows)
+    tactive = trows if target_active_rows is None else int(target_active_rows)
+    offs = kernel_offsets(kernel_size, dilation)
+    k = offs.shape[0]
+    out = dict(
+        in_rows=np.zeros(trows * k, np.int32),
+        out_rows=np.zeros(trows * k, np.int32),
+        kernel_ids=np.zeros(trows * k, np.int32),
+        row_offsets=np.zeros(trows + 1, np.int32),
+        out_coords=target.copy(),
+        counts=np.zeros(2, np.int32),
+    )
+    lib().oracle_target_kernel_relation(
+        coords, rows, active, target, trows, tactive, offs, k,
+        _triple(stride), _triple(padding), out['in_rows'], out['out_rows'],
+        out['kernel_ids'], out['row_offsets'], out['counts'])
+    _add_views(out, rows, k)
+    return out
+
+
+def grouped_view(group_ids: np.ndarray, edge_count: int, group_count: int):
+    group_ids = np.ascontiguousarray(group_ids, dtype=np.int32)
+    offsets = np.zeros(group_count + 1, np.int32)
+    edge_ids = np.zeros(group_ids.shape[0], np.int32)
+    lib().oracle_grouped_view(group_ids, group_ids.shape[0], int(edge_count),
+                              group_count, offsets, edge_ids)
+    return offsets, edge_ids
+
+
+def _add_views(out: dict, in_capacity: int, k: int) -> None:
+    e = int(out['counts'][0])
+    out['in_row_offsets'], out['in_edge_ids'] = grouped_view(
+        out['in_rows'], e, in_capacity)
+    out['kernel_row_offsets'], out['kernel_edge_ids'] = grouped_view(
+        out['kernel_ids'], e, k)
+
+
+def implicit_gemm_view(source_coords, source_active, output_coords,
+                       output_active, offsets, stride=1, padding=0):
+    src = np.ascontiguousarray(source_coords, dtype=np.int32).reshape(-1, 4)
+    dst = np.ascontiguousarray(output_coords, dtype=np.int32).reshape(-1, 4)
+    offs = np.ascontiguousarray(offsets, dtype=np.int32).reshape(-1, 3)
+    k = offs.shape[0]
+    words = (k + 31) // 32
+    out_in_map = np.zeros((dst.shape[0], k), np.int32)
+    row_masks = np.zeros((dst.shape[0], words), np.int32)
+    lib().oracle_implicit_gemm_view(
+        src, src.shape[0], int(source_active), dst, dst.shape[0],
+        int(output_active), offs, k, _triple(stride), _triple(padding),
+        out_in_map, row_masks)
+    return out_in_map, row_masks
+
+
+def conv_features(feats: np.ndarray, weight: np.ndarray, relation: dict,
+                  out_capacity: int | None = None,
+                  threads: int = 0) -> np.ndarray:
+    """Reference CPU float conv (fp32 or fp16 feats; 5D or mapped weight)."""
+    feats = np.ascontiguousarray(feats)
+    weight = np.ascontiguousarray(weight)
+    if feats.dtype == np.float32:
+        dtype = 0
+    elif feats.dtype == np.float16:
+        dtype = 1
+    else:
+        raise ValueError('oracle conv supports float32 and float16.')
+    if weight.dtype != feats.dtype:
+        raise ValueError('weight dtype must match feats.')
+    if weight.ndim == 5:
+        layout, k, c_out = 1, int(np.prod(weight.shape[1:4])), weight.shape[0]
+    elif weight.ndim == 3:
+        layout, k, c_out = 0, weight.shape[0], weight.shape[2]
+    else:
+        raise ValueError('weight must be 3D or 5D.')
+    c_in = feats.shape[1]
+    cap = (relation['row_offsets'].shape[0] - 1
+           if out_capacity is None else out_capacity)
+    out = np.zeros((cap, c_out), dtype=feats.dtype)
+    lib().oracle_conv_features(
+        dtype, feats.ctypes.data, weight.ctypes.data, layout, feats.shape[0],
+        c_in, c_out, k, relation['in_rows'], relation['kernel_ids'],
+        relation['counts'], relation['in_rows'].shape[0],
+        relation['row_offsets'], cap, out.ctypes.data, int(threads))
+    return out
+
+
+def quantized_conv_features(feats, weights, scales, biases, relation: dict,
+                            *, in_channels, out_channels, storage_in_channels,
+                            group_size, bits, out_capacity=None,
+                            threads: int = 0) -> np.ndarray:
+    feats = np.ascontiguousarray(feats)
+    dtype = 0 if feats.dtype == np.float32 else 1
+    scales = np.ascontiguousarray(scales, dtype=feats.dtype)
+    biases = np.ascontiguousarray(biases, dtype=feats.dtype)
+    weights = np.ascontiguousarray(weights, dtype=np.uint32)
+    cap = (relation['row_offsets'].shape[0] - 1
+           if out_capacity is None else out_capacity)
+    out = np.zeros((cap, out_channels), dtype=feats.dtype)
+    lib().oracle_quantized_conv_features(
+        dtype, feats.ctypes.data, weights, scales.ctypes.data,
+        biases.ctypes.data, in_channels, out_channels, storage_in_channels,
+        group_size, bits, weights.shape[0], relation['in_rows'],
+        relation['kernel_ids'], relation['counts'],
+        relation['in_rows'].shape[0], relation['row_offsets'], cap,
+        out.ctypes.data, int(threads))
+    return out
+
+
+def dequantize_mapped(weights, scales, biases, *, in_channels, out_channels,
+                      storage_in_channels, group_size, bits) -> np.ndarray:
+    weights = np.ascontiguousarray(weights, dtype=np.uint32)
+    k = weights.shape[0]
+    out = np.zeros((k, in_channels, out_channels), np.float32)
+    lib().oracle_dequantize_mapped(
+        weights, np.ascontiguousarray(scales, np.float32),
+        np.ascontiguousarray(biases, np.float32), k, in_channels,
+        out_channels, storage_in_channels, group_size, bits, out)
+    return out
+
+
+def conv_features_fp64(feats, weight_mapped, relation: dict,
+                       out_capacity: int | None = None) -> np.ndarray:
+    """Exact-order-free fp64 edge sum ``out[o] += f[in] @ W[k]``.
+
+    Independent of the C restatement: a numpy scatter-add over the active
+    edge prefix, used as the tolerance anchor for float features.
+    """
+    e = int(relation['counts'][0])
+    n_out = int(relation['counts'][1])
+    cap = (relation['row_offsets'].shape[0] - 1
+           if out_capacity is None else out_capacity)
+    w = np.asarray(weight_mapped, dtype=np.float64)
+    f = np.asarray(feats, dtype=np.float64)
+    ins = relation['in_rows'][:e]
+    outs = relation['out_rows'][:e]
+    ks = relation['kernel_ids'][:e]
+    out = np.zeros((cap, w.shape[2]), np.float64)
+    for k in range(w.shape[0]):
+        sel = ks == k
+        if not sel.any():
+            continue
+        np.add.at(out, outs[sel], f[ins[sel]] @ w[k])
+    out[n_out:] = 0.0
+    return out
+
+
+def mapped_weight(weight: np.ndarray) -> np.ndarray:
+    """(C_out, Kx, Ky, Kz, C_in) -> (K, C_in, C_out)
+    (ops/_relation_exec.py:217-250)."""
+    if weight.ndim == 3:
+        return weight
+    c_out = weight.shape[0]
+    c_in = weight.shape[4]
+    return np.ascontiguousarray(
+        weight.transpose(1, 2, 3, 4, 0).reshape(-1, c_in, c_out))
+

@@ -1,0 +1,314 @@
+"""GPU parity of the sparse-convolution feature kernels.
+
+Features are held to the north-star tolerances against an fp64 edge-sum
+restatement built from the oracle's relation: fp32 ``rtol=1e-3``, fp16 /
+bf16 ``rtol=2e-2`` (each with the small ``atol`` written in the test).  The
+reference CPU route (per-FMA fp16 rounding for non-square channels,
+cpu/algorithms.cpp:180-239) is checked against the same fp64 anchor with its
+own, looser bound, because it is less accurate than an fp32-accumulating
+kernel.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import golden, to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+RTOL_F32, ATOL_F32 = 1e-3, 1e-5
+RTOL_F16, ATOL_F16 = 2e-2, 1e-2
+
+
+def _imports():
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor
+
+    return ops, SparseTensor
+
+
+def _tensor(coords, feats, stride=1):
+    _, SparseTensor = _imports()
+    return SparseTensor(torch.as_tensor(coords, dtype=torch.int32).to(DEV),
+                        torch.as_tensor(feats).to(DEV), stride=stride)
+
+
+def _w(values, shape, dtype=torch.float32):
+    return torch.tensor(values, dtype=dtype, device=DEV).reshape(shape)
+
+
+def _active(out):
+    n = int(out.active_rows.item())
+    return to_np(out.coords[:n]), to_np(out.feats[:n].float())
+
+
+# ------------------------------------------------------------ golden ----
+
+
+def test_golden_conv3d_generic_and_fp16():
+    ops, _ = _imports()
+    g = golden('conv3d_generic_line')
+    for dtype in (torch.float32, torch.float16):
+        x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+        x = x.astype(dtype)
+        w = _w(g['weight'], g['weight_5d_shape'], dtype)
+        out = ops.conv3d(x, w, kernel_size=g['kernel_size'])
+        coords, feats = _active(out)
+        assert coords.tolist() == g['coords']
+        assert feats.tolist() == g['expected']
+        assert out.stride == (1, 1, 1)
+        assert out.coord_manager is x.coord_manager
+        assert out.coord_key != x.coord_key
+
+
+def test_golden_target_and_pointwise_target():
+    ops, SparseTensor = _imports()
+    g = golden('conv3d_target_line')
+    x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+    tgt = SparseTensor(torch.tensor(g['target'], dtype=torch.int32, device=DEV),
+                       torch.zeros((2, 1), device=DEV),
+                       coord_manager=x.coord_manager)
+    out = ops.conv3d(x, _w(g['weight'], g['weight_5d_shape']),
+                     kernel_size=g['kernel_size'], coordinates=tgt)
+    coords, feats = _active(out)
+    assert coords.tolist() == g['target']
+    assert feats.tolist() == g['expected']
+    assert out.coord_key == tgt.coord_key
+    g = golden('conv3d_pointwise_target')
+    x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+    out = ops.conv3d(x, _w(g['weight_2d'], (1, 1)), kernel_size=1,
+                     coordinates=torch.tensor(g['target'], dtype=torch.int32,
+                                              device=DEV))
+    assert _active(out)[1].tolist() == g['expected']
+
+
+def test_golden_strided_subm_pointwise():
+    ops, _ = _imports()
+    g = golden('conv3d_strided_pointwise')
+    x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+    out = ops.conv3d(x, _w(g['weight'], g['weight_5d_shape']), kernel_size=1,
+                     stride=2)
+    coords, feats = _active(out)
+    assert coords.tolist() == g['out_coords']
+    assert feats.tolist() == g['expected']
+    assert out.stride == (2, 2, 2)
+    g = golden('subm_conv3d_line')
+    x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+    out = ops.subm_conv3d(x, _w(g['weight'], g['weight_5d_shape']),
+                          kernel_size=g['kernel_size'])
+    assert to_np(out.feats).tolist() == g['expected']
+    assert out.coord_key == x.coord_key
+    g = golden('conv3d_pointwise_linear')
+    x = _tensor(g['coords'], np.array(g['feats'], np.float32))
+    out = ops.conv3d(x, _w(g['weight_2d'], (2, 2)),
+                     torch.tensor(g['bias'], device=DEV), kernel_size=1)
+    assert to_np(out.feats).tolist() == g['expected']
+
+
+def test_contract_errors():
+    ops, _ = _imports()
+    x = _tensor([[0, 0, 0, 0]], np.ones((1, 1), np.float32))
+    with pytest.raises(ValueError, match='odd kernel_size'):
+        ops.subm_conv3d(x, torch.ones((2, 1, 1), device=DEV), kernel_size=2)
+    with pytest.raises(ValueError, match='must divide'):
+        ops.conv_transpose3d(x, torch.ones((2, 1, 1), device=DEV), stride=3)
+    with pytest.raises(ValueError, match='match feature dtype'):
+        ops.subm_conv3d(x, torch.ones((1, 3, 3, 3, 1), device=DEV,
+                                      dtype=torch.float16))
+    with pytest.raises(ValueError, match='kernel rows'):
+        ops.subm_conv3d(x, torch.ones((1, 2, 3, 3, 1), device=DEV))
+
+
+# --------------------------------------------------- seeded clouds ----
+
+
+def _reference(coords, feats, weight5d, relation_kwargs):
+    rel = O.kernel_relation(coords, **relation_kwargs)
+    ref = O.conv_features_fp64(feats.astype(np.float64),
+                               O.mapped_weight(weight5d.astype(np.float64)),
+                               rel)
+    return rel, ref
+
+
+def _run_conv(coords, feats, weight5d, dtype, *, subm, **geom):
+    ops, _ = _imports()
+    x = _tensor(coords, feats).astype(dtype)
+    w = torch.as_tensor(weight5d).to(device=DEV, dtype=dtype)
+    if subm:
+        out = ops.subm_conv3d(x, w, **geom)
+    else:
+        out = ops.conv3d(x, w, **geom)
+    torch.cuda.synchronize()
+    return out
+
+
+def _shell(rows, grid, seed):
+    from mlx_lattice_amd.synthetic import sphere_shell_cloud
+
+    rng = np.random.default_rng(seed)
+    return sphere_shell_cloud(rows, grid, rng=rng), rng
+
+
+def _close(actual, ref, rtol, atol, what):
+    err = np.abs(actual - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), (
+        f'{what}: {bad.sum()} of {bad.size} outside tolerance; max err '
+        f'{err.max():.3e}')
+
+
+def test_config1_fp32_subm_16_to_32():
+    from mlx_lattice_amd.synthetic import config_rng, uniform_grid_cloud
+
+    rng = config_rng(1)
+    coords = uniform_grid_cloud(20000, 64, rng=rng)
+    feats = rng.standard_normal((len(coords), 16)).astype(np.float32)
+    w = (rng.standard_normal((32, 3, 3, 3, 16))
+         / np.sqrt(27 * 16)).astype(np.float32)
+    out = _run_conv(coords, feats, w, torch.float32, subm=True, kernel_size=3)
+    rel, ref = _reference(coords, feats, w, dict(kernel_size=3))
+    _close(to_np(out.feats), ref, RTOL_F32, ATOL_F32, 'config1 vs fp64')
+    cpu = O.conv_features(feats, w, rel)
+    _close(cpu, ref, RTOL_F32, ATOL_F32, 'reference CPU route vs fp64')
+
+
+@pytest.mark.parametrize('c_in,c_out', [(32, 32), (64, 64), (128, 128),
+                                        (64, 128), (128, 256), (32, 16),
+                                        (256, 64)])
+def test_matrix_core_subm_shapes(c_in, c_out):
+    coords, rng = _shell(30000, 160, 11 + c_in + c_out)
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float16)
+    w = (rng.standard_normal((c_out, 3, 3, 3, c_in))
+         * np.sqrt(2.0 / (27 * c_in))).astype(np.float16)
+    print(f'mfma subm c_in={c_in} c_out={c_out}', flush=True)
+    out = _run_conv(coords, feats, w, torch.float16, subm=True, kernel_size=3)
+    _, ref = _reference(coords, feats, w, dict(kernel_size=3))
+    _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16,
+           f'fp16 {c_in}->{c_out}')
+
+
+def test_matrix_core_bf16():
+    coords, rng = _shell(20000, 128, 5)
+    feats = rng.standard_normal((len(coords), 64)).astype(np.float32)
+    w = (rng.standard_normal((64, 3, 3, 3, 64))
+         * np.sqrt(2.0 / (27 * 64))).astype(np.float32)
+    fb = torch.as_tensor(feats).to(torch.bfloat16).float().numpy()
+    wb = torch.as_tensor(w).to(torch.bfloat16).float().numpy()
+    out = _run_conv(coords, fb, wb, torch.bfloat16, subm=True, kernel_size=3)
+    _, ref = _reference(coords, fb, wb, dict(kernel_size=3))
+    _close(to_np(out.feats.float()), ref, 2e-2, 3e-2, 'bf16 64->64')
+
+
+def test_csr_route_fp16_matches():
+    # Channel counts the matrix cores do not tile take the CSR route.
+    coords, rng = _shell(8000, 160, 3)
+    feats = rng.standard_normal((len(coords), 24)).astype(np.float16)
+    w = (rng.standard_normal((40, 3, 3, 3, 24)) * 0.05).astype(np.float16)
+    out = _run_conv(coords, feats, w, torch.float16, subm=True, kernel_size=3)
+    _, ref = _reference(coords, feats, w, dict(kernel_size=3))
+    _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16, 'csr fp16')
+
+
+def test_config2_downsample_fp16():
+    from mlx_lattice_amd.synthetic import config_rng, lidar_cloud
+
+    rng = config_rng(2)
+    coords = lidar_cloud(100000, 2, rng=rng)
+    feats = rng.standard_normal((len(coords), 64)).astype(np.float16)
+    w = (rng.standard_normal((128, 2, 2, 2, 64))
+         * np.sqrt(2.0 / (8 * 64))).astype(np.float16)
+    out = _run_conv(coords, feats, w, torch.float16, subm=False,
+                    kernel_size=2, stride=2)
+    rel, ref = _reference(coords, feats, w, dict(kernel_size=2, stride=2))
+    n = int(rel['counts'][1])
+    assert int(out.active_rows.item()) == n
+    np.testing.assert_array_equal(to_np(out.coords[:n]),
+                                  rel['out_coords'][:n])
+    _close(to_np(out.feats.float())[:n], ref[:n], RTOL_F16, ATOL_F16,
+           'config2')
+
+
+def test_config3_headline_fp16_400k():
+    from mlx_lattice_amd.synthetic import config_rng, kaiming_weight, sphere_shell_cloud
+
+    rng = config_rng(3)
+    coords = sphere_shell_cloud(400000, 512, rng=rng)
+    feats = rng.standard_normal((len(coords), 128)).astype(np.float16)
+    w = kaiming_weight((128, 3, 3, 3, 128), rng=rng).astype(np.float16)
+    out = _run_conv(coords, feats, w, torch.float16, subm=True, kernel_size=3)
+    _, ref = _reference(coords, feats, w, dict(kernel_size=3))
+    _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16, 'config3')
+
+
+# ------------------------------------------------------- quantized ----
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_quantized_dequantized_contract(bits):
+    from mlx_lattice_amd import dequantize_weight, quantize_weight
+
+    ops, _ = _imports()
+    coords, rng = _shell(20000, 128, 21 + bits)
+    feats = rng.standard_normal((len(coords), 64)).astype(np.float16)
+    w = torch.as_tensor((rng.standard_normal((64, 3, 3, 3, 64))
+                         * np.sqrt(2.0 / (27 * 64))).astype(np.float16)).to(DEV)
+    q = quantize_weight(w, group_size=32, bits=bits)
+    deq = dequantize_weight(q)
+    x = _tensor(coords, feats)
+    actual = ops.subm_conv3d(x, q, kernel_size=3)
+    expected = ops.subm_conv3d(x, deq, kernel_size=3)
+    _, ref = _reference(coords, feats.astype(np.float32),
+                        to_np(deq.float()), dict(kernel_size=3))
+    a = to_np(actual.feats.float())
+    _close(a, ref, RTOL_F16, ATOL_F16, f'int{bits} fused vs fp64(dequant)')
+    _close(a, to_np(expected.feats.float()), 3e-2, 2e-2,
+           f'int{bits} fused vs float route')
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_quantized_csr_route_matches_oracle(bits):
+    from mlx_lattice_amd import quantize_weight
+
+    ops, _ = _imports()
+    rng = np.random.default_rng(31)
+    coords = np.array([[0, i, 0, 0] for i in range(12)], np.int32)
+    feats = np.array([[((r + 1) * (c + 3) % 19) / 19 for c in range(16)]
+                      for r in range(12)], np.float16)
+    w = torch.tensor([((i % 37) - 18) / 37 for i in range(12 * 3 * 16)],
+                     dtype=torch.float16, device=DEV).reshape(12, 3, 1, 1, 16)
+    q = quantize_weight(w, bits=bits)
+    assert q.storage_in_channels == 32 and q.in_channels == 16
+    x = _tensor(coords, feats)
+    out = ops.conv3d(x, q, kernel_size=(3, 1, 1))
+    rel = O.kernel_relation(coords, kernel_size=(3, 1, 1))
+    expected = O.quantized_conv_features(
+        feats, to_np(q.weight), to_np(q.scales), to_np(q.biases), rel,
+        in_channels=16, out_channels=12, storage_in_channels=32,
+        group_size=q.group_size, bits=bits)
+    _close(to_np(out.feats.float()), expected.astype(np.float32), 2e-3, 2e-3,
+           'quantized CSR vs oracle')
+    del rng
+
+
+def test_config4_int4_fused_200k():
+    from mlx_lattice_amd import dequantize_weight, quantize_weight
+    from mlx_lattice_amd.synthetic import config_rng, kaiming_weight, sphere_shell_cloud
+
+    ops, _ = _imports()
+    rng = config_rng(4)
+    coords = sphere_shell_cloud(200000, 256, rng=rng)
+    w = torch.as_tensor(kaiming_weight((64, 3, 3, 3, 64), rng=rng)).to(
+        DEV, torch.float16)
+    feats = rng.standard_normal((len(coords), 64)).astype(np.float16)
+    q = quantize_weight(w, group_size=32, bits=4)
+    x = _tensor(coords, feats)
+    out = ops.subm_conv3d(x, q, kernel_size=3)
+    _, ref = _reference(coords, feats.astype(np.float32),
+                        to_np(dequantize_weight(q).float()), dict(kernel_size=3))
+    _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16, 'config4')

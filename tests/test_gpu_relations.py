@@ -1,0 +1,269 @@
+"""GPU parity of the coordinate hash + kernel-map kernels (bit-exact).
+
+Every case runs the gfx950 relation kernels through the native binding
+(which calls the C ABI) and compares with the CPU oracle restating the
+reference route (native/features/coordinates/cpu/relation_build_detail.h:
+3-80, relation_views_detail.h:15-169).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_relation_equal, golden, native_relation_dict, to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+def _ext():
+    from mlx_lattice_amd._native import ext
+
+    return ext
+
+
+def _t(a) -> torch.Tensor:
+    return torch.as_tensor(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)
+
+
+def _active(n: int) -> torch.Tensor:
+    return torch.tensor([n], dtype=torch.int32, device=DEV)
+
+
+def _triple(v):
+    return list(v) if not isinstance(v, int) else [v, v, v]
+
+
+def gpu_forward(coords, active=None, kernel_size=3, stride=1, padding=0,
+                dilation=1) -> dict:
+    c = _t(coords)
+    n = c.shape[0] if active is None else active
+    native = _ext().build_kernel_relation_with_view(
+        c, _active(n), _triple(kernel_size), _triple(stride),
+        _triple(padding), _triple(dilation))
+    torch.cuda.synchronize()
+    return native_relation_dict(native)
+
+
+def gpu_target(coords, target, kernel_size=3, stride=1, padding=0,
+               dilation=1, active=None, target_active=None) -> dict:
+    c = _t(coords)
+    t = _t(target)
+    n = c.shape[0] if active is None else active
+    tn = t.shape[0] if target_active is None else target_active
+    native = _ext().build_target_kernel_relation_with_view(
+        c, _active(n), t, _active(tn), _triple(kernel_size),
+        _triple(stride), _triple(padding), _triple(dilation))
+    torch.cuda.synchronize()
+    return native_relation_dict(native)
+
+
+def check_forward(coords, active=None, **geom) -> dict:
+    print(f'forward relation rows={len(coords)} active={active} {geom}',
+          flush=True)
+    actual = gpu_forward(coords, active, **geom)
+    expected = O.kernel_relation(coords, active, **geom)
+    assert_relation_equal(actual, expected)
+    # The dense view produced by the same pass equals the reference view.
+    offs = O.kernel_offsets(geom.get('kernel_size', 3),
+                            geom.get('dilation', 1))
+    n_out = int(expected['counts'][1])
+    src_active = len(coords) if active is None else active
+    om, rm = O.implicit_gemm_view(coords, src_active, expected['out_coords'],
+                                  n_out, offs, geom.get('stride', 1),
+                                  geom.get('padding', 0))
+    np.testing.assert_array_equal(actual['out_in_map'], om)
+    np.testing.assert_array_equal(actual['row_masks'], rm)
+    return actual
+
+
+# ------------------------------------------------------------ golden ----
+
+
+def test_golden_forward_relation_line():
+    g = golden('forward_relation_line')
+    actual = gpu_forward(g['coords'], kernel_size=g['kernel_size'])
+    e = g['counts'][0]
+    assert actual['counts'].tolist() == g['counts']
+    assert actual['out_coords'].tolist() == g['out_coords']
+    for name in ('in_rows', 'out_rows', 'kernel_ids', 'in_edge_ids',
+                 'kernel_edge_ids'):
+        assert actual[name][:e].tolist() == g[name], name
+    for name in ('row_offsets', 'in_row_offsets', 'kernel_row_offsets'):
+        assert actual[name].tolist() == g[name], name
+
+
+def test_golden_target_relation_line():
+    g = golden('target_relation_line')
+    actual = gpu_target(g['coords'], g['target'], kernel_size=g['kernel_size'])
+    e = g['counts'][0]
+    assert actual['counts'].tolist() == g['counts']
+    for name in ('in_rows', 'out_rows', 'kernel_ids'):
+        assert actual[name][:e].tolist() == g[name], name
+    assert actual['row_offsets'].tolist() == g['row_offsets']
+
+
+def test_golden_strided_relation():
+    g = golden('strided_relation_pointwise')
+    actual = gpu_forward(g['coords'], kernel_size=g['kernel_size'],
+                         stride=g['stride'])
+    assert actual['counts'].tolist() == g['counts']
+    assert actual['out_coords'][:2].tolist() == g['out_coords']
+    assert actual['in_rows'][:2].tolist() == g['in_rows']
+
+
+@pytest.mark.parametrize('name', ['downsample_first_seen',
+                                  'downsample_negative_duplicates'])
+def test_golden_downsample_first_seen(name):
+    g = golden(name)
+    actual = gpu_forward(g['coords'], kernel_size=1, stride=g['stride'])
+    n = int(actual['counts'][1])
+    assert actual['out_coords'][:n].tolist() == g['out_coords']
+
+
+def test_golden_implicit_gemm_views():
+    g = golden('implicit_gemm_view_forward')
+    actual = gpu_forward(g['coords'], kernel_size=g['kernel_size'])
+    assert actual['out_in_map'].tolist() == g['out_in_map']
+    assert actual['row_masks'].tolist() == g['row_masks']
+    g = golden('implicit_gemm_view_target')
+    actual = gpu_target(g['coords'], g['target'], kernel_size=g['kernel_size'])
+    assert actual['out_in_map'].tolist() == g['out_in_map']
+    assert actual['row_masks'].tolist() == g['row_masks']
+    g = golden('implicit_gemm_view_33')
+    actual = gpu_forward(g['coords'], kernel_size=g['kernel_size'])
+    assert list(actual['out_in_map'].shape) == g['out_in_map_shape']
+    assert int(actual['out_in_map'][0, 16]) == g['out_in_map_16']
+    assert actual['row_masks'].tolist() == g['row_masks']
+
+
+def test_golden_standalone_implicit_gemm_view():
+    g = golden('implicit_gemm_view_target')
+    src = _t(g['coords'])
+    dst = _t(g['target'])
+    offs = _t(O.kernel_offsets(g['kernel_size']))
+    om, rm = _ext().build_relation_implicit_gemm_view(
+        src, _active(3), dst, _active(2), offs, [1, 1, 1], [0, 0, 0])
+    assert to_np(om).tolist() == g['out_in_map']
+    assert to_np(rm).tolist() == g['row_masks']
+
+
+def test_golden_sorted_view():
+    g = golden('sorted_view_line')
+    actual = gpu_forward(g['coords'], kernel_size=g['kernel_size'])
+    reorder, sorted_map, kv, tiles = _ext().build_sorted_implicit_gemm_view(
+        _t(actual['out_in_map']), _t(actual['row_masks']))
+    assert to_np(reorder).tolist() == g['reorder_rows']
+    assert to_np(sorted_map).tolist() == g['sorted_out_in_map']
+    assert to_np(kv).tolist() == g['sorted_kv_out_in_map']
+    assert to_np(tiles).tolist() == g['tile_masks']
+
+
+# ----------------------------------------------------- edge cases ----
+
+
+def test_empty_and_inactive_rows():
+    empty = np.zeros((0, 4), np.int32)
+    actual = gpu_forward(empty)
+    assert actual['counts'].tolist() == [0, 0]
+    assert actual['row_offsets'].tolist() == [0]
+    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0], [0, 2, 0, 0],
+                       [0, 3, 0, 0]], np.int32)
+    check_forward(coords, active=2, kernel_size=(3, 1, 1))
+    check_forward(coords, active=0, kernel_size=(3, 1, 1))
+    check_forward(coords, active=3, kernel_size=(3, 1, 1), stride=2)
+
+
+def test_duplicates_negative_and_batches():
+    rng = np.random.default_rng(7)
+    coords = rng.integers(-6, 6, size=(600, 4)).astype(np.int32)
+    coords[:, 0] = rng.integers(0, 3, size=600)
+    check_forward(coords)                                   # duplicates kept
+    check_forward(coords, kernel_size=2, stride=2)          # first-seen cells
+    check_forward(coords, kernel_size=3, stride=2, padding=1)
+    check_forward(coords, kernel_size=3, stride=1, padding=1)
+    check_forward(coords, kernel_size=(3, 3, 3), dilation=2)
+    check_forward(coords, kernel_size=(5, 5, 5))            # K = 125 > 64
+    check_forward(coords, kernel_size=(3, 3, 5))            # K = 45
+    tgt = rng.integers(-4, 4, size=(300, 4)).astype(np.int32)
+    tgt[:, 0] = rng.integers(0, 3, size=300)
+    for geom in (dict(kernel_size=3), dict(kernel_size=2, stride=2),
+                 dict(kernel_size=3, stride=2, padding=1)):
+        actual = gpu_target(coords, tgt, **geom)
+        expected = O.target_kernel_relation(coords, tgt, **geom)
+        assert_relation_equal(actual, expected, check_coords=False)
+
+
+def test_coordinate_range_is_rejected():
+    coords = np.array([[0, 0, 0, 0], [0, 200000, 0, 0]], np.int32)
+    with pytest.raises(ValueError, match='packed-key range'):
+        gpu_forward(coords)
+    coords = np.array([[1023, 0, 0, 0]], np.int32)
+    with pytest.raises(ValueError, match='packed-key range'):
+        gpu_forward(coords)
+
+
+def test_range_edges_are_exact():
+    lo, hi = -131072, 131071
+    coords = np.array([[0, lo, lo, lo], [0, hi, hi, hi], [1022, lo, 0, hi],
+                       [0, lo + 1, lo, lo], [0, hi - 1, hi, hi]], np.int32)
+    check_forward(coords)
+    check_forward(coords, kernel_size=2, stride=2)
+
+
+def test_repeated_builds_are_deterministic():
+    from mlx_lattice_amd.synthetic import config_rng, uniform_grid_cloud
+
+    coords = uniform_grid_cloud(5000, 24, rng=config_rng(1))
+    first = gpu_forward(coords)
+    for _ in range(3):
+        again = gpu_forward(coords)
+        for name in ('in_rows', 'in_edge_ids', 'kernel_edge_ids',
+                     'row_offsets', 'out_in_map'):
+            np.testing.assert_array_equal(first[name], again[name])
+
+
+# ------------------------------------------------ benchmark configs ----
+
+
+def test_config1_submanifold_map():
+    from mlx_lattice_amd.synthetic import config_rng, uniform_grid_cloud
+
+    coords = uniform_grid_cloud(20000, 64, rng=config_rng(1))
+    check_forward(coords, kernel_size=3)
+
+
+def test_config2_downsample_map():
+    from mlx_lattice_amd.synthetic import config_rng, lidar_cloud
+
+    coords = lidar_cloud(100000, 2, rng=config_rng(2))
+    actual = check_forward(coords, kernel_size=2, stride=2)
+    # k=2, s=2, p=0: every active input feeds exactly one (out, k) pair.
+    assert int(actual['counts'][0]) == len(coords)
+
+
+def test_config3_submanifold_map_400k():
+    from mlx_lattice_amd.synthetic import config_rng, sphere_shell_cloud
+
+    coords = sphere_shell_cloud(400000, 512, rng=config_rng(3))
+    actual = check_forward(coords, kernel_size=3)
+    # Every active row of a submanifold map has its own centre edge.
+    n = len(coords)
+    assert (actual['out_in_map'][:n, 13] == np.arange(n)).all()
+
+
+def test_config5_stage_chain():
+    from mlx_lattice_amd.synthetic import config_rng, lidar_cloud
+
+    coords = lidar_cloud(30000, 4, rng=config_rng(5))
+    check_forward(coords, kernel_size=3)
+    level = coords
+    for _ in range(3):
+        rel = check_forward(level, kernel_size=2, stride=2)
+        n = int(rel['counts'][1])
+        level = rel['out_coords'][:n]
+        check_forward(level, kernel_size=3)
