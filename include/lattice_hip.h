@@ -160,30 +160,43 @@ int lattice_hip_sparse_conv_features(
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, int out_capacity, void* out, void* stream);
 
-/* Implicit-GEMM conv over the sorted view: tile row i of the sorted order
- * gathers feats[sorted_out_in_map[i, k]] for every k and scatters its result
- * to out[reorder_rows[i]] (row i itself when reorder_rows is NULL).  fp16/bf16 with c_in % 32 == 0 and
- * c_out % 16 == 0 run on MFMA (fp32 accumulate); other shapes take the
- * bandwidth path. */
+/* Implicit-GEMM conv over the sorted view (the reference's sorted plan):
+ * row i of the mask-sorted order gathers feats[sorted_kv_out_in_map[k, i]]
+ * (-1 = no contribution) for every kernel offset k and writes its result to
+ * out[reorder_rows[i]] (row i itself when reorder_rows is NULL).
+ * tile_masks[4*t + q] is the OR of the row masks of rows 64t+16q..+15 and
+ * decides which offsets a 64-row tile visits.  fp16/bf16 with
+ * c_in % 32 == 0, c_out in {16, 32, 64, 128, 256} and K <= 32 run on the
+ * matrix cores (fp32 accumulate); other shapes return
+ * LATTICE_ERROR_UNSUPPORTED.  weights: (C_out, Kx, Ky, Kz, C_in). */
 int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out,
-    const int32_t* sorted_out_in_map, const int32_t* reorder_rows,
-    int out_capacity, void* out, void* stream);
+    const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
+    const int32_t* reorder_rows, int out_capacity, void* out, void* stream);
+
+/* Tuning knob with no counterpart in the reference: rows of the sorted
+ * order owned by one wavefront in the implicit-GEMM route (32 or 64).
+ * 64 doubles the reuse of each staged weight fragment, 32 halves the
+ * register footprint (two waves per SIMD).  Process-wide. */
+int lattice_hip_set_conv_tile_rows(int rows);
 
 /* Quantized conv (cpu/quantized.cpp:64-141): weights uint32
  * [K, storage_c_in*bits/32, c_out] with codes LSB-first along C_in,
  * scales/biases [K, storage_c_in/group_size, c_out] in the feature dtype,
- * w = q*scale + bias, fp32 accumulator.  When sorted_kv_out_in_map and
- * reorder_rows are non-NULL the MFMA route with the dequant fused into the
- * B-operand load is used (fp16, c_in % 32 == 0); otherwise the CSR route. */
+ * w = q*scale + bias, fp32 accumulator.  When sorted_kv_out_in_map,
+ * tile_masks and reorder_rows are non-NULL the MFMA route with the dequant
+ * fused into the
+ * B-operand staging is used (fp16/bf16, c_in % 32 == 0); otherwise the CSR
+ * route. */
 int lattice_hip_sparse_quantized_conv_features(
     int dtype, const void* feats, int n_in, int c_in, const uint32_t* weights,
     const void* scales, const void* biases, int kernel_count, int c_out,
     int storage_c_in, int group_size, int bits, const int32_t* in_rows,
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
-    const int32_t* reorder_rows, int out_capacity, void* out, void* stream);
+    const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
+    void* out, void* stream);
 
 #ifdef __cplusplus
 }

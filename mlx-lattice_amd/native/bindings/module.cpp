@@ -11,6 +11,7 @@
 
 #include "features/convolution/api.h"
 #include "features/coordinates/relations.h"
+#include "foundation/runtime.h"
 #include "lattice_hip.h"
 
 namespace ln = lattice_native;
@@ -125,6 +126,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("out_in_map"), py::arg("row_masks"),
         "Return (reorder_rows, sorted_out_in_map, sorted_kv_out_in_map, tile_masks).");
 
+    m.def(
+        "set_conv_tile_rows", [](int rows) { lattice_native::check_status(lattice_hip_set_conv_tile_rows(rows)); },
+        py::arg("rows"), "Rows of the sorted order per wavefront in the implicit-GEMM conv (32 or 64).");
     m.def("sparse_conv_features", &ln::sparse_conv_features, py::arg("feats"), py::arg("weights"),
           py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("kernel_row_offsets"),

@@ -141,11 +141,12 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
         weights_in.dim() == 5 ? weights_in.contiguous() : weights_in.permute({2, 0, 1}).contiguous();
     const int64_t c_out = out_channels_of(weights_in);
     at::Tensor out = at::empty({out_capacity, c_out}, feats.options());
-    const at::Tensor map = sorted_out_in_map.contiguous();
+    const at::Tensor kv = sorted_kv_out_in_map.contiguous();
+    const at::Tensor tiles = tile_masks.contiguous();
     const at::Tensor order = reorder_rows.contiguous();
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
-        weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(map),
+        weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(kv), ci32(tiles),
         store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), current_stream(feats)));
     return out;
 }
@@ -220,9 +221,11 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
     const at::Tensor biases = biases_in.contiguous();
     at::Tensor kv;
     at::Tensor order;
+    at::Tensor tiles;
     if (has_plan) {
         kv = sorted_kv_out_in_map.contiguous();
         order = reorder_rows.contiguous();
+        tiles = tile_masks.contiguous();
     }
     at::Tensor out = at::empty({out_capacity, out_channels}, feats.options());
     check_status(lattice_hip_sparse_quantized_conv_features(
@@ -230,7 +233,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
         in_channels, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(),
         n_kernels, out_channels, storage_in_channels, group_size, bits, ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), has_plan ? ci32(kv) : nullptr,
-        has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(), current_stream(feats)));
+        has_plan ? ci32(tiles) : nullptr, has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(),
+        current_stream(feats)));
     return out;
 }
 

@@ -19,14 +19,16 @@ void validate_coords(const at::Tensor& coords, const char* name = "coords") {
     if (coords.scalar_type() != at::kInt) {
         throw std::invalid_argument("GPU sparse relations require int32 coordinates.");
     }
-    require_device(coords, name);
 }
 
 void validate_active_rows(const at::Tensor& active_rows) {
     if (active_rows.dim() != 1 || active_rows.size(0) != 1 || active_rows.scalar_type() != at::kInt) {
         throw std::invalid_argument("active_rows must have shape (1,) and int32 dtype.");
     }
-    require_device(active_rows, "active_rows");
+}
+
+void require_on_device(std::initializer_list<std::pair<const at::Tensor*, const char*>> tensors) {
+    for (const auto& [t, name] : tensors) require_device(*t, name);
 }
 
 void validate_positive(const Triple& v, const char* name) {
@@ -109,6 +111,7 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
     validate_positive(stride, "stride");
     validate_nonnegative(padding, "padding");
     validate_positive(dilation, "dilation");
+    require_on_device({{&coords_in, "coords"}, {&active_rows, "active_rows"}});
     const at::Tensor coords = coords_in.contiguous();
     const int rows = static_cast<int>(coords.size(0));
     const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
@@ -141,6 +144,10 @@ NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, co
     validate_positive(stride, "stride");
     validate_nonnegative(padding, "padding");
     validate_positive(dilation, "dilation");
+    require_on_device({{&coords_in, "coords"},
+                       {&active_rows, "active_rows"},
+                       {&target_in, "target_coords"},
+                       {&target_active_rows, "target_active_rows"}});
     const at::Tensor coords = coords_in.contiguous();
     const at::Tensor target = target_in.contiguous();
     const int rows = static_cast<int>(coords.size(0));
@@ -172,6 +179,10 @@ std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(
     }
     validate_positive(stride, "stride");
     validate_nonnegative(padding, "padding");
+    require_on_device({{&source_in, "source_coords"},
+                       {&source_active_rows, "source_active_rows"},
+                       {&output_in, "output_coords"},
+                       {&output_active_rows, "output_active_rows"}});
     const at::Tensor source = source_in.contiguous();
     const at::Tensor output = output_in.contiguous();
     const at::Tensor offsets = offsets_in.to(source.device()).contiguous();

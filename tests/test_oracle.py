@@ -1,0 +1,351 @@
+"""Pins the CPU oracle (no GPU needed).
+
+The oracle restates the reference CPU route; these tests check it against
+(a) the known answers transcribed from the reference's own tests
+(tests/golden/reference_known_answers.json), (b) an independent numpy
+brute force written from the relation definition (dict lookups, no shared
+code with the C restatement), and (c) closed forms: a dense-box
+submanifold conv equals a zero-padded dense 3D cross-correlation, k=2 s=2
+gives E = N_in, the grouped views are stable partitions.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import golden
+from oracle import oracle as O
+
+
+# ------------------------------------------------------------ golden ----
+
+
+def test_kernel_offsets_golden():
+    g = golden('kernel_offsets_3x1x1')
+    assert O.kernel_offsets(g['kernel_size']).tolist() == g['expected']
+    offs = O.kernel_offsets(3)
+    assert offs.shape == (27, 3)
+    assert offs[13].tolist() == [0, 0, 0]
+    assert O.kernel_offsets(2).tolist()[:3] == [[0, 0, 0], [0, 0, 1],
+                                                [0, 1, 0]]
+
+
+def test_forward_relation_golden():
+    g = golden('forward_relation_line')
+    r = O.kernel_relation(np.array(g['coords']), kernel_size=g['kernel_size'])
+    e = g['counts'][0]
+    assert r['counts'].tolist() == g['counts']
+    assert r['out_coords'].tolist() == g['out_coords']
+    for name in ('in_rows', 'out_rows', 'kernel_ids', 'in_edge_ids',
+                 'kernel_edge_ids'):
+        assert r[name][:e].tolist() == g[name], name
+    for name in ('row_offsets', 'in_row_offsets', 'kernel_row_offsets'):
+        assert r[name].tolist() == g[name], name
+
+
+def test_target_relation_golden():
+    g = golden('target_relation_line')
+    r = O.target_kernel_relation(np.array(g['coords']), np.array(g['target']),
+                                 kernel_size=g['kernel_size'])
+    e = g['counts'][0]
+    assert r['counts'].tolist() == g['counts']
+    for name in ('in_rows', 'out_rows', 'kernel_ids'):
+        assert r[name][:e].tolist() == g[name]
+    assert r['row_offsets'].tolist() == g['row_offsets']
+
+
+def test_strided_and_downsample_golden():
+    g = golden('strided_relation_pointwise')
+    r = O.kernel_relation(np.array(g['coords']), kernel_size=1,
+                          stride=g['stride'])
+    assert r['counts'].tolist() == g['counts']
+    assert r['out_coords'][:2].tolist() == g['out_coords']
+    assert r['in_rows'][:2].tolist() == g['in_rows']
+    for name in ('downsample_first_seen', 'downsample_negative_duplicates'):
+        g = golden(name)
+        r = O.kernel_relation(np.array(g['coords']), kernel_size=1,
+                              stride=g['stride'])
+        n = int(r['counts'][1])
+        assert r['out_coords'][:n].tolist() == g['out_coords']
+
+
+def test_implicit_gemm_view_golden():
+    g = golden('implicit_gemm_view_forward')
+    c = np.array(g['coords'])
+    om, rm = O.implicit_gemm_view(c, 3, c, 3,
+                                  O.kernel_offsets(g['kernel_size']))
+    assert om.tolist() == g['out_in_map']
+    assert rm.tolist() == g['row_masks']
+    g = golden('implicit_gemm_view_target')
+    om, rm = O.implicit_gemm_view(np.array(g['coords']), 3,
+                                  np.array(g['target']), 2,
+                                  O.kernel_offsets(g['kernel_size']))
+    assert om.tolist() == g['out_in_map']
+    assert rm.tolist() == g['row_masks']
+    g = golden('implicit_gemm_view_33')
+    c = np.array(g['coords'])
+    om, rm = O.implicit_gemm_view(c, 1, c, 1,
+                                  O.kernel_offsets(g['kernel_size']))
+    assert list(om.shape) == g['out_in_map_shape']
+    assert int(om[0, 16]) == g['out_in_map_16']
+    assert rm.tolist() == g['row_masks']
+
+
+def _conv_golden(name, **kw):
+    g = golden(name)
+    coords = np.array(g['coords'])
+    rel = O.kernel_relation(coords, **kw)
+    w = np.array(g['weight'], np.float32).reshape(g['weight_5d_shape'])
+    out = O.conv_features(np.array(g['feats'], np.float32), w, rel)
+    n = int(rel['counts'][1])
+    return out[:n].tolist(), g
+
+
+def test_conv_golden():
+    out, g = _conv_golden('conv3d_generic_line', kernel_size=(3, 1, 1))
+    assert out == g['expected']
+    out, g = _conv_golden('subm_conv3d_line', kernel_size=(3, 1, 1))
+    assert out == g['expected']
+    out, g = _conv_golden('conv3d_strided_pointwise', kernel_size=1, stride=2)
+    assert out == g['expected']
+    g = golden('conv3d_target_line')
+    rel = O.target_kernel_relation(np.array(g['coords']),
+                                   np.array(g['target']), kernel_size=(3, 1, 1))
+    w = np.array(g['weight'], np.float32).reshape(g['weight_5d_shape'])
+    out = O.conv_features(np.array(g['feats'], np.float32), w, rel)
+    assert out.tolist() == g['expected']
+
+
+# ------------------------------------------------------- brute force ----
+
+
+def _floor_div(v, s):
+    return v // s  # python floor division
+
+
+def brute_forward(coords, kernel_size=3, stride=1, padding=0, dilation=1,
+                  active=None):
+    coords = [tuple(int(v) for v in row) for row in np.asarray(coords)]
+    if active is not None:
+        coords = coords[:active]
+    first = {}
+    for i, c in enumerate(coords):
+        first.setdefault(c, i)
+    s = (stride,) * 3 if isinstance(stride, int) else tuple(stride)
+    p = (padding,) * 3 if isinstance(padding, int) else tuple(padding)
+    if s == (1, 1, 1) and p == (0, 0, 0):
+        outs = list(coords)
+    else:
+        seen = {}
+        for c in coords:
+            q = (c[0], _floor_div(c[1], s[0]), _floor_div(c[2], s[1]),
+                 _floor_div(c[3], s[2]))
+            seen.setdefault(q, len(seen))
+        outs = list(seen)
+    ks = (kernel_size,) * 3 if isinstance(kernel_size, int) else kernel_size
+    d = (dilation,) * 3 if isinstance(dilation, int) else dilation
+    axes = [list(range(-(k // 2), k // 2 + 1)) if k % 2 else list(range(k))
+            for k in ks]
+    offs = [(x * d[0], y * d[1], z * d[2]) for x in axes[0] for y in axes[1]
+            for z in axes[2]]
+    edges = []
+    for o, c in enumerate(outs):
+        for k, off in enumerate(offs):
+            cand = (c[0], c[1] * s[0] + off[0] - p[0],
+                    c[2] * s[1] + off[1] - p[1], c[3] * s[2] + off[2] - p[2])
+            if cand in first:
+                edges.append((first[cand], o, k))
+    return outs, edges, len(offs)
+
+
+def _check_against_brute(coords, active=None, **geom):
+    r = O.kernel_relation(coords, active, **geom)
+    outs, edges, k = brute_forward(coords, active=active, **geom)
+    e = len(edges)
+    assert r['counts'].tolist() == [e, len(outs)]
+    assert r['out_coords'][:len(outs)].tolist() == [list(c) for c in outs]
+    got = list(zip(r['in_rows'][:e].tolist(), r['out_rows'][:e].tolist(),
+                   r['kernel_ids'][:e].tolist()))
+    assert got == edges
+    # Output CSR: monotone, last = E, rows own contiguous edge ranges.
+    ro = r['row_offsets']
+    assert (np.diff(ro) >= 0).all() and ro[-1] == e
+    outs_arr = np.array([x[1] for x in edges], np.int64)
+    for o in range(len(outs)):
+        assert (outs_arr[ro[o]:ro[o + 1]] == o).all()
+    # Grouped views are stable partitions of the edge ids.
+    for key, groups, name in ((0, r['in_row_offsets'].shape[0] - 1, 'in'),
+                              (2, k, 'kernel')):
+        ids = r[f'{name}_edge_ids'][:e]
+        offs = r[f'{name}_row_offsets' if name == 'kernel' else
+                 'in_row_offsets']
+        expect = sorted(range(e), key=lambda i: (edges[i][key], i))
+        assert ids.tolist() == expect
+        counts = np.bincount([edges[i][key] for i in range(e)],
+                             minlength=groups)
+        assert offs.tolist() == [0] + np.cumsum(counts).tolist()
+
+
+def test_brute_force_small_clouds():
+    rng = np.random.default_rng(3)
+    coords = rng.integers(-5, 5, size=(300, 4)).astype(np.int32)
+    coords[:, 0] = rng.integers(0, 2, size=300)
+    _check_against_brute(coords, kernel_size=3)
+    _check_against_brute(coords, kernel_size=2, stride=2)
+    _check_against_brute(coords, kernel_size=3, stride=2, padding=1)
+    _check_against_brute(coords, kernel_size=(3, 1, 5), dilation=(1, 1, 2))
+    _check_against_brute(coords, active=120, kernel_size=3)
+
+
+def test_k2s2_edge_count_closed_form():
+    rng = np.random.default_rng(4)
+    coords = np.unique(rng.integers(-20, 20, size=(2000, 4)), axis=0)
+    coords[:, 0] = 0
+    coords = np.unique(coords, axis=0).astype(np.int32)
+    r = O.kernel_relation(coords, kernel_size=2, stride=2)
+    assert int(r['counts'][0]) == len(coords)
+
+
+def test_submanifold_self_edge_invariant():
+    rng = np.random.default_rng(5)
+    coords = np.unique(rng.integers(0, 12, size=(500, 4)), axis=0)
+    coords[:, 0] = 0
+    coords = np.unique(coords, axis=0).astype(np.int32)
+    r = O.kernel_relation(coords, kernel_size=3)
+    om, _ = O.implicit_gemm_view(coords, len(coords), coords, len(coords),
+                                 O.kernel_offsets(3))
+    assert (om[:, 13] == np.arange(len(coords))).all()
+    # Symmetry of unique-coordinate submanifold maps: o->i at k  iff
+    # i->o at 26-k.
+    rows, ks = np.nonzero(om >= 0)
+    assert (om[om[rows, ks], 26 - ks] == rows).all()
+    assert int(r['counts'][0]) == int((om >= 0).sum())
+
+
+# ------------------------------------------------------ conv closed form --
+
+
+def test_dense_box_matches_dense_cross_correlation():
+    torch = pytest.importorskip('torch')
+    rng = np.random.default_rng(6)
+    size = 5
+    grid = np.stack(np.meshgrid(np.arange(size), np.arange(size),
+                                np.arange(size), indexing='ij'), -1)
+    coords = np.concatenate([np.zeros((size ** 3, 1), np.int64),
+                             grid.reshape(-1, 3)], 1).astype(np.int32)
+    perm = rng.permutation(len(coords))
+    coords = coords[perm]
+    c_in, c_out = 4, 3
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+    w = rng.standard_normal((c_out, 3, 3, 3, c_in)).astype(np.float32)
+    rel = O.kernel_relation(coords, kernel_size=3)
+    got = O.conv_features(feats, w, rel)
+    dense = np.zeros((1, c_in, size, size, size), np.float64)
+    dense[0, :, coords[:, 1], coords[:, 2], coords[:, 3]] = feats
+    ref = torch.nn.functional.conv3d(
+        torch.from_numpy(dense), torch.from_numpy(
+            w.transpose(0, 4, 1, 2, 3).astype(np.float64)), padding=1)
+    ref = ref[0].numpy()[:, coords[:, 1], coords[:, 2], coords[:, 3]].T
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    f64 = O.conv_features_fp64(feats, O.mapped_weight(w.astype(np.float64)),
+                               rel)
+    np.testing.assert_allclose(f64, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_k2s2_matches_strided_dense_conv():
+    torch = pytest.importorskip('torch')
+    rng = np.random.default_rng(8)
+    size = 6
+    grid = np.stack(np.meshgrid(np.arange(size), np.arange(size),
+                                np.arange(size), indexing='ij'), -1)
+    coords = np.concatenate([np.zeros((size ** 3, 1), np.int64),
+                             grid.reshape(-1, 3)], 1).astype(np.int32)
+    coords = coords[rng.permutation(len(coords))]
+    feats = rng.standard_normal((len(coords), 2)).astype(np.float32)
+    w = rng.standard_normal((3, 2, 2, 2, 2)).astype(np.float32)
+    rel = O.kernel_relation(coords, kernel_size=2, stride=2)
+    got = O.conv_features(feats, w, rel)
+    n = int(rel['counts'][1])
+    dense = np.zeros((1, 2, size, size, size), np.float64)
+    dense[0, :, coords[:, 1], coords[:, 2], coords[:, 3]] = feats
+    ref = torch.nn.functional.conv3d(
+        torch.from_numpy(dense),
+        torch.from_numpy(w.transpose(0, 4, 1, 2, 3).astype(np.float64)),
+        stride=2)[0].numpy()
+    oc = rel['out_coords'][:n]
+    np.testing.assert_allclose(got[:n], ref[:, oc[:, 1], oc[:, 2], oc[:, 3]].T,
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_fp16_routes_rounding_semantics():
+    rng = np.random.default_rng(9)
+    coords = np.unique(rng.integers(0, 10, size=(400, 4)), axis=0)
+    coords[:, 0] = 0
+    coords = np.unique(coords, axis=0).astype(np.int32)
+    rel = O.kernel_relation(coords, kernel_size=3)
+    for c_in, c_out, square in ((32, 32, True), (24, 40, False)):
+        f = rng.standard_normal((len(coords), c_in)).astype(np.float16)
+        w = (rng.standard_normal((c_out, 3, 3, 3, c_in)) * 0.05).astype(
+            np.float16)
+        got = O.conv_features(f, w, rel).astype(np.float64)
+        ref = O.conv_features_fp64(f.astype(np.float64),
+                                   O.mapped_weight(w.astype(np.float64)), rel)
+        err = np.abs(got - ref).max()
+        if square:
+            # fp32 accumulator, single rounding (eval_dense_channels_typed).
+            assert err <= np.abs(ref).max() * 2 ** -10
+        else:
+            # per-FMA fp16 rounding (eval_typed) is measurably worse.
+            assert err > 0
+            assert err < 0.1
+
+
+# ---------------------------------------------------------- quantized ----
+
+
+def test_unpack_formula_on_hand_built_words():
+    # int4: word 0x76543210 holds codes 0..7 for ci 0..7 (LSB first).
+    words = np.zeros((1, 1, 1), np.uint32)
+    words[0, 0, 0] = 0x76543210
+    scales = np.full((1, 1, 1), 0.5, np.float32)
+    biases = np.full((1, 1, 1), -1.0, np.float32)
+    deq = O.dequantize_mapped(words, scales, biases, in_channels=8,
+                              out_channels=1, storage_in_channels=8,
+                              group_size=8, bits=4)
+    assert deq[0, :, 0].tolist() == [0.5 * q - 1.0 for q in range(8)]
+    words = np.zeros((1, 2, 1), np.uint32)
+    words[0, 0, 0] = 0x04030201
+    words[0, 1, 0] = 0xFF000005
+    deq = O.dequantize_mapped(words, np.ones((1, 1, 1), np.float32),
+                              np.zeros((1, 1, 1), np.float32), in_channels=8,
+                              out_channels=1, storage_in_channels=8,
+                              group_size=8, bits=8)
+    assert deq[0, :, 0].tolist() == [1, 2, 3, 4, 5, 0, 0, 255]
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_quantized_route_matches_dequantized_float_route(bits):
+    rng = np.random.default_rng(10 + bits)
+    coords = np.unique(rng.integers(0, 8, size=(200, 4)), axis=0)
+    coords[:, 0] = 0
+    coords = np.unique(coords, axis=0).astype(np.int32)
+    rel = O.kernel_relation(coords, kernel_size=3)
+    k, c_in, c_out, g = 27, 40, 8, 32
+    storage = 64
+    words = rng.integers(0, 2 ** 32, size=(k, storage * bits // 32, c_out),
+                         dtype=np.uint64).astype(np.uint32)
+    scales = (rng.random((k, storage // g, c_out)) * 0.01).astype(np.float32)
+    biases = (rng.standard_normal((k, storage // g, c_out)) * 0.01).astype(
+        np.float32)
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+    got = O.quantized_conv_features(feats, words, scales, biases, rel,
+                                    in_channels=c_in, out_channels=c_out,
+                                    storage_in_channels=storage,
+                                    group_size=g, bits=bits)
+    deq = O.dequantize_mapped(words, scales, biases, in_channels=c_in,
+                              out_channels=c_out,
+                              storage_in_channels=storage, group_size=g,
+                              bits=bits)
+    ref = O.conv_features_fp64(feats, deq.astype(np.float64), rel)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
