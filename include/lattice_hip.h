@@ -88,7 +88,10 @@ int lattice_hip_kernel_offsets(const int kernel_size[3], const int dilation[3],
  * Only active prefixes are defined for in_rows/out_rows/kernel_ids/
  * in_edge_ids/kernel_edge_ids (counts[0] entries); row_offsets, the CSR row
  * offsets, counts, out_coords (zero tail), out_in_map (-1 tail) and
- * row_masks (zero tail) are fully written. */
+ * row_masks (zero tail) are fully written.  The four grouped-view pointers
+ * (in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids) are
+ * either all set, or all NULL to skip the views (they can be built later
+ * with lattice_hip_build_relation_grouped_views). */
 typedef struct lattice_relation_outputs {
     int32_t* in_rows;            /* device [edge_capacity] */
     int32_t* out_rows;           /* device [edge_capacity] */
@@ -127,6 +130,19 @@ int lattice_hip_build_target_kernel_relation(
     const int stride[3], const int padding[3], const int dilation[3],
     const lattice_relation_outputs* out, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Grouped CSR views of a relation: write_relation_grouped_view
+ * (relation_views_detail.h:84-120; relations.cpp:438-476).  Stable
+ * partition of the active edge ids by input row and by kernel offset:
+ * in_row_offsets [in_capacity + 1], kernel_row_offsets [kernel_count + 1];
+ * edge-id arrays [edge_capacity] defined on their first counts[0] entries. */
+size_t lattice_hip_relation_grouped_views_workspace_bytes(int edge_capacity);
+int lattice_hip_build_relation_grouped_views(
+    const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts,
+    int edge_capacity, int in_capacity, int kernel_count,
+    int32_t* in_row_offsets, int32_t* in_edge_ids, int32_t* kernel_row_offsets,
+    int32_t* kernel_edge_ids, void* workspace, size_t workspace_bytes,
+    void* stream);
 
 /* Dense out_in_map + row masks: write_relation_implicit_gemm_view
  * (relation_views_detail.h:122-169).  offsets: device int32 [K, 3]. */

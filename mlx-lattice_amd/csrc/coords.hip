@@ -256,126 +256,37 @@ emit_edges(const int32_t* __restrict__ out_in_map, int out_capacity, int K,
     }
 }
 
-// ------------------------------------------------- kernel-id CSR view ----
+// --------------------------------------------------- grouped CSR views ----
 //
-// Edge ids are partitioned by kernel id, stable in edge order.  The edge
-// array is cut into 1024-edge segments, one wave each: pass 1 counts per
-// (kernel, segment); the counts are scanned kernel-major; pass 2 replays the
-// segment in order and places every edge at its kernel's running cursor.
-
-constexpr int kSegment = 1024;
-
-__global__ void __launch_bounds__(kWave)
-kernel_group_count(const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts,
-                   int edge_capacity, int K, int segments, int32_t* __restrict__ seg_counts) {
-    extern __shared__ int lds_counts[];
-    const int seg = blockIdx.x;
-    for (int k = threadIdx.x; k < K; k += kWave) lds_counts[k] = 0;
-    __syncthreads();
-    const int E = min(counts[0], edge_capacity);
-    const int begin = seg * kSegment;
-    for (int i = threadIdx.x; i < kSegment; i += kWave) {
-        const int e = begin + i;
-        if (e < E) {
-            const int k = kernel_ids[e];
-            if (k >= 0 && k < K) atomicAdd(&lds_counts[k], 1);
-        }
-    }
-    __syncthreads();
-    for (int k = threadIdx.x; k < K; k += kWave) seg_counts[static_cast<long long>(k) * segments + seg] = lds_counts[k];
-}
-
-__global__ void __launch_bounds__(kWave)
-kernel_group_scatter(const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts,
-                     int edge_capacity, int K, int segments,
-                     const int32_t* __restrict__ seg_offsets, int32_t* __restrict__ edge_ids) {
-    extern __shared__ int lds_cursor[];
-    const int seg = blockIdx.x;
-    for (int k = threadIdx.x; k < K; k += kWave) lds_cursor[k] = seg_offsets[static_cast<long long>(k) * segments + seg];
-    __syncthreads();
-    const int E = min(counts[0], edge_capacity);
-    const int begin = seg * kSegment;
-    const int lane = lane_id();
-    for (int c = 0; c < kSegment; c += kWave) {
-        const int e = begin + c + lane;
-        int k = (e < E) ? kernel_ids[e] : -1;
-        if (k >= K) k = -1;
-        bool pending = k >= 0;
-        // Peel one kernel id per iteration: all lanes holding it get their
-        // rank among themselves, then the cursor advances.
-        while (true) {
-            const uint64_t todo = ballot(pending);
-            if (todo == 0) break;
-            const int leader = __ffsll(static_cast<long long>(todo)) - 1;
-            const int k0 = __shfl(k, leader, kWave);
-            const uint64_t same = ballot(pending && k == k0);
-            const int base = lds_cursor[k0];
-            if (pending && k == k0) {
-                edge_ids[base + lanes_below(same)] = e;
-                pending = false;
-            }
-            __syncthreads();
-            if (lane == leader) lds_cursor[k0] = base + __popcll(same);
-            __syncthreads();
-        }
-    }
-}
-
-__global__ void kernel_group_offsets(const int32_t* __restrict__ seg_offsets, int K, int segments,
-                                     const int32_t* __restrict__ counts, int edge_capacity,
-                                     int32_t* __restrict__ row_offsets) {
-    const int E = min(counts[0], edge_capacity);
-    for (int k = threadIdx.x; k <= K; k += blockDim.x) {
-        row_offsets[k] = k < K ? seg_offsets[static_cast<long long>(k) * segments] : E;
-    }
-}
-
-// --------------------------------------------------- input-row CSR view --
-//
-// Group sizes are bounded by the kernel volume (an input row feeds an output
-// row at most once per offset), so edges are placed with atomics and each
-// group is then sorted by edge id, which restores the stable order.
+// write_relation_grouped_view (relation_views_detail.h:84-120) is a stable
+// counting sort of edge ids by a group id (input row or kernel offset).
+// Here: keys = group of each active edge (inactive slots get the sentinel
+// `groups`, which sorts last), a stable LSD radix sort of (key, edge id),
+// and the row offsets read off the sorted keys.
 
 __global__ void __launch_bounds__(kThreads)
-count_groups(const int32_t* __restrict__ group_ids, const int32_t* __restrict__ counts,
-             int edge_capacity, int groups, int32_t* __restrict__ group_counts) {
-    const int E = min(counts[0], edge_capacity);
-    for (int e = blockIdx.x * kThreads + threadIdx.x; e < E; e += gridDim.x * kThreads) {
-        const int g = group_ids[e];
-        if (g >= 0 && g < groups) atomicAdd(group_counts + g, 1);
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-place_groups(const int32_t* __restrict__ group_ids, const int32_t* __restrict__ counts,
-             int edge_capacity, int groups, int32_t* __restrict__ cursors,
-             int32_t* __restrict__ edge_ids) {
-    const int E = min(counts[0], edge_capacity);
-    for (int e = blockIdx.x * kThreads + threadIdx.x; e < E; e += gridDim.x * kThreads) {
-        const int g = group_ids[e];
-        if (g >= 0 && g < groups) edge_ids[atomicAdd(cursors + g, 1)] = e;
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-sort_groups(const int32_t* __restrict__ offsets, int groups, int32_t* __restrict__ edge_ids) {
-    for (int g = blockIdx.x * kThreads + threadIdx.x; g < groups; g += gridDim.x * kThreads) {
-        const int b = offsets[g];
-        const int e = offsets[g + 1];
-        for (int i = b + 1; i < e; ++i) {
-            const int v = edge_ids[i];
-            int j = i - 1;
-            while (j >= b && edge_ids[j] > v) {
-                edge_ids[j + 1] = edge_ids[j];
-                --j;
-            }
-            edge_ids[j + 1] = v;
+group_keys(const int32_t* __restrict__ group_ids, const int32_t* __restrict__ counts, int capacity, int groups,
+           int32_t* __restrict__ keys, int32_t* __restrict__ ids) {
+    const int E = min(max(counts[0], 0), capacity);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < capacity; i += gridDim.x * kThreads) {
+        int g = groups;
+        if (i < E) {
+            const int v = group_ids[i];
+            g = (v >= 0 && v < groups) ? v : groups;
         }
+        keys[i] = g;
+        ids[i] = i;
     }
 }
 
-__global__ void copy_i32(const int32_t* __restrict__ src, int32_t* __restrict__ dst, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) dst[i] = src[i];
+// offsets[g] = number of sorted keys below g, for g in [0, groups].
+__global__ void __launch_bounds__(kThreads)
+group_offsets(const int32_t* __restrict__ sorted_keys, int capacity, int groups, int32_t* __restrict__ offsets) {
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i <= capacity; i += gridDim.x * kThreads) {
+        const int prev = i > 0 ? sorted_keys[i - 1] : -1;
+        const int cur = i < capacity ? sorted_keys[i] : groups + 1;
+        for (int g = prev + 1; g <= min(cur, groups); ++g) offsets[g] = i;
+    }
 }
 
 // ------------------------------------------------------------- helpers ----
@@ -419,55 +330,52 @@ int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int
     return LATTICE_OK;
 }
 
-size_t group_view_bytes(int edge_capacity, int in_capacity, int K) {
-    const long long segments = std::max(1, (edge_capacity + kSegment - 1) / kSegment);
-    size_t bytes = aligned_bytes(static_cast<size_t>(segments) * K * sizeof(int32_t));
-    bytes += scan_workspace_bytes(segments * K);
-    bytes += aligned_bytes(static_cast<size_t>(in_capacity + 1) * sizeof(int32_t));
-    bytes += scan_workspace_bytes(in_capacity + 1);
-    return bytes;
+size_t sort_temp_bytes(int n) {
+    size_t temp = 0;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, static_cast<const int32_t*>(nullptr),
+                                             static_cast<int32_t*>(nullptr), static_cast<const int32_t*>(nullptr),
+                                             static_cast<int32_t*>(nullptr), std::max(n, 1));
+    return temp;
 }
 
-int build_group_views(const lattice_relation_outputs* out, int edge_capacity, int in_capacity,
-                      int K, Workspace& ws, hipStream_t stream) {
-    // kernel-id CSR
-    const int segments = std::max(1, (edge_capacity + kSegment - 1) / kSegment);
-    int32_t* seg = ws.take<int32_t>(static_cast<size_t>(segments) * K);
-    LATTICE_REQUIRE(seg != nullptr, "relation workspace too small for the kernel view");
-    const size_t lds = static_cast<size_t>(K) * sizeof(int);
-    kernel_group_count<<<segments, kWave, lds, stream>>>(out->kernel_ids, out->counts, edge_capacity, K,
-                                                         segments, seg);
-    LATTICE_LAUNCH_CHECK();
-    int rc = exclusive_scan(seg, seg, static_cast<long long>(segments) * K, nullptr, ws, stream);
-    if (rc != LATTICE_OK) return rc;
-    kernel_group_scatter<<<segments, kWave, lds, stream>>>(out->kernel_ids, out->counts, edge_capacity, K,
-                                                           segments, seg, out->kernel_edge_ids);
-    LATTICE_LAUNCH_CHECK();
-    kernel_group_offsets<<<1, 256, 0, stream>>>(seg, K, segments, out->counts, edge_capacity,
-                                               out->kernel_row_offsets);
-    LATTICE_LAUNCH_CHECK();
+size_t group_view_bytes(int edge_capacity) {
+    const size_t n = static_cast<size_t>(std::max(edge_capacity, 1));
+    return 3 * aligned_bytes(n * sizeof(int32_t)) + aligned_bytes(sort_temp_bytes(edge_capacity)) + 1024;
+}
 
-    // input-row CSR
-    rc = fill_i32(out->in_row_offsets, in_capacity + 1, 0, stream);
-    if (rc != LATTICE_OK) return rc;
-    const unsigned eg = grid_for(edge_capacity, kThreads, 8192);
-    count_groups<<<eg, kThreads, 0, stream>>>(out->in_rows, out->counts, edge_capacity, in_capacity,
-                                              out->in_row_offsets);
+int bit_width(int v) {
+    int bits = 1;
+    while ((1 << bits) <= v) ++bits;
+    return bits;
+}
+
+// One grouped view: stable sort of edge ids by group; offsets[groups + 1].
+int build_group_view(const int32_t* group_ids, const int32_t* counts, int edge_capacity, int groups,
+                     int32_t* offsets, int32_t* edge_ids, Workspace ws, hipStream_t stream) {
+    if (edge_capacity <= 0) return fill_i32(offsets, groups + 1, 0, stream);
+    int32_t* keys = ws.take<int32_t>(edge_capacity);
+    int32_t* sorted = ws.take<int32_t>(edge_capacity);
+    int32_t* ids = ws.take<int32_t>(edge_capacity);
+    size_t temp_bytes = sort_temp_bytes(edge_capacity);
+    void* temp = ws.take<char>(temp_bytes);
+    LATTICE_REQUIRE(keys && sorted && ids && temp, "grouped view workspace too small.");
+    const unsigned g = grid_for(edge_capacity, kThreads, 8192);
+    group_keys<<<g, kThreads, 0, stream>>>(group_ids, counts, edge_capacity, groups, keys, ids);
     LATTICE_LAUNCH_CHECK();
-    rc = exclusive_scan(out->in_row_offsets, out->in_row_offsets, in_capacity + 1, nullptr, ws, stream);
-    if (rc != LATTICE_OK) return rc;
-    int32_t* cursors = ws.take<int32_t>(static_cast<size_t>(in_capacity) + 1);
-    LATTICE_REQUIRE(cursors != nullptr, "relation workspace too small for the input view");
-    copy_i32<<<grid_for(in_capacity + 1, kThreads, 4096), kThreads, 0, stream>>>(out->in_row_offsets, cursors,
-                                                                                 in_capacity + 1);
-    LATTICE_LAUNCH_CHECK();
-    place_groups<<<eg, kThreads, 0, stream>>>(out->in_rows, out->counts, edge_capacity, in_capacity, cursors,
-                                              out->in_edge_ids);
-    LATTICE_LAUNCH_CHECK();
-    sort_groups<<<grid_for(in_capacity, kThreads, 4096), kThreads, 0, stream>>>(out->in_row_offsets,
-                                                                                 in_capacity, out->in_edge_ids);
+    LATTICE_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted, ids, edge_ids, edge_capacity,
+                                                       0, bit_width(groups), stream));
+    group_offsets<<<grid_for(edge_capacity + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted, edge_capacity,
+                                                                                       groups, offsets);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
+}
+
+int build_group_views(const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
+                      int in_capacity, int K, int32_t* in_row_offsets, int32_t* in_edge_ids,
+                      int32_t* kernel_row_offsets, int32_t* kernel_edge_ids, Workspace& ws, hipStream_t stream) {
+    int rc = build_group_view(kernel_ids, counts, edge_capacity, K, kernel_row_offsets, kernel_edge_ids, ws, stream);
+    if (rc != LATTICE_OK) return rc;
+    return build_group_view(in_rows, counts, edge_capacity, in_capacity, in_row_offsets, in_edge_ids, ws, stream);
 }
 
 int validate_geometry(const int* size, const int* stride, const int* padding, const int* dilation) {
@@ -532,16 +440,21 @@ int finish_relation(QueryArgs q, int in_capacity, const lattice_relation_outputs
     if (rc != LATTICE_OK) return rc;
     rc = launch_emit(q.out_in_map, out_capacity, K, out, stream);
     if (rc != LATTICE_OK) return rc;
-    return build_group_views(out, out_capacity * K, in_capacity, K, ws, stream);
+    if (out->in_edge_ids == nullptr && out->kernel_edge_ids == nullptr) return LATTICE_OK;  // views on demand
+    return build_group_views(out->in_rows, out->kernel_ids, out->counts, out_capacity * K, in_capacity, K,
+                             out->in_row_offsets, out->in_edge_ids, out->kernel_row_offsets, out->kernel_edge_ids,
+                             ws, stream);
 }
 
 int check_outputs(const lattice_relation_outputs* out, bool need_coords, long long out_capacity, int K) {
     LATTICE_REQUIRE(out != nullptr, "relation outputs are required.");
-    LATTICE_REQUIRE(out->row_offsets && out->counts && out->in_row_offsets && out->kernel_row_offsets && out->status,
-                    "relation output pointers must be non-null.");
+    LATTICE_REQUIRE(out->row_offsets && out->counts && out->status, "relation output pointers must be non-null.");
+    const bool views = out->in_edge_ids != nullptr || out->kernel_edge_ids != nullptr;
+    LATTICE_REQUIRE(!views || (out->in_edge_ids && out->kernel_edge_ids && out->in_row_offsets &&
+                               out->kernel_row_offsets),
+                    "grouped view outputs must be all set or all null.");
     if (out_capacity > 0) {
-        LATTICE_REQUIRE(out->in_rows && out->out_rows && out->kernel_ids && out->in_edge_ids &&
-                            out->kernel_edge_ids && out->out_in_map && out->row_masks,
+        LATTICE_REQUIRE(out->in_rows && out->out_rows && out->kernel_ids && out->out_in_map && out->row_masks,
                         "relation output pointers must be non-null.");
         LATTICE_REQUIRE(!need_coords || out->out_coords != nullptr, "out_coords must be non-null.");
     }
@@ -556,7 +469,7 @@ size_t forward_relation_bytes(int rows, int K) {
     bytes += 2 * aligned_bytes(static_cast<size_t>(rows) * sizeof(int32_t)); // flags + positions
     bytes += scan_workspace_bytes(rows);
     bytes += scan_workspace_bytes(static_cast<long long>(rows) + 1);
-    bytes += group_view_bytes(rows * K, rows, K);
+    bytes += group_view_bytes(rows * K);
     return bytes + 4096;
 }
 
@@ -593,8 +506,7 @@ extern "C" size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kern
 extern "C" size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows, int kernel_count) {
     size_t bytes = table_bytes(std::max(rows, 0));
     bytes += scan_workspace_bytes(static_cast<long long>(std::max(target_rows, 0)) + 1);
-    bytes += group_view_bytes(std::max(target_rows, 0) * std::max(kernel_count, 1), std::max(rows, 0),
-                              std::max(kernel_count, 1));
+    bytes += group_view_bytes(std::max(target_rows, 0) * std::max(kernel_count, 1));
     return bytes + 4096;
 }
 
@@ -707,6 +619,28 @@ extern "C" int lattice_hip_build_target_kernel_relation(
     return finish_relation(q, rows, out, ws, stream);
 }
 
+extern "C" size_t lattice_hip_relation_grouped_views_workspace_bytes(int edge_capacity) {
+    return group_view_bytes(std::max(edge_capacity, 0));
+}
+
+extern "C" int lattice_hip_build_relation_grouped_views(const int32_t* in_rows, const int32_t* kernel_ids,
+                                                        const int32_t* counts, int edge_capacity, int in_capacity,
+                                                        int kernel_count, int32_t* in_row_offsets,
+                                                        int32_t* in_edge_ids, int32_t* kernel_row_offsets,
+                                                        int32_t* kernel_edge_ids, void* workspace,
+                                                        size_t workspace_bytes, void* stream_ptr) {
+    LATTICE_REQUIRE(edge_capacity >= 0 && in_capacity >= 0 && kernel_count > 0,
+                    "grouped views need non-negative capacities and a positive kernel count.");
+    LATTICE_REQUIRE(counts && in_row_offsets && kernel_row_offsets, "grouped view pointers must be non-null.");
+    LATTICE_REQUIRE(edge_capacity == 0 || (in_rows && kernel_ids && in_edge_ids && kernel_edge_ids),
+                    "grouped view pointers must be non-null.");
+    LATTICE_REQUIRE(workspace_bytes >= lattice_hip_relation_grouped_views_workspace_bytes(edge_capacity),
+                    "grouped view workspace too small.");
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    return build_group_views(in_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, in_row_offsets,
+                             in_edge_ids, kernel_row_offsets, kernel_edge_ids, ws, as_stream(stream_ptr));
+}
+
 extern "C" size_t lattice_hip_implicit_gemm_view_workspace_bytes(int source_rows) {
     return table_bytes(std::max(source_rows, 0)) + 4096;
 }
@@ -765,16 +699,32 @@ first_word_and_iota(const int32_t* __restrict__ row_masks, int rows, int words, 
     }
 }
 
+// Gathers 64 sorted rows of out_in_map per block through LDS: rows are
+// read as contiguous K-int segments, the sorted map is written as one
+// contiguous block and the K-major view as 64-int runs per offset.
+constexpr int kGatherRows = 64;
+
 __global__ void __launch_bounds__(kThreads)
 gather_sorted(const int32_t* __restrict__ out_in_map, int rows, int K, const int32_t* __restrict__ order,
               int32_t* __restrict__ sorted_map, int32_t* __restrict__ kv_map) {
-    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        const long long src = static_cast<long long>(order[i]) * K;
-        for (int k = 0; k < K; ++k) {
-            const int v = out_in_map[src + k];
-            sorted_map[static_cast<long long>(i) * K + k] = v;
-            kv_map[static_cast<long long>(k) * rows + i] = v;
-        }
+    __shared__ int32_t tile[kGatherRows * 33];
+    __shared__ int32_t src_rows[kGatherRows];
+    const int row0 = blockIdx.x * kGatherRows;
+    const int n = min(kGatherRows, rows - row0);
+    if (threadIdx.x < n) src_rows[threadIdx.x] = order[row0 + threadIdx.x];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n * K; i += kThreads) {
+        const int r = i / K;
+        const int k = i - r * K;
+        const int v = out_in_map[static_cast<long long>(src_rows[r]) * K + k];
+        tile[r * 33 + k] = v;
+        sorted_map[static_cast<long long>(row0) * K + i] = v;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n * K; i += kThreads) {
+        const int k = i / n;
+        const int r = i - k * n;
+        kv_map[static_cast<long long>(k) * rows + row0 + r] = tile[r * 33 + k];
     }
 }
 
@@ -829,9 +779,8 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
     LATTICE_LAUNCH_CHECK();
     LATTICE_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted_keys, ids, reorder_rows,
                                                        rows, 0, 32, stream));
-    gather_sorted<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(out_in_map, rows, kernel_count,
-                                                                          reorder_rows, sorted_out_in_map,
-                                                                          sorted_kv_out_in_map);
+    gather_sorted<<<(rows + kGatherRows - 1) / kGatherRows, kThreads, 0, stream>>>(
+        out_in_map, rows, kernel_count, reorder_rows, sorted_out_in_map, sorted_kv_out_in_map);
     LATTICE_LAUNCH_CHECK();
     tile_quarter_masks<<<grid_for(tiles * 4, kThreads, 4096), kThreads, 0, stream>>>(sorted_keys, rows, tiles,
                                                                                     tile_masks);

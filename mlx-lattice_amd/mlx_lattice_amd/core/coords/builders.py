@@ -167,6 +167,13 @@ def _kernel_relation_from_native(
                            else out_coords)
     implicit = (RelationImplicitGemmView(view[0], row_masks=view[1])
                 if len(view) == 2 else None)
+    grouped_views = None
+    if in_row_offsets is None:
+        n_kernels = len(offsets)
+
+        def grouped_views():
+            return _ext().build_relation_grouped_views(
+                in_rows, kernel_ids, counts, in_capacity, n_kernels)
     return KernelRelation(
         in_rows, out_rows, kernel_ids, row_offsets=row_offsets,
         counts=counts, in_row_offsets=in_row_offsets,
@@ -177,7 +184,8 @@ def _kernel_relation_from_native(
         n_kernels=len(offsets), source_coords=source_coords,
         source_active_rows=source_active_rows, target_coords=target_coords,
         target_active_rows=target_active_rows, stride=stride,
-        padding=padding, kind=kind, implicit_gemm=implicit)
+        padding=padding, kind=kind, implicit_gemm=implicit,
+        grouped_views=grouped_views)
 
 
 def _require_positive(values: Triple, name: str) -> None:

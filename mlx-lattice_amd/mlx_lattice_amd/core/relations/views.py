@@ -9,6 +9,7 @@ relation's device; counts stay on the device.
 
 from __future__ import annotations
 
+from collections.abc import Callable
 from dataclasses import dataclass
 from typing import Literal
 
@@ -184,8 +185,9 @@ class KernelRelation:
     contract: SparseRelationContract
     edges: RelationEdges
     output_csr: RelationCSRView
-    input_csr: RelationCSRView
-    kernel_csr: RelationCSRView
+    _input_csr: RelationCSRView | None
+    _kernel_csr: RelationCSRView | None
+    _grouped_views: Callable[[], tuple] | None
     implicit_gemm: RelationImplicitGemmView | None = None
     sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
 
@@ -215,7 +217,13 @@ class KernelRelation:
         kind: RelationKind = 'forward',
         implicit_gemm: RelationImplicitGemmView | None = None,
         sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None,
+        grouped_views: Callable[[], tuple] | None = None,
     ) -> None:
+        """``grouped_views``, when given and the input/kernel CSR arrays are
+        not, is called on first access of ``input_csr`` / ``kernel_csr`` and
+        returns ``(in_row_offsets, in_edge_ids, kernel_row_offsets,
+        kernel_edge_ids)``; the forward convolution never reads those
+        views, so they are only built for consumers that do."""
         device = in_rows.device
         if counts is None:
             counts = torch.tensor(
@@ -238,20 +246,24 @@ class KernelRelation:
                                       device=device)
         _validate_row_offsets(row_offsets)
         edges = RelationEdges(in_rows, out_rows, kernel_ids)
-        if in_row_offsets is None:
+        lazy_views = grouped_views is not None and in_row_offsets is None
+        if lazy_views:
+            pass
+        elif in_row_offsets is None:
             cap = int(contract.n_in_capacity or 0)
             in_row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
                                          device=device)
-        if in_edge_ids is None:
-            in_edge_ids = torch.zeros(edges.capacity, dtype=torch.int32,
-                                      device=device)
-        if kernel_row_offsets is None:
-            cap = int(contract.n_kernels or 0)
-            kernel_row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
-                                             device=device)
-        if kernel_edge_ids is None:
-            kernel_edge_ids = torch.zeros(edges.capacity, dtype=torch.int32,
+        if not lazy_views:
+            if in_edge_ids is None:
+                in_edge_ids = torch.zeros(edges.capacity, dtype=torch.int32,
                                           device=device)
+            if kernel_row_offsets is None:
+                cap = int(contract.n_kernels or 0)
+                kernel_row_offsets = torch.zeros(cap + 1, dtype=torch.int32,
+                                                 device=device)
+            if kernel_edge_ids is None:
+                kernel_edge_ids = torch.zeros(edges.capacity,
+                                              dtype=torch.int32, device=device)
         if (contract.n_out_capacity is not None
                 and int(row_offsets.shape[0])
                 != int(contract.n_out_capacity) + 1):
@@ -260,13 +272,37 @@ class KernelRelation:
         object.__setattr__(self, 'contract', contract)
         object.__setattr__(self, 'edges', edges)
         object.__setattr__(self, 'output_csr', RelationCSRView(row_offsets))
-        object.__setattr__(self, 'input_csr',
-                           RelationCSRView(in_row_offsets, in_edge_ids))
-        object.__setattr__(self, 'kernel_csr',
-                           RelationCSRView(kernel_row_offsets,
-                                           kernel_edge_ids))
+        object.__setattr__(
+            self, '_input_csr', None if lazy_views
+            else RelationCSRView(in_row_offsets, in_edge_ids))
+        object.__setattr__(
+            self, '_kernel_csr', None if lazy_views
+            else RelationCSRView(kernel_row_offsets, kernel_edge_ids))
+        object.__setattr__(self, '_grouped_views',
+                           grouped_views if lazy_views else None)
         object.__setattr__(self, 'implicit_gemm', implicit_gemm)
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
+
+    @property
+    def input_csr(self) -> RelationCSRView:
+        """Edges grouped by input row (stable in edge order)."""
+        if self._input_csr is None:
+            self._materialize_grouped_views()
+        return self._input_csr
+
+    @property
+    def kernel_csr(self) -> RelationCSRView:
+        """Edges grouped by kernel offset (stable in edge order)."""
+        if self._kernel_csr is None:
+            self._materialize_grouped_views()
+        return self._kernel_csr
+
+    def _materialize_grouped_views(self) -> None:
+        in_offsets, in_ids, k_offsets, k_ids = self._grouped_views()
+        object.__setattr__(self, '_input_csr',
+                           RelationCSRView(in_offsets, in_ids))
+        object.__setattr__(self, '_kernel_csr',
+                           RelationCSRView(k_offsets, k_ids))
 
     @property
     def edge_capacity(self) -> int:

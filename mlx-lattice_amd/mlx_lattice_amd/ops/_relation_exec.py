@@ -85,10 +85,9 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
         view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
         relation.edges.in_rows, relation.edges.out_rows,
         relation.edges.kernel_ids, relation.counts,
-        relation.output_csr.row_offsets, relation.input_csr.row_offsets,
-        relation.in_edge_ids, relation.kernel_csr.row_offsets,
-        relation.kernel_edge_ids, relation.n_out_capacity,
-        relation.n_kernels, store_sorted=store_sorted)
+        relation.output_csr.row_offsets, None, None, None, None,
+        relation.n_out_capacity, relation.n_kernels,
+        store_sorted=store_sorted)
 
 
 def sparse_quantized_conv_features_from_relation(

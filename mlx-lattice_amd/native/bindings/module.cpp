@@ -30,10 +30,11 @@ py::tuple relation_tuple(const ln::NativeKernelRelation& r) {
                           r.in_row_offsets, r.in_edge_ids, r.kernel_row_offsets, r.kernel_edge_ids);
 }
 
+// Grouped views are not built here (None); build_relation_grouped_views
+// makes them on demand.
 py::tuple relation_tuple_with_view(const ln::NativeKernelRelation& r) {
     return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
-                          r.in_row_offsets, r.in_edge_ids, r.kernel_row_offsets, r.kernel_edge_ids, r.out_in_map,
-                          r.row_masks);
+                          py::none(), py::none(), py::none(), py::none(), r.out_in_map, r.row_masks);
 }
 
 }  // namespace
@@ -57,7 +58,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
             auto r = ln::make_kernel_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
                                               triple_from_values(stride, "stride"),
                                               triple_from_values(padding, "padding"),
-                                              triple_from_values(dilation, "dilation"), check_range);
+                                              triple_from_values(dilation, "dilation"), check_range, !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
@@ -73,7 +74,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                            const std::vector<int>& kernel_size, const std::vector<int>& dilation, bool check_range) {
             auto r = ln::make_submanifold_kernel_relation(coords, active_rows,
                                                           triple_from_values(kernel_size, "kernel_size"),
-                                                          triple_from_values(dilation, "dilation"), check_range);
+                                                          triple_from_values(dilation, "dilation"), check_range, !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
@@ -91,7 +92,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
             auto r = ln::make_target_kernel_relation(
                 coords, active_rows, target_coords, target_active_rows,
                 triple_from_values(kernel_size, "kernel_size"), triple_from_values(stride, "stride"),
-                triple_from_values(padding, "padding"), triple_from_values(dilation, "dilation"), check_range);
+                triple_from_values(padding, "padding"), triple_from_values(dilation, "dilation"), check_range,
+                !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
@@ -103,6 +105,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
           py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
 
+    m.def(
+        "build_relation_grouped_views",
+        [](const at::Tensor& in_rows, const at::Tensor& kernel_ids, const at::Tensor& counts, int in_capacity,
+           int n_kernels) {
+            auto r = ln::make_relation_grouped_views(in_rows, kernel_ids, counts, in_capacity, n_kernels);
+            return py::make_tuple(std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r));
+        },
+        py::arg("in_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("in_capacity"), py::arg("n_kernels"),
+        "Return (in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids).");
     m.def(
         "build_relation_implicit_gemm_view",
         [](const at::Tensor& source_coords, const at::Tensor& source_active_rows, const at::Tensor& output_coords,
@@ -137,10 +148,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "sparse_conv_features_sorted_implicit_gemm",
         [](const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& sorted_out_in_map,
            const at::Tensor& sorted_kv_out_in_map, const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
-           const at::Tensor& /*in_rows*/, const at::Tensor& /*out_rows*/, const at::Tensor& /*kernel_ids*/,
-           const at::Tensor& /*counts*/, const at::Tensor& /*row_offsets*/, const at::Tensor& /*in_row_offsets*/,
-           const at::Tensor& /*in_edge_ids*/, const at::Tensor& /*kernel_row_offsets*/,
-           const at::Tensor& /*kernel_edge_ids*/, int out_capacity, int n_kernels, bool store_sorted) {
+           // The relation arrays of the reference signature are accepted and
+           // not read: the sorted view already holds the map.
+           const py::object& /*in_rows*/, const py::object& /*out_rows*/, const py::object& /*kernel_ids*/,
+           const py::object& /*counts*/, const py::object& /*row_offsets*/, const py::object& /*in_row_offsets*/,
+           const py::object& /*in_edge_ids*/, const py::object& /*kernel_row_offsets*/,
+           const py::object& /*kernel_edge_ids*/, int out_capacity, int n_kernels, bool store_sorted) {
             return ln::sparse_conv_features_sorted_implicit_gemm(feats, weights, sorted_out_in_map,
                                                                  sorted_kv_out_in_map, reorder_rows, tile_masks,
                                                                  out_capacity, n_kernels, store_sorted);

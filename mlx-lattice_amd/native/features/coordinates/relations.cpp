@@ -53,7 +53,8 @@ void check_coordinate_range(const at::Tensor& status) {
     }
 }
 
-NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_capacity, int K, bool coords) {
+NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_capacity, int K, bool coords,
+                              bool views) {
     const int64_t edges = static_cast<int64_t>(out_capacity) * K;
     NativeKernelRelation r;
     r.in_rows = empty_i32({edges}, like);
@@ -62,10 +63,12 @@ NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_c
     r.output_row_offsets = empty_i32({out_capacity + 1}, like);
     if (coords) r.out_coords = empty_i32({out_capacity, 4}, like);
     r.counts = empty_i32({2}, like);
-    r.in_row_offsets = empty_i32({in_capacity + 1}, like);
-    r.in_edge_ids = empty_i32({edges}, like);
-    r.kernel_row_offsets = empty_i32({K + 1}, like);
-    r.kernel_edge_ids = empty_i32({edges}, like);
+    if (views) {
+        r.in_row_offsets = empty_i32({in_capacity + 1}, like);
+        r.in_edge_ids = empty_i32({edges}, like);
+        r.kernel_row_offsets = empty_i32({K + 1}, like);
+        r.kernel_edge_ids = empty_i32({edges}, like);
+    }
     r.out_in_map = empty_i32({out_capacity, K}, like);
     r.row_masks = empty_i32({out_capacity, (K + 31) / 32}, like);
     return r;
@@ -79,10 +82,11 @@ lattice_relation_outputs outputs_of(NativeKernelRelation& r, at::Tensor& status)
     o.row_offsets = i32(r.output_row_offsets);
     o.out_coords = r.out_coords.defined() ? i32(r.out_coords) : nullptr;
     o.counts = i32(r.counts);
-    o.in_row_offsets = i32(r.in_row_offsets);
-    o.in_edge_ids = i32(r.in_edge_ids);
-    o.kernel_row_offsets = i32(r.kernel_row_offsets);
-    o.kernel_edge_ids = i32(r.kernel_edge_ids);
+    const bool views = r.in_edge_ids.defined();
+    o.in_row_offsets = views ? i32(r.in_row_offsets) : nullptr;
+    o.in_edge_ids = views ? i32(r.in_edge_ids) : nullptr;
+    o.kernel_row_offsets = views ? i32(r.kernel_row_offsets) : nullptr;
+    o.kernel_edge_ids = views ? i32(r.kernel_edge_ids) : nullptr;
     o.out_in_map = i32(r.out_in_map);
     o.row_masks = i32(r.row_masks);
     o.status = i32(status);
@@ -104,7 +108,7 @@ std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation) {
 
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool check_range) {
+                                          bool check_range, bool with_views) {
     validate_coords(coords_in);
     validate_active_rows(active_rows);
     validate_positive(kernel_size, "kernel_size");
@@ -115,7 +119,7 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
     const at::Tensor coords = coords_in.contiguous();
     const int rows = static_cast<int>(coords.size(0));
     const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
-    NativeKernelRelation r = allocate(coords, rows, rows, K, true);
+    NativeKernelRelation r = allocate(coords, rows, rows, K, true, with_views);
     at::Tensor status = empty_i32({1}, coords);
     lattice_relation_outputs o = outputs_of(r, status);
     at::Tensor ws = workspace(lattice_hip_kernel_relation_workspace_bytes(rows, K), coords);
@@ -128,14 +132,16 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
 }
 
 NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
-                                                      Triple kernel_size, Triple dilation, bool check_range) {
-    return make_kernel_relation(coords, active_rows, kernel_size, {1, 1, 1}, {0, 0, 0}, dilation, check_range);
+                                                      Triple kernel_size, Triple dilation, bool check_range,
+                                                      bool with_views) {
+    return make_kernel_relation(coords, active_rows, kernel_size, {1, 1, 1}, {0, 0, 0}, dilation, check_range,
+                                with_views);
 }
 
 NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                                  const at::Tensor& target_in, const at::Tensor& target_active_rows,
                                                  Triple kernel_size, Triple stride, Triple padding,
-                                                 Triple dilation, bool check_range) {
+                                                 Triple dilation, bool check_range, bool with_views) {
     validate_coords(coords_in);
     validate_coords(target_in, "target_coords");
     validate_active_rows(active_rows);
@@ -153,7 +159,7 @@ NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, co
     const int rows = static_cast<int>(coords.size(0));
     const int target_rows = static_cast<int>(target.size(0));
     const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
-    NativeKernelRelation r = allocate(coords, target_rows, rows, K, false);
+    NativeKernelRelation r = allocate(coords, target_rows, rows, K, false, with_views);
     r.out_coords = target;
     at::Tensor status = empty_i32({1}, coords);
     lattice_relation_outputs o = outputs_of(r, status);
@@ -165,6 +171,35 @@ NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, co
         static_cast<size_t>(ws.numel()), current_stream(coords)));
     if (check_range) check_coordinate_range(status);
     return r;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_relation_grouped_views(
+    const at::Tensor& in_rows_in, const at::Tensor& kernel_ids_in, const at::Tensor& counts, int in_capacity,
+    int kernel_count) {
+    if (in_rows_in.dim() != 1 || kernel_ids_in.dim() != 1 || in_rows_in.scalar_type() != at::kInt ||
+        kernel_ids_in.scalar_type() != at::kInt || in_rows_in.size(0) != kernel_ids_in.size(0)) {
+        throw std::invalid_argument("relation rows and kernel_ids must be equal-length int32 arrays.");
+    }
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("relation counts must have shape (2,) and int32 dtype.");
+    }
+    if (in_capacity < 0 || kernel_count <= 0) {
+        throw std::invalid_argument("grouped views need a non-negative input capacity and positive n_kernels.");
+    }
+    require_on_device({{&in_rows_in, "in_rows"}, {&kernel_ids_in, "kernel_ids"}, {&counts, "counts"}});
+    const at::Tensor in_rows = in_rows_in.contiguous();
+    const at::Tensor kernel_ids = kernel_ids_in.contiguous();
+    const int edges = static_cast<int>(in_rows.size(0));
+    at::Tensor in_offsets = empty_i32({in_capacity + 1}, in_rows);
+    at::Tensor in_ids = empty_i32({edges}, in_rows);
+    at::Tensor k_offsets = empty_i32({kernel_count + 1}, in_rows);
+    at::Tensor k_ids = empty_i32({edges}, in_rows);
+    at::Tensor ws = workspace(lattice_hip_relation_grouped_views_workspace_bytes(edges), in_rows);
+    check_status(lattice_hip_build_relation_grouped_views(
+        ci32(in_rows), ci32(kernel_ids), ci32(counts), edges, in_capacity, kernel_count, i32(in_offsets),
+        i32(in_ids), i32(k_offsets), i32(k_ids), ws.data_ptr(), static_cast<size_t>(ws.numel()),
+        current_stream(in_rows)));
+    return {in_offsets, in_ids, k_offsets, k_ids};
 }
 
 std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(

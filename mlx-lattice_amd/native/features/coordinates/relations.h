@@ -33,19 +33,26 @@ std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation);
 
 // check_range: read the device status word after the build and raise when an
 // active coordinate does not fit the packed key (one host wait).
+// with_views: also build the grouped CSR views (otherwise their tensors
+// stay undefined and make_relation_grouped_views builds them on demand).
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool check_range = true);
+                                          bool check_range = true, bool with_views = true);
 
 NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                                       Triple kernel_size, Triple dilation,
-                                                      bool check_range = true);
+                                                      bool check_range = true, bool with_views = true);
 
 NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                                  const at::Tensor& target_coords,
                                                  const at::Tensor& target_active_rows, Triple kernel_size,
                                                  Triple stride, Triple padding, Triple dilation,
-                                                 bool check_range = true);
+                                                 bool check_range = true, bool with_views = true);
+
+// (in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids)
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_relation_grouped_views(
+    const at::Tensor& in_rows, const at::Tensor& kernel_ids, const at::Tensor& counts, int in_capacity,
+    int kernel_count);
 
 std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(
     const at::Tensor& source_coords, const at::Tensor& source_active_rows, const at::Tensor& output_coords,

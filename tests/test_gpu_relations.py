@@ -38,6 +38,14 @@ def _triple(v):
     return list(v) if not isinstance(v, int) else [v, v, v]
 
 
+def _with_grouped_views(native, in_capacity, k):
+    """The *_with_view builders skip the grouped CSR views; build them with
+    the on-demand entry point, as the Python relation does."""
+    views = _ext().build_relation_grouped_views(native[0], native[2], native[5],
+                                                in_capacity, k)
+    return tuple(native[:6]) + tuple(views) + tuple(native[10:])
+
+
 def gpu_forward(coords, active=None, kernel_size=3, stride=1, padding=0,
                 dilation=1) -> dict:
     c = _t(coords)
@@ -45,6 +53,8 @@ def gpu_forward(coords, active=None, kernel_size=3, stride=1, padding=0,
     native = _ext().build_kernel_relation_with_view(
         c, _active(n), _triple(kernel_size), _triple(stride),
         _triple(padding), _triple(dilation))
+    k = len(O.kernel_offsets(kernel_size, dilation))
+    native = _with_grouped_views(native, c.shape[0], k)
     torch.cuda.synchronize()
     return native_relation_dict(native)
 
@@ -58,6 +68,8 @@ def gpu_target(coords, target, kernel_size=3, stride=1, padding=0,
     native = _ext().build_target_kernel_relation_with_view(
         c, _active(n), t, _active(tn), _triple(kernel_size),
         _triple(stride), _triple(padding), _triple(dilation))
+    k = len(O.kernel_offsets(kernel_size, dilation))
+    native = _with_grouped_views(native, c.shape[0], k)
     torch.cuda.synchronize()
     return native_relation_dict(native)
 
@@ -95,6 +107,22 @@ def test_golden_forward_relation_line():
         assert actual[name][:e].tolist() == g[name], name
     for name in ('row_offsets', 'in_row_offsets', 'kernel_row_offsets'):
         assert actual[name].tolist() == g[name], name
+
+
+def test_eager_ten_tuple_matches_on_demand_views():
+    from mlx_lattice_amd.synthetic import config_rng, uniform_grid_cloud
+
+    coords = uniform_grid_cloud(3000, 20, rng=config_rng(1))
+    lazy = gpu_forward(coords, kernel_size=3)
+    eager = native_relation_dict(_ext().build_kernel_relation(
+        _t(coords), _active(len(coords)), [3, 3, 3], [1, 1, 1], [0, 0, 0],
+        [1, 1, 1]))
+    assert_relation_equal(eager, lazy)
+    expected = O.kernel_relation(coords, kernel_size=3)
+    assert_relation_equal(eager, expected)
+    assert len(_ext().build_kernel_relation(
+        _t(coords), _active(len(coords)), [3, 3, 3], [1, 1, 1], [0, 0, 0],
+        [1, 1, 1])) == 10
 
 
 def test_golden_target_relation_line():
@@ -271,3 +299,50 @@ def test_config5_stage_chain():
         n = int(rel['counts'][1])
         level = rel['out_coords'][:n]
         check_forward(level, kernel_size=3)
+
+
+def test_sorted_view_matches_stable_argsort():
+    from mlx_lattice_amd.synthetic import config_rng, sphere_shell_cloud
+
+    coords = sphere_shell_cloud(30000, 160, rng=config_rng(3))
+    actual = gpu_forward(coords, kernel_size=3)
+    reorder, sorted_map, kv, tiles = _ext().build_sorted_implicit_gemm_view(
+        _t(actual['out_in_map']), _t(actual['row_masks']))
+    masks = actual['row_masks'][:, 0]
+    expect = np.argsort(masks, kind='stable')
+    np.testing.assert_array_equal(to_np(reorder), expect)
+    smap = actual['out_in_map'][expect]
+    np.testing.assert_array_equal(to_np(sorted_map), smap)
+    np.testing.assert_array_equal(to_np(kv), smap.T)
+    n = len(coords)
+    pad = (-n) % 64
+    sm = np.concatenate([masks[expect], np.zeros(pad, masks.dtype)])
+    quarters = np.bitwise_or.reduce(sm.reshape(-1, 16), axis=1)
+    np.testing.assert_array_equal(to_np(tiles), quarters)
+
+
+def test_python_relation_views_on_demand():
+    from mlx_lattice_amd.core.coords.builders import (
+        build_kernel_relation,
+        build_submanifold_kernel_relation,
+    )
+    from mlx_lattice_amd.synthetic import config_rng, uniform_grid_cloud
+
+    coords = uniform_grid_cloud(4000, 24, rng=config_rng(1))
+    for build, kw, geom in ((build_submanifold_kernel_relation,
+                             dict(kernel_size=3), dict(kernel_size=3)),
+                            (build_kernel_relation,
+                             dict(kernel_size=2, stride=2),
+                             dict(kernel_size=2, stride=2))):
+        rel = build(_t(coords), **kw)
+        assert rel._input_csr is None  # not built by the forward path
+        expected = O.kernel_relation(coords, **geom)
+        e = int(expected['counts'][0])
+        np.testing.assert_array_equal(to_np(rel.in_row_offsets),
+                                      expected['in_row_offsets'])
+        np.testing.assert_array_equal(to_np(rel.in_edge_ids)[:e],
+                                      expected['in_edge_ids'][:e])
+        np.testing.assert_array_equal(to_np(rel.kernel_row_offsets),
+                                      expected['kernel_row_offsets'])
+        np.testing.assert_array_equal(to_np(rel.kernel_edge_ids)[:e],
+                                      expected['kernel_edge_ids'][:e])
