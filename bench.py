@@ -33,6 +33,10 @@ for _p in (ROOT, ROOT / 'mlx-lattice_amd'):
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# HBM bytes per conv_igemm launch on this workload, from rocprofv3 FETCH_SIZE
+# and WRITE_SIZE passes scaled by a 1 GiB copy's counter readings
+# (profiles/conv_igemm_config3_traffic.md).  Re-measure when the kernel changes.
+CONV_TRAFFIC_BYTES = 1.160e9
 
 
 def parse_args():
@@ -46,7 +50,24 @@ def parse_args():
     p.add_argument('--cpu-sample-rows', type=int, default=131072,
                    help='output rows of the bounded CPU-baseline sample')
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--copy-probe-mib', type=int, default=0,
+                   help='only run a plain device copy of this many MiB '
+                        '(5 launches) and exit: the reference kernel that '
+                        'scales the FETCH_SIZE / WRITE_SIZE counters')
     return p.parse_args()
+
+
+def copy_probe(mib: int) -> int:
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device='cuda:0')
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_probe_bytes': n, 'launches': 5}), flush=True)
+    return 0
 
 
 def make_workload():
@@ -113,6 +134,8 @@ def main() -> int:
               'exchange (see DESIGN.md), so run one process per GPU.',
               file=sys.stderr)
         return 2
+    if args.copy_probe_mib:
+        return copy_probe(args.copy_probe_mib)
     import torch
 
     from mlx_lattice_amd._native import ext
@@ -208,7 +231,7 @@ def main() -> int:
             'peak': PEAK_FP16_TFLOPS,
             'unit': 'TFLOP/s',
             'frac': round(conv_tflops / PEAK_FP16_TFLOPS, 5),
-            'traffic': None,
+            'traffic': CONV_TRAFFIC_BYTES,
             'kernel': 'conv_igemm<_Float16,128,FloatB>',
         },
     }

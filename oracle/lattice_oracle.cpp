@@ -10,6 +10,27 @@
 // candidate coordinates never wrap.
 //
 // Build: see oracle/Makefile (g++ -O3 -mf16c -shared -fPIC).
+//
+// How each function is pinned (tests/test_oracle.py):
+//   oracle_kernel_offsets          reference known answers (golden JSON).
+//   oracle_kernel_relation         reference known answers (forward, strided,
+//                                  first-seen downsample, negative duplicates),
+//                                  brute force over small seeded clouds, E = N
+//                                  for k2s2, a self edge per submanifold row.
+//   oracle_target_kernel_relation  reference known answers, brute force.
+//   oracle_grouped_view            reference known answers (the 10-tuple's
+//                                  grouped CSR entries).
+//   oracle_implicit_gemm_view      reference known answers (forward, target,
+//                                  K = 33 two-word masks).
+//   oracle_conv_features           reference known answers, dense box ==
+//                                  torch conv3d(padding=1), k2s2 == strided
+//                                  dense conv3d, fp16 rounding of the two CPU
+//                                  routes checked against a float64 sum.
+//   oracle_quantized_conv_features unpack formula on hand-built words, equal
+//   oracle_dequantize_mapped       to the float route on dequantized weights.
+// Not restated here, hence parity unpinned: the reference's quantizer
+// (mx.quantize codes and scales; the product defines its own) and the tie
+// order of the reference's mask argsort beyond its three-row known answer.
 
 #include <immintrin.h>
 
