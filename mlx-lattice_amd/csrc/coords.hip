@@ -72,6 +72,35 @@ clear_table(uint64_t* keys, int32_t* rows, int capacity) {
     }
 }
 
+// Clears a block table: key = empty, all eight rows absent (0).  One thread
+// per 16-byte quarter of a bucket.
+__global__ void __launch_bounds__(kThreads)
+clear_blocks(BlockBucket* buckets, long long quarters) {
+    int4* q = reinterpret_cast<int4*>(buckets);
+    for (long long i = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; i < quarters;
+         i += static_cast<long long>(gridDim.x) * kThreads) {
+        q[i] = (i & 3) == 0 ? make_int4(-1, -1, 0, 0) : make_int4(0, 0, 0, 0);
+    }
+}
+
+// Inserts the active rows into the block table; flags coordinates outside
+// the packed-key range.
+__global__ void __launch_bounds__(kThreads)
+insert_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
+              const int32_t* __restrict__ active_rows, int32_t* status) {
+    const int active = min(max(*active_rows, 0), rows);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < active; i += gridDim.x * kThreads) {
+        const int4 c = load_coord(coords, i);
+        uint64_t block_key;
+        int octant;
+        if (!block_of(c.x, c.y, c.z, c.w, &block_key, &octant)) {
+            status[0] = LATTICE_STATUS_COORD_RANGE;
+            continue;
+        }
+        table.insert(block_key, octant, i);
+    }
+}
+
 // Inserts active rows keyed by their coordinate (cell_stride == 1) or by the
 // floor-divided cell (cell_stride > 1 on an axis).
 __global__ void __launch_bounds__(kThreads)
@@ -166,7 +195,7 @@ struct QueryArgs {
     const int32_t* offsets;      // device [K,3] or null (closed form)
     KernelGeometry geom;
     int words;
-    CoordTable table;
+    BlockTable table;
     int32_t* out_in_map;         // [out_capacity, K]
     int32_t* row_masks;          // [out_capacity, words]
     int32_t* degrees;            // [out_capacity] or null
@@ -202,8 +231,9 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
                 int64_t x = static_cast<int64_t>(oc.y) * a.geom.stride.x + off.x - a.geom.padding.x;
                 int64_t y = static_cast<int64_t>(oc.z) * a.geom.stride.y + off.y - a.geom.padding.y;
                 int64_t z = static_cast<int64_t>(oc.w) * a.geom.stride.z + off.z - a.geom.padding.z;
-                uint64_t key;
-                if (pack_key(oc.x, x, y, z, &key)) found = a.table.find(key);
+                uint64_t block_key;
+                int octant;
+                if (block_of(oc.x, x, y, z, &block_key, &octant)) found = a.table.find(block_key, octant);
             }
             if (row_ok && k < K) a.out_in_map[row * K + k] = found;
             const uint64_t hits = ballot(found >= 0);
@@ -325,6 +355,39 @@ int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int
     if (rows > 0) {
         insert_rows<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
             *table, coords, rows, active_rows, cell, status);
+        LATTICE_LAUNCH_CHECK();
+    }
+    return LATTICE_OK;
+}
+
+// Bucket count of the block table: a power of two above 1.5x the row count,
+// so the load factor stays below 2/3 even when every voxel has its own block.
+int block_capacity(int rows) {
+    int cap = 1;
+    const long long want = std::max(static_cast<long long>(rows) + rows / 2 + 1, 1ll);
+    while (cap < want) cap <<= 1;
+    return cap;
+}
+
+size_t block_table_bytes(int rows) {
+    return aligned_bytes(static_cast<size_t>(block_capacity(rows)) * sizeof(BlockBucket));
+}
+
+int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows, int32_t* status, Workspace& ws,
+                      hipStream_t stream, BlockTable* table) {
+    const int cap = block_capacity(rows);
+    table->buckets = ws.take<BlockBucket>(cap);
+    table->mask = static_cast<uint32_t>(cap - 1);
+    if (table->buckets == nullptr) {
+        set_error("relation workspace too small for the coordinate table");
+        return LATTICE_ERROR_INVALID_ARGUMENT;
+    }
+    const long long quarters = 4ll * cap;
+    clear_blocks<<<grid_for(quarters, kThreads, 8192), kThreads, 0, stream>>>(table->buckets, quarters);
+    LATTICE_LAUNCH_CHECK();
+    if (rows > 0) {
+        insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows,
+                                                                              status);
         LATTICE_LAUNCH_CHECK();
     }
     return LATTICE_OK;
@@ -465,7 +528,7 @@ int check_outputs(const lattice_relation_outputs* out, bool need_coords, long lo
 }  // namespace
 
 size_t forward_relation_bytes(int rows, int K) {
-    size_t bytes = 2 * table_bytes(rows);                                  // coords + cells
+    size_t bytes = block_table_bytes(rows) + table_bytes(rows);           // coords + cells
     bytes += 2 * aligned_bytes(static_cast<size_t>(rows) * sizeof(int32_t)); // flags + positions
     bytes += scan_workspace_bytes(rows);
     bytes += scan_workspace_bytes(static_cast<long long>(rows) + 1);
@@ -504,7 +567,7 @@ extern "C" size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kern
 }
 
 extern "C" size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows, int kernel_count) {
-    size_t bytes = table_bytes(std::max(rows, 0));
+    size_t bytes = block_table_bytes(std::max(rows, 0));
     bytes += scan_workspace_bytes(static_cast<long long>(std::max(target_rows, 0)) + 1);
     bytes += group_view_bytes(std::max(target_rows, 0) * std::max(kernel_count, 1));
     return bytes + 4096;
@@ -531,8 +594,8 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
 
     rc = fill_i32(out->status, 1, 0, stream);
     if (rc != LATTICE_OK) return rc;
-    CoordTable table;
-    rc = build_table(coords, rows, active_rows, Int3{1, 1, 1}, out->status, ws, stream, &table);
+    BlockTable table;
+    rc = build_block_table(coords, rows, active_rows, out->status, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
 
     const bool identity = stride[0] == 1 && stride[1] == 1 && stride[2] == 1 && padding[0] == 0 &&
@@ -601,8 +664,8 @@ extern "C" int lattice_hip_build_target_kernel_relation(
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     rc = fill_i32(out->status, 1, 0, stream);
     if (rc != LATTICE_OK) return rc;
-    CoordTable table;
-    rc = build_table(coords, rows, active_rows, Int3{1, 1, 1}, out->status, ws, stream, &table);
+    BlockTable table;
+    rc = build_block_table(coords, rows, active_rows, out->status, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
     set_out_count<<<1, 64, 0, stream>>>(target_active_rows, target_rows, out->counts);
     LATTICE_LAUNCH_CHECK();
@@ -642,7 +705,7 @@ extern "C" int lattice_hip_build_relation_grouped_views(const int32_t* in_rows, 
 }
 
 extern "C" size_t lattice_hip_implicit_gemm_view_workspace_bytes(int source_rows) {
-    return table_bytes(std::max(source_rows, 0)) + 4096;
+    return block_table_bytes(std::max(source_rows, 0)) + 4096;
 }
 
 extern "C" int lattice_hip_build_relation_implicit_gemm_view(
@@ -664,8 +727,8 @@ extern "C" int lattice_hip_build_relation_implicit_gemm_view(
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     int rc = fill_i32(status, 1, 0, stream);
     if (rc != LATTICE_OK) return rc;
-    CoordTable table;
-    rc = build_table(source_coords, source_rows, source_active_rows, Int3{1, 1, 1}, status, ws, stream, &table);
+    BlockTable table;
+    rc = build_block_table(source_coords, source_rows, source_active_rows, status, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
     QueryArgs q{};
     q.out_coords = output_coords;

@@ -145,6 +145,68 @@ struct CoordTable {
     }
 };
 
+// Block-bucketed coordinate table for the kernel-map queries.  A bucket is
+// one 64-byte line holding a 2x2x2 block of the lattice: the packed key of
+// the block (batch, x>>1, y>>1, z>>1) and the first input row of each of its
+// eight voxels.  The 27 neighbours of a voxel lie in at most eight blocks,
+// so a row's probes touch at most eight lines, lanes probing the same block
+// share one line request, and a probe reads its key and its row from the
+// same line.  Rows are stored as kRowBias - row so that the cleared value 0
+// means "absent" and atomicMax keeps the smallest (first) row.
+constexpr int32_t kRowBias = 0x7fffffff;
+
+struct alignas(64) BlockBucket {
+    unsigned long long key;
+    int32_t rows[8];
+    int32_t pad[6];
+};
+static_assert(sizeof(BlockBucket) == 64, "one bucket per 64-byte line");
+
+// Block key and octant of a voxel; false when it does not fit the packed key.
+__host__ __device__ inline bool block_of(int64_t b, int64_t x, int64_t y, int64_t z, uint64_t* block_key,
+                                         int* octant) {
+    uint64_t key;
+    if (!pack_key(b, x, y, z, &key)) return false;
+    pack_key(b, x >> 1, y >> 1, z >> 1, block_key);  // arithmetic shift = floor(v / 2)
+    *octant = static_cast<int>(((x & 1) << 2) | ((y & 1) << 1) | (z & 1));
+    return true;
+}
+
+struct BlockTable {
+    BlockBucket* buckets;
+    uint32_t mask;  // bucket count - 1; the count exceeds the block count
+
+    __device__ inline void insert(uint64_t block_key, int octant, int32_t row) const {
+        uint32_t slot = static_cast<uint32_t>(mix64(block_key)) & mask;
+        while (true) {
+            unsigned long long* kp = &buckets[slot].key;
+            unsigned long long k = __atomic_load_n(kp, __ATOMIC_RELAXED);
+            if (k == kEmptyKey) {
+                k = atomicCAS(kp, static_cast<unsigned long long>(kEmptyKey),
+                              static_cast<unsigned long long>(block_key));
+                if (k == kEmptyKey) k = block_key;
+            }
+            if (k == block_key) {
+                atomicMax(&buckets[slot].rows[octant], kRowBias - row);
+                return;
+            }
+            slot = (slot + 1) & mask;
+        }
+    }
+
+    // First row of the voxel, or -1.
+    __device__ inline int32_t find(uint64_t block_key, int octant) const {
+        uint32_t slot = static_cast<uint32_t>(mix64(block_key)) & mask;
+        while (true) {
+            const unsigned long long k = buckets[slot].key;
+            const int32_t r = buckets[slot].rows[octant];
+            if (k == block_key) return r == 0 ? -1 : kRowBias - r;
+            if (k == kEmptyKey) return -1;
+            slot = (slot + 1) & mask;
+        }
+    }
+};
+
 // floor division for a positive divisor (quantization_detail.h:3-10).
 __host__ __device__ inline int64_t floor_div_pos(int64_t v, int64_t d) {
     int64_t q = v / d;
