@@ -193,8 +193,9 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
 
 /* Tuning knob with no counterpart in the reference: rows of the sorted
  * order owned by one wavefront in the implicit-GEMM route (32 or 64).
- * 64 doubles the reuse of each staged weight fragment, 32 halves the
- * register footprint (two waves per SIMD).  Process-wide. */
+ * 64 doubles the reuse of each staged weight fragment; 32 (the default)
+ * keeps the register footprint low enough for three blocks per CU.
+ * Process-wide. */
 int lattice_hip_set_conv_tile_rows(int rows);
 
 /* Quantized conv (cpu/quantized.cpp:64-141): weights uint32

@@ -140,26 +140,27 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
 
 // ------------------------------------------------------ implicit GEMM ----
 //
-// Block = 4 waves.  Each wave owns 64 consecutive rows of the mask-sorted
-// order and WAVE_COLS = min(C_OUT, 128) output channels, so its fp32
-// accumulators (64 x WAVE_COLS) live in registers for the whole kernel.
-// The pipeline walks stages (k, 128-channel chunk of C_in) over the offsets
-// any row of the block uses:
-//   * B = W[k][co][chunk] is staged once per block into one of two LDS
-//     buffers while the previous stage computes (loads issued before the
-//     MFMAs, stored after them);
-//   * A is gathered per wave straight from global memory into the MFMA
-//     operand registers (16 bytes per lane per 32-channel step), zero where
-//     the map says -1, so no LDS traffic or barrier is spent on A;
-//   * a wave skips the MFMAs of offsets its own 64 rows never use (its mask
-//     is the OR of its tile's four quarter masks).
-// The epilogue stages the tile through LDS and writes whole output rows
-// (16 bytes per lane) to out[reorder_rows[row]].
+// Block = WAVES waves.  Each wave owns WAVE_ROWS consecutive rows of the
+// mask-sorted order and WAVE_COLS = min(C_OUT, 128) output channels; its
+// fp32 accumulators stay in registers for the whole kernel.  The pipeline
+// walks stages s = (k, 128-channel chunk of C_in) over the offsets any row
+// of the block uses.  During stage s a wave
+//   * issues the row indices of stage s+DEPTH+1 (k-major map: one
+//     contiguous run of rows per offset),
+//   * issues the loads of B(s+1) = W[k][:, chunk] into registers,
+//   * issues the gather of A(s+DEPTH) (16 bytes per lane per 32-channel
+//     step, straight into MFMA operand registers),
+//   * runs the MFMAs of stage s on A(s), loaded DEPTH stages earlier, and
+//     on B(s) from LDS, skipping offsets that none of its rows uses,
+//   * stores B(s+1) into the other LDS buffer, then meets the block at a
+//     barrier.
+// Every load is an ordinary load the compiler tracks, so it waits only for
+// the operands each step uses and the gathers of DEPTH stages stay in flight
+// across the MFMAs.  Missing rows (map entry -1) load row 0 and are zeroed
+// at use, so every lane issues the same loads.  The epilogue stages the tile
+// through LDS and writes whole output rows (16 bytes per lane) to
+// out[reorder_rows[row]].
 
-constexpr int kBlock = 256;
-constexpr int kWaveRows = 64;
-constexpr int kChunk = 128;  // input channels per pipeline stage
-constexpr int kBPad = 8;     // halves of padding per staged B row (bank spread)
 
 template <typename T> struct MfmaOps;
 template <> struct MfmaOps<_Float16> {
@@ -175,35 +176,66 @@ template <> struct MfmaOps<__bf16> {
     }
 };
 
-template <int C_OUT, int WAVE_ROWS> struct IgemmShape {
+// Tile and pipeline shape of the matrix-core kernel.
+//   C_OUT      output channels (the block covers all of them);
+//   WAVE_ROWS  sorted rows per wave (16-row MFMA blocks: RB = WAVE_ROWS/16);
+//   WAVES      waves per block;
+//   CHUNK      input channels per stage (64 or 128);
+//   DEPTH      stages of A gathers in flight ahead of the computing stage;
+//   BPIPE      read the B fragments of the next 32-channel step from LDS
+//              while the current step's MFMAs run;
+//   OCC        blocks per CU the register allocation must allow.
+template <int C_OUT_, int WAVE_ROWS_, int WAVES_, int CHUNK_ = 128, int DEPTH_ = 1, bool BPIPE_ = false,
+          int OCC_ = (WAVE_ROWS_ == 32 ? 2 : 1)>
+struct IgemmShape {
+    static constexpr int OCC = OCC_;
+    static constexpr int C_OUT = C_OUT_;
+    static constexpr int WAVE_ROWS = WAVE_ROWS_;
+    static constexpr int WAVES = WAVES_;
+    static constexpr int CHUNK = CHUNK_;
+    static constexpr int DEPTH = DEPTH_;
+    static constexpr bool BPIPE = BPIPE_;
     static constexpr int WAVE_COLS = C_OUT < 128 ? C_OUT : 128;
+    static constexpr int THREADS = WAVES * 64;
     static constexpr int CG = C_OUT / WAVE_COLS;  // column groups
-    static constexpr int RG = 4 / CG;             // row groups
+    static constexpr int RG = WAVES / CG;         // row groups
     static constexpr int BLOCK_ROWS = WAVE_ROWS * RG;
     static constexpr int CB = WAVE_COLS / 16;     // 16-col blocks per wave
     static constexpr int RB = WAVE_ROWS / 16;     // 16-row blocks per wave
-    static constexpr int ST = kChunk / 32;        // 32-channel steps per stage
-    // Staged B: C_OUT rows of kChunk halves (256 bytes, sixteen 16-byte
-    // pieces); piece p of row r lives at slot p ^ (r % 16), so the sixteen
-    // rows read by one MFMA fragment hit sixteen different bank groups.
-    static constexpr int BROW = kChunk;
+    static constexpr int ST = CHUNK / 32;         // 32-channel steps per stage
+    static constexpr int NA = DEPTH + 1;          // A register buffers
+    // Unrolled stages per loop trip: a multiple of the two B buffers and
+    // of the NA A buffers, so every buffer is a compile-time choice, and
+    // long enough that most blocks never take the loop back-edge (where the
+    // compiler's wait bookkeeping turns conservative and drains all loads).
+    static constexpr int UNROLL = NA == 3 ? 12 : 16;
+    static_assert(UNROLL % 2 == 0 && UNROLL % NA == 0, "unroll must cycle every buffer");
+    // Staged B: C_OUT rows of CHUNK halves (PIECES 16-byte pieces); piece p
+    // of row r lives at slot p ^ (r % PIECES), so the rows read by one MFMA
+    // fragment hit distinct bank groups.
+    static constexpr int PIECES = CHUNK / 8;
+    static constexpr int BROW = CHUNK;
     static constexpr int BBUF = C_OUT * BROW;     // one B buffer (halves)
     static constexpr int EROW = WAVE_COLS;        // epilogue row (halves, swizzled pieces)
     static constexpr int EPIECES = WAVE_COLS / 8;  // 16-byte pieces per epilogue row
-    static constexpr int B_PIECES = C_OUT * kChunk / 8 / kBlock;  // 16-byte pieces per thread
-    static constexpr int B_DMA = C_OUT / 16;      // direct loads per wave (4 rows each)
-    static_assert(2 * WAVE_ROWS * EROW <= BBUF, "epilogue staging must fit one B buffer per wave pair");
+    static constexpr int B_PIECES = C_OUT * CHUNK / 8 / THREADS;  // 16-byte pieces per thread
+    static constexpr int MAX_STAGES = 32 * (512 / CHUNK);  // K <= 32 offsets x C_in <= 512
+    static_assert(CHUNK == 64 || CHUNK == 128, "stage chunk is 64 or 128 channels");
+    static_assert(B_PIECES >= 1, "B tile must cover every thread");
+    // One LDS array holds the two B buffers and, after the main loop, the
+    // epilogue staging of every wave's tile.
+    static constexpr int EPI = WAVES * WAVE_ROWS * EROW;
+    static constexpr int LDS_HALVES = 2 * BBUF > EPI ? 2 * BBUF : EPI;
 };
 
-__device__ inline int swizzle_piece(int piece, int row) { return piece ^ (row & 15); }
+template <int PIECES>
+__device__ inline int swizzle_piece(int piece, int row) { return piece ^ (row & (PIECES - 1)); }
 
 // B operand sources.  `load(k, co, ci0)` returns 8 consecutive input
 // channels ci0..ci0+7 of W[k][:, co] as one 16-byte vector.
 template <typename T> struct FloatB {
-    static constexpr bool kDirect = true;  // staged with direct global->LDS loads
     const T* w;
     long long s_co, s_k;  // element strides; C_in is contiguous
-    __device__ inline const T* ptr(int k, int co, int ci0) const { return w + co * s_co + k * s_k + ci0; }
     __device__ inline typename MfmaOps<T>::vec load(int k, int co, int ci0) const {
         return *reinterpret_cast<const typename MfmaOps<T>::vec*>(w + co * s_co + k * s_k + ci0);
     }
@@ -211,7 +243,6 @@ template <typename T> struct FloatB {
 
 // Packed affine codes: w = q * scale + bias, dequantised while staging B.
 template <typename T> struct PackedB {
-    static constexpr bool kDirect = false;  // dequantised in registers, then stored
     const uint32_t* w;
     const T* scales;
     const T* biases;
@@ -241,17 +272,9 @@ template <typename T> struct PackedB {
     }
 };
 
-template <typename V>
-__device__ inline V zero_vec() {
-    V v;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = 0;
-    return v;
-}
-
-// Row indices of this wave's A operand for stage (k): rows row0 + 16*rb +
-// lane%16 of the sorted order; -1 where there is no input row.
-// Rows past the end re-read the last row; their result is never stored.
+// Row indices of this wave's A operand for offset k: rows row0 + 16*rb +
+// lane%16 of the sorted order; -1 where there is no input row.  Rows past
+// the end re-read the last row; their result is never stored.
 template <int RB>
 __device__ inline void load_rows(int (&idx)[RB], const int32_t* __restrict__ kv_map, int rows, int row0, int k,
                                  int lr) {
@@ -262,193 +285,152 @@ __device__ inline void load_rows(int (&idx)[RB], const int32_t* __restrict__ kv_
     }
 }
 
+// Feature rows as a raw buffer of n_in * c_in elements (under 2 GiB, which
+// the route check enforces).  A row address is a 32-bit byte offset; the
+// buffer's range check returns zeros past the end, and a missing input row
+// (map entry -1) wraps to an offset past the end, so it reads as zeros with
+// no select at use.
+template <typename T>
+__device__ inline __amdgpu_buffer_rsrc_t feature_rows(const T* feats, int n_in, int c_in) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(feats), 0,
+                                             static_cast<int>(static_cast<long long>(n_in) * c_in * sizeof(T)),
+                                             0x00020000);
+}
+
 // A operand of one stage: RB x ST fragments of 16 bytes per lane (channels
 // ci_base + 32*st + 8*(lane/16) .. +7).  Every lane issues the same loads
-// on every stage (missing rows read row 0, steps past the chunk re-read its
-// first step), so the loads in flight are the same on all paths and the
-// compiler's waits stay partial; rows without input are zeroed at use.
+// (steps past the chunk re-read its first step).
 template <typename T, typename V, int RB, int ST>
-__device__ inline void load_a(V (&a)[RB][ST], const int (&idx)[RB], const T* __restrict__ feats, int c_in,
+__device__ inline void load_a(V (&a)[RB][ST], const int (&idx)[RB], __amdgpu_buffer_rsrc_t rows_rsrc, int c_in,
                               int ci_base, int cw, int lk) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        const T* src = feats + static_cast<long long>(idx[rb] >= 0 ? idx[rb] : 0) * c_in + ci_base + lk;
+        const unsigned row = static_cast<unsigned>(idx[rb]) * static_cast<unsigned>(c_in * sizeof(T));
 #pragma unroll
         for (int st = 0; st < ST; ++st) {
             const int off = st * 32 < cw ? st * 32 : 0;
-            a[rb][st] = *reinterpret_cast<const V*>(src + off);
+            a[rb][st] = __builtin_bit_cast(
+                V, __builtin_amdgcn_raw_buffer_load_b128(
+                       rows_rsrc, static_cast<int>(row + (ci_base + lk + off) * sizeof(T)), 0, 0));
         }
     }
 }
 
-constexpr int kMaxStages = 32 * 4;  // K <= 32 offsets x C_in <= 512 in 128-channel chunks
-
-// Direct global->LDS staging of one B tile (float weights): each wave
-// issues B_DMA loads; one load moves four 256-byte rows, lane l filling
-// slot l%16 of row l/16 with the piece that the swizzle maps there.
-template <typename T, int C_OUT, int WAVE_ROWS, typename BSource>
-__device__ inline void stage_b_direct(const BSource& bsrc, int k, int ci0, int cw, T* dst, int wave, int lane) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
-#pragma unroll
-    for (int i = 0; i < S::B_DMA; ++i) {
-        const int r0 = (i * 4 + wave) * 4;
-        const int row = r0 + (lane >> 4);
-        const int piece = swizzle_piece(lane & 15, row);
-        const int ci = piece * 8 < cw ? piece * 8 : 0;
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(bsrc.ptr(k, row, ci0 + ci)),
-                                         (__attribute__((address_space(3))) void*)(dst + r0 * S::BROW),
-                                         16, 0, 0);
-    }
-}
-
-// Register staging of one B tile (packed weights, dequantised on load).
-template <typename T, int C_OUT, int WAVE_ROWS, typename BSource, typename VT>
-__device__ inline void stage_b_load(const BSource& bsrc, int k, int ci0, int cw,
-                                    VT (&breg)[IgemmShape<C_OUT, WAVE_ROWS>::B_PIECES]) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
+// Register staging of one B tile: thread t holds pieces t + i*THREADS
+// (row co = piece / 16), four consecutive rows per wave per load.
+template <typename T, typename S, typename BSource, typename V>
+__device__ inline void stage_b_load(const BSource& bsrc, int k, int ci0, int cw, V (&breg)[S::B_PIECES]) {
 #pragma unroll
     for (int i = 0; i < S::B_PIECES; ++i) {
-        const int p = threadIdx.x + i * kBlock;
-        const int co = p / (kChunk / 8);
-        const int piece = p - co * (kChunk / 8);
+        const int p = threadIdx.x + i * S::THREADS;
+        const int co = p / S::PIECES;
+        const int piece = p - co * S::PIECES;
         breg[i] = bsrc.load(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0));
     }
 }
 
-template <typename T, int C_OUT, int WAVE_ROWS, typename VT>
-__device__ inline void stage_b_store(T* dst, const VT (&breg)[IgemmShape<C_OUT, WAVE_ROWS>::B_PIECES]) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
+template <typename T, typename S, typename V>
+__device__ inline void stage_b_store(T* dst, const V (&breg)[S::B_PIECES]) {
 #pragma unroll
     for (int i = 0; i < S::B_PIECES; ++i) {
-        const int p = threadIdx.x + i * kBlock;
-        const int co = p / (kChunk / 8);
-        const int piece = p - co * (kChunk / 8);
-        *reinterpret_cast<VT*>(dst + co * S::BROW + swizzle_piece(piece, co) * 8) = breg[i];
+        const int p = threadIdx.x + i * S::THREADS;
+        const int co = p / S::PIECES;
+        const int piece = p - co * S::PIECES;
+        *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = breg[i];
     }
 }
 
-// s_waitcnt immediate that waits until at most `n` vector-memory operations
-// are outstanding and leaves the other counters alone (gfx9 encoding).
-constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
-
-template <typename T>
-__device__ inline uint32_t lds_address(const T* p) {
-    return static_cast<uint32_t>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) void*)p));
+// B fragments of 32-channel step `st` for the wave's CB column blocks.
+template <typename T, typename S, typename V>
+__device__ inline void read_b_step(V (&b)[S::CB], const T* brow, int st, int lane, int lr) {
+    const T* bp = brow + swizzle_piece<S::PIECES>(st * 4 + (lane >> 4), lr) * 8;
+#pragma unroll
+    for (int cb = 0; cb < S::CB; ++cb) b[cb] = *reinterpret_cast<const V*>(bp + cb * 16 * S::BROW);
 }
 
-// Reads CB B fragments (16 bytes per lane, STRIDE bytes apart) from LDS and
-// waits for them.  The reads are issued as inline assembly: the compiler
-// would otherwise treat them as possibly aliasing the direct global->LDS
-// loads in flight into the other B buffer and drain every vector-memory
-// load first.  The buffer read here was completed by the explicit wait and
-// barrier that ended the previous stage.  The empty asm statements tie the
-// fragment registers to the wait so no MFMA can be scheduled above it.
-template <typename V, int CB, int STRIDE>
-__device__ inline void read_b_fragments(V (&b)[CB], uint32_t addr) {
+template <typename T, typename S, typename V>
+__device__ inline void mfma_step(float4_t (&acc)[S::RB][S::CB], const V (&a)[S::RB][S::ST], const V (&b)[S::CB],
+                                 int st) {
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(b[cb]) : "v"(addr), "i"(cb * STRIDE));
+    for (int cb = 0; cb < S::CB; ++cb) {
+#pragma unroll
+        for (int rb = 0; rb < S::RB; ++rb) acc[rb][cb] = MfmaOps<T>::mfma(a[rb][st], b[cb], acc[rb][cb]);
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) asm volatile("" : "+v"(b[cb]));
 }
 
-// One pipeline stage.  `bcur` holds this stage's B tile, `bnext` receives
-// the next one; the caller alternates two distinct LDS arrays so the
-// compiler can tell the direct loads into `bnext` from the reads of `bcur`.
-template <typename T, int C_OUT, int WAVE_ROWS, typename BSource, typename V>
-__device__ inline void igemm_stage(int s, int nstages, const unsigned char* stage_k, const unsigned char* stage_chunk,
-                                   const T* __restrict__ bcur, T* __restrict__ bnext, const T* __restrict__ feats,
-                                   int c_in,
-                                   const BSource& bsrc, const int32_t* __restrict__ kv_map, int rows, int row0,
-                                   int wave, int wc, int lane, uint32_t wmask,
-                                   int (&idx_cur)[IgemmShape<C_OUT, WAVE_ROWS>::RB],
-                                   int (&idx_next)[IgemmShape<C_OUT, WAVE_ROWS>::RB],
-                                   V (&a_cur)[IgemmShape<C_OUT, WAVE_ROWS>::RB][IgemmShape<C_OUT, WAVE_ROWS>::ST],
-                                   float4_t (&acc)[IgemmShape<C_OUT, WAVE_ROWS>::RB][IgemmShape<C_OUT, WAVE_ROWS>::CB]) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
-    const int lr = lane & 15;
-    const int lk = (lane >> 4) * 8;
-    const int s1 = min(s + 1, nstages - 1);
-    const int s2 = min(s + 2, nstages - 1);
-    const int k = stage_k[s];
-    const int chunk = stage_chunk[s];
-    const int k1 = stage_k[s1];
-    const int ci1 = stage_chunk[s1] * kChunk;
-    const int cw1 = min(kChunk, c_in - ci1);
-    // Issue, in this order: row indices two stages ahead, the next B tile,
-    // the next A operand.  The scheduling fences keep the order so the wait
-    // before the barrier can leave the A loads in flight.
-    int idx_next2[S::RB];
-    load_rows<S::RB>(idx_next2, kv_map, rows, row0, stage_k[s2], lr);
-    V breg[BSource::kDirect ? 1 : S::B_PIECES];
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (BSource::kDirect) {
-        stage_b_direct<T, C_OUT, WAVE_ROWS>(bsrc, k1, ci1, cw1, bnext, wave, lane);
-    } else {
-        stage_b_load<T, C_OUT, WAVE_ROWS>(bsrc, k1, ci1, cw1, breg);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    V a_next[S::RB][S::ST];
-    load_a<T, V, S::RB, S::ST>(a_next, idx_next, feats, c_in, ci1, cw1, lk);
-    __builtin_amdgcn_sched_barrier(0);
+// Per-wave pipeline state shared by the stages of one block.
+struct StageCtx {
+    const unsigned char* stage_k;
+    const unsigned char* stage_chunk;
+    int nstages, c_in, rows, row0, wc, lane;
+    uint32_t wmask;
+};
 
-    if ((wmask >> k) & 1u) {
-        const int nst = min(kChunk, c_in - chunk * kChunk) / 32;
-        const uint32_t brow = lds_address(bcur + (wc * S::WAVE_COLS + lr) * S::BROW);
-        const V zero = zero_vec<V>();
+// Stage s.  `a_use` holds A(s); `idx_a` holds the row indices of stage
+// s+DEPTH, whose gather goes to `a_fill`; `idx_fill` receives the indices
+// of stage s+DEPTH+1.
+template <typename T, typename S, typename BSource, typename V>
+__device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* bnext,
+                                   __amdgpu_buffer_rsrc_t rows_rsrc, const BSource& bsrc,
+                                   const int32_t* __restrict__ kv_map, const int (&idx_a)[S::RB],
+                                   int (&idx_fill)[S::RB], const V (&a_use)[S::RB][S::ST], V (&a_fill)[S::RB][S::ST],
+                                   float4_t (&acc)[S::RB][S::CB]) {
+    const int lr = c.lane & 15;
+    const int lk = (c.lane >> 4) * 8;
+    const int last = c.nstages - 1;
+    const int sb = min(s + 1, last);
+    const int sa = min(s + S::DEPTH, last);
+    const int si = min(s + S::DEPTH + 1, last);
+    load_rows<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], lr);
+    V breg[S::B_PIECES];
+    const int cib = c.stage_chunk[sb] * S::CHUNK;
+    stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
+    const int cia = c.stage_chunk[sa] * S::CHUNK;
+    load_a<T, V, S::RB, S::ST>(a_fill, idx_a, rows_rsrc, c.c_in, cia, min(S::CHUNK, c.c_in - cia), lk);
+
+    const int k = c.stage_k[s];
+    if ((c.wmask >> k) & 1u) {
+        const int nst = min(S::CHUNK, c.c_in - c.stage_chunk[s] * S::CHUNK) / 32;
+        // Rows wc*WAVE_COLS + 16*cb + lr all share lr's low bits, so piece
+        // 4*st + lane/16 sits in the same slot for every column block.
+        const T* brow = bcur + (c.wc * S::WAVE_COLS + lr) * S::BROW;
+        if (S::BPIPE && nst == S::ST) {
+            V bf[2][S::CB];
+            read_b_step<T, S>(bf[0], brow, 0, c.lane, lr);
 #pragma unroll
-        for (int st = 0; st < S::ST; ++st) {
-            if (st < nst) {
-                // Rows wc*WAVE_COLS + 16*cb + lr all have lr as their low four
-                // bits, so piece 4*st + lane/16 sits in the same slot for every
-                // column block.
-                const uint32_t addr = brow + swizzle_piece(st * 4 + (lane >> 4), lr) * 16;
-                V b[S::CB];
-                read_b_fragments<V, S::CB, 16 * S::BROW * 2>(b, addr);
-                V a[S::RB];
+            for (int st = 0; st < S::ST; ++st) {
+                if (st + 1 < S::ST) read_b_step<T, S>(bf[(st + 1) & 1], brow, st + 1, c.lane, lr);
+                mfma_step<T, S>(acc, a_use, bf[st & 1], st);
+            }
+        } else {
 #pragma unroll
-                for (int rb = 0; rb < S::RB; ++rb) a[rb] = idx_cur[rb] >= 0 ? a_cur[rb][st] : zero;
-#pragma unroll
-                for (int cb = 0; cb < S::CB; ++cb) {
-#pragma unroll
-                    for (int rb = 0; rb < S::RB; ++rb) acc[rb][cb] = MfmaOps<T>::mfma(a[rb], b[cb], acc[rb][cb]);
+            for (int st = 0; st < S::ST; ++st) {
+                if (st < nst) {
+                    V b[S::CB];
+                    read_b_step<T, S>(b, brow, st, c.lane, lr);
+                    mfma_step<T, S>(acc, a_use, b, st);
                 }
             }
         }
     }
-    if constexpr (BSource::kDirect) {
-        // The next B tile must have landed in LDS before any wave reads it;
-        // the A loads issued after it may stay in flight.
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::RB * S::ST));
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-    } else {
-        stage_b_store<T, C_OUT, WAVE_ROWS>(bnext, breg);
-        __syncthreads();
-    }
-#pragma unroll
-    for (int rb = 0; rb < S::RB; ++rb) {
-        idx_cur[rb] = idx_next[rb];
-        idx_next[rb] = idx_next2[rb];
-#pragma unroll
-        for (int st = 0; st < S::ST; ++st) a_cur[rb][st] = a_next[rb][st];
-    }
+    stage_b_store<T, S>(bnext, breg);
+    __syncthreads();
 }
 
-template <typename T, int C_OUT, int WAVE_ROWS, typename BSource>
-__global__ void __launch_bounds__(kBlock, 1)
-conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
+template <typename T, typename S, typename BSource>
+__global__ void __launch_bounds__(S::THREADS, S::OCC)
+conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
            T* __restrict__ out) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
     using V = typename MfmaOps<T>::vec;
-    __shared__ __align__(16) T bbuf0[S::BBUF];
-    __shared__ __align__(16) T bbuf1[S::BBUF];
-    __shared__ unsigned char stage_k[kMaxStages];
-    __shared__ unsigned char stage_chunk[kMaxStages];
+    constexpr int WAVES = S::WAVES;
+    constexpr int WAVE_ROWS = S::WAVE_ROWS;
+    constexpr int C_OUT = S::C_OUT;
+    __shared__ __align__(16) T lds[S::LDS_HALVES];
+    T* const bbuf0 = lds;
+    T* const bbuf1 = lds + S::BBUF;
+    __shared__ unsigned char stage_k[S::MAX_STAGES];
+    __shared__ unsigned char stage_chunk[S::MAX_STAGES];
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -468,7 +450,7 @@ conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* _
         bmask |= m;
         if (q / S::RB == wr) wmask |= m;
     }
-    const int nchunks = (c_in + kChunk - 1) / kChunk;
+    const int nchunks = (c_in + S::CHUNK - 1) / S::CHUNK;
     const int nstages = __popc(bmask) * nchunks;
     if (threadIdx.x == 0) {
         uint32_t m = bmask;
@@ -476,9 +458,9 @@ conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* _
         while (m) {
             const int k = __builtin_ctz(m);
             m &= m - 1;
-            for (int c = 0; c < nchunks; ++c, ++s) {
+            for (int ch = 0; ch < nchunks; ++ch, ++s) {
                 stage_k[s] = static_cast<unsigned char>(k);
-                stage_chunk[s] = static_cast<unsigned char>(c);
+                stage_chunk[s] = static_cast<unsigned char>(ch);
             }
         }
     }
@@ -494,32 +476,39 @@ conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* _
     __syncthreads();
 
     if (nstages > 0) {
-        // Prologue: B tile of stage 0 in LDS, A of stage 0 and row indices
-        // of stage 1 in registers.
-        const int k0 = stage_k[0];
-        const int c0 = min(kChunk, c_in);
-        if constexpr (BSource::kDirect) {
-            stage_b_direct<T, C_OUT, WAVE_ROWS>(bsrc, k0, 0, c0, bbuf0, wave, lane);
-        } else {
+        const StageCtx ctx{stage_k, stage_chunk, nstages, c_in, rows, row0, wc, lane, wmask};
+        const int last = nstages - 1;
+        // Prologue: B(0) in LDS; A(0) .. A(DEPTH-1) gathered; indices of
+        // stage DEPTH ready for stage 0 to gather A(DEPTH).
+        int idx[S::NA][S::RB];
+        V a[S::NA][S::RB][S::ST];
+        const __amdgpu_buffer_rsrc_t rows_rsrc = feature_rows(feats, n_in, c_in);
+#pragma unroll
+        for (int j = 0; j <= S::DEPTH; ++j) load_rows<S::RB>(idx[j], kv_map, rows, row0, stage_k[min(j, last)], lr);
+        {
             V breg[S::B_PIECES];
-            stage_b_load<T, C_OUT, WAVE_ROWS>(bsrc, k0, 0, c0, breg);
-            stage_b_store<T, C_OUT, WAVE_ROWS>(bbuf0, breg);
+            stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
+            stage_b_store<T, S>(bbuf0, breg);
         }
-        int idx_cur[S::RB];
-        load_rows<S::RB>(idx_cur, kv_map, rows, row0, k0, lr);
-        V a_cur[S::RB][S::ST];
-        load_a<T, V, S::RB, S::ST>(a_cur, idx_cur, feats, c_in, 0, c0, lk);
-        int idx_next[S::RB];
-        load_rows<S::RB>(idx_next, kv_map, rows, row0, stage_k[min(1, nstages - 1)], lr);
+#pragma unroll
+        for (int j = 0; j < S::DEPTH; ++j) {
+            const int sj = min(j, last);
+            const int ci = stage_chunk[sj] * S::CHUNK;
+            load_a<T, V, S::RB, S::ST>(a[j], idx[j], rows_rsrc, c_in, ci, min(S::CHUNK, c_in - ci), lk);
+        }
         __syncthreads();
-        for (int s = 0; s < nstages; s += 2) {
-            igemm_stage<T, C_OUT, WAVE_ROWS, BSource, V>(s, nstages, stage_k, stage_chunk, bbuf0, bbuf1, feats, c_in,
-                                                          bsrc, kv_map, rows, row0, wave, wc, lane, wmask, idx_cur,
-                                                          idx_next, a_cur, acc);
-            if (s + 1 < nstages) {
-                igemm_stage<T, C_OUT, WAVE_ROWS, BSource, V>(s + 1, nstages, stage_k, stage_chunk, bbuf1, bbuf0,
-                                                              feats, c_in, bsrc, kv_map, rows, row0, wave, wc, lane,
-                                                              wmask, idx_cur, idx_next, a_cur, acc);
+        // Stage s = base + j uses A buffer j % NA, gathers into (j + DEPTH) %
+        // NA with the indices in idx[(j + DEPTH) % NA], and refills idx[j %
+        // NA] with the indices of stage s + DEPTH + 1 (buffer j % NA is free
+        // once its gather has been issued).
+        for (int base = 0; base < nstages; base += S::UNROLL) {
+#pragma unroll
+            for (int j = 0; j < S::UNROLL; ++j) {
+                if (base + j >= nstages) break;
+                const int u = j % S::NA;
+                const int f = (j + S::DEPTH) % S::NA;
+                igemm_stage<T, S, BSource, V>(base + j, ctx, (j & 1) ? bbuf1 : bbuf0, (j & 1) ? bbuf0 : bbuf1,
+                                              rows_rsrc, bsrc, kv_map, idx[f], idx[u], a[u], a[f], acc);
             }
         }
     }
@@ -527,7 +516,7 @@ conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* _
 
     // Epilogue: stage this wave's tile in LDS (pieces swizzled by row), then
     // write whole rows with 16-byte stores to out[reorder_rows[row]].
-    T* stage = (wave < 2 ? bbuf0 : bbuf1) + (wave & 1) * WAVE_ROWS * S::EROW;
+    T* stage = lds + wave * WAVE_ROWS * S::EROW;
 #pragma unroll
     for (int rb = 0; rb < S::RB; ++rb) {
 #pragma unroll
@@ -554,33 +543,64 @@ conv_igemm(const T* __restrict__ feats, int c_in, BSource bsrc, const int32_t* _
     }
 }
 
-template <typename T, int C_OUT, int WAVE_ROWS, typename BSource>
-int launch_igemm_shape(const T* feats, int c_in, const BSource& b, const int32_t* kv_map,
+template <typename T, typename S, typename BSource>
+int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, T* out,
                        hipStream_t stream) {
-    using S = IgemmShape<C_OUT, WAVE_ROWS>;
     const unsigned blocks = static_cast<unsigned>((rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS);
-    conv_igemm<T, C_OUT, WAVE_ROWS, BSource><<<blocks, kBlock, 0, stream>>>(feats, c_in, b, kv_map, tile_masks,
-                                                                           reorder_rows, rows, out);
+    conv_igemm<T, S, BSource><<<blocks, S::THREADS, 0, stream>>>(feats, n_in, c_in, b, kv_map, tile_masks,
+                                                               reorder_rows, rows, out);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
 
-// Wave tile rows: 64 doubles B reuse from LDS, 32 halves the registers
-// (two waves per SIMD).  Chosen per launch; see igemm_wave_rows().
+// Wave tile rows: 64 doubles the reuse of each B fragment read from LDS;
+// 32 (the default) keeps registers low enough for three blocks per CU.
 int g_igemm_wave_rows = 32;
+#ifdef LATTICE_IGEMM_SWEEP
+int g_igemm_sweep = -1;
+extern "C" void lattice_hip_sweep_variant(int v) { g_igemm_sweep = v; }
+#endif
 
 template <typename T, typename BSource>
-int launch_igemm(const T* feats, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
+int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
                  const int32_t* tile_masks, const int32_t* reorder_rows, int rows, T* out, hipStream_t stream) {
     if (rows <= 0) return LATTICE_OK;
-#define LATTICE_IGEMM_CASE(C)                                                                              \
-    case C:                                                                                                \
-        return g_igemm_wave_rows == 64                                                                     \
-                   ? launch_igemm_shape<T, C, 64>(feats, c_in, b, kv_map, tile_masks, reorder_rows, rows, out, \
-                                                  stream)                                                  \
-                   : launch_igemm_shape<T, C, 32>(feats, c_in, b, kv_map, tile_masks, reorder_rows, rows, out, \
-                                                  stream);
+#define LATTICE_IGEMM_LAUNCH(...) \
+    launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, out, \
+                                                   stream)
+#ifdef LATTICE_IGEMM_SWEEP
+    if (c_out == 128 && g_igemm_sweep >= 0) {
+        switch (g_igemm_sweep) {
+            case 0: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, false);
+            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 2, false);
+            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true);
+            case 3: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, true);
+            case 4: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, true);
+            case 5: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false);
+            case 6: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false);
+            case 7: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, true);
+            case 8: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, true);
+            case 9: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 3, true);
+            case 10: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 3);
+            case 11: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4);
+            case 12: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 3);
+            case 13: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 2);
+            case 14: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true, 3);
+            case 15: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 3, false, 2);
+            case 16: return LATTICE_IGEMM_LAUNCH(128, 16, 4, 64, 1, false, 4);
+            case 17: return LATTICE_IGEMM_LAUNCH(128, 32, 2, 64, 1, false, 6);
+            default: break;
+        }
+    }
+#endif
+// Default shape: 32-row wave tiles, four waves, 64-channel stages (the
+// smaller B tile and register set let three blocks share a CU); c_out = 16
+// keeps 128-channel stages so its B tile still covers every thread.
+#define LATTICE_IGEMM_CASE(C)                                                  \
+    case C:                                                                    \
+        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(C, 64, 4);   \
+        return LATTICE_IGEMM_LAUNCH(C, 32, 4, (C >= 32 ? 64 : 128));
     switch (c_out) {
         LATTICE_IGEMM_CASE(16)
         LATTICE_IGEMM_CASE(32)
@@ -588,15 +608,19 @@ int launch_igemm(const T* feats, int c_in, int c_out, const BSource& b, const in
         LATTICE_IGEMM_CASE(128)
         LATTICE_IGEMM_CASE(256)
 #undef LATTICE_IGEMM_CASE
+#undef LATTICE_IGEMM_LAUNCH
     default:
         set_error("implicit GEMM supports c_out in {16, 32, 64, 128, 256}.");
         return LATTICE_ERROR_UNSUPPORTED;
     }
 }
 
-bool igemm_shape_ok(int c_in, int c_out, int K) {
+// Shapes the matrix-core kernel handles; the feature table must also fit
+// the 32-bit offsets of its buffer loads (under 2 GiB).
+bool igemm_shape_ok(int n_in, int c_in, int c_out, int K) {
     return c_in > 0 && c_in % 32 == 0 && c_in <= 512 && K > 0 && K <= 32 &&
-           (c_out == 16 || c_out == 32 || c_out == 64 || c_out == 128 || c_out == 256);
+           (c_out == 16 || c_out == 32 || c_out == 64 || c_out == 128 || c_out == 256) &&
+           static_cast<long long>(n_in) * c_in * 2 < (1ll << 31);
 }
 
 int check_dtype(int dtype) {
@@ -665,8 +689,9 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     LATTICE_REQUIRE(n_in >= 0 && out_capacity >= 0, "feats must have shape (N, C_in).");
     LATTICE_REQUIRE(weight_layout == LATTICE_WEIGHT_DENSE_5D,
                     "the implicit GEMM route takes (C_out, Kx, Ky, Kz, C_in) weights.");
-    if (!igemm_shape_ok(c_in, c_out, kernel_count)) {
-        set_error("implicit GEMM needs c_in % 32 == 0, c_out in {16,32,64,128,256} and K <= 32.");
+    if (!igemm_shape_ok(n_in, c_in, c_out, kernel_count)) {
+        set_error("implicit GEMM needs c_in % 32 == 0 (<= 512), c_out in {16,32,64,128,256}, K <= 32 and "
+                  "feats under 2 GiB.");
         return LATTICE_ERROR_UNSUPPORTED;
     }
     LATTICE_REQUIRE(sorted_kv_out_in_map && tile_masks && out && weights && (feats || n_in == 0),
@@ -676,11 +701,11 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     const long long s_k = c_in;
     if (dtype == LATTICE_F16) {
         FloatB<_Float16> b{static_cast<const _Float16*>(weights), s_co, s_k};
-        return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), c_in, c_out, b, sorted_kv_out_in_map,
+        return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                       tile_masks, reorder_rows, out_capacity, static_cast<_Float16*>(out), stream);
     }
     FloatB<__bf16> b{static_cast<const __bf16*>(weights), s_co, s_k};
-    return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), c_in, c_out, b, sorted_kv_out_in_map,
+    return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                 tile_masks, reorder_rows, out_capacity, static_cast<__bf16*>(out), stream);
 }
 
@@ -705,17 +730,17 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const int packed_words = storage_c_in * bits / 32;
     const int groups = storage_c_in / group_size;
     const bool sorted = sorted_kv_out_in_map != nullptr && tile_masks != nullptr && reorder_rows != nullptr;
-    if (sorted && dtype != LATTICE_F32 && igemm_shape_ok(c_in, c_out, kernel_count)) {
+    if (sorted && dtype != LATTICE_F32 && igemm_shape_ok(n_in, c_in, c_out, kernel_count)) {
         if (dtype == LATTICE_F16) {
             PackedB<_Float16> b{weights, static_cast<const _Float16*>(scales), static_cast<const _Float16*>(biases),
                                 packed_words, groups, group_size, c_out, bits};
-            return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), c_in, c_out, b, sorted_kv_out_in_map,
+            return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                           tile_masks, reorder_rows, out_capacity, static_cast<_Float16*>(out),
                                           stream);
         }
         PackedB<__bf16> b{weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases),
                           packed_words, groups, group_size, c_out, bits};
-        return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), c_in, c_out, b, sorted_kv_out_in_map,
+        return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                     tile_masks, reorder_rows, out_capacity, static_cast<__bf16*>(out), stream);
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");

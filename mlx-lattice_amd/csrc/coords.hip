@@ -21,7 +21,9 @@
 //      kernel id and by input row.
 // Nothing in this file reads device memory back to the host.
 
-#include <hipcub/hipcub.hpp>
+#include <cstring>
+
+#include <rocprim/rocprim.hpp>
 
 #include <algorithm>
 #include <climits>
@@ -393,13 +395,24 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
     return LATTICE_OK;
 }
 
-size_t sort_temp_bytes(int n) {
+// Stable radix sort of (int32 key, int32 value) pairs over key bits
+// [0, end_bit).  rocPRIM's default dispatch is kept: below 2^20 items it
+// block-sorts and merges, which measured faster at 400k rows than its
+// onesweep path, and it enqueues no memset nodes.
+
+hipError_t radix_sort_pairs(void* temp, size_t& temp_bytes, const int32_t* keys_in, int32_t* keys_out,
+                            const int32_t* values_in, int32_t* values_out, int n, int end_bit, hipStream_t stream) {
+    return rocprim::radix_sort_pairs(temp, temp_bytes, keys_in, keys_out, values_in, values_out, n, 0u,
+                                                   static_cast<unsigned>(end_bit), stream);
+}
+
+size_t radix_sort_temp_bytes(int n) {
     size_t temp = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, static_cast<const int32_t*>(nullptr),
-                                             static_cast<int32_t*>(nullptr), static_cast<const int32_t*>(nullptr),
-                                             static_cast<int32_t*>(nullptr), std::max(n, 1));
+    (void)radix_sort_pairs(nullptr, temp, nullptr, nullptr, nullptr, nullptr, std::max(n, 1), 32, nullptr);
     return temp;
 }
+
+size_t sort_temp_bytes(int n) { return radix_sort_temp_bytes(n); }
 
 size_t group_view_bytes(int edge_capacity) {
     const size_t n = static_cast<size_t>(std::max(edge_capacity, 1));
@@ -425,8 +438,8 @@ int build_group_view(const int32_t* group_ids, const int32_t* counts, int edge_c
     const unsigned g = grid_for(edge_capacity, kThreads, 8192);
     group_keys<<<g, kThreads, 0, stream>>>(group_ids, counts, edge_capacity, groups, keys, ids);
     LATTICE_LAUNCH_CHECK();
-    LATTICE_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted, ids, edge_ids, edge_capacity,
-                                                       0, bit_width(groups), stream));
+    LATTICE_HIP_TRY(radix_sort_pairs(temp, temp_bytes, keys, sorted, ids, edge_ids, edge_capacity, bit_width(groups),
+                                     stream));
     group_offsets<<<grid_for(edge_capacity + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted, edge_capacity,
                                                                                        groups, offsets);
     LATTICE_LAUNCH_CHECK();
@@ -801,13 +814,7 @@ tile_quarter_masks(const int32_t* __restrict__ sorted_keys, int rows, int tiles,
     }
 }
 
-size_t radix_temp_bytes(int rows) {
-    size_t temp = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, static_cast<const int32_t*>(nullptr),
-                                       static_cast<int32_t*>(nullptr), static_cast<const int32_t*>(nullptr),
-                                       static_cast<int32_t*>(nullptr), std::max(rows, 1));
-    return temp;
-}
+size_t radix_temp_bytes(int rows) { return radix_sort_temp_bytes(rows); }
 
 }  // namespace
 }  // namespace lattice
@@ -840,8 +847,10 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
     const int words = 1;
     first_word_and_iota<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(row_masks, rows, words, keys, ids);
     LATTICE_LAUNCH_CHECK();
-    LATTICE_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted_keys, ids, reorder_rows,
-                                                       rows, 0, 32, stream));
+    // Masks of K < 32 offsets are non-negative and fit in K bits; a 32-bit
+    // mask sorts as a signed word, like the reference's int32 argsort.
+    LATTICE_HIP_TRY(radix_sort_pairs(temp, temp_bytes, keys, sorted_keys, ids, reorder_rows, rows,
+                                     kernel_count < 32 ? kernel_count : 32, stream));
     gather_sorted<<<(rows + kGatherRows - 1) / kGatherRows, kThreads, 0, stream>>>(
         out_in_map, rows, kernel_count, reorder_rows, sorted_out_in_map, sorted_kv_out_in_map);
     LATTICE_LAUNCH_CHECK();

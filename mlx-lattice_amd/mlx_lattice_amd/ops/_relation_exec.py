@@ -34,11 +34,15 @@ def _require_static(relation: KernelRelation) -> None:
 
 
 def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
-                          relation: KernelRelation) -> bool:
+                          relation: KernelRelation, n_in: int = 0) -> bool:
+    """Shapes the matrix-core kernel takes; its 32-bit gather offsets need
+    the feature table under 2 GiB."""
     return (relation.contract.kind in ('forward', 'target', 'submanifold')
             and dtype in (torch.float16, torch.bfloat16)
-            and c_in % 32 == 0 and c_out in _MATRIX_CORE_C_OUT
-            and relation.n_kernels is not None and relation.n_kernels <= 32)
+            and c_in % 32 == 0 and c_in <= 512
+            and c_out in _MATRIX_CORE_C_OUT
+            and relation.n_kernels is not None and relation.n_kernels <= 32
+            and n_in * c_in * 2 < 2 ** 31)
 
 
 def sparse_conv_features_from_relation(feats: torch.Tensor,
@@ -50,7 +54,8 @@ def sparse_conv_features_from_relation(feats: torch.Tensor,
     _require_static(relation)
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
     if feats.ndim == 2 and _matrix_core_eligible(
-            feats.dtype, int(feats.shape[1]), c_out, relation):
+            feats.dtype, int(feats.shape[1]), c_out, relation,
+            int(feats.shape[0])):
         return sparse_conv_features_sorted_from_relation(feats, weight,
                                                          relation)
     input_csr = relation.input_csr
@@ -75,7 +80,7 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
     _require_static(relation)
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
     if not _matrix_core_eligible(feats.dtype, int(feats.shape[1]), c_out,
-                                 relation):
+                                 relation, int(feats.shape[0])):
         raise ValueError(
             'sorted implicit GEMM is not supported for this relation, '
             'feature tensor, or weight tensor.')
@@ -102,7 +107,8 @@ def sparse_quantized_conv_features_from_relation(
     device = feats.device
     kv = reorder = tiles = _empty_i32(device)
     if _matrix_core_eligible(feats.dtype, weight.in_channels,
-                             weight.out_channels, relation):
+                             weight.out_channels, relation,
+                             int(feats.shape[0])):
         view = relation.require_sorted_implicit_gemm()
         kv = view.sorted_kv_out_in_map
         reorder = view.reorder_rows
