@@ -184,12 +184,18 @@ int lattice_hip_sparse_conv_features(
  * decides which offsets a 64-row tile visits.  fp16/bf16 with
  * c_in % 32 == 0, c_out in {16, 32, 64, 128, 256} and K <= 32 run on the
  * matrix cores (fp32 accumulate); other shapes return
- * LATTICE_ERROR_UNSUPPORTED.  weights: (C_out, Kx, Ky, Kz, C_in). */
+ * LATTICE_ERROR_UNSUPPORTED (as do feature tables of 2 GiB or more, whose
+ * rows the kernel addresses with 32-bit offsets).  weights: (C_out, Kx, Ky,
+ * Kz, C_in).  workspace (optional, lattice_hip_conv_workspace_bytes) holds
+ * the launch's tile schedule: with it, row tiles run longest-first; with
+ * NULL they run in order.  The result does not depend on the schedule. */
+size_t lattice_hip_conv_workspace_bytes(int out_capacity);
 int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out,
     const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
-    const int32_t* reorder_rows, int out_capacity, void* out, void* stream);
+    const int32_t* reorder_rows, int out_capacity, void* out, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Tuning knob with no counterpart in the reference: rows of the sorted
  * order owned by one wavefront in the implicit-GEMM route (32 or 64).
@@ -213,7 +219,7 @@ int lattice_hip_sparse_quantized_conv_features(
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
     const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
-    void* out, void* stream);
+    void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -421,7 +421,7 @@ template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
-           T* __restrict__ out) {
+           const int32_t* __restrict__ block_order, T* __restrict__ out) {
     using V = typename MfmaOps<T>::vec;
     constexpr int WAVES = S::WAVES;
     constexpr int WAVE_ROWS = S::WAVE_ROWS;
@@ -436,7 +436,10 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     const int wave = threadIdx.x / kWave;
     const int wr = wave / S::CG;
     const int wc = wave % S::CG;
-    const int block_row0 = blockIdx.x * S::BLOCK_ROWS;
+    // block_order (optional) lists the row tiles longest-first, so the
+    // costliest tiles start early and the launch drains evenly.
+    const int tile = block_order != nullptr ? block_order[blockIdx.x] : static_cast<int>(blockIdx.x);
+    const int block_row0 = tile * S::BLOCK_ROWS;
     const int row0 = block_row0 + wr * WAVE_ROWS;
     const int quarters = ((rows + 63) / 64) * 4;
 
@@ -543,13 +546,66 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     }
 }
 
+// Longest-first order of the row tiles of one launch: the cost of a tile is
+// the number of offsets its rows use (stages it runs); a counting sort by
+// descending cost fills `order`.  One workgroup: costs are read with 16-byte
+// loads of the quarter masks and kept in LDS between the count and the
+// placement pass.  Ties land in any order (a tile's output does not depend
+// on when it runs).  Launches with more tiles than kMaxScheduledTiles run in
+// order.
+constexpr int kScheduleThreads = 1024;
+constexpr int kMaxScheduledTiles = 32768;
+
+template <int QUARTERS>
+__global__ void __launch_bounds__(kScheduleThreads)
+schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, int32_t* __restrict__ order) {
+    static_assert(QUARTERS % 4 == 0, "tiles span whole 64-row mask groups");
+    __shared__ int count[33];
+    __shared__ int next[33];
+    __shared__ unsigned char cost[kMaxScheduledTiles];
+    const int quarters = ((rows + 63) / 64) * 4;  // tile_masks length, a multiple of 4
+    if (threadIdx.x < 33) count[threadIdx.x] = 0;
+    __syncthreads();
+    const int4* masks4 = reinterpret_cast<const int4*>(tile_masks);
+#pragma unroll 4
+    for (int b = threadIdx.x; b < nblocks; b += kScheduleThreads) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int v = 0; v < QUARTERS / 4; ++v) {
+            const int q = b * QUARTERS + 4 * v;
+            if (q < quarters) {
+                const int4 w = masks4[q / 4];
+                m |= static_cast<uint32_t>(w.x | w.y | w.z | w.w);
+            }
+        }
+        const int c = __popc(m);
+        cost[b] = static_cast<unsigned char>(c);
+        atomicAdd(&count[c], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int start = 0;
+        for (int c = 32; c >= 0; --c) {
+            next[c] = start;
+            start += count[c];
+        }
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < nblocks; b += kScheduleThreads) order[atomicAdd(&next[cost[b]], 1)] = b;
+}
+
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
-                       const int32_t* tile_masks, const int32_t* reorder_rows, int rows, T* out,
-                       hipStream_t stream) {
-    const unsigned blocks = static_cast<unsigned>((rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS);
-    conv_igemm<T, S, BSource><<<blocks, S::THREADS, 0, stream>>>(feats, n_in, c_in, b, kv_map, tile_masks,
-                                                               reorder_rows, rows, out);
+                       const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
+                       T* out, hipStream_t stream) {
+    const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
+    if (blocks > kMaxScheduledTiles) schedule = nullptr;
+    if (schedule != nullptr) {
+        schedule_tiles<S::BLOCK_ROWS / 16><<<1, kScheduleThreads, 0, stream>>>(tile_masks, rows, blocks, schedule);
+        LATTICE_LAUNCH_CHECK();
+    }
+    conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks), S::THREADS, 0, stream>>>(
+        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -564,11 +620,12 @@ extern "C" void lattice_hip_sweep_variant(int v) { g_igemm_sweep = v; }
 
 template <typename T, typename BSource>
 int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
-                 const int32_t* tile_masks, const int32_t* reorder_rows, int rows, T* out, hipStream_t stream) {
+                 const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, T* out,
+                 hipStream_t stream) {
     if (rows <= 0) return LATTICE_OK;
 #define LATTICE_IGEMM_LAUNCH(...) \
-    launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, out, \
-                                                   stream)
+    launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, \
+                                                   schedule, out, stream)
 #ifdef LATTICE_IGEMM_SWEEP
     if (c_out == 128 && g_igemm_sweep >= 0) {
         switch (g_igemm_sweep) {
@@ -615,6 +672,18 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
     }
 }
 
+// Workspace of the matrix-core conv: the tile schedule, one int per row
+// tile (tiles are at least 64 rows).  NULL workspace = tiles in order.
+size_t conv_schedule_bytes(int rows) { return (static_cast<size_t>(std::max(rows, 0)) / 64 + 1) * sizeof(int32_t); }
+
+int conv_schedule(void* workspace, size_t workspace_bytes, int rows, int32_t** schedule) {
+    *schedule = nullptr;
+    if (workspace == nullptr) return LATTICE_OK;
+    LATTICE_REQUIRE(workspace_bytes >= conv_schedule_bytes(rows), "conv workspace too small.");
+    *schedule = static_cast<int32_t*>(workspace);
+    return LATTICE_OK;
+}
+
 // Shapes the matrix-core kernel handles; the feature table must also fit
 // the 32-bit offsets of its buffer loads (under 2 GiB).
 bool igemm_shape_ok(int n_in, int c_in, int c_out, int K) {
@@ -633,6 +702,8 @@ int check_dtype(int dtype) {
 }  // namespace lattice
 
 using namespace lattice;
+
+extern "C" size_t lattice_hip_conv_workspace_bytes(int out_capacity) { return conv_schedule_bytes(out_capacity); }
 
 extern "C" int lattice_hip_set_conv_tile_rows(int rows) {
     LATTICE_REQUIRE(rows == 32 || rows == 64, "conv tile rows must be 32 or 64.");
@@ -682,7 +753,7 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
 extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights, int weight_layout, int kernel_count,
     int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
-    int out_capacity, void* out, void* stream_ptr) {
+    int out_capacity, void* out, void* workspace, size_t workspace_bytes, void* stream_ptr) {
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(dtype != LATTICE_F32, "the implicit GEMM route runs on fp16/bf16 matrix cores.");
@@ -696,17 +767,21 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     }
     LATTICE_REQUIRE(sorted_kv_out_in_map && tile_masks && out && weights && (feats || n_in == 0),
                     "conv pointers must be non-null.");
+    int32_t* schedule = nullptr;
+    rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule);
+    if (rc != LATTICE_OK) return rc;
     hipStream_t stream = as_stream(stream_ptr);
     const long long s_co = static_cast<long long>(kernel_count) * c_in;
     const long long s_k = c_in;
     if (dtype == LATTICE_F16) {
         FloatB<_Float16> b{static_cast<const _Float16*>(weights), s_co, s_k};
         return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                      tile_masks, reorder_rows, out_capacity, static_cast<_Float16*>(out), stream);
+                                      tile_masks, reorder_rows, out_capacity, schedule,
+                                      static_cast<_Float16*>(out), stream);
     }
     FloatB<__bf16> b{static_cast<const __bf16*>(weights), s_co, s_k};
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                tile_masks, reorder_rows, out_capacity, static_cast<__bf16*>(out), stream);
+                                tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out), stream);
 }
 
 extern "C" int lattice_hip_sparse_quantized_conv_features(
@@ -714,7 +789,8 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const void* biases, int kernel_count, int c_out, int storage_c_in, int group_size, int bits,
     const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
-    const int32_t* reorder_rows, int out_capacity, void* out, void* stream_ptr) {
+    const int32_t* reorder_rows, int out_capacity, void* out, void* workspace, size_t workspace_bytes,
+    void* stream_ptr) {
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized convolution bits must be 4 or 8.");
@@ -731,17 +807,21 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const int groups = storage_c_in / group_size;
     const bool sorted = sorted_kv_out_in_map != nullptr && tile_masks != nullptr && reorder_rows != nullptr;
     if (sorted && dtype != LATTICE_F32 && igemm_shape_ok(n_in, c_in, c_out, kernel_count)) {
+        int32_t* schedule = nullptr;
+        rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule);
+        if (rc != LATTICE_OK) return rc;
         if (dtype == LATTICE_F16) {
             PackedB<_Float16> b{weights, static_cast<const _Float16*>(scales), static_cast<const _Float16*>(biases),
                                 packed_words, groups, group_size, c_out, bits};
             return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                          tile_masks, reorder_rows, out_capacity, static_cast<_Float16*>(out),
-                                          stream);
+                                          tile_masks, reorder_rows, out_capacity, schedule,
+                                          static_cast<_Float16*>(out), stream);
         }
         PackedB<__bf16> b{weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases),
                           packed_words, groups, group_size, c_out, bits};
         return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                    tile_masks, reorder_rows, out_capacity, static_cast<__bf16*>(out), stream);
+                                    tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
+                                    stream);
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");
     QuantIndex q{kernel_count, c_in, c_out, packed_words, groups, group_size, bits};

@@ -144,10 +144,13 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     const at::Tensor kv = sorted_kv_out_in_map.contiguous();
     const at::Tensor tiles = tile_masks.contiguous();
     const at::Tensor order = reorder_rows.contiguous();
+    const size_t ws_bytes = lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity));
+    at::Tensor ws = workspace(ws_bytes, feats);
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(kv), ci32(tiles),
-        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), current_stream(feats)));
+        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), ws.data_ptr(), ws_bytes,
+        current_stream(feats)));
     return out;
 }
 
@@ -228,13 +231,15 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
         tiles = tile_masks.contiguous();
     }
     at::Tensor out = at::empty({out_capacity, out_channels}, feats.options());
+    const size_t ws_bytes = has_plan ? lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity)) : 0;
+    at::Tensor ws = workspace(ws_bytes, feats);
     check_status(lattice_hip_sparse_quantized_conv_features(
         dtype_code(feats, "quantized sparse convolution"), feats.data_ptr(), static_cast<int>(feats.size(0)),
         in_channels, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(),
         n_kernels, out_channels, storage_in_channels, group_size, bits, ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), has_plan ? ci32(kv) : nullptr,
         has_plan ? ci32(tiles) : nullptr, has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(),
-        current_stream(feats)));
+        has_plan ? ws.data_ptr() : nullptr, ws_bytes, current_stream(feats)));
     return out;
 }
 
