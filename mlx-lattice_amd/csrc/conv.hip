@@ -184,9 +184,10 @@ template <> struct MfmaOps<__bf16> {
 //   DEPTH      stages of A gathers in flight ahead of the computing stage;
 //   BPIPE      read the B fragments of the next 32-channel step from LDS
 //              while the current step's MFMAs run;
-//   OCC        blocks per CU the register allocation must allow.
+//   OCC        blocks per CU the register allocation must allow;
+//   WCOLS      output channels per wave (at most 128).
 template <int C_OUT_, int WAVE_ROWS_, int WAVES_, int CHUNK_ = 128, int DEPTH_ = 1, bool BPIPE_ = false,
-          int OCC_ = (WAVE_ROWS_ == 32 ? 2 : 1)>
+          int OCC_ = (WAVE_ROWS_ == 32 ? 2 : 1), int WCOLS_ = 128>
 struct IgemmShape {
     static constexpr int OCC = OCC_;
     static constexpr int C_OUT = C_OUT_;
@@ -195,7 +196,7 @@ struct IgemmShape {
     static constexpr int CHUNK = CHUNK_;
     static constexpr int DEPTH = DEPTH_;
     static constexpr bool BPIPE = BPIPE_;
-    static constexpr int WAVE_COLS = C_OUT < 128 ? C_OUT : 128;
+    static constexpr int WAVE_COLS = C_OUT < WCOLS_ ? C_OUT : WCOLS_;
     static constexpr int THREADS = WAVES * 64;
     static constexpr int CG = C_OUT / WAVE_COLS;  // column groups
     static constexpr int RG = WAVES / CG;         // row groups
@@ -647,6 +648,12 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
             case 15: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 3, false, 2);
             case 16: return LATTICE_IGEMM_LAUNCH(128, 16, 4, 64, 1, false, 4);
             case 17: return LATTICE_IGEMM_LAUNCH(128, 32, 2, 64, 1, false, 6);
+            case 18: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4, 64);
+            case 19: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 5, 64);
+            case 20: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, false, 3, 64);
+            case 21: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 4, 64);
+            case 22: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2, 64);
+            case 23: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 2, 64);
             default: break;
         }
     }

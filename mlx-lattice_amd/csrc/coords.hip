@@ -23,13 +23,13 @@
 
 #include <cstring>
 
-#include <rocprim/rocprim.hpp>
 
 #include <algorithm>
 #include <climits>
 
 #include "lattice_common.h"
 #include "scan.h"
+#include "sort.h"
 
 namespace lattice {
 namespace {
@@ -293,23 +293,8 @@ emit_edges(const int32_t* __restrict__ out_in_map, int out_capacity, int K,
 // write_relation_grouped_view (relation_views_detail.h:84-120) is a stable
 // counting sort of edge ids by a group id (input row or kernel offset).
 // Here: keys = group of each active edge (inactive slots get the sentinel
-// `groups`, which sorts last), a stable LSD radix sort of (key, edge id),
-// and the row offsets read off the sorted keys.
-
-__global__ void __launch_bounds__(kThreads)
-group_keys(const int32_t* __restrict__ group_ids, const int32_t* __restrict__ counts, int capacity, int groups,
-           int32_t* __restrict__ keys, int32_t* __restrict__ ids) {
-    const int E = min(max(counts[0], 0), capacity);
-    for (int i = blockIdx.x * kThreads + threadIdx.x; i < capacity; i += gridDim.x * kThreads) {
-        int g = groups;
-        if (i < E) {
-            const int v = group_ids[i];
-            g = (v >= 0 && v < groups) ? v : groups;
-        }
-        keys[i] = g;
-        ids[i] = i;
-    }
-}
+// `groups`, which sorts last), a stable radix sort of (key, edge id), and
+// the row offsets read off the sorted keys.
 
 // offsets[g] = number of sorted keys below g, for g in [0, groups].
 __global__ void __launch_bounds__(kThreads)
@@ -395,28 +380,9 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
     return LATTICE_OK;
 }
 
-// Stable radix sort of (int32 key, int32 value) pairs over key bits
-// [0, end_bit).  rocPRIM's default dispatch is kept: below 2^20 items it
-// block-sorts and merges, which measured faster at 400k rows than its
-// onesweep path, and it enqueues no memset nodes.
-
-hipError_t radix_sort_pairs(void* temp, size_t& temp_bytes, const int32_t* keys_in, int32_t* keys_out,
-                            const int32_t* values_in, int32_t* values_out, int n, int end_bit, hipStream_t stream) {
-    return rocprim::radix_sort_pairs(temp, temp_bytes, keys_in, keys_out, values_in, values_out, n, 0u,
-                                                   static_cast<unsigned>(end_bit), stream);
-}
-
-size_t radix_sort_temp_bytes(int n) {
-    size_t temp = 0;
-    (void)radix_sort_pairs(nullptr, temp, nullptr, nullptr, nullptr, nullptr, std::max(n, 1), 32, nullptr);
-    return temp;
-}
-
-size_t sort_temp_bytes(int n) { return radix_sort_temp_bytes(n); }
-
 size_t group_view_bytes(int edge_capacity) {
     const size_t n = static_cast<size_t>(std::max(edge_capacity, 1));
-    return 3 * aligned_bytes(n * sizeof(int32_t)) + aligned_bytes(sort_temp_bytes(edge_capacity)) + 1024;
+    return aligned_bytes(n * sizeof(int32_t)) + radix_sort_workspace_bytes(edge_capacity, 32) + 1024;
 }
 
 int bit_width(int v) {
@@ -429,17 +395,11 @@ int bit_width(int v) {
 int build_group_view(const int32_t* group_ids, const int32_t* counts, int edge_capacity, int groups,
                      int32_t* offsets, int32_t* edge_ids, Workspace ws, hipStream_t stream) {
     if (edge_capacity <= 0) return fill_i32(offsets, groups + 1, 0, stream);
-    int32_t* keys = ws.take<int32_t>(edge_capacity);
     int32_t* sorted = ws.take<int32_t>(edge_capacity);
-    int32_t* ids = ws.take<int32_t>(edge_capacity);
-    size_t temp_bytes = sort_temp_bytes(edge_capacity);
-    void* temp = ws.take<char>(temp_bytes);
-    LATTICE_REQUIRE(keys && sorted && ids && temp, "grouped view workspace too small.");
-    const unsigned g = grid_for(edge_capacity, kThreads, 8192);
-    group_keys<<<g, kThreads, 0, stream>>>(group_ids, counts, edge_capacity, groups, keys, ids);
-    LATTICE_LAUNCH_CHECK();
-    LATTICE_HIP_TRY(radix_sort_pairs(temp, temp_bytes, keys, sorted, ids, edge_ids, edge_capacity, bit_width(groups),
-                                     stream));
+    LATTICE_REQUIRE(sorted, "grouped view workspace too small.");
+    const SortKeys keys{group_ids, 1, counts, groups, false};
+    int rc = radix_sort_indices(keys, edge_capacity, bit_width(groups), sorted, edge_ids, ws, stream);
+    if (rc != LATTICE_OK) return rc;
     group_offsets<<<grid_for(edge_capacity + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted, edge_capacity,
                                                                                        groups, offsets);
     LATTICE_LAUNCH_CHECK();
@@ -766,15 +726,6 @@ extern "C" int lattice_hip_build_relation_implicit_gemm_view(
 namespace lattice {
 namespace {
 
-__global__ void __launch_bounds__(kThreads)
-first_word_and_iota(const int32_t* __restrict__ row_masks, int rows, int words, int32_t* __restrict__ keys,
-                    int32_t* __restrict__ ids) {
-    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        keys[i] = row_masks[static_cast<long long>(i) * words];
-        ids[i] = i;
-    }
-}
-
 // Gathers 64 sorted rows of out_in_map per block through LDS: rows are
 // read as contiguous K-int segments, the sorted map is written as one
 // contiguous block and the K-major view as 64-int runs per offset.
@@ -814,14 +765,12 @@ tile_quarter_masks(const int32_t* __restrict__ sorted_keys, int rows, int tiles,
     }
 }
 
-size_t radix_temp_bytes(int rows) { return radix_sort_temp_bytes(rows); }
-
 }  // namespace
 }  // namespace lattice
 
 extern "C" size_t lattice_hip_sorted_view_workspace_bytes(int rows) {
     const size_t n = static_cast<size_t>(std::max(rows, 1));
-    return 3 * aligned_bytes(n * sizeof(int32_t)) + aligned_bytes(radix_temp_bytes(rows)) + 4096;
+    return aligned_bytes(n * sizeof(int32_t)) + radix_sort_workspace_bytes(rows, 32) + 4096;
 }
 
 extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in_map, const int32_t* row_masks,
@@ -838,19 +787,13 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const int tiles = (rows + 63) / 64;
     if (rows == 0) return LATTICE_OK;
-    int32_t* keys = ws.take<int32_t>(rows);
     int32_t* sorted_keys = ws.take<int32_t>(rows);
-    int32_t* ids = ws.take<int32_t>(rows);
-    size_t temp_bytes = radix_temp_bytes(rows);
-    void* temp = ws.take<char>(temp_bytes);
-    LATTICE_REQUIRE(keys && sorted_keys && ids && temp, "sorted view workspace too small.");
-    const int words = 1;
-    first_word_and_iota<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(row_masks, rows, words, keys, ids);
-    LATTICE_LAUNCH_CHECK();
+    LATTICE_REQUIRE(sorted_keys, "sorted view workspace too small.");
     // Masks of K < 32 offsets are non-negative and fit in K bits; a 32-bit
     // mask sorts as a signed word, like the reference's int32 argsort.
-    LATTICE_HIP_TRY(radix_sort_pairs(temp, temp_bytes, keys, sorted_keys, ids, reorder_rows, rows,
-                                     kernel_count < 32 ? kernel_count : 32, stream));
+    const SortKeys keys{row_masks, 1, nullptr, -1, kernel_count == 32};
+    int rc = radix_sort_indices(keys, rows, kernel_count, sorted_keys, reorder_rows, ws, stream);
+    if (rc != LATTICE_OK) return rc;
     gather_sorted<<<(rows + kGatherRows - 1) / kGatherRows, kThreads, 0, stream>>>(
         out_in_map, rows, kernel_count, reorder_rows, sorted_out_in_map, sorted_kv_out_in_map);
     LATTICE_LAUNCH_CHECK();

@@ -321,6 +321,36 @@ def test_sorted_view_matches_stable_argsort():
     np.testing.assert_array_equal(to_np(tiles), quarters)
 
 
+@pytest.mark.parametrize('rows,k,seed', [(1, 27, 0), (2047, 27, 1),
+                                          (2048, 27, 2), (2049, 27, 3),
+                                          (50000, 5, 4), (70001, 32, 5),
+                                          (300000, 27, 6)])
+def test_sorted_view_sort_edge_cases(rows, k, seed):
+    """The device radix sort behind the sorted view, against numpy's stable
+    argsort: tile boundaries (2048 items per tile), one-pass keys (K = 5),
+    32-bit masks ordered as signed int32 (sign bit set), and many ties."""
+    rng = np.random.default_rng(seed)
+    if k == 32:
+        masks = rng.integers(-2**31, 2**31, size=rows, dtype=np.int64)
+    else:
+        # few distinct masks -> long runs of ties across tiles
+        pool = rng.integers(0, 2**k, size=max(1, rows // 500))
+        masks = pool[rng.integers(0, len(pool), size=rows)]
+    masks = masks.astype(np.int32).reshape(rows, 1)
+    out_in_map = rng.integers(-1, 1000, size=(rows, k)).astype(np.int32)
+    reorder, sorted_map, kv, tiles = _ext().build_sorted_implicit_gemm_view(
+        _t(out_in_map), _t(masks))
+    expect = np.argsort(masks[:, 0], kind='stable')
+    np.testing.assert_array_equal(to_np(reorder), expect)
+    np.testing.assert_array_equal(to_np(sorted_map), out_in_map[expect])
+    np.testing.assert_array_equal(to_np(kv), out_in_map[expect].T)
+    pad = (-rows) % 64
+    sm = np.concatenate([masks[expect, 0], np.zeros(pad, np.int32)])
+    np.testing.assert_array_equal(to_np(tiles),
+                                  np.bitwise_or.reduce(sm.reshape(-1, 16),
+                                                       axis=1))
+
+
 def test_python_relation_views_on_demand():
     from mlx_lattice_amd.core.coords.builders import (
         build_kernel_relation,
