@@ -74,14 +74,42 @@ clear_table(uint64_t* keys, int32_t* rows, int capacity) {
     }
 }
 
-// Clears a block table: key = empty, all eight rows absent (0).  One thread
-// per 16-byte quarter of a bucket.
+// Small writes a relation build needs before its first query, folded into
+// the table clear so they cost no launch of their own: zero the status
+// word, set counts[1] (the active output rows), copy the active input
+// coordinates to out_coords (zero tail).  Each part is skipped when its
+// pointer is null.
+struct Prologue {
+    int32_t* status;
+    const int32_t* count_src;  // counts[1] = clamp(*count_src, 0, count_limit)
+    int count_limit;
+    int32_t* counts;
+    const int32_t* copy_src;   // out_coords rows [0, copy_rows)
+    const int32_t* copy_active;
+    int copy_rows;
+    int32_t* copy_dst;
+};
+
+// Clears a block table (key = empty, all eight rows absent: one thread per
+// 16-byte quarter of a bucket) and runs the prologue.
 __global__ void __launch_bounds__(kThreads)
-clear_blocks(BlockBucket* buckets, long long quarters) {
+clear_blocks(BlockBucket* buckets, long long quarters, Prologue p) {
+    const long long tid = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x;
+    const long long step = static_cast<long long>(gridDim.x) * kThreads;
     int4* q = reinterpret_cast<int4*>(buckets);
-    for (long long i = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; i < quarters;
-         i += static_cast<long long>(gridDim.x) * kThreads) {
+    for (long long i = tid; i < quarters; i += step) {
         q[i] = (i & 3) == 0 ? make_int4(-1, -1, 0, 0) : make_int4(0, 0, 0, 0);
+    }
+    if (tid == 0) {
+        if (p.status != nullptr) p.status[0] = 0;
+        if (p.count_src != nullptr) p.counts[1] = min(max(*p.count_src, 0), p.count_limit);
+    }
+    if (p.copy_src != nullptr) {
+        const int active = min(max(*p.copy_active, 0), p.copy_rows);
+        int4* out = reinterpret_cast<int4*>(p.copy_dst);
+        for (long long i = tid; i < p.copy_rows; i += step) {
+            out[i] = i < active ? reinterpret_cast<const int4*>(p.copy_src)[i] : make_int4(0, 0, 0, 0);
+        }
     }
 }
 
@@ -170,25 +198,15 @@ scatter_cells(const int32_t* __restrict__ coords, int rows, const int32_t* __res
 }
 
 // Identity output support: out_coords = active prefix of coords, zero tail.
-__global__ void __launch_bounds__(kThreads)
-copy_active_coords(const int32_t* __restrict__ coords, int rows,
-                   const int32_t* __restrict__ active_rows, int32_t* __restrict__ out_coords) {
-    const int active = min(max(*active_rows, 0), rows);
-    int4* out = reinterpret_cast<int4*>(out_coords);
-    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        out[i] = i < active ? load_coord(coords, i) : make_int4(0, 0, 0, 0);
-    }
-}
-
-__global__ void set_out_count(const int32_t* __restrict__ src, int limit, int32_t* counts) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) counts[1] = min(max(*src, 0), limit);
-}
-
 // ------------------------------------------------------------ map query --
 //
 // Lanes per output row: 32 when K <= 32 (two rows per wave), else 64 with a
 // loop over 64-offset chunks.  Each lane probes one offset; the ballot of
-// hits gives the row mask words and the degree.
+// hits gives the row mask words and the degree.  A block owns kQueryRows
+// consecutive output rows; it writes their degrees and (optionally) their
+// sum, from which the row offsets are scanned per block.
+
+constexpr int kQueryRows = 64;
 
 struct QueryArgs {
     const int32_t* out_coords;   // coordinates of the output rows
@@ -201,20 +219,24 @@ struct QueryArgs {
     int32_t* out_in_map;         // [out_capacity, K]
     int32_t* row_masks;          // [out_capacity, words]
     int32_t* degrees;            // [out_capacity] or null
+    int32_t* block_totals;       // [ceil(out_capacity / kQueryRows)] or null
 };
 
 template <int kLanes>
 __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
     constexpr int kRowsPerWave = kWave / kLanes;
+    constexpr int kRowsPerPass = kRowsPerWave * (kThreads / kWave);
+    __shared__ int wave_sum[kThreads / kWave];
     const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
     const int sub = lane / kLanes;          // row slot within the wave
     const int k_lane = lane % kLanes;
     const int K = a.geom.volume;
     const int n_active = min(max(*a.out_active, 0), a.out_capacity);
-    const long long waves = static_cast<long long>(gridDim.x) * (kThreads / kWave);
-    const long long wave_id = static_cast<long long>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
-    for (long long base = wave_id * kRowsPerWave; base < a.out_capacity; base += waves * kRowsPerWave) {
-        const long long row = base + sub;
+    int degree_sum = 0;
+    for (int pass = 0; pass < kQueryRows / kRowsPerPass; ++pass) {
+        const long long row = static_cast<long long>(blockIdx.x) * kQueryRows + pass * kRowsPerPass +
+                              wave * kRowsPerWave + sub;
         const bool row_ok = row < a.out_capacity;
         const bool row_active = row < n_active;
         int4 oc = make_int4(0, 0, 0, 0);
@@ -249,28 +271,109 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
                 }
             }
         }
-        if (row_ok && k_lane == 0 && a.degrees != nullptr) a.degrees[row] = degree;
+        if (row_ok && k_lane == 0) {
+            if (a.degrees != nullptr) a.degrees[row] = degree;
+            degree_sum += degree;
+        }
+    }
+    if (a.block_totals == nullptr) return;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) degree_sum += __shfl_xor(degree_sum, off, kWave);
+    if (lane == 0) wave_sum[wave] = degree_sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int total = 0;
+        for (int w = 0; w < kThreads / kWave; ++w) total += wave_sum[w];
+        a.block_totals[blockIdx.x] = total;
     }
 }
 
-// Edge emission in (out_row, kernel) order from out_in_map and row_offsets.
+// Exclusive prefix of the per-block degree totals (one workgroup); the sum
+// of all is the edge count, counts[0].  Each thread owns a contiguous run;
+// loads are issued kScanBatch at a time before use.
+constexpr int kBlockScanThreads = 1024;
+constexpr int kScanBatch = 16;
+
+__global__ void __launch_bounds__(kBlockScanThreads)
+scan_block_totals(const int32_t* __restrict__ totals, int blocks, int32_t* __restrict__ offsets,
+                  int32_t* __restrict__ counts) {
+    __shared__ int wave_sum[kBlockScanThreads / kWave];
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    const int per = (blocks + kBlockScanThreads - 1) / kBlockScanThreads;
+    const int begin = threadIdx.x * per;
+    const int end = min(begin + per, blocks);
+    int sum = 0;
+    for (int i0 = begin; i0 < end; i0 += kScanBatch) {
+        int v[kScanBatch];
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j) v[j] = i0 + j < end ? totals[i0 + j] : 0;
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j) sum += v[j];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int u = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += u;
+    }
+    if (lane == kWave - 1) wave_sum[wave] = incl;
+    __syncthreads();
+    int run = incl - sum;
+    for (int w = 0; w < wave; ++w) run += wave_sum[w];
+    if (threadIdx.x == kBlockScanThreads - 1) counts[0] = run + sum;
+    for (int i0 = begin; i0 < end; i0 += kScanBatch) {
+        int v[kScanBatch];
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j) v[j] = i0 + j < end ? totals[i0 + j] : 0;
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j) {
+            if (i0 + j < end) offsets[i0 + j] = run;
+            run += v[j];
+        }
+    }
+}
+
+// Edge emission in (out_row, kernel) order.  A block owns the same
+// kQueryRows rows as in the query: it turns their degrees (read from
+// row_offsets, where the query left them) into row offsets with its block
+// offset, writes them back, and emits each row's edges from out_in_map.
+// The block holding the last row also writes row_offsets[out_capacity].
 template <int kLanes>
 __global__ void __launch_bounds__(kThreads)
 emit_edges(const int32_t* __restrict__ out_in_map, int out_capacity, int K,
-           const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ counts,
-           int32_t* __restrict__ in_rows, int32_t* __restrict__ out_rows,
+           const int32_t* __restrict__ block_offsets, const int32_t* __restrict__ counts,
+           int32_t* __restrict__ row_offsets, int32_t* __restrict__ in_rows, int32_t* __restrict__ out_rows,
            int32_t* __restrict__ kernel_ids) {
+    static_assert(kQueryRows == kWave, "one wave scans a block's row degrees");
     constexpr int kRowsPerWave = kWave / kLanes;
+    constexpr int kRowsPerPass = kRowsPerWave * (kThreads / kWave);
+    __shared__ int start[kQueryRows];
     const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
     const int sub = lane / kLanes;
     const int k_lane = lane % kLanes;
-    const int n_out = min(counts[1], out_capacity);
-    const long long waves = static_cast<long long>(gridDim.x) * (kThreads / kWave);
-    const long long wave_id = static_cast<long long>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
-    for (long long base = wave_id * kRowsPerWave; base < n_out; base += waves * kRowsPerWave) {
-        const long long row = base + sub;
-        const bool row_ok = row < n_out;
-        int cursor = row_ok ? row_offsets[row] : 0;
+    const long long row0 = static_cast<long long>(blockIdx.x) * kQueryRows;
+    if (wave == 0) {
+        const long long r = row0 + lane;
+        const int d = r < out_capacity ? row_offsets[r] : 0;
+        int incl = d;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int u = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += u;
+        }
+        const int s0 = block_offsets[blockIdx.x] + incl - d;
+        start[lane] = s0;
+        if (r < out_capacity) row_offsets[r] = s0;
+        if (r == out_capacity - 1) row_offsets[out_capacity] = counts[0];
+    }
+    __syncthreads();
+    for (int pass = 0; pass < kQueryRows / kRowsPerPass; ++pass) {
+        const int local = pass * kRowsPerPass + wave * kRowsPerWave + sub;
+        const long long row = row0 + local;
+        const bool row_ok = row < out_capacity;
+        int cursor = row_ok ? start[local] : 0;
         for (int k0 = 0; k0 < K; k0 += kLanes) {
             const int k = k0 + k_lane;
             const int in = (row_ok && k < K) ? out_in_map[row * K + k] : -1;
@@ -360,8 +463,8 @@ size_t block_table_bytes(int rows) {
     return aligned_bytes(static_cast<size_t>(block_capacity(rows)) * sizeof(BlockBucket));
 }
 
-int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows, int32_t* status, Workspace& ws,
-                      hipStream_t stream, BlockTable* table) {
+int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows, int32_t* status,
+                      const Prologue& prologue, Workspace& ws, hipStream_t stream, BlockTable* table) {
     const int cap = block_capacity(rows);
     table->buckets = ws.take<BlockBucket>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
@@ -370,7 +473,8 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
         return LATTICE_ERROR_INVALID_ARGUMENT;
     }
     const long long quarters = 4ll * cap;
-    clear_blocks<<<grid_for(quarters, kThreads, 8192), kThreads, 0, stream>>>(table->buckets, quarters);
+    clear_blocks<<<grid_for(std::max<long long>(quarters, prologue.copy_rows), kThreads, 8192), kThreads, 0, stream>>>(
+        table->buckets, quarters, prologue);
     LATTICE_LAUNCH_CHECK();
     if (rows > 0) {
         insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows,
@@ -434,48 +538,61 @@ KernelGeometry make_geometry(const int* size, const int* stride, const int* padd
     return g;
 }
 
+int query_blocks(int out_capacity) { return (out_capacity + kQueryRows - 1) / kQueryRows; }
+
 int launch_query(const QueryArgs& a, hipStream_t stream) {
     if (a.out_capacity <= 0) return LATTICE_OK;
+    const unsigned blocks = static_cast<unsigned>(query_blocks(a.out_capacity));
     if (a.geom.volume <= 32) {
-        const long long waves = (a.out_capacity + 1) / 2;
-        query_map<32><<<grid_for(waves, kThreads / kWave, 1u << 16), kThreads, 0, stream>>>(a);
+        query_map<32><<<blocks, kThreads, 0, stream>>>(a);
     } else {
-        query_map<64><<<grid_for(a.out_capacity, kThreads / kWave, 1u << 16), kThreads, 0, stream>>>(a);
+        query_map<64><<<blocks, kThreads, 0, stream>>>(a);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
 
-int launch_emit(const int32_t* map, int out_capacity, int K, const lattice_relation_outputs* out,
-                hipStream_t stream) {
-    if (out_capacity <= 0) return LATTICE_OK;
+int launch_emit(const int32_t* map, int out_capacity, int K, const int32_t* block_offsets,
+                const lattice_relation_outputs* out, hipStream_t stream) {
+    const unsigned blocks = static_cast<unsigned>(query_blocks(out_capacity));
     if (K <= 32) {
-        const long long waves = (out_capacity + 1) / 2;
-        emit_edges<32><<<grid_for(waves, kThreads / kWave, 1u << 16), kThreads, 0, stream>>>(
-            map, out_capacity, K, out->row_offsets, out->counts, out->in_rows, out->out_rows, out->kernel_ids);
+        emit_edges<32><<<blocks, kThreads, 0, stream>>>(map, out_capacity, K, block_offsets, out->counts,
+                                                        out->row_offsets, out->in_rows, out->out_rows,
+                                                        out->kernel_ids);
     } else {
-        emit_edges<64><<<grid_for(out_capacity, kThreads / kWave, 1u << 16), kThreads, 0, stream>>>(
-            map, out_capacity, K, out->row_offsets, out->counts, out->in_rows, out->out_rows, out->kernel_ids);
+        emit_edges<64><<<blocks, kThreads, 0, stream>>>(map, out_capacity, K, block_offsets, out->counts,
+                                                        out->row_offsets, out->in_rows, out->out_rows,
+                                                        out->kernel_ids);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
 
-// Common tail: query -> degrees -> scan -> emit -> views.
+// Common tail: query (degrees + per-block totals) -> scan of the block
+// totals -> emit (row offsets + edges) -> grouped views when requested.
 int finish_relation(QueryArgs q, int in_capacity, const lattice_relation_outputs* out, Workspace& ws,
                     hipStream_t stream) {
     const int K = q.geom.volume;
     const int out_capacity = q.out_capacity;
-    q.degrees = out->row_offsets;  // degrees land in row_offsets, then scan in place
-    int rc = launch_query(q, stream);
-    if (rc != LATTICE_OK) return rc;
-    rc = fill_i32(out->row_offsets + out_capacity, 1, 0, stream);
-    if (rc != LATTICE_OK) return rc;
-    rc = exclusive_scan(out->row_offsets, out->row_offsets, static_cast<long long>(out_capacity) + 1,
-                        out->counts, ws, stream);
-    if (rc != LATTICE_OK) return rc;
-    rc = launch_emit(q.out_in_map, out_capacity, K, out, stream);
-    if (rc != LATTICE_OK) return rc;
+    if (out_capacity <= 0) {
+        int rc = fill_i32(out->row_offsets, 1, 0, stream);
+        if (rc != LATTICE_OK) return rc;
+        rc = fill_i32(out->counts, 1, 0, stream);
+        if (rc != LATTICE_OK) return rc;
+    } else {
+        const int blocks = query_blocks(out_capacity);
+        int32_t* totals = ws.take<int32_t>(blocks);
+        int32_t* offsets = ws.take<int32_t>(blocks);
+        LATTICE_REQUIRE(totals && offsets, "relation workspace too small.");
+        q.degrees = out->row_offsets;  // degrees land in row_offsets; emit turns them into offsets
+        q.block_totals = totals;
+        int rc = launch_query(q, stream);
+        if (rc != LATTICE_OK) return rc;
+        scan_block_totals<<<1, kBlockScanThreads, 0, stream>>>(totals, blocks, offsets, out->counts);
+        LATTICE_LAUNCH_CHECK();
+        rc = launch_emit(q.out_in_map, out_capacity, K, offsets, out, stream);
+        if (rc != LATTICE_OK) return rc;
+    }
     if (out->in_edge_ids == nullptr && out->kernel_edge_ids == nullptr) return LATTICE_OK;  // views on demand
     return build_group_views(out->in_rows, out->kernel_ids, out->counts, out_capacity * K, in_capacity, K,
                              out->in_row_offsets, out->in_edge_ids, out->kernel_row_offsets, out->kernel_edge_ids,
@@ -504,7 +621,7 @@ size_t forward_relation_bytes(int rows, int K) {
     size_t bytes = block_table_bytes(rows) + table_bytes(rows);           // coords + cells
     bytes += 2 * aligned_bytes(static_cast<size_t>(rows) * sizeof(int32_t)); // flags + positions
     bytes += scan_workspace_bytes(rows);
-    bytes += scan_workspace_bytes(static_cast<long long>(rows) + 1);
+    bytes += 2 * aligned_bytes(static_cast<size_t>(query_blocks(rows) + 1) * sizeof(int32_t));  // block sums
     bytes += group_view_bytes(rows * K);
     return bytes + 4096;
 }
@@ -541,7 +658,7 @@ extern "C" size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kern
 
 extern "C" size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows, int kernel_count) {
     size_t bytes = block_table_bytes(std::max(rows, 0));
-    bytes += scan_workspace_bytes(static_cast<long long>(std::max(target_rows, 0)) + 1);
+    bytes += 2 * aligned_bytes(static_cast<size_t>(query_blocks(std::max(target_rows, 0)) + 1) * sizeof(int32_t));
     bytes += group_view_bytes(std::max(target_rows, 0) * std::max(kernel_count, 1));
     return bytes + 4096;
 }
@@ -565,14 +682,23 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     hipStream_t stream = as_stream(stream_ptr);
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
 
-    rc = fill_i32(out->status, 1, 0, stream);
-    if (rc != LATTICE_OK) return rc;
-    BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, out->status, ws, stream, &table);
-    if (rc != LATTICE_OK) return rc;
-
     const bool identity = stride[0] == 1 && stride[1] == 1 && stride[2] == 1 && padding[0] == 0 &&
                           padding[1] == 0 && padding[2] == 0;
+    Prologue prologue{out->status, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr};
+    if (identity) {
+        // submanifold: out_coords = the active input coords, counts[1] = active rows
+        prologue.count_src = active_rows;
+        prologue.count_limit = rows;
+        prologue.counts = out->counts;
+        prologue.copy_src = coords;
+        prologue.copy_active = active_rows;
+        prologue.copy_rows = rows;
+        prologue.copy_dst = out->out_coords;
+    }
+    BlockTable table;
+    rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
+    if (rc != LATTICE_OK) return rc;
+
     QueryArgs q{};
     q.out_capacity = rows;
     q.offsets = nullptr;
@@ -582,13 +708,6 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     q.out_in_map = out->out_in_map;
     q.row_masks = out->row_masks;
     if (identity) {
-        if (rows > 0) {
-            copy_active_coords<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(coords, rows, active_rows,
-                                                                                       out->out_coords);
-            LATTICE_LAUNCH_CHECK();
-        }
-        set_out_count<<<1, 64, 0, stream>>>(active_rows, rows, out->counts);
-        LATTICE_LAUNCH_CHECK();
         q.out_coords = coords;
         q.out_active = out->counts + 1;
     } else {
@@ -635,13 +754,10 @@ extern "C" int lattice_hip_build_target_kernel_relation(
                     "relation workspace too small.");
     hipStream_t stream = as_stream(stream_ptr);
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
-    rc = fill_i32(out->status, 1, 0, stream);
-    if (rc != LATTICE_OK) return rc;
+    const Prologue prologue{out->status, target_active_rows, target_rows, out->counts, nullptr, nullptr, 0, nullptr};
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, out->status, ws, stream, &table);
+    rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
-    set_out_count<<<1, 64, 0, stream>>>(target_active_rows, target_rows, out->counts);
-    LATTICE_LAUNCH_CHECK();
     QueryArgs q{};
     q.out_coords = target_coords;
     q.out_capacity = target_rows;
@@ -698,10 +814,9 @@ extern "C" int lattice_hip_build_relation_implicit_gemm_view(
                     "implicit GEMM view workspace too small.");
     hipStream_t stream = as_stream(stream_ptr);
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
-    int rc = fill_i32(status, 1, 0, stream);
-    if (rc != LATTICE_OK) return rc;
+    const Prologue prologue{status, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr};
     BlockTable table;
-    rc = build_block_table(source_coords, source_rows, source_active_rows, status, ws, stream, &table);
+    int rc = build_block_table(source_coords, source_rows, source_active_rows, status, prologue, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
     QueryArgs q{};
     q.out_coords = output_coords;
