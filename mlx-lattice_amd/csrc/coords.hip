@@ -288,6 +288,117 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
     }
 }
 
+// 3x3x3 offsets, unit stride and dilation, no padding (submanifold and
+// k=3 target maps): one lane per output row.  The 27 neighbours of a voxel
+// lie in the 2x2x2 blocks (v-1)>>1 .. +1 on each axis, 8 blocks in all, so a
+// row costs 8 hash probes instead of 27, and all 8 bucket reads are issued
+// before any is used.  The buckets' rows form a 4x4x4 window around the
+// voxel; the neighbour at offset d sits at window index d + 2 - (v & 1) per
+// axis, picked with selects on the coordinate parities.  The wave's 64 map
+// rows are staged in LDS and written out contiguously.
+__global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
+    constexpr int K = 27;
+    __shared__ int32_t stage[kQueryRows * K];
+    const int lane = lane_id();
+    const long long row0 = static_cast<long long>(blockIdx.x) * kQueryRows;
+    const long long row = row0 + lane;
+    const int n_active = min(max(*a.out_active, 0), a.out_capacity);
+    const bool row_ok = row < a.out_capacity;
+    const bool active = row < n_active;
+    const int4 c = active ? load_coord(a.out_coords, row) : make_int4(0, 0, 0, 0);
+    const int bx = (c.y - 1) >> 1, by = (c.z - 1) >> 1, bz = (c.w - 1) >> 1;  // floor division
+    uint64_t keys[8];
+    bool key_ok[8];
+    uint32_t slot[8];
+    uint4 lo[8], mid[8];
+    uint2 hi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        key_ok[j] = active && pack_key(c.x, bx + (j >> 2), by + ((j >> 1) & 1), bz + (j & 1), &keys[j]);
+        slot[j] = static_cast<uint32_t>(mix64(keys[j])) & a.table.mask;
+        const uint4* bucket = reinterpret_cast<const uint4*>(a.table.buckets + slot[j]);
+        lo[j] = bucket[0];   // key, rows 0..1
+        mid[j] = bucket[1];  // rows 2..5
+        hi[j] = *reinterpret_cast<const uint2*>(bucket + 2);  // rows 6..7
+    }
+    uint32_t rows[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint64_t k = (static_cast<uint64_t>(lo[j].y) << 32) | lo[j].x;
+        while (key_ok[j] && k != keys[j] && k != kEmptyKey) {  // linear probing, rare
+            slot[j] = (slot[j] + 1) & a.table.mask;
+            const uint4* bucket = reinterpret_cast<const uint4*>(a.table.buckets + slot[j]);
+            lo[j] = bucket[0];
+            mid[j] = bucket[1];
+            hi[j] = *reinterpret_cast<const uint2*>(bucket + 2);
+            k = (static_cast<uint64_t>(lo[j].y) << 32) | lo[j].x;
+        }
+        const bool found = key_ok[j] && k == keys[j];
+        rows[j][0] = found ? lo[j].z : 0u;
+        rows[j][1] = found ? lo[j].w : 0u;
+        rows[j][2] = found ? mid[j].x : 0u;
+        rows[j][3] = found ? mid[j].y : 0u;
+        rows[j][4] = found ? mid[j].z : 0u;
+        rows[j][5] = found ? mid[j].w : 0u;
+        rows[j][6] = found ? hi[j].x : 0u;
+        rows[j][7] = found ? hi[j].y : 0u;
+    }
+    // window[lx][ly][lz], l in 0..3 = 2 * block + octant bit
+    const bool px = c.y & 1, py = c.z & 1, pz = c.w & 1;
+    uint32_t wx[3][4][4];  // x picked
+#pragma unroll
+    for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+        for (int ly = 0; ly < 4; ++ly)
+#pragma unroll
+            for (int lz = 0; lz < 4; ++lz) {
+                const int l0 = dx + 1, l1 = dx;  // window x for even / odd voxel x
+                const uint32_t even = rows[(l0 >> 1) * 4 + (ly >> 1) * 2 + (lz >> 1)][(l0 & 1) * 4 + (ly & 1) * 2 + (lz & 1)];
+                const uint32_t odd = rows[(l1 >> 1) * 4 + (ly >> 1) * 2 + (lz >> 1)][(l1 & 1) * 4 + (ly & 1) * 2 + (lz & 1)];
+                wx[dx][ly][lz] = px ? odd : even;
+            }
+    uint32_t mask = 0;
+    int degree = 0;
+#pragma unroll
+    for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+        for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+            for (int dz = 0; dz < 3; ++dz) {
+                const uint32_t y0 = py ? wx[dx][dy][dz] : wx[dx][dy + 1][dz];
+                const uint32_t y1 = py ? wx[dx][dy][dz + 1] : wx[dx][dy + 1][dz + 1];
+                const uint32_t raw = pz ? y0 : y1;
+                const int k = dx * 9 + dy * 3 + dz;
+                const int32_t v = raw == 0 ? -1 : kRowBias - static_cast<int32_t>(raw);
+                stage[lane * K + k] = v;
+                if (raw != 0) {
+                    mask |= 1u << k;
+                    ++degree;
+                }
+            }
+    if (row_ok) {
+        a.row_masks[row] = static_cast<int32_t>(mask);
+        if (a.degrees != nullptr) a.degrees[row] = degree;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(min(static_cast<long long>(kQueryRows), a.out_capacity - row0)) * K;
+    int32_t* dst = a.out_in_map + row0 * K;
+    for (int i = lane; i < n; i += kWave) dst[i] = stage[i];
+    if (a.block_totals != nullptr) {
+        int sum = row_ok ? degree : 0;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+        if (lane == 0) a.block_totals[blockIdx.x] = sum;
+    }
+}
+
+bool is_unit_k3(const QueryArgs& a) {
+    const KernelGeometry& g = a.geom;
+    return a.offsets == nullptr && g.volume == 27 && g.size.x == 3 && g.size.y == 3 && g.size.z == 3 &&
+           g.dilation.x == 1 && g.dilation.y == 1 && g.dilation.z == 1 && g.stride.x == 1 && g.stride.y == 1 &&
+           g.stride.z == 1 && g.padding.x == 0 && g.padding.y == 0 && g.padding.z == 0 && a.words == 1;
+}
+
 // Exclusive prefix of the per-block degree totals (one workgroup); the sum
 // of all is the edge count, counts[0].  Each thread owns a contiguous run;
 // loads are issued kScanBatch at a time before use.
@@ -543,7 +654,9 @@ int query_blocks(int out_capacity) { return (out_capacity + kQueryRows - 1) / kQ
 int launch_query(const QueryArgs& a, hipStream_t stream) {
     if (a.out_capacity <= 0) return LATTICE_OK;
     const unsigned blocks = static_cast<unsigned>(query_blocks(a.out_capacity));
-    if (a.geom.volume <= 32) {
+    if (is_unit_k3(a)) {
+        query_map_k3<<<blocks, kWave, 0, stream>>>(a);
+    } else if (a.geom.volume <= 32) {
         query_map<32><<<blocks, kThreads, 0, stream>>>(a);
     } else {
         query_map<64><<<blocks, kThreads, 0, stream>>>(a);
