@@ -179,13 +179,10 @@ struct BlockTable {
     __device__ inline void insert(uint64_t block_key, int octant, int32_t row) const {
         uint32_t slot = static_cast<uint32_t>(mix64(block_key)) & mask;
         while (true) {
-            unsigned long long* kp = &buckets[slot].key;
-            unsigned long long k = __atomic_load_n(kp, __ATOMIC_RELAXED);
-            if (k == kEmptyKey) {
-                k = atomicCAS(kp, static_cast<unsigned long long>(kEmptyKey),
-                              static_cast<unsigned long long>(block_key));
-                if (k == kEmptyKey) k = block_key;
-            }
+            // One compare-and-swap claims an empty slot or reports its key.
+            unsigned long long k = atomicCAS(&buckets[slot].key, static_cast<unsigned long long>(kEmptyKey),
+                                             static_cast<unsigned long long>(block_key));
+            if (k == kEmptyKey) k = block_key;
             if (k == block_key) {
                 atomicMax(&buckets[slot].rows[octant], kRowBias - row);
                 return;
