@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per conv_igemm launch on this workload, from rocprofv3 FETCH_SIZE
 # and WRITE_SIZE passes scaled by a 1 GiB copy's counter readings
 # (profiles/conv_igemm_config3_traffic.md).  Re-measure when the kernel changes.
-CONV_TRAFFIC_BYTES = 1.160e9
+CONV_TRAFFIC_BYTES = 1.202e9
 
 
 def parse_args():
@@ -232,7 +232,7 @@ def main() -> int:
             'unit': 'TFLOP/s',
             'frac': round(conv_tflops / PEAK_FP16_TFLOPS, 5),
             'traffic': CONV_TRAFFIC_BYTES,
-            'kernel': 'conv_igemm<_Float16,128,FloatB>',
+            'kernel': 'conv_igemm<f16, IgemmShape<128,32,4,64>, FloatB>',
         },
     }
     if not args.no_cpu_baseline:
