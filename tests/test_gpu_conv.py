@@ -11,6 +11,8 @@ kernel.
 
 from __future__ import annotations
 
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -21,6 +23,8 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 DEV = 'cuda'
+ROOT_LIB = (Path(__file__).resolve().parent.parent / 'mlx-lattice_amd' /
+            'mlx_lattice_amd' / 'liblattice_hip.so')
 RTOL_F32, ATOL_F32 = 1e-3, 1e-5
 RTOL_F16, ATOL_F16 = 2e-2, 1e-2
 
@@ -312,3 +316,71 @@ def test_config4_int4_fused_200k():
     _, ref = _reference(coords, feats.astype(np.float32),
                         to_np(dequantize_weight(q).float()), dict(kernel_size=3))
     _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16, 'config4')
+
+
+def test_tile_schedule_does_not_change_results():
+    """The longest-first tile schedule (conv workspace) only reorders row
+    tiles: through the C ABI, the matrix-core conv with a workspace and
+    with none (tiles in order) must agree bit for bit, for float and packed
+    weights, and for C_out 16 (128-channel stages) and 128."""
+    import ctypes
+
+    from mlx_lattice_amd import quantize_weight
+    from mlx_lattice_amd._native import ext
+
+    lib = ctypes.CDLL(str(ROOT_LIB))
+    lib.lattice_hip_conv_workspace_bytes.restype = ctypes.c_size_t
+    P, I = ctypes.c_void_p, ctypes.c_int
+    sorted_conv = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm
+    sorted_conv.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P,
+                            ctypes.c_size_t, P]
+    quant_conv = lib.lattice_hip_sparse_quantized_conv_features
+    quant_conv.argtypes = [I, P, I, I, P, P, P, I, I, I, I, I, P, P, P, I, P,
+                           P, P, P, I, P, P, ctypes.c_size_t, P]
+    coords, rng = _shell(30000, 128, 31)
+    n = len(coords)
+    c = torch.as_tensor(coords, dtype=torch.int32).to(DEV)
+    active = torch.tensor([n], dtype=torch.int32, device=DEV)
+    rel = ext.build_submanifold_kernel_relation_with_view(c, active, [3, 3, 3],
+                                                          [1, 1, 1])
+    reorder, _, kv, tiles = ext.build_sorted_implicit_gemm_view(rel[10],
+                                                                rel[11])
+    stream = torch.cuda.current_stream().cuda_stream
+    wsb = lib.lattice_hip_conv_workspace_bytes(n)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    feats = torch.as_tensor(rng.standard_normal((n, 64)).astype(
+        np.float16)).to(DEV)
+    for c_out in (16, 128):
+        w = torch.as_tensor((rng.standard_normal((c_out, 3, 3, 3, 64)) * 0.05)
+                            .astype(np.float16)).to(DEV)
+        outs = []
+        for workspace, nbytes in ((ws.data_ptr(), wsb), (None, 0)):
+            out = torch.empty((n, c_out), dtype=torch.float16, device=DEV)
+            assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1,
+                               27, c_out, kv.data_ptr(), tiles.data_ptr(),
+                               reorder.data_ptr(), n, out.data_ptr(),
+                               workspace, nbytes, stream) == 0
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), c_out
+        q = quantize_weight(w, group_size=32, bits=4)
+        qouts = []
+        for workspace, nbytes in ((ws.data_ptr(), wsb), (None, 0)):
+            out = torch.empty((n, c_out), dtype=torch.float16, device=DEV)
+            assert quant_conv(1, feats.data_ptr(), n, 64, q.weight.data_ptr(),
+                              q.scales.data_ptr(), q.biases.data_ptr(), 27,
+                              c_out, q.storage_in_channels, 32, 4,
+                              rel[0].data_ptr(), rel[2].data_ptr(),
+                              rel[5].data_ptr(), int(rel[0].shape[0]),
+                              rel[3].data_ptr(), kv.data_ptr(),
+                              tiles.data_ptr(), reorder.data_ptr(), n,
+                              out.data_ptr(), workspace, nbytes,
+                              stream) == 0
+            qouts.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(qouts[0], qouts[1]), c_out
+    # a workspace that is too small is an argument error, not a fault
+    out = torch.empty((n, 128), dtype=torch.float16, device=DEV)
+    assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27, 128,
+                       kv.data_ptr(), tiles.data_ptr(), reorder.data_ptr(), n,
+                       out.data_ptr(), ws.data_ptr(), 4, stream) == 1
