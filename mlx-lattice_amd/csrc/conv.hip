@@ -235,7 +235,6 @@ __device__ inline int swizzle_piece(int piece, int row) { return piece ^ (row & 
 // B operand sources.  `load(k, co, ci0)` returns 8 consecutive input
 // channels ci0..ci0+7 of W[k][:, co] as one 16-byte vector.
 template <typename T> struct FloatB {
-    static constexpr bool kDirect = true;  // copied global -> LDS without registers
     const T* w;
     long long s_co, s_k;  // element strides; C_in is contiguous
     __device__ inline typename MfmaOps<T>::vec load(int k, int co, int ci0) const {
@@ -245,7 +244,6 @@ template <typename T> struct FloatB {
 
 // Packed affine codes: w = q * scale + bias, dequantised while staging B.
 template <typename T> struct PackedB {
-    static constexpr bool kDirect = false;  // dequantised in registers, then stored
     const uint32_t* w;
     const T* scales;
     const T* biases;
@@ -343,35 +341,6 @@ __device__ inline void stage_b_store(T* dst, const V (&breg)[S::B_PIECES]) {
     }
 }
 
-// Direct global -> LDS copy of this wave's share of a float B tile.  One
-// copy moves 64 lanes x 16 bytes; lane i lands at LDS base + 16 i, i.e. row
-// i / PIECES, slot i % PIECES, so it fetches the piece the swizzle puts in
-// that slot.  The copies are written as inline assembly: issued through the
-// builtin, the compiler cannot tell them from the LDS reads of the other
-// buffer and drains every load before those reads.  The caller waits for
-// them (vector-memory counter) before the barrier that publishes the tile.
-template <typename T, typename S>
-__device__ inline void stage_b_copy(const FloatB<T>& bsrc, int k, int ci0, int cw, T* dst, int wave, int lane) {
-    constexpr int kRowsPerCopy = kWave / S::PIECES;
-#pragma unroll
-    for (int j = 0; j < S::B_PIECES; ++j) {
-        const int r0 = (j * S::WAVES + wave) * kRowsPerCopy;
-        const int row = r0 + lane / S::PIECES;
-        const int piece = swizzle_piece<S::PIECES>(lane % S::PIECES, row);
-        const T* src = bsrc.w + row * bsrc.s_co + k * bsrc.s_k + ci0 + (piece * 8 < cw ? piece * 8 : 0);
-        const uint32_t base = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-            reinterpret_cast<size_t>((const __attribute__((address_space(3))) void*)(dst + r0 * S::BROW))));
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src) : "memory", "m0");
-    }
-}
-
-// Waits until at most `n` vector-memory operations of this wave are in
-// flight.
-template <int N>
-__device__ inline void wait_vmem() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // B fragments of 32-channel step `st` for the wave's CB column blocks.
 template <typename T, typename S, typename V>
 __device__ inline void read_b_step(V (&b)[S::CB], const T* brow, int st, int lane, int lr) {
@@ -414,13 +383,9 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
     const int sa = min(s + S::DEPTH, last);
     const int si = min(s + S::DEPTH + 1, last);
     load_rows<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], lr);
-    V breg[BSource::kDirect ? 1 : S::B_PIECES];
+    V breg[S::B_PIECES];
     const int cib = c.stage_chunk[sb] * S::CHUNK;
-    if constexpr (BSource::kDirect) {
-        stage_b_copy<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), bnext, threadIdx.x / kWave, c.lane);
-    } else {
-        stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
-    }
+    stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
     const int cia = c.stage_chunk[sa] * S::CHUNK;
     load_a<T, V, S::RB, S::ST>(a_fill, idx_a, rows_rsrc, c.c_in, cia, min(S::CHUNK, c.c_in - cia), lk);
 
@@ -449,13 +414,7 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
             }
         }
     }
-    if constexpr (BSource::kDirect) {
-        // the copies of B(s+1) were issued before this stage's A gathers,
-        // which may stay in flight
-        wait_vmem<S::RB * S::ST>();
-    } else {
-        stage_b_store<T, S>(bnext, breg);
-    }
+    stage_b_store<T, S>(bnext, breg);
     __syncthreads();
 }
 
@@ -530,9 +489,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         const __amdgpu_buffer_rsrc_t rows_rsrc = feature_rows(feats, n_in, c_in);
 #pragma unroll
         for (int j = 0; j <= S::DEPTH; ++j) load_rows<S::RB>(idx[j], kv_map, rows, row0, stage_k[min(j, last)], lr);
-        if constexpr (BSource::kDirect) {
-            stage_b_copy<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), bbuf0, wave, lane);
-        } else {
+        {
             V breg[S::B_PIECES];
             stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
             stage_b_store<T, S>(bbuf0, breg);
@@ -543,7 +500,6 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
             const int ci = stage_chunk[sj] * S::CHUNK;
             load_a<T, V, S::RB, S::ST>(a[j], idx[j], rows_rsrc, c_in, ci, min(S::CHUNK, c_in - ci), lk);
         }
-        if constexpr (BSource::kDirect) wait_vmem<S::DEPTH * S::RB * S::ST>();  // B(0) landed
         __syncthreads();
         // Stage s = base + j uses A buffer j % NA, gathers into (j + DEPTH) %
         // NA with the indices in idx[(j + DEPTH) % NA], and refills idx[j %
