@@ -50,6 +50,8 @@ def parse_args():
     p.add_argument('--cpu-sample-rows', type=int, default=131072,
                    help='output rows of the bounded CPU-baseline sample')
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--no-secondary', action='store_true',
+                   help='skip the timings of configs 2, 4 and 5')
     p.add_argument('--copy-probe-mib', type=int, default=0,
                    help='only run a plain device copy of this many MiB '
                         '(5 launches) and exit: the reference kernel that '
@@ -124,6 +126,130 @@ def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int):
         'map_build_ms': round(t_map * 1e3, 3),
         'mvoxels_per_s': round(n / t_conv / 1e6, 6),
     }
+
+
+def _timed(fn, steps: int, warmup: int) -> float:
+    """Mean milliseconds of ``fn`` over ``steps`` calls, HIP events on the
+    current stream (the one the bindings launch on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
+    """Configs 2, 4 and 5 through the operator API.
+
+    ``layer_ms`` builds a fresh coordinate manager every call, so it covers
+    the kernel-map build, the sorted view, the conv and the bias;
+    ``conv_ms`` reuses the cached relation and times the conv alone, which
+    is what the effective TFLOP/s is computed from.
+    """
+    import numpy as np
+    import torch
+
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor, quantize_weight
+    from mlx_lattice_amd.nn import Conv3d, SubmConv3d
+    from mlx_lattice_amd.nn.quantized_conv import (QuantizedConv3d,
+                                                   QuantizedSubmConv3d)
+    from mlx_lattice_amd.synthetic import (config_rng, encoder_layers,
+                                           kaiming_weight, lidar_cloud,
+                                           sphere_shell_cloud)
+
+    dev = torch.device('cuda:0')
+    out = {}
+
+    def layer(coords, feats, run, c_in, c_out, workload):
+        x = SparseTensor(coords, feats)
+        y = run(x)
+        torch.cuda.synchronize()
+        rel = x.coord_manager._kernel_relations
+        relation = next(iter(rel.values()))
+        edges = int(relation.counts[0].item())
+        n_out = int(relation.counts[1].item())
+        layer_ms = _timed(lambda: run(SparseTensor(coords, feats)), steps,
+                          warmup)
+        conv_ms = _timed(lambda: run(x), steps, warmup)
+        del y
+        return {
+            'workload': workload,
+            'voxels_in': int(coords.shape[0]), 'voxels_out': n_out,
+            'edges': edges,
+            'layer_ms': round(layer_ms, 4), 'conv_ms': round(conv_ms, 4),
+            'tflops': round(2.0 * edges * c_in * c_out / conv_ms / 1e9, 3),
+            'mvoxels_per_s': round(n_out / conv_ms / 1e3, 3),
+        }
+
+    rng = config_rng(2)
+    c2 = torch.as_tensor(lidar_cloud(100000, 2, rng=rng)).to(dev)
+    f2 = torch.as_tensor(rng.standard_normal((c2.shape[0], 64)).astype(
+        np.float16)).to(dev)
+    w2 = torch.as_tensor((rng.standard_normal((128, 2, 2, 2, 64))
+                          * np.sqrt(2.0 / (8 * 64))).astype(np.float16)).to(dev)
+    out['config2'] = layer(
+        c2, f2, lambda x: ops.conv3d(x, w2, kernel_size=2, stride=2), 64, 128,
+        'conv3d k=2 s=2 fp16 64->128, 2 x ~100k LiDAR-like voxels')
+
+    rng = config_rng(4)
+    c4 = torch.as_tensor(sphere_shell_cloud(200000, 256, rng=rng)).to(dev)
+    w4 = torch.as_tensor(kaiming_weight((64, 3, 3, 3, 64), rng=rng)).to(
+        dev, torch.float16)
+    f4 = torch.as_tensor(rng.standard_normal((c4.shape[0], 64)).astype(
+        np.float16)).to(dev)
+    q4 = quantize_weight(w4, group_size=32, bits=4)
+    out['config4'] = layer(
+        c4, f4, lambda x: ops.subm_conv3d(x, q4, kernel_size=3), 64, 64,
+        'QuantizedConv3d subm k=3 int4 g32 fp16 64->64, 200k sphere-shell '
+        'voxels')
+
+    rng = config_rng(5)
+    c5 = torch.as_tensor(lidar_cloud(120000, 4, rng=rng)).to(dev)
+    f5 = torch.as_tensor(rng.random((c5.shape[0], 4)).astype(np.float16)).to(
+        dev)
+    mods = []
+    for spec in encoder_layers(rng):
+        c_out_l, *_, c_in_l = spec['weight'].shape
+        if spec['kind'] == 'subm':
+            dense = SubmConv3d(c_in_l, c_out_l, kernel_size=3, device=dev,
+                               dtype=torch.float16)
+            cls = QuantizedSubmConv3d
+        else:
+            dense = Conv3d(c_in_l, c_out_l, kernel_size=2, stride=2,
+                           device=dev, dtype=torch.float16)
+            cls = QuantizedConv3d
+        dense.weight.data.copy_(torch.as_tensor(spec['weight']))
+        dense.bias.data.copy_(torch.as_tensor(spec['bias']))
+        mods.append(cls.from_conv(dense, group_size=32, bits=8))
+
+    def encoder(x):
+        for mod in mods:
+            x = mod(x)
+            x = x.replace(feats=torch.relu(x.feats))
+        return x
+
+    x5 = SparseTensor(c5, f5)
+    encoder(x5)
+    out['config5'] = {
+        'workload': 'int8 g32 sparse encoder (stem subm 4->32, 3 x [k2s2 '
+                    'down + 2 x subm], 32->64->128->256, bias + ReLU), '
+                    f'4 x ~120k LiDAR-like voxels ({int(c5.shape[0])} rows)',
+        'forward_ms': round(_timed(lambda: encoder(SparseTensor(c5, f5)),
+                                   steps, warmup), 4),
+        'forward_cached_maps_ms': round(_timed(lambda: encoder(x5), steps,
+                                               warmup), 4),
+    }
+    return out
 
 
 def main() -> int:
@@ -235,6 +361,8 @@ def main() -> int:
             'kernel': 'conv_igemm<f16, IgemmShape<128,32,4,64>, FloatB>',
         },
     }
+    if not args.no_secondary:
+        record['secondary'] = secondary_workloads()
     if not args.no_cpu_baseline:
         record['cpu_baseline'] = cpu_baseline(
             coords_np, feats_np, weight_np, args.cpu_threads,

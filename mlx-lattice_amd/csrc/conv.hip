@@ -60,13 +60,30 @@ struct WeightIndex {
     }
 };
 
+// Weights of at most kCsrLdsFloats floats are staged once per block in LDS
+// as float32, (k, ci, co) with co fastest, so the lanes of a row read
+// consecutive banks; the launch then caps the grid so each block walks many
+// rows.  Larger weights are read from global memory at each use.
+constexpr int kCsrLdsFloats = 16384;
+constexpr unsigned kCsrStagedBlocks = 2048;
+
 template <typename T>
 __global__ void __launch_bounds__(256)
 conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, WeightIndex widx,
          const int32_t* __restrict__ in_rows, const int32_t* __restrict__ kernel_ids,
          const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ row_offsets,
-         int out_capacity, T* __restrict__ out) {
+         int out_capacity, T* __restrict__ out, bool staged) {
+    extern __shared__ float wlds[];
     const int c_out = widx.c_out;
+    if (staged) {
+        const int nw = widx.K * c_in * c_out;
+        for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+            const int co = i % c_out;
+            const int kc = i / c_out;
+            wlds[i] = Elem<T>::load(weights, widx(kc / c_in, kc % c_in, co));
+        }
+        __syncthreads();
+    }
     const int E = min(counts[0], edge_capacity);
     const int n_out = min(counts[1], out_capacity);
     const long long total = static_cast<long long>(out_capacity) * c_out;
@@ -83,8 +100,13 @@ conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, W
                 const int k = kernel_ids[e];
                 if (in < 0 || k < 0 || k >= widx.K) continue;
                 const T* f = feats + static_cast<long long>(in) * c_in;
-                for (int ci = 0; ci < c_in; ++ci) {
-                    acc += Elem<T>::load(f, ci) * Elem<T>::load(weights, widx(k, ci, co));
+                if (staged) {
+                    const float* wk = wlds + static_cast<long long>(k) * c_in * c_out + co;
+                    for (int ci = 0; ci < c_in; ++ci) acc += Elem<T>::load(f, ci) * wk[ci * c_out];
+                } else {
+                    for (int ci = 0; ci < c_in; ++ci) {
+                        acc += Elem<T>::load(f, ci) * Elem<T>::load(weights, widx(k, ci, co));
+                    }
                 }
             }
         }
@@ -112,7 +134,17 @@ __global__ void __launch_bounds__(256)
 quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights, const T* __restrict__ scales,
                const T* __restrict__ biases, QuantIndex q, const int32_t* __restrict__ in_rows,
                const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
-               const int32_t* __restrict__ row_offsets, int out_capacity, T* __restrict__ out) {
+               const int32_t* __restrict__ row_offsets, int out_capacity, T* __restrict__ out, bool staged) {
+    extern __shared__ float wlds[];
+    if (staged) {
+        const int nw = q.K * q.c_in * q.c_out;
+        for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+            const int co = i % q.c_out;
+            const int kc = i / q.c_out;
+            wlds[i] = dequant(weights, scales, biases, q, kc / q.c_in, kc % q.c_in, co);
+        }
+        __syncthreads();
+    }
     const int E = min(counts[0], edge_capacity);
     const int n_out = min(counts[1], out_capacity);
     const long long total = static_cast<long long>(out_capacity) * q.c_out;
@@ -129,8 +161,13 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
                 const int k = kernel_ids[e];
                 if (in < 0 || k < 0 || k >= q.K) continue;
                 const T* f = feats + static_cast<long long>(in) * q.c_in;
-                for (int ci = 0; ci < q.c_in; ++ci) {
-                    acc += Elem<T>::load(f, ci) * dequant(weights, scales, biases, q, k, ci, co);
+                if (staged) {
+                    const float* wk = wlds + static_cast<long long>(k) * q.c_in * q.c_out + co;
+                    for (int ci = 0; ci < q.c_in; ++ci) acc += Elem<T>::load(f, ci) * wk[ci * q.c_out];
+                } else {
+                    for (int ci = 0; ci < q.c_in; ++ci) {
+                        acc += Elem<T>::load(f, ci) * dequant(weights, scales, biases, q, k, ci, co);
+                    }
                 }
             }
         }
@@ -661,6 +698,9 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
+// c_out = 256 splits the columns over two waves per row group and uses
+// eight waves, so each thread stages four B pieces instead of eight (with
+// eight, the packed-weight variant spills to scratch).
 #define LATTICE_IGEMM_CASE(C)                                                  \
     case C:                                                                    \
         if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(C, 64, 4);   \
@@ -670,7 +710,9 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
         LATTICE_IGEMM_CASE(32)
         LATTICE_IGEMM_CASE(64)
         LATTICE_IGEMM_CASE(128)
-        LATTICE_IGEMM_CASE(256)
+    case 256:
+        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(256, 64, 4);
+        return LATTICE_IGEMM_LAUNCH(256, 32, 8, 64);
 #undef LATTICE_IGEMM_CASE
 #undef LATTICE_IGEMM_LAUNCH
     default:
@@ -736,22 +778,25 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
     hipStream_t stream = as_stream(stream_ptr);
     WeightIndex widx{weight_layout, kernel_count, c_in, c_out};
     const long long total = static_cast<long long>(out_capacity) * c_out;
-    const unsigned grid = grid_for(total, 256, 1u << 16);
+    const long long nw = static_cast<long long>(kernel_count) * c_in * c_out;
+    const bool staged = nw <= kCsrLdsFloats;
+    const unsigned grid = grid_for(total, 256, staged ? kCsrStagedBlocks : 1u << 16);
+    const size_t lds = staged ? static_cast<size_t>(nw) * sizeof(float) : 0;
     if (dtype == LATTICE_F32) {
-        conv_csr<float><<<grid, 256, 0, stream>>>(static_cast<const float*>(feats), c_in,
+        conv_csr<float><<<grid, 256, lds, stream>>>(static_cast<const float*>(feats), c_in,
                                                   static_cast<const float*>(weights), widx, in_rows, kernel_ids,
                                                   counts, edge_capacity, row_offsets, out_capacity,
-                                                  static_cast<float*>(out));
+                                                  static_cast<float*>(out), staged);
     } else if (dtype == LATTICE_F16) {
-        conv_csr<_Float16><<<grid, 256, 0, stream>>>(static_cast<const _Float16*>(feats), c_in,
+        conv_csr<_Float16><<<grid, 256, lds, stream>>>(static_cast<const _Float16*>(feats), c_in,
                                                      static_cast<const _Float16*>(weights), widx, in_rows,
                                                      kernel_ids, counts, edge_capacity, row_offsets, out_capacity,
-                                                     static_cast<_Float16*>(out));
+                                                     static_cast<_Float16*>(out), staged);
     } else {
-        conv_csr<__bf16><<<grid, 256, 0, stream>>>(static_cast<const __bf16*>(feats), c_in,
+        conv_csr<__bf16><<<grid, 256, lds, stream>>>(static_cast<const __bf16*>(feats), c_in,
                                                    static_cast<const __bf16*>(weights), widx, in_rows, kernel_ids,
                                                    counts, edge_capacity, row_offsets, out_capacity,
-                                                   static_cast<__bf16*>(out));
+                                                   static_cast<__bf16*>(out), staged);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
@@ -832,22 +877,26 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");
     QuantIndex q{kernel_count, c_in, c_out, packed_words, groups, group_size, bits};
-    const unsigned grid = grid_for(static_cast<long long>(out_capacity) * c_out, 256, 1u << 16);
+    const long long nw = static_cast<long long>(kernel_count) * c_in * c_out;
+    const bool staged = nw <= kCsrLdsFloats;
+    const unsigned grid =
+        grid_for(static_cast<long long>(out_capacity) * c_out, 256, staged ? kCsrStagedBlocks : 1u << 16);
+    const size_t lds = staged ? static_cast<size_t>(nw) * sizeof(float) : 0;
     if (dtype == LATTICE_F32) {
-        quant_conv_csr<float><<<grid, 256, 0, stream>>>(
+        quant_conv_csr<float><<<grid, 256, lds, stream>>>(
             static_cast<const float*>(feats), weights, static_cast<const float*>(scales),
             static_cast<const float*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<float*>(out));
+            out_capacity, static_cast<float*>(out), staged);
     } else if (dtype == LATTICE_F16) {
-        quant_conv_csr<_Float16><<<grid, 256, 0, stream>>>(
+        quant_conv_csr<_Float16><<<grid, 256, lds, stream>>>(
             static_cast<const _Float16*>(feats), weights, static_cast<const _Float16*>(scales),
             static_cast<const _Float16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<_Float16*>(out));
+            out_capacity, static_cast<_Float16*>(out), staged);
     } else {
-        quant_conv_csr<__bf16><<<grid, 256, 0, stream>>>(
+        quant_conv_csr<__bf16><<<grid, 256, lds, stream>>>(
             static_cast<const __bf16*>(feats), weights, static_cast<const __bf16*>(scales),
             static_cast<const __bf16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<__bf16*>(out));
+            out_capacity, static_cast<__bf16*>(out), staged);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;

@@ -23,6 +23,7 @@ __all__ = [
     'lidar_cloud',
     'sphere_shell_cloud',
     'kaiming_weight',
+    'encoder_layers',
     'unique_rows_first_seen',
 ]
 
@@ -171,3 +172,32 @@ def kaiming_weight(shape: tuple[int, ...], *, rng: np.random.Generator,
     fan_in = int(np.prod(shape[1:]))
     return (rng.standard_normal(shape) * np.sqrt(2.0 / fan_in)).astype(
         np.float32)
+
+
+def encoder_layers(rng: np.random.Generator, *, in_channels: int = 4,
+                   widths: tuple[int, ...] = (32, 64, 128, 256),
+                   ) -> list[dict]:
+    """Layer list of the config-5 int8 sparse encoder, as plain numpy.
+
+    Stem: submanifold k=3, ``in_channels -> widths[0]``.  Each following
+    stage: a k=2 stride-2 downsample to the next width, then two submanifold
+    k=3 convs at that width.  Weights are Kaiming-normal float32 in the
+    ``(C_out, Kx, Ky, Kz, C_in)`` layout; ``bias`` stands for a BatchNorm
+    folded into the conv (shift ~ N(0, 0.1^2)), and every layer is followed
+    by ReLU.  Quantization is left to the caller.
+    """
+    layers = []
+
+    def add(kind: str, c_in: int, c_out: int) -> None:
+        k = 3 if kind == 'subm' else 2
+        layers.append(dict(
+            kind=kind, kernel_size=k, stride=1 if kind == 'subm' else 2,
+            weight=kaiming_weight((c_out, k, k, k, c_in), rng=rng),
+            bias=(0.1 * rng.standard_normal(c_out)).astype(np.float32)))
+
+    add('subm', in_channels, widths[0])
+    for c_prev, c_next in zip(widths[:-1], widths[1:]):
+        add('down', c_prev, c_next)
+        add('subm', c_next, c_next)
+        add('subm', c_next, c_next)
+    return layers
