@@ -358,7 +358,7 @@ def main() -> int:
             'unit': 'TFLOP/s',
             'frac': round(conv_tflops / PEAK_FP16_TFLOPS, 5),
             'traffic': CONV_TRAFFIC_BYTES,
-            'kernel': 'conv_igemm<f16, IgemmShape<128,32,4,64>, FloatB>',
+            'kernel': 'conv_igemm<f16, IgemmShape<128 cols, 32-row waves, 4 waves, 64-channel stages, A via LDS>, FloatB>',
         },
     }
     if not args.no_secondary:

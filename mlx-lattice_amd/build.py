@@ -51,7 +51,8 @@ def hipcc() -> str:
 def build_hip_library(verbose: bool = False) -> Path:
     out = PKG / 'liblattice_hip.so'
     tmp = PKG / 'liblattice_hip.so.tmp'
-    cmd = [hipcc(), *HIP_FLAGS, '-shared', f'-I{INCLUDE}', f'-I{CSRC}',
+    extra = os.environ.get('LATTICE_HIPCC_FLAGS', '').split()
+    cmd = [hipcc(), *HIP_FLAGS, *extra, '-shared', f'-I{INCLUDE}', f'-I{CSRC}',
            *[str(CSRC / s) for s in HIP_SOURCES], '-o', str(tmp)]
     if verbose:
         print(' '.join(cmd), flush=True)

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "lattice_common.h"
 #include "scan.h"
@@ -191,6 +192,10 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
 //     on B(s) from LDS, skipping offsets that none of its rows uses,
 //   * stores B(s+1) into the other LDS buffer, then meets the block at a
 //     barrier.
+// With IgemmShape::ALDS (the default for 32..128 output channels) the A
+// gather of stage s+1 instead covers whole 128-byte row lines and goes
+// through a per-wave LDS buffer (see igemm_stage_alds): half the cache lines
+// per load instruction, which the vector-memory path is bound by.
 // Every load is an ordinary load the compiler tracks, so it waits only for
 // the operands each step uses and the gathers of DEPTH stages stay in flight
 // across the MFMAs.  Missing rows (map entry -1) load row 0 and are zeroed
@@ -224,8 +229,14 @@ template <> struct MfmaOps<__bf16> {
 //   OCC        blocks per CU the register allocation must allow;
 //   WCOLS      output channels per wave (at most 128).
 template <int C_OUT_, int WAVE_ROWS_, int WAVES_, int CHUNK_ = 128, int DEPTH_ = 1, bool BPIPE_ = false,
-          int OCC_ = (WAVE_ROWS_ == 32 ? 2 : 1), int WCOLS_ = 128>
+          int OCC_ = (WAVE_ROWS_ == 32 ? 2 : 1), int WCOLS_ = 128, bool WSKIP_ = false, bool ALDS_ = false>
 struct IgemmShape {
+    // ALDS: gather A in whole 128-byte lines (8 rows x 64 channels per
+    // load) into a per-wave LDS buffer and read the MFMA fragments from
+    // there; needs 64-channel stages and one stage of prefetch.
+    static constexpr bool ALDS = ALDS_;
+    static constexpr int A_LDS = ALDS_ ? WAVES_ * WAVE_ROWS_ * 64 : 1;  // halves
+    static constexpr bool WSKIP = WSKIP_;  // gather A only for offsets the wave's own rows use
     static constexpr int OCC = OCC_;
     static constexpr int C_OUT = C_OUT_;
     static constexpr int WAVE_ROWS = WAVE_ROWS_;
@@ -259,6 +270,7 @@ struct IgemmShape {
     static constexpr int B_PIECES = C_OUT * CHUNK / 8 / THREADS;  // 16-byte pieces per thread
     static constexpr int MAX_STAGES = 32 * (512 / CHUNK);  // K <= 32 offsets x C_in <= 512
     static_assert(CHUNK == 64 || CHUNK == 128, "stage chunk is 64 or 128 channels");
+    static_assert(!ALDS_ || (CHUNK_ == 64 && DEPTH_ == 1 && WAVE_ROWS_ % 16 == 0), "ALDS shape");
     static_assert(B_PIECES >= 1, "B tile must cover every thread");
     // One LDS array holds the two B buffers and, after the main loop, the
     // epilogue staging of every wave's tile.
@@ -419,12 +431,16 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
     const int sb = min(s + 1, last);
     const int sa = min(s + S::DEPTH, last);
     const int si = min(s + S::DEPTH + 1, last);
-    load_rows<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], lr);
+    if (!S::WSKIP || ((c.wmask >> c.stage_k[si]) & 1u)) {
+        load_rows<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], lr);
+    }
     V breg[S::B_PIECES];
     const int cib = c.stage_chunk[sb] * S::CHUNK;
     stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
-    const int cia = c.stage_chunk[sa] * S::CHUNK;
-    load_a<T, V, S::RB, S::ST>(a_fill, idx_a, rows_rsrc, c.c_in, cia, min(S::CHUNK, c.c_in - cia), lk);
+    if (!S::WSKIP || ((c.wmask >> c.stage_k[sa]) & 1u)) {
+        const int cia = c.stage_chunk[sa] * S::CHUNK;
+        load_a<T, V, S::RB, S::ST>(a_fill, idx_a, rows_rsrc, c.c_in, cia, min(S::CHUNK, c.c_in - cia), lk);
+    }
 
     const int k = c.stage_k[s];
     if ((c.wmask >> k) & 1u) {
@@ -455,6 +471,103 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
     __syncthreads();
 }
 
+
+// ---- line-coalesced A through LDS (IgemmShape::ALDS) ----
+//
+// A gather instruction covers 8 consecutive rows of the wave tile with 8
+// lanes per row, so each of its 16-byte lanes lands in one of 8 whole
+// 128-byte lines (one 64-channel fp16 row chunk), instead of 16 rows x 64
+// bytes in the MFMA fragment layout.  Lane l loads row 8h + l/8 of each
+// 16-row block, piece l%8.  The rows go to this wave's LDS buffer with piece
+// p of row r at slot p ^ (r % 8); the MFMA fragment reads (16 rows, one
+// piece each) then spread over distinct banks.  Only the wave reads its own
+// buffer, so no barrier guards it: LDS operations of one wave complete in
+// issue order.
+
+template <int RB>
+__device__ inline void load_rows_coal(int (&idx)[RB][2], const int32_t* __restrict__ kv_map, int rows, int row0,
+                                      int k, int lane) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = min(row0 + rb * 16 + 8 * h + (lane >> 3), rows - 1);
+            idx[rb][h] = kv_map[static_cast<long long>(k) * rows + r];
+        }
+    }
+}
+
+template <typename T, typename V, int RB>
+__device__ inline void load_a_coal(V (&a)[RB][2], const int (&idx)[RB][2], __amdgpu_buffer_rsrc_t rows_rsrc,
+                                   int c_in, int ci_base, int cw, int lane) {
+    const int piece = lane & 7;
+    const int off = piece * 8 < cw ? piece * 8 : 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const unsigned row = static_cast<unsigned>(idx[rb][h]) * static_cast<unsigned>(c_in * sizeof(T));
+            a[rb][h] = __builtin_bit_cast(
+                V, __builtin_amdgcn_raw_buffer_load_b128(rows_rsrc, static_cast<int>(row + (ci_base + off) * sizeof(T)),
+                                                         0, 0));
+        }
+    }
+}
+
+template <typename T, typename V, int RB>
+__device__ inline void store_a_coal(T* abuf, const V (&a)[RB][2], int lane) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = rb * 16 + 8 * h + (lane >> 3);
+            *reinterpret_cast<V*>(abuf + r * 64 + ((lane & 7) ^ (r & 7)) * 8) = a[rb][h];
+        }
+    }
+}
+
+// Stage s of the ALDS pipeline.  `idx_a` holds the row indices of stage
+// s+1, whose gather is issued here and written to the wave's LDS buffer at
+// the end of the stage (after this stage's fragment reads, in issue order);
+// `idx_fill` receives the indices of stage s+2.
+template <typename T, typename S, typename BSource, typename V>
+__device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur, T* bnext, T* abuf,
+                                        __amdgpu_buffer_rsrc_t rows_rsrc, const BSource& bsrc,
+                                        const int32_t* __restrict__ kv_map, const int (&idx_a)[S::RB][2],
+                                        int (&idx_fill)[S::RB][2], float4_t (&acc)[S::RB][S::CB]) {
+    const int lr = c.lane & 15;
+    const int last = c.nstages - 1;
+    const int sb = min(s + 1, last);
+    const int si = min(s + 2, last);
+    load_rows_coal<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], c.lane);
+    V breg[S::B_PIECES];
+    const int cib = c.stage_chunk[sb] * S::CHUNK;
+    stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
+    V areg[S::RB][2];
+    load_a_coal<T, V, S::RB>(areg, idx_a, rows_rsrc, c.c_in, cib, min(S::CHUNK, c.c_in - cib), c.lane);
+
+    const int k = c.stage_k[s];
+    if ((c.wmask >> k) & 1u) {
+        const int nst = min(S::CHUNK, c.c_in - c.stage_chunk[s] * S::CHUNK) / 32;
+        const T* brow = bcur + (c.wc * S::WAVE_COLS + lr) * S::BROW;
+#pragma unroll
+        for (int st = 0; st < S::ST; ++st) {
+            if (st < nst) {
+                V af[S::RB][S::ST];
+                const int slot = ((st * 4 + (c.lane >> 4)) ^ (lr & 7)) * 8;
+#pragma unroll
+                for (int rb = 0; rb < S::RB; ++rb) af[rb][st] = *reinterpret_cast<const V*>(abuf + (rb * 16 + lr) * 64 + slot);
+                V b[S::CB];
+                read_b_step<T, S>(b, brow, st, c.lane, lr);
+                mfma_step<T, S>(acc, af, b, st);
+            }
+        }
+    }
+    stage_b_store<T, S>(bnext, breg);
+    store_a_coal<T, V, S::RB>(abuf, areg, c.lane);
+    __syncthreads();
+}
+
 template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
@@ -469,6 +582,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     T* const bbuf1 = lds + S::BBUF;
     __shared__ unsigned char stage_k[S::MAX_STAGES];
     __shared__ unsigned char stage_chunk[S::MAX_STAGES];
+    __shared__ __align__(16) T alds[S::A_LDS];
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -516,7 +630,37 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     const int lk = (lane >> 4) * 8;
     __syncthreads();
 
-    if (nstages > 0) {
+    if constexpr (S::ALDS) {
+        if (nstages > 0) {
+            const StageCtx ctx{stage_k, stage_chunk, nstages, c_in, rows, row0, wc, lane, wmask};
+            const int last = nstages - 1;
+            T* const abuf = alds + wave * WAVE_ROWS * 64;
+            const __amdgpu_buffer_rsrc_t rows_rsrc = feature_rows(feats, n_in, c_in);
+            int idx[2][S::RB][2];
+            load_rows_coal<S::RB>(idx[0], kv_map, rows, row0, stage_k[0], lane);
+            load_rows_coal<S::RB>(idx[1], kv_map, rows, row0, stage_k[min(1, last)], lane);
+            {
+                V breg[S::B_PIECES];
+                stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
+                V areg[S::RB][2];
+                load_a_coal<T, V, S::RB>(areg, idx[0], rows_rsrc, c_in, 0, min(S::CHUNK, c_in), lane);
+                stage_b_store<T, S>(bbuf0, breg);
+                store_a_coal<T, V, S::RB>(abuf, areg, lane);
+            }
+            __syncthreads();
+            // Stage base + j gathers with idx[(j + 1) % 2] (stage s+1) and
+            // refills idx[j % 2] with stage s+2.
+            for (int base = 0; base < nstages; base += S::UNROLL) {
+#pragma unroll
+                for (int j = 0; j < S::UNROLL; ++j) {
+                    if (base + j >= nstages) break;
+                    igemm_stage_alds<T, S, BSource, V>(base + j, ctx, (j & 1) ? bbuf1 : bbuf0,
+                                                       (j & 1) ? bbuf0 : bbuf1, abuf, rows_rsrc, bsrc, kv_map,
+                                                       idx[(j + 1) & 1], idx[j & 1], acc);
+                }
+            }
+        }
+    } else if (nstages > 0) {
         const StageCtx ctx{stage_k, stage_chunk, nstages, c_in, rows, row0, wc, lane, wmask};
         const int last = nstages - 1;
         // Prologue: B(0) in LDS; A(0) .. A(DEPTH-1) gathered; indices of
@@ -667,30 +811,19 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 #ifdef LATTICE_IGEMM_SWEEP
     if (c_out == 128 && g_igemm_sweep >= 0) {
         switch (g_igemm_sweep) {
-            case 0: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, false);
-            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 2, false);
-            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true);
-            case 3: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, true);
-            case 4: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, true);
-            case 5: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false);
-            case 6: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false);
-            case 7: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, true);
-            case 8: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, true);
-            case 9: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 3, true);
-            case 10: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 3);
-            case 11: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4);
-            case 12: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 3);
-            case 13: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 2);
-            case 14: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true, 3);
-            case 15: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 3, false, 2);
-            case 16: return LATTICE_IGEMM_LAUNCH(128, 16, 4, 64, 1, false, 4);
-            case 17: return LATTICE_IGEMM_LAUNCH(128, 32, 2, 64, 1, false, 6);
-            case 18: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4, 64);
-            case 19: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 5, 64);
-            case 20: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 128, 1, false, 3, 64);
-            case 21: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 4, 64);
-            case 22: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2, 64);
-            case 23: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 2, 64);
+            case 0: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64);
+            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 2, 128, true);
+            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 2, 128, true);
+            case 3: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64);
+            case 4: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 2, 128, true);
+            case 5: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 2, false, 2, 128, true);
+            case 6: return LATTICE_IGEMM_LAUNCH(128, 16, 8, 64, 1, false, 2, 128, true);
+            case 7: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 1, 128, true);
+            case 8: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2);
+            case 9: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, true, 2);
+            case 10: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 2, 128, false, true);
+            case 11: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true, 2, 128, false, true);
+            case 12: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4, 128, false, true);
             default: break;
         }
     }
@@ -701,12 +834,18 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 // c_out = 256 splits the columns over two waves per row group and uses
 // eight waves, so each thread stages four B pieces instead of eight (with
 // eight, the packed-weight variant spills to scratch).
+// c_out 32..128 gather A in whole lines through LDS (ALDS), three blocks
+// per CU for float weights; packed weights need the registers of their
+// dequantisation and run two.
+    constexpr int kAldsOcc = std::is_same<BSource, FloatB<T>>::value ? 3 : 2;
 #define LATTICE_IGEMM_CASE(C)                                                  \
     case C:                                                                    \
         if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(C, 64, 4);   \
-        return LATTICE_IGEMM_LAUNCH(C, 32, 4, (C >= 32 ? 64 : 128));
+        return LATTICE_IGEMM_LAUNCH(C, 32, 4, 64, 1, false, kAldsOcc, 128, false, true);
     switch (c_out) {
-        LATTICE_IGEMM_CASE(16)
+    case 16:
+        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(16, 64, 4);
+        return LATTICE_IGEMM_LAUNCH(16, 32, 4, 128);
         LATTICE_IGEMM_CASE(32)
         LATTICE_IGEMM_CASE(64)
         LATTICE_IGEMM_CASE(128)
