@@ -235,7 +235,7 @@ struct IgemmShape {
     // load) into a per-wave LDS buffer and read the MFMA fragments from
     // there; needs 64-channel stages and one stage of prefetch.
     static constexpr bool ALDS = ALDS_;
-    static constexpr int A_LDS = ALDS_ ? WAVES_ * WAVE_ROWS_ * 64 : 1;  // halves
+    static constexpr int A_LDS = WAVES_ * WAVE_ROWS_ * 64;  // halves, when ALDS
     static constexpr bool WSKIP = WSKIP_;  // gather A only for offsets the wave's own rows use
     static constexpr int OCC = OCC_;
     static constexpr int C_OUT = C_OUT_;
@@ -275,7 +275,9 @@ struct IgemmShape {
     // One LDS array holds the two B buffers and, after the main loop, the
     // epilogue staging of every wave's tile.
     static constexpr int EPI = WAVES * WAVE_ROWS * EROW;
-    static constexpr int LDS_HALVES = 2 * BBUF > EPI ? 2 * BBUF : EPI;
+    // The ALDS A buffers follow the two B buffers; the epilogue reuses all.
+    static constexpr int MAIN_HALVES = 2 * BBUF + (ALDS_ ? A_LDS : 0);
+    static constexpr int LDS_HALVES = MAIN_HALVES > EPI ? MAIN_HALVES : EPI;
 };
 
 template <int PIECES>
@@ -539,12 +541,17 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
     const int last = c.nstages - 1;
     const int sb = min(s + 1, last);
     const int si = min(s + 2, last);
-    load_rows_coal<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], c.lane);
+    if (!S::WSKIP || ((c.wmask >> c.stage_k[si]) & 1u)) {
+        load_rows_coal<S::RB>(idx_fill, kv_map, c.rows, c.row0, c.stage_k[si], c.lane);
+    }
     V breg[S::B_PIECES];
     const int cib = c.stage_chunk[sb] * S::CHUNK;
     stage_b_load<T, S>(bsrc, c.stage_k[sb], cib, min(S::CHUNK, c.c_in - cib), breg);
     V areg[S::RB][2];
-    load_a_coal<T, V, S::RB>(areg, idx_a, rows_rsrc, c.c_in, cib, min(S::CHUNK, c.c_in - cib), c.lane);
+    const bool need_a = !S::WSKIP || ((c.wmask >> c.stage_k[sb]) & 1u);
+    if (need_a) {
+        load_a_coal<T, V, S::RB>(areg, idx_a, rows_rsrc, c.c_in, cib, min(S::CHUNK, c.c_in - cib), c.lane);
+    }
 
     const int k = c.stage_k[s];
     if ((c.wmask >> k) & 1u) {
@@ -564,7 +571,7 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
         }
     }
     stage_b_store<T, S>(bnext, breg);
-    store_a_coal<T, V, S::RB>(abuf, areg, c.lane);
+    if (need_a) store_a_coal<T, V, S::RB>(abuf, areg, c.lane);
     __syncthreads();
 }
 
@@ -582,7 +589,6 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     T* const bbuf1 = lds + S::BBUF;
     __shared__ unsigned char stage_k[S::MAX_STAGES];
     __shared__ unsigned char stage_chunk[S::MAX_STAGES];
-    __shared__ __align__(16) T alds[S::A_LDS];
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -634,7 +640,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         if (nstages > 0) {
             const StageCtx ctx{stage_k, stage_chunk, nstages, c_in, rows, row0, wc, lane, wmask};
             const int last = nstages - 1;
-            T* const abuf = alds + wave * WAVE_ROWS * 64;
+            T* const abuf = lds + 2 * S::BBUF + wave * WAVE_ROWS * 64;
             const __amdgpu_buffer_rsrc_t rows_rsrc = feature_rows(feats, n_in, c_in);
             int idx[2][S::RB][2];
             load_rows_coal<S::RB>(idx[0], kv_map, rows, row0, stage_k[0], lane);
@@ -811,19 +817,13 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 #ifdef LATTICE_IGEMM_SWEEP
     if (c_out == 128 && g_igemm_sweep >= 0) {
         switch (g_igemm_sweep) {
+            // the shape before line-coalesced A
             case 0: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64);
-            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 2, 128, true);
-            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 2, 128, true);
-            case 3: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64);
-            case 4: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 2, false, 2, 128, true);
-            case 5: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 2, false, 2, 128, true);
-            case 6: return LATTICE_IGEMM_LAUNCH(128, 16, 8, 64, 1, false, 2, 128, true);
-            case 7: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 1, 128, true);
-            case 8: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2);
-            case 9: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, true, 2);
-            case 10: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 2, 128, false, true);
-            case 11: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, true, 2, 128, false, true);
-            case 12: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 4, 128, false, true);
+            // line-coalesced A, skipping the offsets the wave does not use
+            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 3, 128, true, true);
+            // line-coalesced A with 256-row tiles
+            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 4, 128, false, true);
+            case 3: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2, 128, false, true);
             default: break;
         }
     }
