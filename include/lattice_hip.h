@@ -156,7 +156,8 @@ int lattice_hip_build_relation_implicit_gemm_view(
     int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Tile-sorted view (core/relations/views.py:467-510): reorder_rows = stable
- * argsort of the single-word row masks; sorted_out_in_map [rows, K];
+ * argsort of the single-word row masks; sorted_out_in_map [rows, K] (may be
+ * NULL: the same values are the transpose of the K-major view);
  * sorted_kv_out_in_map [K, rows]; tile_masks [ceil(rows/64)*4] = OR of the
  * masks of each 16-row quarter of each 64-row tile.  K <= 32. */
 size_t lattice_hip_sorted_view_workspace_bytes(int rows);

@@ -296,11 +296,13 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
 // voxel; the neighbour at offset d sits at window index d + 2 - (v & 1) per
 // axis, picked with selects on the coordinate parities.  The wave's 64 map
 // rows are staged in LDS and written out contiguously.
-__global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
-    constexpr int K = 27;
-    __shared__ int32_t stage[kQueryRows * K];
-    const int lane = lane_id();
-    const long long row0 = static_cast<long long>(blockIdx.x) * kQueryRows;
+constexpr int kK3 = 27;
+
+// Queries the 64 rows row0 .. row0 + 63 (one per lane): stages their map
+// rows in `stage`, writes row_masks, returns the lane's degree (0 past the
+// active rows).  The caller copies `stage` to out_in_map.
+__device__ inline int query_rows_k3(const QueryArgs& a, long long row0, int lane, int32_t* stage) {
+    constexpr int K = kK3;
     const long long row = row0 + lane;
     const int n_active = min(max(*a.out_active, 0), a.out_capacity);
     const bool row_ok = row < a.out_capacity;
@@ -376,16 +378,27 @@ __global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
                     ++degree;
                 }
             }
-    if (row_ok) {
-        a.row_masks[row] = static_cast<int32_t>(mask);
-        if (a.degrees != nullptr) a.degrees[row] = degree;
-    }
-    __syncthreads();
-    const int n = static_cast<int>(min(static_cast<long long>(kQueryRows), a.out_capacity - row0)) * K;
-    int32_t* dst = a.out_in_map + row0 * K;
+    if (row_ok) a.row_masks[row] = static_cast<int32_t>(mask);
+    return row_ok ? degree : 0;
+}
+
+// Copies the staged map rows of row0 .. row0 + 63 to out_in_map.
+__device__ inline void store_map_rows_k3(const QueryArgs& a, long long row0, int lane, const int32_t* stage) {
+    const int n = static_cast<int>(min(static_cast<long long>(kQueryRows), a.out_capacity - row0)) * kK3;
+    int32_t* dst = a.out_in_map + row0 * kK3;
     for (int i = lane; i < n; i += kWave) dst[i] = stage[i];
+}
+
+__global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
+    __shared__ int32_t stage[kQueryRows * kK3];
+    const int lane = lane_id();
+    const long long row0 = static_cast<long long>(blockIdx.x) * kQueryRows;
+    const int degree = query_rows_k3(a, row0, lane, stage);
+    if (a.degrees != nullptr && row0 + lane < a.out_capacity) a.degrees[row0 + lane] = degree;
+    __syncthreads();
+    store_map_rows_k3(a, row0, lane, stage);
     if (a.block_totals != nullptr) {
-        int sum = row_ok ? degree : 0;
+        int sum = degree;
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
         if (lane == 0) a.block_totals[blockIdx.x] = sum;
@@ -955,41 +968,42 @@ namespace lattice {
 namespace {
 
 // Gathers 64 sorted rows of out_in_map per block through LDS: rows are
-// read as contiguous K-int segments, the sorted map is written as one
-// contiguous block and the K-major view as 64-int runs per offset.
+// read as contiguous K-int segments, the K-major view is written as 64-int
+// runs per offset and, when requested (non-null), the row-major sorted map
+// as one contiguous block.
 constexpr int kGatherRows = 64;
 
 __global__ void __launch_bounds__(kThreads)
-gather_sorted(const int32_t* __restrict__ out_in_map, int rows, int K, const int32_t* __restrict__ order,
-              int32_t* __restrict__ sorted_map, int32_t* __restrict__ kv_map) {
+gather_sorted(const int32_t* __restrict__ out_in_map, const int32_t* __restrict__ row_masks, int rows, int K,
+              const int32_t* __restrict__ order, int32_t* __restrict__ sorted_map, int32_t* __restrict__ kv_map,
+              int32_t* __restrict__ tile_masks) {
     __shared__ int32_t tile[kGatherRows * 33];
     __shared__ int32_t src_rows[kGatherRows];
     const int row0 = blockIdx.x * kGatherRows;
     const int n = min(kGatherRows, rows - row0);
-    if (threadIdx.x < n) src_rows[threadIdx.x] = order[row0 + threadIdx.x];
+    if (threadIdx.x < kGatherRows) {
+        // the quarter masks of this 64-row tile: OR of 16 sorted row masks
+        // (rows past the end count as 0)
+        const int src = threadIdx.x < n ? order[row0 + threadIdx.x] : -1;
+        if (threadIdx.x < n) src_rows[threadIdx.x] = src;
+        int m = src >= 0 ? row_masks[src] : 0;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) m |= __shfl_xor(m, off, 16);
+        if ((threadIdx.x & 15) == 0) tile_masks[blockIdx.x * 4 + threadIdx.x / 16] = m;
+    }
     __syncthreads();
     for (int i = threadIdx.x; i < n * K; i += kThreads) {
         const int r = i / K;
         const int k = i - r * K;
         const int v = out_in_map[static_cast<long long>(src_rows[r]) * K + k];
         tile[r * 33 + k] = v;
-        sorted_map[static_cast<long long>(row0) * K + i] = v;
+        if (sorted_map != nullptr) sorted_map[static_cast<long long>(row0) * K + i] = v;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < n * K; i += kThreads) {
         const int k = i / n;
         const int r = i - k * n;
         kv_map[static_cast<long long>(k) * rows + row0 + r] = tile[r * 33 + k];
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-tile_quarter_masks(const int32_t* __restrict__ sorted_keys, int rows, int tiles, int32_t* __restrict__ tile_masks) {
-    for (int w = blockIdx.x * kThreads + threadIdx.x; w < tiles * 4; w += gridDim.x * kThreads) {
-        int acc = 0;
-        const int start = w * 16;
-        for (int r = start; r < start + 16 && r < rows; ++r) acc |= sorted_keys[r];
-        tile_masks[w] = acc;
     }
 }
 
@@ -1015,18 +1029,13 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const int tiles = (rows + 63) / 64;
     if (rows == 0) return LATTICE_OK;
-    int32_t* sorted_keys = ws.take<int32_t>(rows);
-    LATTICE_REQUIRE(sorted_keys, "sorted view workspace too small.");
     // Masks of K < 32 offsets are non-negative and fit in K bits; a 32-bit
     // mask sorts as a signed word, like the reference's int32 argsort.
     const SortKeys keys{row_masks, 1, nullptr, -1, kernel_count == 32};
-    int rc = radix_sort_indices(keys, rows, kernel_count, sorted_keys, reorder_rows, ws, stream);
+    int rc = radix_sort_indices(keys, rows, kernel_count, nullptr, reorder_rows, ws, stream);
     if (rc != LATTICE_OK) return rc;
-    gather_sorted<<<(rows + kGatherRows - 1) / kGatherRows, kThreads, 0, stream>>>(
-        out_in_map, rows, kernel_count, reorder_rows, sorted_out_in_map, sorted_kv_out_in_map);
-    LATTICE_LAUNCH_CHECK();
-    tile_quarter_masks<<<grid_for(tiles * 4, kThreads, 4096), kThreads, 0, stream>>>(sorted_keys, rows, tiles,
-                                                                                    tile_masks);
+    gather_sorted<<<tiles, kThreads, 0, stream>>>(out_in_map, row_masks, rows, kernel_count, reorder_rows,
+                                                  sorted_out_in_map, sorted_kv_out_in_map, tile_masks);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }

@@ -46,7 +46,8 @@ void validate_nonnegative(const Triple& v, const char* name) {
 // Raises when a builder flagged an active coordinate that does not fit the
 // packed key (reads one device word; the only host wait of a build).
 void check_coordinate_range(const at::Tensor& status) {
-    if (status.item<int32_t>() & LATTICE_STATUS_COORD_RANGE) {
+    const int32_t flags = status.item<int32_t>();
+    if (flags & LATTICE_STATUS_COORD_RANGE) {
         throw std::invalid_argument(
             "coordinates exceed the GPU packed-key range: batch must lie in [0, 1022] and x, y, z in "
             "[-131072, 131071].");
@@ -255,14 +256,17 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_sorted_implicit_
     const int rows = static_cast<int>(map.size(0));
     const int K = static_cast<int>(map.size(1));
     at::Tensor reorder = empty_i32({rows}, map);
-    at::Tensor sorted = empty_i32({rows, K}, map);
     at::Tensor kv = empty_i32({K, rows}, map);
     at::Tensor tiles = empty_i32({((rows + 63) / 64) * 4}, map);
     at::Tensor ws = workspace(lattice_hip_sorted_view_workspace_bytes(rows), map);
     check_status(lattice_hip_build_sorted_implicit_gemm_view(ci32(map), ci32(masks), rows, K, i32(reorder),
-                                                             i32(sorted), i32(kv), i32(tiles), ws.data_ptr(),
+                                                             nullptr, i32(kv), i32(tiles), ws.data_ptr(),
                                                              static_cast<size_t>(ws.numel()), current_stream(map)));
-    return {reorder, sorted, kv, tiles};
+    // The row-major sorted map is the transpose of the K-major one: it is
+    // returned as that (non-contiguous) view and copied only by a consumer
+    // that needs contiguous rows, the way the reference's lazy graph leaves
+    // an unused output unevaluated.
+    return {reorder, kv.t(), kv, tiles};
 }
 
 }  // namespace lattice_native
