@@ -35,8 +35,8 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per conv_igemm launch on this workload, from rocprofv3 FETCH_SIZE
 # and WRITE_SIZE passes scaled by a 1 GiB copy's counter readings
-# (profiles/conv_igemm_config3_traffic.md).  Re-measure when the kernel changes.
-CONV_TRAFFIC_BYTES = 1.202e9
+# (profiles/config3_kernel_traffic.md).  Re-measure when the kernel changes.
+CONV_TRAFFIC_BYTES = 1.1997e9
 
 
 def parse_args():
