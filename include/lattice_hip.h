@@ -29,6 +29,9 @@
  *                                    api.cpp:248-281, bindings/convolution.cpp:147-234
  *   sparse_quantized_conv_features   convolution/quantized.cpp:198-268,
  *                                    bindings/convolution.cpp:12-89
+ *   conv input / weight gradients    convolution/primitive.cpp:137-176,
+ *                                    597-680 (the conv primitive's vjp),
+ *                                    cpu/algorithms.cpp:355-481
  */
 #ifndef LATTICE_HIP_H_
 #define LATTICE_HIP_H_
@@ -221,6 +224,56 @@ int lattice_hip_sparse_quantized_conv_features(
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
     const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
     void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Input gradient of the float conv (SparseConvFeaturesInputGrad,
+ * primitive.cpp:192-260, 597-639; cpu/algorithms.cpp:355-410):
+ * grad[in, ci] = sum over the edges of input row `in` in the input-grouped
+ * CSR (in_row_offsets [in_capacity + 1], in_edge_ids) and over co of
+ * cot[out_rows[e], co] * W[kernel_ids[e], ci, co], fp32 accumulator, one
+ * rounding.  cot [out_capacity, c_out]; grad [in_capacity, c_in], both in
+ * `dtype`; rows without edges are zero. */
+int lattice_hip_sparse_conv_input_grad(
+    int dtype, const void* cot, int out_capacity, int c_out,
+    const void* weights, int weight_layout, int kernel_count, int c_in,
+    const int32_t* out_rows, const int32_t* kernel_ids, const int32_t* counts,
+    int edge_capacity, const int32_t* in_row_offsets,
+    const int32_t* in_edge_ids, int in_capacity, void* grad, void* stream);
+
+/* Transposed dense map of a forward or submanifold relation, for the
+ * input gradient on the matrix cores (no counterpart in the reference, whose
+ * Metal route walks the input-grouped CSR): in_out_map [in_capacity, K]
+ * holds the output row of edge (in, out, k) or -1, row_masks
+ * [in_capacity, ceil(K/32)] its offset bits, in the layout of
+ * build_relation_implicit_gemm_view (relations.cpp:498-538).  The sorted
+ * view of this map and the implicit-GEMM conv with the weight transposed to
+ * (C_in, Kx, Ky, Kz, C_out) then give the input gradient.  Requires at most
+ * one output row per (input row, k), which forward and submanifold
+ * relations guarantee. */
+int lattice_hip_build_transposed_implicit_gemm_map(
+    const int32_t* in_rows, const int32_t* out_rows, const int32_t* kernel_ids,
+    const int32_t* counts, int edge_capacity, int in_capacity,
+    int kernel_count, int32_t* in_out_map, int32_t* row_masks, void* stream);
+
+/* Weight gradient of the float conv (SparseConvFeaturesWeightGrad,
+ * primitive.cpp:403-440, 641-680; cpu/algorithms.cpp:413-481):
+ * grad[k, ci, co] = sum over the edges of offset k in the kernel-grouped CSR
+ * (kernel_row_offsets [K + 1], kernel_edge_ids) of
+ * feats[in_rows[e], ci] * cot[out_rows[e], co], fp32 accumulator, one
+ * rounding, written in `weight_layout`.  fp16/bf16 with c_in and c_out
+ * multiples of 8 run on the matrix cores and need the workspace
+ * (lattice_hip_conv_weight_grad_workspace_bytes, 0 for other shapes); the
+ * result is deterministic.  Other shapes take a lane-per-weight kernel. */
+size_t lattice_hip_conv_weight_grad_workspace_bytes(int dtype,
+                                                    int kernel_count,
+                                                    int c_in, int c_out,
+                                                    int edge_capacity);
+int lattice_hip_sparse_conv_weight_grad(
+    int dtype, const void* feats, int n_in, int c_in, const void* cot,
+    int out_capacity, int c_out, int weight_layout, int kernel_count,
+    const int32_t* in_rows, const int32_t* out_rows, const int32_t* counts,
+    int edge_capacity, const int32_t* kernel_row_offsets,
+    const int32_t* kernel_edge_ids, void* grad, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,7 @@ NATIVE = HERE / 'native'
 INCLUDE = REPO / 'include'
 ARCH = 'gfx950'
 
-HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip']
+HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip', 'conv_grad.hip']
 HOST_SOURCES = [
     'native/features/coordinates/relations.cpp',
     'native/features/convolution/api.cpp',

@@ -1,0 +1,441 @@
+// Gradients of the sparse convolution (the reference's vjp:
+// native/features/convolution/primitive.cpp:137-176, 597-680; CPU routines
+// cpu/algorithms.cpp:355-481).
+//
+//  * Input gradient, CSR route: one lane per (input row, input channel)
+//    walks the row's edges in the input-grouped CSR (in_row_offsets /
+//    in_edge_ids) with an fp32 accumulator over the edges and every output
+//    channel, one rounding at the end (eval_input_grad_typed).  Small
+//    weights are staged once per block in LDS as fp32, (k, co, ci) with ci
+//    fastest, so the lanes of a row read consecutive banks.
+//  * Input gradient, matrix-core route: for a forward or submanifold
+//    relation every (input row, k) pair has at most one output row, so the
+//    relation transposes into a dense map in_out_map[in][k] with the same
+//    row masks as the forward's out_in_map.  `transposed_map` scatters it
+//    from the edges; the forward's sorted view and implicit-GEMM kernel then
+//    compute grad[in][ci] = sum_k sum_co cot[map[in][k]][co] * W[k][ci][co]
+//    with the weight transposed to (C_in, K, C_out).
+//  * Weight gradient: dW[k] = sum over the edges of k of
+//    feats[in]^T cot[out] (eval_weight_grad_typed), a contraction over
+//    edges.  The matrix-core kernel splits each k's edges (kernel-grouped
+//    CSR: kernel_row_offsets / kernel_edge_ids) over S blocks per 64 x 64
+//    channel tile; a block stages 32 edges of both operands transposed in
+//    LDS (channel-major, so an MFMA fragment is 8 consecutive edges) and
+//    accumulates in fp32.  Each split writes its partial tile; a second
+//    kernel sums the S partials in split order and rounds once, so results
+//    are deterministic.  Other dtypes and shapes take a one-lane-per-weight
+//    kernel.
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "lattice_common.h"
+#include "scan.h"
+
+namespace lattice {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> __device__ inline float to_f(T v) { return static_cast<float>(v); }
+
+struct GradWeightIndex {
+    int layout;  // LATTICE_WEIGHT_*
+    int K, c_in, c_out;
+    __device__ inline long long operator()(int k, int ci, int co) const {
+        if (layout == LATTICE_WEIGHT_KERNEL_MAJOR) return (static_cast<long long>(k) * c_in + ci) * c_out + co;
+        return (static_cast<long long>(co) * K + k) * c_in + ci;
+    }
+};
+
+constexpr int kGradLdsFloats = 16384;
+constexpr unsigned kGradStagedBlocks = 2048;
+
+// ------------------------------------------------- input gradient (CSR) --
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+input_grad_csr(const T* __restrict__ cot, int out_capacity, const T* __restrict__ weights, GradWeightIndex widx,
+               const int32_t* __restrict__ out_rows, const int32_t* __restrict__ kernel_ids,
+               const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ in_row_offsets,
+               const int32_t* __restrict__ in_edge_ids, int in_capacity, T* __restrict__ grad, bool staged) {
+    extern __shared__ float wlds[];
+    const int c_in = widx.c_in;
+    const int c_out = widx.c_out;
+    if (staged) {
+        const int nw = widx.K * c_in * c_out;
+        for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+            const int ci = i % c_in;
+            const int kc = i / c_in;  // k * c_out + co
+            wlds[i] = to_f(weights[widx(kc / c_out, ci, kc % c_out)]);
+        }
+        __syncthreads();
+    }
+    const int E = min(counts[0], edge_capacity);
+    const long long total = static_cast<long long>(in_capacity) * c_in;
+    for (long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int row = static_cast<int>(t / c_in);
+        const int ci = static_cast<int>(t - static_cast<long long>(row) * c_in);
+        float acc = 0.0f;
+        const int end = in_row_offsets[row + 1];
+        for (int cur = in_row_offsets[row]; cur < end; ++cur) {
+            const int e = in_edge_ids[cur];
+            if (e < 0 || e >= E) continue;
+            const int o = out_rows[e];
+            const int k = kernel_ids[e];
+            if (o < 0 || o >= out_capacity || k < 0 || k >= widx.K) continue;
+            const T* g = cot + static_cast<long long>(o) * c_out;
+            if (staged) {
+                const float* wk = wlds + static_cast<long long>(k) * c_out * c_in + ci;
+                for (int co = 0; co < c_out; ++co) acc += to_f(g[co]) * wk[co * c_in];
+            } else {
+                for (int co = 0; co < c_out; ++co) acc += to_f(g[co]) * to_f(weights[widx(k, ci, co)]);
+            }
+        }
+        grad[t] = static_cast<T>(acc);
+    }
+}
+
+// ---------------------------------------- transposed map (matrix cores) --
+
+__global__ void __launch_bounds__(256)
+transposed_map(const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
+               const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
+               int in_capacity, int K, int words, int32_t* __restrict__ in_out_map,
+               int32_t* __restrict__ row_masks) {
+    const int E = min(counts[0], edge_capacity);
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
+        const int in = in_rows[e];
+        const int o = out_rows[e];
+        const int k = kernel_ids[e];
+        if (in < 0 || in >= in_capacity || o < 0 || k < 0 || k >= K) continue;
+        in_out_map[static_cast<long long>(in) * K + k] = o;
+        atomicOr(reinterpret_cast<unsigned*>(row_masks) + static_cast<long long>(in) * words + (k >> 5),
+                 1u << (k & 31));
+    }
+}
+
+// --------------------------------------- weight gradient (matrix cores) --
+
+template <typename T> struct GradMfma;
+template <> struct GradMfma<_Float16> {
+    typedef half8_t vec;
+    __device__ static float4_t mfma(vec a, vec b, float4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct GradMfma<__bf16> {
+    typedef bf16x8_t vec;
+    __device__ static float4_t mfma(vec a, vec b, float4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+constexpr int kWgTile = 64;    // channels per tile side
+constexpr int kWgEdges = 32;   // edges per MFMA step
+constexpr int kWgRow = 40;     // LDS row stride in elements (32 edges + 8 pad: conflict-free fragment reads)
+
+// Block (tile_ci * tiles_co + tile_co, k, split): channel tile 64 x 64,
+// four waves of 32 x 32.  Thread t stages edge t/8, 8-channel piece t%8 of
+// both operands per step.
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ cot, int n_out, int c_out,
+                 const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
+                 const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
+                 const int32_t* __restrict__ kedges, int splits, int tiles_co, float* __restrict__ partial) {
+    using V = typename GradMfma<T>::vec;
+    __shared__ __align__(16) T a_t[kWgTile * kWgRow];
+    __shared__ __align__(16) T b_t[kWgTile * kWgRow];
+    const int K = gridDim.y;
+    const int k = blockIdx.y;
+    const int s = blockIdx.z;
+    const int ci0 = (blockIdx.x / tiles_co) * kWgTile;
+    const int co0 = (blockIdx.x % tiles_co) * kWgTile;
+    const int E = min(counts[0], edge_capacity);
+    const int lo_k = koff[k];
+    const int n_k = koff[k + 1] - lo_k;
+    const int lo = lo_k + static_cast<int>(static_cast<long long>(n_k) * s / splits);
+    const int hi = lo_k + static_cast<int>(static_cast<long long>(n_k) * (s + 1) / splits);
+
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave & 1;
+    const int wn = wave >> 1;
+    const int lr = lane & 15;
+    const int g = lane >> 4;
+    const int j = threadIdx.x >> 3;  // edge within the step
+    const int p = threadIdx.x & 7;   // 8-channel piece
+    float4_t acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int base = lo; base < hi; base += kWgEdges) {
+        V av{}, bv{};
+        const int cur = base + j;
+        if (cur < hi) {
+            const int e = kedges[cur];
+            if (e >= 0 && e < E) {
+                const int in = in_rows[e];
+                const int o = out_rows[e];
+                if (in >= 0 && in < n_in && o >= 0 && o < n_out) {
+                    if (ci0 + 8 * p < c_in)
+                        av = *reinterpret_cast<const V*>(feats + static_cast<long long>(in) * c_in + ci0 + 8 * p);
+                    if (co0 + 8 * p < c_out)
+                        bv = *reinterpret_cast<const V*>(cot + static_cast<long long>(o) * c_out + co0 + 8 * p);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            a_t[(8 * p + c) * kWgRow + j] = av[c];
+            b_t[(8 * p + c) * kWgRow + j] = bv[c];
+        }
+        __syncthreads();
+        V af[2], bf[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            af[m] = *reinterpret_cast<const V*>(a_t + (32 * wm + 16 * m + lr) * kWgRow + 8 * g);
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+            bf[n] = *reinterpret_cast<const V*>(b_t + (32 * wn + 16 * n + lr) * kWgRow + 8 * g);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int n = 0; n < 2; ++n) acc[m][n] = GradMfma<T>::mfma(af[m], bf[n], acc[m][n]);
+        __syncthreads();
+    }
+    // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
+    float* out = partial + (static_cast<long long>(s) * K + k) * c_in * c_out;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int ci = ci0 + 32 * wm + 16 * m + 4 * g + q;
+                const int co = co0 + 32 * wn + 16 * n + lr;
+                if (ci < c_in && co < c_out) out[static_cast<long long>(ci) * c_out + co] = acc[m][n][q];
+            }
+}
+
+// Sum of the split partials in split order, one rounding, written in the
+// weight's layout.
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_grad_reduce(const float* __restrict__ partial, int splits, GradWeightIndex widx, T* __restrict__ grad) {
+    const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < per;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        float acc = 0.0f;
+        for (int s = 0; s < splits; ++s) acc += partial[s * per + i];
+        const int co = static_cast<int>(i % widx.c_out);
+        const long long kc = i / widx.c_out;
+        grad[widx(static_cast<int>(kc / widx.c_in), static_cast<int>(kc % widx.c_in), co)] = static_cast<T>(acc);
+    }
+}
+
+// One lane per weight entry (k, ci, co), co fastest: the kernel-grouped
+// edges of k in order with an fp32 accumulator (eval_weight_grad_typed's
+// loop).  Used for fp32 and for channel counts the matrix-core kernel does
+// not take.
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_grad_simple(const T* __restrict__ feats, int n_in, const T* __restrict__ cot, int n_out,
+                   const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
+                   const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
+                   const int32_t* __restrict__ kedges, GradWeightIndex widx, T* __restrict__ grad) {
+    const int c_in = widx.c_in;
+    const int c_out = widx.c_out;
+    const int E = min(counts[0], edge_capacity);
+    const long long total = static_cast<long long>(widx.K) * c_in * c_out;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int co = static_cast<int>(i % c_out);
+        const int ci = static_cast<int>((i / c_out) % c_in);
+        const int k = static_cast<int>(i / (static_cast<long long>(c_in) * c_out));
+        float acc = 0.0f;
+        for (int cur = koff[k]; cur < koff[k + 1]; ++cur) {
+            const int e = kedges[cur];
+            if (e < 0 || e >= E) continue;
+            const int in = in_rows[e];
+            const int o = out_rows[e];
+            if (in < 0 || in >= n_in || o < 0 || o >= n_out) continue;
+            acc += to_f(feats[static_cast<long long>(in) * c_in + ci]) * to_f(cot[static_cast<long long>(o) * c_out + co]);
+        }
+        grad[widx(k, ci, co)] = static_cast<T>(acc);
+    }
+}
+
+int check_grad_dtype(int dtype) {
+    LATTICE_REQUIRE(dtype == LATTICE_F32 || dtype == LATTICE_F16 || dtype == LATTICE_BF16,
+                    "convolution gradients support float32, float16 and bfloat16.");
+    return LATTICE_OK;
+}
+
+// Splits of each kernel offset's edges for the matrix-core weight gradient.
+int weight_grad_splits(int edge_capacity, int kernel_count) {
+    const long long per_k = std::max(1LL, static_cast<long long>(edge_capacity) / std::max(kernel_count, 1));
+    return static_cast<int>(std::min<long long>(64, std::max<long long>(1, per_k / 4096)));
+}
+
+bool weight_grad_mfma_ok(int dtype, int c_in, int c_out) {
+    return (dtype == LATTICE_F16 || dtype == LATTICE_BF16) && c_in % 8 == 0 && c_out % 8 == 0;
+}
+
+template <typename T>
+void launch_input_grad(const void* cot, int out_capacity, const void* weights, GradWeightIndex widx,
+                       const int32_t* out_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
+                       const int32_t* in_row_offsets, const int32_t* in_edge_ids, int in_capacity, void* grad,
+                       hipStream_t stream) {
+    const long long nw = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
+    const bool staged = nw <= kGradLdsFloats;
+    const unsigned grid = grid_for(static_cast<long long>(in_capacity) * widx.c_in, 256,
+                                   staged ? kGradStagedBlocks : 1u << 16);
+    input_grad_csr<T><<<grid, 256, staged ? nw * sizeof(float) : 0, stream>>>(
+        static_cast<const T*>(cot), out_capacity, static_cast<const T*>(weights), widx, out_rows, kernel_ids, counts,
+        edge_capacity, in_row_offsets, in_edge_ids, in_capacity, static_cast<T*>(grad), staged);
+}
+
+template <typename T>
+int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, int n_out, GradWeightIndex widx,
+                       const int32_t* in_rows, const int32_t* out_rows, const int32_t* counts, int edge_capacity,
+                       const int32_t* koff, const int32_t* kedges, void* grad, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+    if (weight_grad_mfma_ok(dtype, widx.c_in, widx.c_out) && workspace != nullptr) {
+        if constexpr (!std::is_same<T, float>::value) {
+            const int splits = weight_grad_splits(edge_capacity, widx.K);
+            const size_t need = static_cast<size_t>(splits) * widx.K * widx.c_in * widx.c_out * sizeof(float);
+            LATTICE_REQUIRE(workspace_bytes >= need, "weight gradient workspace too small.");
+            const int tiles_ci = (widx.c_in + kWgTile - 1) / kWgTile;
+            const int tiles_co = (widx.c_out + kWgTile - 1) / kWgTile;
+            dim3 grid(static_cast<unsigned>(tiles_ci * tiles_co), static_cast<unsigned>(widx.K),
+                      static_cast<unsigned>(splits));
+            float* partial = static_cast<float*>(workspace);
+            weight_grad_mfma<T><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,
+                                                          static_cast<const T*>(cot), n_out, widx.c_out, in_rows,
+                                                          out_rows, counts, edge_capacity, koff, kedges, splits,
+                                                          tiles_co, partial);
+            LATTICE_LAUNCH_CHECK();
+            const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
+            weight_grad_reduce<T><<<grid_for(per, 256, 4096), 256, 0, stream>>>(partial, splits, widx,
+                                                                              static_cast<T*>(grad));
+            LATTICE_LAUNCH_CHECK();
+            return LATTICE_OK;
+        }
+    }
+    const long long total = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
+    weight_grad_simple<T><<<grid_for(total, 256, 1u << 16), 256, 0, stream>>>(
+        static_cast<const T*>(feats), n_in, static_cast<const T*>(cot), n_out, in_rows, out_rows, counts,
+        edge_capacity, koff, kedges, widx, static_cast<T*>(grad));
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+}  // namespace
+}  // namespace lattice
+
+using namespace lattice;
+
+extern "C" int lattice_hip_sparse_conv_input_grad(int dtype, const void* cot, int out_capacity, int c_out,
+                                                  const void* weights, int weight_layout, int kernel_count, int c_in,
+                                                  const int32_t* out_rows, const int32_t* kernel_ids,
+                                                  const int32_t* counts, int edge_capacity,
+                                                  const int32_t* in_row_offsets, const int32_t* in_edge_ids,
+                                                  int in_capacity, void* grad, void* stream_ptr) {
+    int rc = check_grad_dtype(dtype);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(out_capacity >= 0 && in_capacity >= 0 && c_in > 0 && c_out > 0 && kernel_count > 0,
+                    "gradient shapes must be positive.");
+    LATTICE_REQUIRE(weight_layout == LATTICE_WEIGHT_KERNEL_MAJOR || weight_layout == LATTICE_WEIGHT_DENSE_5D,
+                    "weights must have shape (K, C_in, C_out) or (C_out, Kx, Ky, Kz, C_in).");
+    if (in_capacity == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(weights && out_rows && kernel_ids && counts && in_row_offsets && in_edge_ids && grad &&
+                        (cot || out_capacity == 0),
+                    "gradient pointers must be non-null.");
+    hipStream_t stream = as_stream(stream_ptr);
+    GradWeightIndex widx{weight_layout, kernel_count, c_in, c_out};
+    if (dtype == LATTICE_F32) {
+        launch_input_grad<float>(cot, out_capacity, weights, widx, out_rows, kernel_ids, counts, edge_capacity,
+                                 in_row_offsets, in_edge_ids, in_capacity, grad, stream);
+    } else if (dtype == LATTICE_F16) {
+        launch_input_grad<_Float16>(cot, out_capacity, weights, widx, out_rows, kernel_ids, counts, edge_capacity,
+                                    in_row_offsets, in_edge_ids, in_capacity, grad, stream);
+    } else {
+        launch_input_grad<__bf16>(cot, out_capacity, weights, widx, out_rows, kernel_ids, counts, edge_capacity,
+                                  in_row_offsets, in_edge_ids, in_capacity, grad, stream);
+    }
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_rows, const int32_t* out_rows,
+                                                             const int32_t* kernel_ids, const int32_t* counts,
+                                                             int edge_capacity, int in_capacity, int kernel_count,
+                                                             int32_t* in_out_map, int32_t* row_masks,
+                                                             void* stream_ptr) {
+    LATTICE_REQUIRE(edge_capacity >= 0 && in_capacity >= 0 && kernel_count > 0,
+                    "transposed map shapes must be nonnegative with a positive kernel count.");
+    if (in_capacity == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(in_out_map && row_masks && counts && (edge_capacity == 0 || (in_rows && out_rows && kernel_ids)),
+                    "transposed map pointers must be non-null.");
+    hipStream_t stream = as_stream(stream_ptr);
+    const int words = (kernel_count + 31) / 32;
+    int rc = fill_i32(in_out_map, static_cast<long long>(in_capacity) * kernel_count, -1, stream);
+    if (rc != LATTICE_OK) return rc;
+    rc = fill_i32(row_masks, static_cast<long long>(in_capacity) * words, 0, stream);
+    if (rc != LATTICE_OK) return rc;
+    if (edge_capacity == 0) return LATTICE_OK;
+    transposed_map<<<grid_for(edge_capacity, 256, 1u << 16), 256, 0, stream>>>(
+        in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, words, in_out_map,
+        row_masks);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" size_t lattice_hip_conv_weight_grad_workspace_bytes(int dtype, int kernel_count, int c_in, int c_out,
+                                                                int edge_capacity) {
+    if (!weight_grad_mfma_ok(dtype, c_in, c_out) || kernel_count <= 0) return 0;
+    return static_cast<size_t>(weight_grad_splits(edge_capacity, kernel_count)) * kernel_count * c_in * c_out *
+           sizeof(float);
+}
+
+extern "C" int lattice_hip_sparse_conv_weight_grad(int dtype, const void* feats, int n_in, int c_in, const void* cot,
+                                                   int out_capacity, int c_out, int weight_layout, int kernel_count,
+                                                   const int32_t* in_rows, const int32_t* out_rows,
+                                                   const int32_t* counts, int edge_capacity,
+                                                   const int32_t* kernel_row_offsets,
+                                                   const int32_t* kernel_edge_ids, void* grad, void* workspace,
+                                                   size_t workspace_bytes, void* stream_ptr) {
+    int rc = check_grad_dtype(dtype);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(n_in >= 0 && out_capacity >= 0 && c_in > 0 && c_out > 0 && kernel_count > 0,
+                    "gradient shapes must be positive.");
+    LATTICE_REQUIRE(weight_layout == LATTICE_WEIGHT_KERNEL_MAJOR || weight_layout == LATTICE_WEIGHT_DENSE_5D,
+                    "weights must have shape (K, C_in, C_out) or (C_out, Kx, Ky, Kz, C_in).");
+    LATTICE_REQUIRE(grad && counts && kernel_row_offsets && (edge_capacity == 0 || (in_rows && out_rows && kernel_edge_ids)),
+                    "gradient pointers must be non-null.");
+    hipStream_t stream = as_stream(stream_ptr);
+    GradWeightIndex widx{weight_layout, kernel_count, c_in, c_out};
+    if (dtype == LATTICE_F32) {
+        return launch_weight_grad<float>(dtype, feats, n_in, cot, out_capacity, widx, in_rows, out_rows, counts,
+                                         edge_capacity, kernel_row_offsets, kernel_edge_ids, grad, workspace,
+                                         workspace_bytes, stream);
+    }
+    if (dtype == LATTICE_F16) {
+        return launch_weight_grad<_Float16>(dtype, feats, n_in, cot, out_capacity, widx, in_rows, out_rows, counts,
+                                            edge_capacity, kernel_row_offsets, kernel_edge_ids, grad, workspace,
+                                            workspace_bytes, stream);
+    }
+    return launch_weight_grad<__bf16>(dtype, feats, n_in, cot, out_capacity, widx, in_rows, out_rows, counts,
+                                      edge_capacity, kernel_row_offsets, kernel_edge_ids, grad, workspace,
+                                      workspace_bytes, stream);
+}

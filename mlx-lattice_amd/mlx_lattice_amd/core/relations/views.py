@@ -190,6 +190,7 @@ class KernelRelation:
     _grouped_views: Callable[[], tuple] | None
     implicit_gemm: RelationImplicitGemmView | None = None
     sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
+    transposed_sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
 
     def __init__(
         self,
@@ -282,6 +283,7 @@ class KernelRelation:
                            grouped_views if lazy_views else None)
         object.__setattr__(self, 'implicit_gemm', implicit_gemm)
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
+        object.__setattr__(self, 'transposed_sorted_implicit_gemm', None)
 
     @property
     def input_csr(self) -> RelationCSRView:
@@ -409,6 +411,37 @@ class KernelRelation:
             reorder_rows=reorder, tile_masks=tiles)
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_view)
         return sorted_view
+
+    def require_transposed_sorted_implicit_gemm(
+            self) -> RelationSortedImplicitGemmView:
+        """Mask-sorted view of the transposed relation (input row -> output
+        row per offset), built on first use and cached: the matrix-core
+        route of the input gradient runs the forward's implicit GEMM over
+        it.  Forward and submanifold relations have at most one output row
+        per (input row, offset), so the transposed map is dense; target
+        relations (whose target may repeat a coordinate) are refused."""
+        if self.transposed_sorted_implicit_gemm is not None:
+            return self.transposed_sorted_implicit_gemm
+        if self.contract.kind not in ('forward', 'submanifold'):
+            raise ValueError('the transposed implicit-GEMM view needs a '
+                             'forward or submanifold relation.')
+        if self.n_in_capacity is None or self.n_kernels is None:
+            raise ValueError('kernel relation is missing static shape metadata.')
+        if self.n_kernels > 32:
+            raise ValueError(
+                'sorted implicit GEMM view currently supports K <= 32.')
+        from mlx_lattice_amd._native import ext
+
+        in_out_map, row_masks = ext.build_transposed_implicit_gemm_map(
+            self.edges.in_rows, self.edges.out_rows, self.edges.kernel_ids,
+            self.counts, int(self.n_in_capacity), int(self.n_kernels))
+        reorder, sorted_map, kv_map, tiles = ext.build_sorted_implicit_gemm_view(
+            in_out_map, row_masks)
+        view = RelationSortedImplicitGemmView(
+            sorted_out_in_map=sorted_map, sorted_kv_out_in_map=kv_map,
+            reorder_rows=reorder, tile_masks=tiles)
+        object.__setattr__(self, 'transposed_sorted_implicit_gemm', view)
+        return view
 
 
 # ---------------------------------------------------------------- helpers --

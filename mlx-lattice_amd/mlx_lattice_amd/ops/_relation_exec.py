@@ -50,8 +50,106 @@ def sparse_conv_features_from_relation(feats: torch.Tensor,
                                        relation: KernelRelation,
                                        ) -> torch.Tensor:
     """Execute sparse convolution over a prebuilt relation
-    (_relation_exec.py:84-116)."""
+    (_relation_exec.py:84-116).  Differentiable in ``feats`` and ``weight``:
+    the backward pass is the reference primitive's vjp
+    (native/features/convolution/primitive.cpp:137-176)."""
     _require_static(relation)
+    if torch.is_grad_enabled() and (feats.requires_grad
+                                    or weight.requires_grad):
+        return _SparseConvFeatures.apply(feats, weight, relation)
+    return _conv_features(feats, weight, relation)
+
+
+class _SparseConvFeatures(torch.autograd.Function):
+    """Sparse conv features with the reference's gradients: the input
+    gradient over the input-grouped CSR and the weight gradient over the
+    kernel-grouped CSR (cpu/algorithms.cpp:355-481)."""
+
+    @staticmethod
+    def forward(ctx, feats, weight, relation):
+        ctx.relation = relation
+        ctx.save_for_backward(feats, weight)
+        return _conv_features(feats, weight, relation)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        feats, weight = ctx.saved_tensors
+        relation = ctx.relation
+        grad_out = grad_out.contiguous()
+        grad_feats = grad_weight = None
+        if ctx.needs_input_grad[0]:
+            grad_feats = sparse_conv_input_grad_from_relation(
+                grad_out, weight, relation, int(feats.shape[0]))
+        if ctx.needs_input_grad[1]:
+            grad_weight = sparse_conv_weight_grad_from_relation(
+                feats, grad_out, weight, relation)
+        return grad_feats, grad_weight, None
+
+
+def _input_grad_matrix_core_eligible(cot: torch.Tensor, weight: torch.Tensor,
+                                     relation: KernelRelation) -> bool:
+    """The input gradient is the forward's implicit GEMM over the
+    transposed relation: its contraction runs over C_out and it writes C_in
+    columns."""
+    c_in = int(weight.shape[1] if weight.ndim == 3 else weight.shape[4])
+    c_out = int(cot.shape[1])
+    return (relation.contract.kind in ('forward', 'submanifold')
+            and cot.dtype in (torch.float16, torch.bfloat16)
+            and c_out % 32 == 0 and c_out <= 512
+            and c_in in _MATRIX_CORE_C_OUT
+            and relation.n_kernels is not None and relation.n_kernels <= 32
+            and int(cot.shape[0]) * c_out * 2 < 2 ** 31)
+
+
+def _transposed_weight(weight: torch.Tensor) -> torch.Tensor:
+    """(C_out, Kx, Ky, Kz, C_in) or (K, C_in, C_out) -> the 5D weight of the
+    transposed conv, (C_in, Kx, Ky, Kz, C_out)."""
+    if weight.ndim == 5:
+        return weight.permute(4, 1, 2, 3, 0).contiguous()
+    k, c_in, c_out = weight.shape
+    return weight.permute(1, 0, 2).contiguous().reshape(c_in, k, 1, 1, c_out)
+
+
+def sparse_conv_input_grad_from_relation(cot: torch.Tensor,
+                                         weight: torch.Tensor,
+                                         relation: KernelRelation,
+                                         in_capacity: int) -> torch.Tensor:
+    """Input gradient ``(in_capacity, C_in)`` (make_sparse_conv_features_
+    input_grad, primitive.cpp:597-639): on the matrix cores over the
+    transposed sorted view when the shapes allow, otherwise over the
+    input-grouped CSR."""
+    _require_static(relation)
+    if _input_grad_matrix_core_eligible(cot, weight, relation):
+        view = relation.require_transposed_sorted_implicit_gemm()
+        return ext.sparse_conv_features_sorted_implicit_gemm(
+            cot, _transposed_weight(weight), view.sorted_out_in_map,
+            view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
+            None, None, None, None, None, None, None, None, None,
+            in_capacity, relation.n_kernels)
+    input_csr = relation.input_csr
+    return ext.sparse_conv_input_grad(
+        cot, weight, relation.edges.out_rows, relation.edges.kernel_ids,
+        relation.counts, input_csr.row_offsets, input_csr.edge_ids,
+        in_capacity, relation.n_kernels)
+
+
+def sparse_conv_weight_grad_from_relation(feats: torch.Tensor,
+                                          cot: torch.Tensor,
+                                          weight: torch.Tensor,
+                                          relation: KernelRelation,
+                                          ) -> torch.Tensor:
+    """Weight gradient in ``weight``'s shape (make_sparse_conv_features_
+    weight_grad, primitive.cpp:641-680) over the kernel-grouped CSR."""
+    _require_static(relation)
+    kernel_csr = relation.kernel_csr
+    return ext.sparse_conv_weight_grad(
+        feats, cot, weight, relation.edges.in_rows, relation.edges.out_rows,
+        relation.counts, kernel_csr.row_offsets, kernel_csr.edge_ids,
+        relation.n_kernels)
+
+
+def _conv_features(feats: torch.Tensor, weight: torch.Tensor,
+                   relation: KernelRelation) -> torch.Tensor:
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
     if feats.ndim == 2 and _matrix_core_eligible(
             feats.dtype, int(feats.shape[1]), c_out, relation,

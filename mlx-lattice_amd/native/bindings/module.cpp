@@ -169,4 +169,23 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("out_capacity"), py::arg("n_kernels"),
           py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"), py::arg("group_size"),
           py::arg("bits"));
+
+    m.def("sparse_conv_input_grad", &ln::sparse_conv_input_grad, py::arg("cotangent"), py::arg("weights"),
+          py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("in_row_offsets"),
+          py::arg("in_edge_ids"), py::arg("in_capacity"), py::arg("n_kernels"),
+          "Input gradient of the sparse conv over the input-grouped CSR: (in_capacity, C_in).");
+    m.def(
+        "build_transposed_implicit_gemm_map",
+        [](const at::Tensor& in_rows, const at::Tensor& out_rows, const at::Tensor& kernel_ids,
+           const at::Tensor& counts, int in_capacity, int n_kernels) {
+            auto r = ln::build_transposed_implicit_gemm_map(in_rows, out_rows, kernel_ids, counts, in_capacity,
+                                                            n_kernels);
+            return py::make_tuple(std::get<0>(r), std::get<1>(r));
+        },
+        py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("in_capacity"),
+        py::arg("n_kernels"), "Return (in_out_map, row_masks) of a forward or submanifold relation.");
+    m.def("sparse_conv_weight_grad", &ln::sparse_conv_weight_grad, py::arg("feats"), py::arg("cotangent"),
+          py::arg("weights"), py::arg("in_rows"), py::arg("out_rows"), py::arg("counts"),
+          py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("n_kernels"),
+          "Weight gradient of the sparse conv over the kernel-grouped CSR, in the layout of `weights`.");
 }

@@ -243,4 +243,118 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
     return out;
 }
 
+at::Tensor sparse_conv_input_grad(const at::Tensor& cot_in, const at::Tensor& weights_in, const at::Tensor& out_rows,
+                                  const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                  const at::Tensor& in_row_offsets, const at::Tensor& in_edge_ids, int in_capacity,
+                                  int n_kernels) {
+    const char* op = "sparse_conv_input_grad";
+    if (cot_in.dim() != 2) throw std::invalid_argument("cotangent must have shape (N_out, C_out).");
+    if (weights_in.dim() != 3 && weights_in.dim() != 5) {
+        throw std::invalid_argument("weights must have shape (K, C_in, C_out) or (C_out, Kx, Ky, Kz, C_in).");
+    }
+    const int64_t c_out = out_channels_of(weights_in);
+    const int64_t c_in = weights_in.dim() == 3 ? weights_in.size(1) : weights_in.size(4);
+    if (cot_in.size(1) != c_out) throw std::invalid_argument("cotangent channels must match weights output channels.");
+    if (weights_in.scalar_type() != cot_in.scalar_type()) {
+        throw std::invalid_argument(std::string(op) + " weights must match the cotangent dtype.");
+    }
+    if (in_capacity < 0 || n_kernels <= 0) {
+        throw std::invalid_argument("in_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    require_i32_vector(out_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(kernel_ids, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(in_row_offsets, "plan row_offsets must be one-dimensional int32 arrays.");
+    require_i32_vector(in_edge_ids, "plan edge_ids must be one-dimensional int32 arrays.");
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("counts must have shape (2,) and int32 dtype.");
+    }
+    if (in_row_offsets.size(0) != in_capacity + 1) {
+        throw std::invalid_argument("in_row_offsets length must match input capacity + 1.");
+    }
+    if (out_rows.size(0) != kernel_ids.size(0) || in_edge_ids.size(0) != out_rows.size(0)) {
+        throw std::invalid_argument("plan edge_ids must match relation edge capacity.");
+    }
+    require_device(cot_in, "cotangent");
+    require_device(weights_in, "weights");
+    const at::Tensor cot = cot_in.contiguous();
+    const at::Tensor weights = weights_in.contiguous();
+    at::Tensor grad = at::empty({in_capacity, c_in}, cot.options());
+    check_status(lattice_hip_sparse_conv_input_grad(
+        dtype_code(cot, op), cot.data_ptr(), static_cast<int>(cot.size(0)), static_cast<int>(c_out),
+        weights.data_ptr(), weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D, n_kernels,
+        static_cast<int>(c_in), ci32(out_rows), ci32(kernel_ids), ci32(counts), static_cast<int>(out_rows.size(0)),
+        ci32(in_row_offsets), ci32(in_edge_ids), in_capacity, grad.data_ptr(), current_stream(cot)));
+    return grad;
+}
+
+std::tuple<at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
+                                                                      const at::Tensor& out_rows,
+                                                                      const at::Tensor& kernel_ids,
+                                                                      const at::Tensor& counts, int in_capacity,
+                                                                      int n_kernels) {
+    require_i32_vector(in_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(out_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(kernel_ids, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    if (in_rows.size(0) != out_rows.size(0) || in_rows.size(0) != kernel_ids.size(0)) {
+        throw std::invalid_argument("relation row arrays and kernel_ids must have equal capacity.");
+    }
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("counts must have shape (2,) and int32 dtype.");
+    }
+    if (in_capacity < 0 || n_kernels <= 0) {
+        throw std::invalid_argument("in_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    require_device(in_rows, "in_rows");
+    at::Tensor map = empty_i32({in_capacity, n_kernels}, in_rows);
+    at::Tensor masks = empty_i32({in_capacity, (n_kernels + 31) / 32}, in_rows);
+    check_status(lattice_hip_build_transposed_implicit_gemm_map(
+        ci32(in_rows), ci32(out_rows), ci32(kernel_ids), ci32(counts), static_cast<int>(in_rows.size(0)),
+        in_capacity, n_kernels, i32(map), i32(masks), current_stream(in_rows)));
+    return {map, masks};
+}
+
+at::Tensor sparse_conv_weight_grad(const at::Tensor& feats_in, const at::Tensor& cot_in, const at::Tensor& weights,
+                                   const at::Tensor& in_rows, const at::Tensor& out_rows, const at::Tensor& counts,
+                                   const at::Tensor& kernel_row_offsets, const at::Tensor& kernel_edge_ids,
+                                   int n_kernels) {
+    const char* op = "sparse_conv_weight_grad";
+    validate_weights(feats_in, weights, n_kernels, op);
+    const int64_t c_out = out_channels_of(weights);
+    if (cot_in.dim() != 2 || cot_in.size(1) != c_out) {
+        throw std::invalid_argument("cotangent must have shape (N_out, C_out).");
+    }
+    if (cot_in.scalar_type() != feats_in.scalar_type()) {
+        throw std::invalid_argument(std::string(op) + " cotangent must match feats dtype.");
+    }
+    require_i32_vector(in_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(out_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(kernel_row_offsets, "plan row_offsets must be one-dimensional int32 arrays.");
+    require_i32_vector(kernel_edge_ids, "plan edge_ids must be one-dimensional int32 arrays.");
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("counts must have shape (2,) and int32 dtype.");
+    }
+    if (kernel_row_offsets.size(0) != n_kernels + 1) {
+        throw std::invalid_argument("kernel_row_offsets length must match n_kernels + 1.");
+    }
+    if (in_rows.size(0) != out_rows.size(0) || kernel_edge_ids.size(0) != in_rows.size(0)) {
+        throw std::invalid_argument("plan edge_ids must match relation edge capacity.");
+    }
+    require_device(cot_in, "cotangent");
+    const at::Tensor feats = feats_in.contiguous();
+    const at::Tensor cot = cot_in.contiguous();
+    const int dtype = dtype_code(feats, op);
+    const int c_in = static_cast<int>(feats.size(1));
+    const int edge_cap = static_cast<int>(in_rows.size(0));
+    at::Tensor grad = at::empty(weights.sizes(), cot.options());
+    const size_t ws_bytes =
+        lattice_hip_conv_weight_grad_workspace_bytes(dtype, n_kernels, c_in, static_cast<int>(c_out), edge_cap);
+    at::Tensor ws = workspace(ws_bytes, feats);
+    check_status(lattice_hip_sparse_conv_weight_grad(
+        dtype, feats.data_ptr(), static_cast<int>(feats.size(0)), c_in, cot.data_ptr(), static_cast<int>(cot.size(0)),
+        static_cast<int>(c_out), weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D,
+        n_kernels, ci32(in_rows), ci32(out_rows), ci32(counts), edge_cap, ci32(kernel_row_offsets),
+        ci32(kernel_edge_ids), grad.data_ptr(), ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, current_stream(feats)));
+    return grad;
+}
+
 }  // namespace lattice_native

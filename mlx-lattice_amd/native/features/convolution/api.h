@@ -29,4 +29,27 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits);
 
+// Gradients (the reference conv primitive's vjp, primitive.cpp:137-176):
+// input gradient over the input-grouped CSR, (in_capacity, C_in) in the
+// cotangent dtype.
+at::Tensor sparse_conv_input_grad(const at::Tensor& cot, const at::Tensor& weights, const at::Tensor& out_rows,
+                                  const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                  const at::Tensor& in_row_offsets, const at::Tensor& in_edge_ids, int in_capacity,
+                                  int n_kernels);
+
+// Transposed dense map (in_out_map (in_capacity, K), row_masks) of a
+// forward or submanifold relation, for the matrix-core input gradient.
+std::tuple<at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
+                                                                      const at::Tensor& out_rows,
+                                                                      const at::Tensor& kernel_ids,
+                                                                      const at::Tensor& counts, int in_capacity,
+                                                                      int n_kernels);
+
+// Weight gradient over the kernel-grouped CSR, in the shape and layout of
+// `weights` (5D or mapped) and the cotangent dtype.
+at::Tensor sparse_conv_weight_grad(const at::Tensor& feats, const at::Tensor& cot, const at::Tensor& weights,
+                                   const at::Tensor& in_rows, const at::Tensor& out_rows, const at::Tensor& counts,
+                                   const at::Tensor& kernel_row_offsets, const at::Tensor& kernel_edge_ids,
+                                   int n_kernels);
+
 }  // namespace lattice_native

@@ -26,6 +26,11 @@
 //                                  torch conv3d(padding=1), k2s2 == strided
 //                                  dense conv3d, fp16 rounding of the two CPU
 //                                  routes checked against a float64 sum.
+//   oracle_conv_input_grad         reference known answers (gradients of
+//   oracle_conv_weight_grad        tests/ops/test_conv.py:401-487), torch
+//                                  autograd of the dense conv3d on a fully
+//                                  occupied box, adjointness with
+//                                  oracle_conv_features on seeded clouds.
 //   oracle_quantized_conv_features unpack formula on hand-built words, equal
 //   oracle_dequantize_mapped       to the float route on dequantized weights.
 // Not restated here, hence parity unpinned: the reference's quantizer
@@ -413,6 +418,109 @@ void oracle_conv_features(int dtype, const void* feats, const void* weights,
                  static_cast<uint16_t*>(p)[i] = float_to_half(v);
              },
              [](float v) { return half_to_float(float_to_half(v)); });
+    }
+}
+
+// Input gradient, eval_input_grad_typed (cpu/algorithms.cpp:355-410): for
+// every input row and input channel, one fp32 accumulator over the row's
+// edges in the input-grouped CSR (in_row_offsets / in_edge_ids) and every
+// output channel, cot[out][co] * W[k, ci, co]; one rounding to the feature
+// dtype.  Edges past counts[0] and out rows past out_capacity are skipped.
+void oracle_conv_input_grad(int dtype, const void* cot, const void* weights,
+                            int weight_layout, int in_capacity, int c_in,
+                            int c_out, int K, const int32_t* out_rows,
+                            const int32_t* kernel_ids, const int32_t* counts,
+                            int edge_capacity, const int32_t* in_row_offsets,
+                            const int32_t* in_edge_ids, int out_capacity,
+                            void* grad, int threads) {
+    int edge_total = std::min(counts[0], edge_capacity);
+    int nthreads = hardware_threads(threads);
+    auto widx = [&](int k, int ci, int co) -> size_t {
+        if (weight_layout == 0) {
+            return (static_cast<size_t>(k) * c_in + ci) * c_out + co;
+        }
+        return (static_cast<size_t>(co) * K + k) * c_in + ci;
+    };
+    auto body = [&](auto load, auto store) {
+        parallel_for(0, in_capacity, nthreads, [&](int in_row) {
+            for (int ci = 0; ci < c_in; ++ci) {
+                float acc = 0.0f;
+                for (int cur = in_row_offsets[in_row]; cur < in_row_offsets[in_row + 1]; ++cur) {
+                    int e = in_edge_ids[cur];
+                    if (e < 0 || e >= edge_total) continue;
+                    int o = out_rows[e];
+                    int k = kernel_ids[e];
+                    if (o < 0 || k < 0 || o >= out_capacity) continue;
+                    for (int co = 0; co < c_out; ++co) {
+                        acc += load(cot, static_cast<size_t>(o) * c_out + co) *
+                               load(weights, widx(k, ci, co));
+                    }
+                }
+                store(grad, static_cast<size_t>(in_row) * c_in + ci, acc);
+            }
+        });
+    };
+    if (dtype == 0) {
+        body([](const void* p, size_t i) { return static_cast<const float*>(p)[i]; },
+             [](void* p, size_t i, float v) { static_cast<float*>(p)[i] = v; });
+    } else {
+        body([](const void* p, size_t i) {
+                 return half_to_float(static_cast<const uint16_t*>(p)[i]);
+             },
+             [](void* p, size_t i, float v) {
+                 static_cast<uint16_t*>(p)[i] = float_to_half(v);
+             });
+    }
+}
+
+// Weight gradient, eval_weight_grad_typed (cpu/algorithms.cpp:413-481): for
+// every (k, ci, co), one fp32 accumulator over the edges of kernel k in the
+// kernel-grouped CSR (kernel_row_offsets / kernel_edge_ids) of
+// feats[in][ci] * cot[out][co]; one rounding, written in the weight's
+// layout.
+void oracle_conv_weight_grad(int dtype, const void* feats, const void* cot,
+                             int weight_layout, int c_in, int c_out, int K,
+                             const int32_t* in_rows, const int32_t* out_rows,
+                             const int32_t* counts, int edge_capacity,
+                             const int32_t* kernel_row_offsets,
+                             const int32_t* kernel_edge_ids, int out_capacity,
+                             void* grad, int threads) {
+    int edge_total = std::min(counts[0], edge_capacity);
+    int nthreads = hardware_threads(threads);
+    auto widx = [&](int k, int ci, int co) -> size_t {
+        if (weight_layout == 0) {
+            return (static_cast<size_t>(k) * c_in + ci) * c_out + co;
+        }
+        return (static_cast<size_t>(co) * K + k) * c_in + ci;
+    };
+    auto body = [&](auto load, auto store) {
+        parallel_for(0, K * c_in * c_out, nthreads, [&](int index) {
+            int co = index % c_out;
+            int ci = (index / c_out) % c_in;
+            int k = index / (c_in * c_out);
+            float acc = 0.0f;
+            for (int cur = kernel_row_offsets[k]; cur < kernel_row_offsets[k + 1]; ++cur) {
+                int e = kernel_edge_ids[cur];
+                if (e < 0 || e >= edge_total) continue;
+                int in = in_rows[e];
+                int o = out_rows[e];
+                if (in < 0 || o < 0 || o >= out_capacity) continue;
+                acc += load(feats, static_cast<size_t>(in) * c_in + ci) *
+                       load(cot, static_cast<size_t>(o) * c_out + co);
+            }
+            store(grad, widx(k, ci, co), acc);
+        });
+    };
+    if (dtype == 0) {
+        body([](const void* p, size_t i) { return static_cast<const float*>(p)[i]; },
+             [](void* p, size_t i, float v) { static_cast<float*>(p)[i] = v; });
+    } else {
+        body([](const void* p, size_t i) {
+                 return half_to_float(static_cast<const uint16_t*>(p)[i]);
+             },
+             [](void* p, size_t i, float v) {
+                 static_cast<uint16_t*>(p)[i] = float_to_half(v);
+             });
     }
 }
 

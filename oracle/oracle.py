@@ -18,6 +18,10 @@ Pinning (what checks each function besides this restatement):
 - conv_features: known answers (tests/ops/test_conv.py:44-83, 326-398,
   638-671) and the textbook identity with a dense 3D cross-correlation on a
   fully occupied box, plus an fp64 edge-sum restatement.
+- conv_input_grad, conv_weight_grad: the reference's gradient known
+  answers (tests/ops/test_conv.py:401-487), torch autograd of the dense
+  conv3d on a fully occupied box, and adjointness with conv_features
+  (<conv(x, W), g> = <x, input_grad(g)> = <W, weight_grad(x, g)>).
 - quantized_conv_features: the dequantized contract (packed conv equals the
   float conv of the dequantized weight) and the unpack formula on hand-built
   words.
@@ -71,6 +75,12 @@ def lib() -> ctypes.CDLL:
         handle.oracle_conv_features.argtypes = [
             _int, _vp, _vp, _int, _int, _int, _int, _int, _i32p, _i32p,
             _i32p, _int, _i32p, _int, _vp, _int]
+        handle.oracle_conv_input_grad.argtypes = [
+            _int, _vp, _vp, _int, _int, _int, _int, _int, _i32p, _i32p,
+            _i32p, _int, _i32p, _i32p, _int, _vp, _int]
+        handle.oracle_conv_weight_grad.argtypes = [
+            _int, _vp, _vp, _int, _int, _int, _int, _i32p, _i32p, _i32p,
+            _int, _i32p, _i32p, _int, _vp, _int]
         handle.oracle_quantized_conv_features.argtypes = [
             _int, _vp, _u32p, _vp, _vp, _int, _int, _int, _int, _int, _int,
             _i32p, _i32p, _i32p, _int, _i32p, _int, _vp, _int]
@@ -213,6 +223,57 @@ def conv_features(feats: np.ndarray, weight: np.ndarray, relation: dict,
         relation['counts'], relation['in_rows'].shape[0],
         relation['row_offsets'], cap, out.ctypes.data, int(threads))
     return out
+
+
+def _float_dtype(arr: np.ndarray) -> int:
+    if arr.dtype == np.float32:
+        return 0
+    if arr.dtype == np.float16:
+        return 1
+    raise ValueError('oracle gradients support float32 and float16.')
+
+
+def _weight_layout(weight_shape) -> tuple[int, int, int, int]:
+    """(layout, K, C_in, C_out) of a 5D or mapped weight shape."""
+    if len(weight_shape) == 5:
+        return 1, int(np.prod(weight_shape[1:4])), weight_shape[4], weight_shape[0]
+    if len(weight_shape) == 3:
+        return 0, weight_shape[0], weight_shape[1], weight_shape[2]
+    raise ValueError('weight must be 3D or 5D.')
+
+
+def conv_input_grad(cot: np.ndarray, weight: np.ndarray, relation: dict,
+                    in_capacity: int, threads: int = 0) -> np.ndarray:
+    """Reference CPU input gradient (eval_input_grad_typed): ``(in_capacity,
+    C_in)`` in the cotangent dtype."""
+    cot = np.ascontiguousarray(cot)
+    weight = np.ascontiguousarray(weight, dtype=cot.dtype)
+    layout, k, c_in, c_out = _weight_layout(weight.shape)
+    grad = np.zeros((in_capacity, c_in), dtype=cot.dtype)
+    lib().oracle_conv_input_grad(
+        _float_dtype(cot), cot.ctypes.data, weight.ctypes.data, layout,
+        in_capacity, c_in, c_out, k, relation['out_rows'],
+        relation['kernel_ids'], relation['counts'],
+        relation['in_rows'].shape[0], relation['in_row_offsets'],
+        relation['in_edge_ids'], cot.shape[0], grad.ctypes.data, int(threads))
+    return grad
+
+
+def conv_weight_grad(feats: np.ndarray, cot: np.ndarray, weight_shape,
+                     relation: dict, threads: int = 0) -> np.ndarray:
+    """Reference CPU weight gradient (eval_weight_grad_typed), in the
+    weight's shape and the cotangent dtype."""
+    feats = np.ascontiguousarray(feats)
+    cot = np.ascontiguousarray(cot, dtype=feats.dtype)
+    layout, k, c_in, c_out = _weight_layout(tuple(weight_shape))
+    grad = np.zeros(tuple(weight_shape), dtype=cot.dtype)
+    lib().oracle_conv_weight_grad(
+        _float_dtype(cot), feats.ctypes.data, cot.ctypes.data, layout, c_in,
+        c_out, k, relation['in_rows'], relation['out_rows'],
+        relation['counts'], relation['in_rows'].shape[0],
+        relation['kernel_row_offsets'], relation['kernel_edge_ids'],
+        cot.shape[0], grad.ctypes.data, int(threads))
+    return grad
 
 
 def quantized_conv_features(feats, weights, scales, biases, relation: dict,

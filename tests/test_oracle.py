@@ -349,3 +349,96 @@ def test_quantized_route_matches_dequantized_float_route(bits):
                               bits=bits)
     ref = O.conv_features_fp64(feats, deq.astype(np.float64), rel)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------ gradients --
+
+
+@pytest.mark.parametrize('name', ['grad_conv3d_generic_line',
+                                  'grad_subm_conv3d_line',
+                                  'grad_conv3d_target_line'])
+def test_gradients_golden(name):
+    g = golden(name)
+    coords = np.array(g['coords'], np.int32)
+    feats = np.array(g['feats'], np.float32)
+    weight = np.array(g['weight'], np.float32)
+    if 'target' in g:
+        rel = O.target_kernel_relation(coords, np.array(g['target'], np.int32),
+                                       kernel_size=g['kernel_size'])
+        n_out = len(g['target'])
+    else:
+        rel = O.kernel_relation(coords, kernel_size=g['kernel_size'])
+        n_out = len(coords)
+    cot = np.ones((n_out, weight.shape[0]), np.float32)
+    assert O.conv_input_grad(cot, weight, rel, len(coords)).tolist() == \
+        g['grad_feats']
+    assert O.conv_weight_grad(feats, cot, weight.shape, rel).tolist() == \
+        g['grad_weight']
+
+
+def _box(size, rng):
+    grid = np.stack(np.meshgrid(np.arange(size), np.arange(size),
+                                np.arange(size), indexing='ij'), -1)
+    coords = np.concatenate([np.zeros((size ** 3, 1), np.int64),
+                             grid.reshape(-1, 3)], 1).astype(np.int32)
+    return coords[rng.permutation(len(coords))]
+
+
+def test_gradients_match_dense_autograd_on_a_full_box():
+    """On a fully occupied box the submanifold conv is a zero-padded dense
+    cross-correlation, so its gradients are torch's conv3d gradients."""
+    torch = pytest.importorskip('torch')
+    rng = np.random.default_rng(9)
+    size, c_in, c_out = 5, 3, 4
+    coords = _box(size, rng)
+    feats = rng.standard_normal((len(coords), c_in))
+    w = rng.standard_normal((c_out, 3, 3, 3, c_in))
+    cot = rng.standard_normal((len(coords), c_out))
+    rel = O.kernel_relation(coords, kernel_size=3)
+    x = torch.zeros((1, c_in, size, size, size), dtype=torch.float64,
+                    requires_grad=True)
+    dense_feats = torch.zeros((1, c_in, size, size, size), dtype=torch.float64)
+    dense_feats[0, :, coords[:, 1], coords[:, 2], coords[:, 3]] = \
+        torch.from_numpy(feats).T
+    x = dense_feats.clone().requires_grad_(True)
+    wt = torch.from_numpy(w.transpose(0, 4, 1, 2, 3).copy()).requires_grad_(True)
+    y = torch.nn.functional.conv3d(x, wt, padding=1)
+    g = torch.zeros_like(y)
+    g[0, :, coords[:, 1], coords[:, 2], coords[:, 3]] = torch.from_numpy(cot).T
+    (y * g).sum().backward()
+    ref_in = x.grad[0].numpy()[:, coords[:, 1], coords[:, 2], coords[:, 3]].T
+    ref_w = wt.grad.numpy().transpose(0, 2, 3, 4, 1)
+    got_in = O.conv_input_grad(cot.astype(np.float32), w.astype(np.float32),
+                               rel, len(coords))
+    got_w = O.conv_weight_grad(feats.astype(np.float32),
+                               cot.astype(np.float32), w.shape, rel)
+    np.testing.assert_allclose(got_in, ref_in, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(got_w, ref_w, rtol=1e-4, atol=1e-4)
+
+
+def test_gradients_adjoint_to_the_forward_conv():
+    """<conv(x, W), g> = <x, input_grad(g)> = <W, weight_grad(x, g)> on a
+    strided (k2s2) and a submanifold relation over a sparse cloud."""
+    rng = np.random.default_rng(10)
+    coords = np.unique(rng.integers(0, 12, (300, 3)), axis=0)
+    coords = np.concatenate([rng.integers(0, 2, (len(coords), 1)), coords],
+                            1).astype(np.int32)
+    coords = coords[rng.permutation(len(coords))]
+    for ks, stride in ((3, 1), (2, 2)):
+        rel = O.kernel_relation(coords, kernel_size=ks, stride=stride)
+        c_in, c_out = 5, 3
+        feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+        w = rng.standard_normal((c_out, ks, ks, ks, c_in)).astype(np.float32)
+        n_out = int(rel['counts'][1])
+        y = O.conv_features_fp64(feats, O.mapped_weight(w.astype(np.float64)),
+                                 rel)
+        g = np.zeros((len(coords), c_out), np.float32)
+        g[:n_out] = rng.standard_normal((n_out, c_out))
+        lhs = float((y * g).sum())
+        gin = O.conv_input_grad(g, w, rel, len(coords)).astype(np.float64)
+        gw = O.conv_weight_grad(feats, g, w.shape, rel).astype(np.float64)
+        assert abs(lhs - float((feats * gin).sum())) < 1e-3 * (1 + abs(lhs))
+        assert abs(lhs - float((w * gw).sum())) < 1e-3 * (1 + abs(lhs))
+        # the mapped layout gives the same numbers, transposed
+        gw_mapped = O.conv_weight_grad(feats, g, (ks ** 3, c_in, c_out), rel)
+        np.testing.assert_allclose(O.mapped_weight(gw), gw_mapped, rtol=1e-6)
