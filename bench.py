@@ -252,6 +252,48 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
     return out
 
 
+def backward_workload(feats, weight, coords, active, edges: int, steps: int,
+                      warmup: int) -> dict:
+    """Gradients of the config-3 conv (the reference primitive's vjp):
+    the input gradient on the matrix cores over the transposed sorted view,
+    the weight gradient by the split-edge MFMA kernel.  The transposed view
+    is built once per relation and cached, like the forward's sorted view;
+    its build time is reported separately."""
+    import torch
+
+    from mlx_lattice_amd import SparseTensor
+    from mlx_lattice_amd.ops._relation_exec import (
+        sparse_conv_input_grad_from_relation,
+        sparse_conv_weight_grad_from_relation,
+    )
+
+    x = SparseTensor(coords, feats)
+    rel = x.coord_manager.submanifold_kernel_relation(x.coord_key,
+                                                      kernel_size=3)
+    n = int(coords.shape[0])
+    gen = torch.Generator(device=feats.device).manual_seed(7)
+    cot = torch.randn(feats.shape, generator=gen, device=feats.device,
+                      dtype=torch.float32).to(feats.dtype)
+    rel.kernel_csr  # grouped views, built once like the forward's views
+    t_view = _timed(lambda: (object.__setattr__(
+        rel, 'transposed_sorted_implicit_gemm', None),
+        rel.require_transposed_sorted_implicit_gemm()), 3, 1)
+    t_in = _timed(lambda: sparse_conv_input_grad_from_relation(
+        cot, weight, rel, n), steps, warmup)
+    t_w = _timed(lambda: sparse_conv_weight_grad_from_relation(
+        feats, cot, weight, rel), steps, warmup)
+    flops = 2.0 * edges * 128 * 128
+    return {
+        'workload': 'config3 gradients: input grad (matrix cores, transposed '
+                    'sorted view) and weight grad (split-edge MFMA)',
+        'input_grad_ms': round(t_in, 4),
+        'input_grad_tflops': round(flops / t_in / 1e9, 2),
+        'weight_grad_ms': round(t_w, 4),
+        'weight_grad_tflops': round(flops / t_w / 1e9, 2),
+        'transposed_view_ms': round(t_view, 4),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -361,6 +403,8 @@ def main() -> int:
             'kernel': 'conv_igemm<f16, IgemmShape<128 cols, 32-row waves, 4 waves, 64-channel stages, A via LDS>, FloatB>',
         },
     }
+    record['backward'] = backward_workload(feats, weight, coords, active,
+                                           edges, args.steps, args.warmup)
     if not args.no_secondary:
         record['secondary'] = secondary_workloads()
     if not args.no_cpu_baseline:

@@ -18,8 +18,10 @@
 //  * Weight gradient: dW[k] = sum over the edges of k of
 //    feats[in]^T cot[out] (eval_weight_grad_typed), a contraction over
 //    edges.  The matrix-core kernel splits each k's edges (kernel-grouped
-//    CSR: kernel_row_offsets / kernel_edge_ids) over S blocks per 64 x 64
-//    channel tile; a block stages 32 edges of both operands transposed in
+//    CSR: kernel_row_offsets / kernel_edge_ids) over S blocks per channel
+//    tile (128 x 128 when the channels fill it, so an edge's rows are
+//    gathered once for every channel pair); a block stages 32 edges of both
+//    operands transposed in
 //    LDS (channel-major, so an MFMA fragment is 8 consecutive edges) and
 //    accumulates in fp32.  Each split writes its partial tile; a second
 //    kernel sums the S partials in split order and rounds once, so results
@@ -107,8 +109,7 @@ input_grad_csr(const T* __restrict__ cot, int out_capacity, const T* __restrict_
 __global__ void __launch_bounds__(256)
 transposed_map(const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
-               int in_capacity, int K, int words, int32_t* __restrict__ in_out_map,
-               int32_t* __restrict__ row_masks) {
+               int in_capacity, int K, int32_t* __restrict__ in_out_map) {
     const int E = min(counts[0], edge_capacity);
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
         const int in = in_rows[e];
@@ -116,8 +117,20 @@ transposed_map(const int32_t* __restrict__ in_rows, const int32_t* __restrict__ 
         const int k = kernel_ids[e];
         if (in < 0 || in >= in_capacity || o < 0 || k < 0 || k >= K) continue;
         in_out_map[static_cast<long long>(in) * K + k] = o;
-        atomicOr(reinterpret_cast<unsigned*>(row_masks) + static_cast<long long>(in) * words + (k >> 5),
-                 1u << (k & 31));
+    }
+}
+
+// Offset bits of each input row, from its row of the transposed map.
+__global__ void __launch_bounds__(256)
+transposed_masks(const int32_t* __restrict__ in_out_map, int in_capacity, int K, int words,
+                 int32_t* __restrict__ row_masks) {
+    for (int row = blockIdx.x * blockDim.x + threadIdx.x; row < in_capacity; row += gridDim.x * blockDim.x) {
+        const int32_t* m = in_out_map + static_cast<long long>(row) * K;
+        for (int w = 0; w < words; ++w) {
+            uint32_t bits = 0;
+            for (int k = 32 * w; k < min(K, 32 * w + 32); ++k) bits |= (m[k] >= 0 ? 1u : 0u) << (k & 31);
+            row_masks[static_cast<long long>(row) * words + w] = static_cast<int32_t>(bits);
+        }
     }
 }
 
@@ -137,27 +150,33 @@ template <> struct GradMfma<__bf16> {
     }
 };
 
-constexpr int kWgTile = 64;    // channels per tile side
-constexpr int kWgEdges = 32;   // edges per MFMA step
-constexpr int kWgRow = 40;     // LDS row stride in elements (32 edges + 8 pad: conflict-free fragment reads)
+constexpr int kWgEdges = 64;   // edges per staged step (two 32-edge MFMA steps)
+constexpr int kWgRow = 72;     // LDS row stride in elements (64 edges + 8 pad)
 
-// Block (tile_ci * tiles_co + tile_co, k, split): channel tile 64 x 64,
-// four waves of 32 x 32.  Thread t stages edge t/8, 8-channel piece t%8 of
-// both operands per step.
-template <typename T>
+// LDS slot of edge column j in channel row r: the 16-byte chunk j/8 is
+// XOR-swizzled by r/8, so a wave's transposing stores (8 edges x 8 channel
+// pieces) and the fragment reads (16 rows, one chunk) spread over the banks.
+__device__ inline int wg_slot(int r, int j) { return r * kWgRow + (((j >> 3) ^ ((r >> 3) & 7)) << 3) + (j & 7); }
+
+// Block (tile_ci * tiles_co + tile_co, k, split): channel tile TCI x TCO,
+// four waves of (TCI/2) x (TCO/2).  Per step of 32 edges the block stages
+// both operands transposed into channel-major LDS rows (64 edges per step).
+template <typename T, int TCI, int TCO>
 __global__ void __launch_bounds__(256)
 weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ cot, int n_out, int c_out,
                  const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                  const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
                  const int32_t* __restrict__ kedges, int splits, int tiles_co, float* __restrict__ partial) {
     using V = typename GradMfma<T>::vec;
-    __shared__ __align__(16) T a_t[kWgTile * kWgRow];
-    __shared__ __align__(16) T b_t[kWgTile * kWgRow];
+    constexpr int MB = TCI / 32;  // 16-row blocks per wave
+    constexpr int NB = TCO / 32;  // 16-column blocks per wave
+    __shared__ __align__(16) T a_t[TCI * kWgRow];
+    __shared__ __align__(16) T b_t[TCO * kWgRow];
     const int K = gridDim.y;
     const int k = blockIdx.y;
     const int s = blockIdx.z;
-    const int ci0 = (blockIdx.x / tiles_co) * kWgTile;
-    const int co0 = (blockIdx.x % tiles_co) * kWgTile;
+    const int ci0 = (blockIdx.x / tiles_co) * TCI;
+    const int co0 = (blockIdx.x % tiles_co) * TCO;
     const int E = min(counts[0], edge_capacity);
     const int lo_k = koff[k];
     const int n_k = koff[k + 1] - lo_k;
@@ -170,59 +189,89 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     const int wn = wave >> 1;
     const int lr = lane & 15;
     const int g = lane >> 4;
-    const int j = threadIdx.x >> 3;  // edge within the step
-    const int p = threadIdx.x & 7;   // 8-channel piece
-    float4_t acc[2][2];
+    float4_t acc[MB][NB];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < MB; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < NB; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int base = lo; base < hi; base += kWgEdges) {
-        V av{}, bv{};
-        const int cur = base + j;
-        if (cur < hi) {
+    // Thread t stages edges t/8 and t/8 + 32 of the step: 8-channel pieces
+    // t%8 + 8i of their feature rows (i < TCI/64) and cotangent rows
+    // (i < TCO/64), so a wave's loads cover eight whole 128-byte row lines.
+    constexpr int PA = TCI / 64;
+    constexpr int PB = TCO / 64;
+    const int j = threadIdx.x >> 3;
+    const int p = threadIdx.x & 7;
+    V av[2][PA], bv[2][PB];
+    // Rows of step `base`: edges base + j + 32h, zeros past the split's end.
+    auto gather = [&](int base) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < PA; ++i) av[h][i] = V{};
+#pragma unroll
+            for (int i = 0; i < PB; ++i) bv[h][i] = V{};
+            const int cur = base + j + 32 * h;
+            if (cur >= hi) continue;
             const int e = kedges[cur];
-            if (e >= 0 && e < E) {
-                const int in = in_rows[e];
-                const int o = out_rows[e];
-                if (in >= 0 && in < n_in && o >= 0 && o < n_out) {
-                    if (ci0 + 8 * p < c_in)
-                        av = *reinterpret_cast<const V*>(feats + static_cast<long long>(in) * c_in + ci0 + 8 * p);
-                    if (co0 + 8 * p < c_out)
-                        bv = *reinterpret_cast<const V*>(cot + static_cast<long long>(o) * c_out + co0 + 8 * p);
-                }
+            if (e < 0 || e >= E) continue;
+            const int in = in_rows[e];
+            const int o = out_rows[e];
+            if (in < 0 || in >= n_in || o < 0 || o >= n_out) continue;
+#pragma unroll
+            for (int i = 0; i < PA; ++i) {
+                const int c = ci0 + 8 * (p + 8 * i);
+                if (c < c_in) av[h][i] = *reinterpret_cast<const V*>(feats + static_cast<long long>(in) * c_in + c);
+            }
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {
+                const int c = co0 + 8 * (p + 8 * i);
+                if (c < c_out) bv[h][i] = *reinterpret_cast<const V*>(cot + static_cast<long long>(o) * c_out + c);
             }
         }
+    };
+    // The gathers of step s+1 are issued before the MFMAs of step s.
+    gather(lo);
+    for (int base = lo; base < hi; base += kWgEdges) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            a_t[(8 * p + c) * kWgRow + j] = av[c];
-            b_t[(8 * p + c) * kWgRow + j] = bv[c];
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < PA; ++i)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) a_t[wg_slot(8 * (p + 8 * i) + c, j + 32 * h)] = av[h][i][c];
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) b_t[wg_slot(8 * (p + 8 * i) + c, j + 32 * h)] = bv[h][i][c];
         }
         __syncthreads();
-        V af[2], bf[2];
+        gather(base + kWgEdges);
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
-            af[m] = *reinterpret_cast<const V*>(a_t + (32 * wm + 16 * m + lr) * kWgRow + 8 * g);
+        for (int ks = 0; ks < 2; ++ks) {
+            V af[MB], bf[NB];
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
-            bf[n] = *reinterpret_cast<const V*>(b_t + (32 * wn + 16 * n + lr) * kWgRow + 8 * g);
+            for (int m = 0; m < MB; ++m)
+                af[m] = *reinterpret_cast<const V*>(a_t + wg_slot((TCI / 2) * wm + 16 * m + lr, 32 * ks + 8 * g));
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+            for (int n = 0; n < NB; ++n)
+                bf[n] = *reinterpret_cast<const V*>(b_t + wg_slot((TCO / 2) * wn + 16 * n + lr, 32 * ks + 8 * g));
 #pragma unroll
-            for (int n = 0; n < 2; ++n) acc[m][n] = GradMfma<T>::mfma(af[m], bf[n], acc[m][n]);
+            for (int m = 0; m < MB; ++m)
+#pragma unroll
+                for (int n = 0; n < NB; ++n) acc[m][n] = GradMfma<T>::mfma(af[m], bf[n], acc[m][n]);
+        }
         __syncthreads();
     }
     // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
     float* out = partial + (static_cast<long long>(s) * K + k) * c_in * c_out;
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < MB; ++m)
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+        for (int n = 0; n < NB; ++n)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int ci = ci0 + 32 * wm + 16 * m + 4 * g + q;
-                const int co = co0 + 32 * wn + 16 * n + lr;
+                const int ci = ci0 + (TCI / 2) * wm + 16 * m + 4 * g + q;
+                const int co = co0 + (TCO / 2) * wn + 16 * n + lr;
                 if (ci < c_in && co < c_out) out[static_cast<long long>(ci) * c_out + co] = acc[m][n][q];
             }
 }
@@ -315,15 +364,25 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
             const int splits = weight_grad_splits(edge_capacity, widx.K);
             const size_t need = static_cast<size_t>(splits) * widx.K * widx.c_in * widx.c_out * sizeof(float);
             LATTICE_REQUIRE(workspace_bytes >= need, "weight gradient workspace too small.");
-            const int tiles_ci = (widx.c_in + kWgTile - 1) / kWgTile;
-            const int tiles_co = (widx.c_out + kWgTile - 1) / kWgTile;
+            float* partial = static_cast<float*>(workspace);
+            // 128-channel tiles where the channels fill them: one gather of
+            // an edge's rows then serves every channel pair of the tile.
+            const int tci = widx.c_in > 64 ? 128 : 64;
+            const int tco = widx.c_out > 64 ? 128 : 64;
+            const int tiles_ci = (widx.c_in + tci - 1) / tci;
+            const int tiles_co = (widx.c_out + tco - 1) / tco;
             dim3 grid(static_cast<unsigned>(tiles_ci * tiles_co), static_cast<unsigned>(widx.K),
                       static_cast<unsigned>(splits));
-            float* partial = static_cast<float*>(workspace);
-            weight_grad_mfma<T><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,
-                                                          static_cast<const T*>(cot), n_out, widx.c_out, in_rows,
-                                                          out_rows, counts, edge_capacity, koff, kedges, splits,
-                                                          tiles_co, partial);
+#define LATTICE_WG_LAUNCH(A, B)                                                                                 \
+    weight_grad_mfma<T, A, B><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,          \
+                                                        static_cast<const T*>(cot), n_out, widx.c_out, in_rows,  \
+                                                        out_rows, counts, edge_capacity, koff, kedges, splits,   \
+                                                        tiles_co, partial)
+            if (tci == 128 && tco == 128) LATTICE_WG_LAUNCH(128, 128);
+            else if (tci == 128) LATTICE_WG_LAUNCH(128, 64);
+            else if (tco == 128) LATTICE_WG_LAUNCH(64, 128);
+            else LATTICE_WG_LAUNCH(64, 64);
+#undef LATTICE_WG_LAUNCH
             LATTICE_LAUNCH_CHECK();
             const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
             weight_grad_reduce<T><<<grid_for(per, 256, 4096), 256, 0, stream>>>(partial, splits, widx,
@@ -391,12 +450,13 @@ extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_
     const int words = (kernel_count + 31) / 32;
     int rc = fill_i32(in_out_map, static_cast<long long>(in_capacity) * kernel_count, -1, stream);
     if (rc != LATTICE_OK) return rc;
-    rc = fill_i32(row_masks, static_cast<long long>(in_capacity) * words, 0, stream);
-    if (rc != LATTICE_OK) return rc;
-    if (edge_capacity == 0) return LATTICE_OK;
-    transposed_map<<<grid_for(edge_capacity, 256, 1u << 16), 256, 0, stream>>>(
-        in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, words, in_out_map,
-        row_masks);
+    if (edge_capacity > 0) {
+        transposed_map<<<grid_for(edge_capacity, 256, 1u << 16), 256, 0, stream>>>(
+            in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, in_out_map);
+        LATTICE_LAUNCH_CHECK();
+    }
+    transposed_masks<<<grid_for(in_capacity, 256, 1u << 16), 256, 0, stream>>>(in_out_map, in_capacity,
+                                                                              kernel_count, words, row_masks);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
