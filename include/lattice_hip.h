@@ -32,6 +32,10 @@
  *   conv input / weight gradients    convolution/primitive.cpp:137-176,
  *                                    597-680 (the conv primitive's vjp),
  *                                    cpu/algorithms.cpp:355-481
+ *   sparse_pool_features (+ vjp)     native/features/pooling/primitive.cpp,
+ *                                    pooling/cpu/algorithms.cpp:180-331,
+ *                                    bindings/pooling.cpp:15-66
+ *   global pools                     mlx_lattice/ops/pool.py:198-236
  */
 #ifndef LATTICE_HIP_H_
 #define LATTICE_HIP_H_
@@ -274,6 +278,40 @@ int lattice_hip_sparse_conv_weight_grad(
     int edge_capacity, const int32_t* kernel_row_offsets,
     const int32_t* kernel_edge_ids, void* grad, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Sparse pooling over a kernel relation (SparsePoolFeatures,
+ * pooling/cpu/algorithms.cpp:180-242; binding sparse_pool_features,
+ * bindings/pooling.cpp:15-66).  mode 0 sum, 1 max, 2 avg; fp32 features
+ * [n_in, channels].  Every output row starts at the reduction identity
+ * (-inf for max, 0 otherwise); rows below counts[1] reduce
+ * feats[in_rows[e]] over their CSR edges (row_offsets [out_capacity + 1]);
+ * avg divides by max(degree, 1).  out [out_capacity, channels]. */
+int lattice_hip_sparse_pool_features(
+    int mode, const float* feats, int n_in, int channels,
+    const int32_t* in_rows, int edge_capacity, const int32_t* row_offsets,
+    const int32_t* counts, int out_capacity, float* out, void* stream);
+
+/* Pooling gradient (the primitive's vjp, pooling/primitive.cpp:109-160,
+ * cpu/algorithms.cpp:245-331) over the input-grouped CSR (in_row_offsets
+ * [n_in + 1], in_edge_ids): grad[in, c] = sum over the row's edges into out
+ * rows below counts[1] of cot[out, c] * scale, scale 1 (sum),
+ * 1/max(degree, 1) (avg), and for max 1/(tied inputs of the out row) when
+ * feats[in, c] equals pooled[out, c], else 0.  grad [n_in, channels]. */
+int lattice_hip_sparse_pool_features_grad(
+    int mode, const float* cot, const float* feats, const float* pooled,
+    int n_in, int channels, const int32_t* in_rows, const int32_t* out_rows,
+    int edge_capacity, const int32_t* row_offsets, const int32_t* counts,
+    const int32_t* in_row_offsets, const int32_t* in_edge_ids,
+    int out_capacity, float* grad, void* stream);
+
+/* Per-batch global pooling (global_sum_pool / global_avg_pool /
+ * global_max_pool, ops/pool.py:139-236): out[b, c] reduces rows
+ * batch_offsets[b] .. batch_offsets[b+1] of feats [rows, channels] (fp32);
+ * avg divides by the batch's row count (empty batches give zeros for sum and
+ * avg; callers reject empty batches for max, as the reference does). */
+int lattice_hip_global_pool(int mode, const float* feats, int channels,
+                            const int64_t* batch_offsets, int batches,
+                            float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,10 +28,11 @@ NATIVE = HERE / 'native'
 INCLUDE = REPO / 'include'
 ARCH = 'gfx950'
 
-HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip', 'conv_grad.hip']
+HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip', 'conv_grad.hip', 'pool.hip']
 HOST_SOURCES = [
     'native/features/coordinates/relations.cpp',
     'native/features/convolution/api.cpp',
+    'native/features/pooling/pooling.cpp',
     'native/bindings/module.cpp',
 ]
 

@@ -221,6 +221,53 @@ def sparse_quantized_conv_features_from_relation(
         weight.bits)
 
 
+def sparse_pool_features_from_relation(feats: torch.Tensor,
+                                       relation: KernelRelation, *,
+                                       input_exclusive: bool,
+                                       mode: str) -> torch.Tensor:
+    """Sparse pooling over a prebuilt kernel relation
+    (_relation_exec.py:253-276), differentiable in ``feats``."""
+    _require_static(relation)
+    if torch.is_grad_enabled() and feats.requires_grad:
+        return _SparsePoolFeatures.apply(feats, relation, input_exclusive,
+                                         mode)
+    return _pool_features(feats, relation, input_exclusive, mode)
+
+
+def _pool_features(feats, relation, input_exclusive, mode):
+    return ext.sparse_pool_features(
+        feats, relation.edges.in_rows, relation.edges.out_rows,
+        relation.edges.kernel_ids, relation.output_csr.row_offsets,
+        relation.counts, input_exclusive, mode, relation.n_out_capacity,
+        relation.n_kernels)
+
+
+class _SparsePoolFeatures(torch.autograd.Function):
+    """Pooling with the reference's vjp (pooling/primitive.cpp:109-160):
+    the gradient walks the input-grouped CSR; max routes the cotangent to
+    the inputs equal to the pooled value, split over ties."""
+
+    @staticmethod
+    def forward(ctx, feats, relation, input_exclusive, mode):
+        pooled = _pool_features(feats, relation, input_exclusive, mode)
+        ctx.relation = relation
+        ctx.mode = mode
+        ctx.save_for_backward(feats, pooled)
+        return pooled
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        feats, pooled = ctx.saved_tensors
+        relation = ctx.relation
+        input_csr = relation.input_csr
+        grad = ext.sparse_pool_features_grad(
+            grad_out.contiguous(), feats, pooled, relation.edges.in_rows,
+            relation.edges.out_rows, relation.output_csr.row_offsets,
+            relation.counts, input_csr.row_offsets, input_csr.edge_ids,
+            ctx.mode)
+        return grad, None, None, None
+
+
 def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:
     """5D weights go to the kernels as they are (C_in contiguous per
     (C_out, k)); a mapped ``(K, C_in, C_out)`` weight is transposed once to

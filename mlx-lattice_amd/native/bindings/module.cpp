@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "features/convolution/api.h"
+#include "features/pooling/api.h"
 #include "features/coordinates/relations.h"
 #include "foundation/runtime.h"
 #include "lattice_hip.h"
@@ -188,4 +189,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("weights"), py::arg("in_rows"), py::arg("out_rows"), py::arg("counts"),
           py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("n_kernels"),
           "Weight gradient of the sparse conv over the kernel-grouped CSR, in the layout of `weights`.");
+
+    m.def("sparse_pool_features", &ln::sparse_pool_features, py::arg("feats"), py::arg("in_rows"),
+          py::arg("out_rows"), py::arg("kernel_ids"), py::arg("row_offsets"), py::arg("counts"),
+          py::arg("input_exclusive"), py::arg("reduce"), py::arg("out_capacity"), py::arg("n_kernels"),
+          "Run sparse pooling feature reduction over a kernel relation.");
+    m.def("sparse_pool_features_grad", &ln::sparse_pool_features_grad, py::arg("cotangent"), py::arg("feats"),
+          py::arg("pooled"), py::arg("in_rows"), py::arg("out_rows"), py::arg("row_offsets"), py::arg("counts"),
+          py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("reduce"),
+          "Gradient of sparse pooling with respect to the input features.");
+    m.def("global_pool", &ln::global_pool, py::arg("feats"), py::arg("batch_counts"), py::arg("mode"),
+          "Per-batch global pooling: (B, C).");
 }

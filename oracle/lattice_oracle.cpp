@@ -31,6 +31,9 @@
 //                                  autograd of the dense conv3d on a fully
 //                                  occupied box, adjointness with
 //                                  oracle_conv_features on seeded clouds.
+//   oracle_pool_features           reference known answers (tests/ops/
+//   oracle_pool_grad               test_pool.py:32-117), a numpy brute force,
+//                                  sum pooling == conv with all-ones weights.
 //   oracle_quantized_conv_features unpack formula on hand-built words, equal
 //   oracle_dequantize_mapped       to the float route on dequantized weights.
 // Not restated here, hence parity unpinned: the reference's quantizer
@@ -44,6 +47,7 @@
 #include <chrono>
 #include <cstdint>
 #include <cstring>
+#include <limits>
 #include <thread>
 #include <unordered_map>
 #include <unordered_set>
@@ -521,6 +525,77 @@ void oracle_conv_weight_grad(int dtype, const void* feats, const void* cot,
              [](void* p, size_t i, float v) {
                  static_cast<uint16_t*>(p)[i] = float_to_half(v);
              });
+    }
+}
+
+// Sparse pooling, native/features/pooling/cpu/algorithms.cpp:180-242 (eval):
+// every output row starts at the reduction identity (-inf for max, 0
+// otherwise); rows below counts[1] reduce feats[in_rows[e]] over their CSR
+// edges; avg divides by max(degree, 1).  mode: 0 sum, 1 max, 2 avg; fp32.
+void oracle_pool_features(int mode, const float* feats, int channels,
+                          const int32_t* in_rows, const int32_t* row_offsets,
+                          const int32_t* counts, int out_capacity,
+                          float* out) {
+    int out_count = std::min(counts[1], out_capacity);
+    float identity = mode == 1 ? -std::numeric_limits<float>::infinity() : 0.0f;
+    std::fill(out, out + static_cast<size_t>(out_capacity) * channels, identity);
+    for (int o = 0; o < out_count; ++o) {
+        float* row = out + static_cast<size_t>(o) * channels;
+        for (int e = row_offsets[o]; e < row_offsets[o + 1]; ++e) {
+            const float* f = feats + static_cast<size_t>(in_rows[e]) * channels;
+            for (int c = 0; c < channels; ++c) {
+                row[c] = mode == 1 ? std::max(row[c], f[c]) : row[c] + f[c];
+            }
+        }
+    }
+    if (mode != 2) return;
+    for (int o = 0; o < out_count; ++o) {
+        float scale = 1.0f / static_cast<float>(std::max(row_offsets[o + 1] - row_offsets[o], 1));
+        float* row = out + static_cast<size_t>(o) * channels;
+        for (int c = 0; c < channels; ++c) row[c] *= scale;
+    }
+}
+
+// Pooling gradient, pooling/cpu/algorithms.cpp:245-331 (eval_grad) over the
+// input-grouped CSR (the exclusive layout's direct edge is the same single
+// edge): grad[in][c] = sum over the row's edges whose out row is below
+// counts[1] of cot[out][c] * scale; scale 1 (sum), 1/max(degree(out), 1)
+// (avg), and for max 1/(number of the out row's edges whose feature equals
+// the pooled value) when feats[in][c] equals it, else 0.
+void oracle_pool_grad(int mode, const float* cot, const float* feats,
+                      const float* pooled, int channels,
+                      const int32_t* in_rows, const int32_t* out_rows,
+                      const int32_t* row_offsets, const int32_t* counts,
+                      const int32_t* in_row_offsets,
+                      const int32_t* in_edge_ids, int in_capacity,
+                      int out_capacity, float* grad) {
+    int out_count = std::min(counts[1], out_capacity);
+    for (int in = 0; in < in_capacity; ++in) {
+        for (int c = 0; c < channels; ++c) {
+            float value = 0.0f;
+            for (int cur = in_row_offsets[in]; cur < in_row_offsets[in + 1]; ++cur) {
+                int e = in_edge_ids[cur];
+                if (e < 0) continue;
+                int o = out_rows[e];
+                if (o < 0 || o >= out_count) continue;
+                float scale = 1.0f;
+                if (mode == 1) {
+                    float fv = feats[static_cast<size_t>(in) * channels + c];
+                    float pv = pooled[static_cast<size_t>(o) * channels + c];
+                    if (fv != pv) continue;
+                    int ties = 0;
+                    for (int e2 = row_offsets[o]; e2 < row_offsets[o + 1]; ++e2) {
+                        if (feats[static_cast<size_t>(in_rows[e2]) * channels + c] == pv) ++ties;
+                    }
+                    if (ties == 0) continue;
+                    scale = 1.0f / static_cast<float>(ties);
+                } else if (mode == 2) {
+                    scale = 1.0f / static_cast<float>(std::max(row_offsets[o + 1] - row_offsets[o], 1));
+                }
+                value += cot[static_cast<size_t>(o) * channels + c] * scale;
+            }
+            grad[static_cast<size_t>(in) * channels + c] = value;
+        }
     }
 }
 

@@ -22,6 +22,9 @@ Pinning (what checks each function besides this restatement):
   answers (tests/ops/test_conv.py:401-487), torch autograd of the dense
   conv3d on a fully occupied box, and adjointness with conv_features
   (<conv(x, W), g> = <x, input_grad(g)> = <W, weight_grad(x, g)>).
+- pool_features, pool_grad: the reference's pooling known answers
+  (tests/ops/test_pool.py:32-117), a numpy brute force and the identity
+  sum pooling == conv with all-ones weights.
 - quantized_conv_features: the dequantized contract (packed conv equals the
   float conv of the dequantized weight) and the unpack formula on hand-built
   words.
@@ -81,6 +84,11 @@ def lib() -> ctypes.CDLL:
         handle.oracle_conv_weight_grad.argtypes = [
             _int, _vp, _vp, _int, _int, _int, _int, _i32p, _i32p, _i32p,
             _int, _i32p, _i32p, _int, _vp, _int]
+        handle.oracle_pool_features.argtypes = [
+            _int, _f32p, _int, _i32p, _i32p, _i32p, _int, _f32p]
+        handle.oracle_pool_grad.argtypes = [
+            _int, _f32p, _f32p, _f32p, _int, _i32p, _i32p, _i32p, _i32p,
+            _i32p, _i32p, _int, _int, _f32p]
         handle.oracle_quantized_conv_features.argtypes = [
             _int, _vp, _u32p, _vp, _vp, _int, _int, _int, _int, _int, _int,
             _i32p, _i32p, _i32p, _int, _i32p, _int, _vp, _int]
@@ -273,6 +281,38 @@ def conv_weight_grad(feats: np.ndarray, cot: np.ndarray, weight_shape,
         relation['counts'], relation['in_rows'].shape[0],
         relation['kernel_row_offsets'], relation['kernel_edge_ids'],
         cot.shape[0], grad.ctypes.data, int(threads))
+    return grad
+
+
+_POOL_MODES = {'sum': 0, 'max': 1, 'avg': 2}
+
+
+def pool_features(feats: np.ndarray, relation: dict, mode: str,
+                  out_capacity: int | None = None) -> np.ndarray:
+    """Reference CPU sparse pooling (pooling/cpu/algorithms.cpp eval)."""
+    feats = np.ascontiguousarray(feats, dtype=np.float32)
+    cap = (relation['row_offsets'].shape[0] - 1
+           if out_capacity is None else out_capacity)
+    out = np.zeros((cap, feats.shape[1]), np.float32)
+    lib().oracle_pool_features(_POOL_MODES[mode], feats, feats.shape[1],
+                               relation['in_rows'], relation['row_offsets'],
+                               relation['counts'], cap, out)
+    return out
+
+
+def pool_grad(cot: np.ndarray, feats: np.ndarray, pooled: np.ndarray,
+              relation: dict, mode: str) -> np.ndarray:
+    """Reference CPU pooling gradient (pooling/cpu/algorithms.cpp
+    eval_grad) over the input-grouped CSR."""
+    cot = np.ascontiguousarray(cot, dtype=np.float32)
+    feats = np.ascontiguousarray(feats, dtype=np.float32)
+    pooled = np.ascontiguousarray(pooled, dtype=np.float32)
+    grad = np.zeros(feats.shape, np.float32)
+    lib().oracle_pool_grad(
+        _POOL_MODES[mode], cot, feats, pooled, feats.shape[1],
+        relation['in_rows'], relation['out_rows'], relation['row_offsets'],
+        relation['counts'], relation['in_row_offsets'],
+        relation['in_edge_ids'], feats.shape[0], cot.shape[0], grad)
     return grad
 
 

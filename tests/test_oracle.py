@@ -442,3 +442,85 @@ def test_gradients_adjoint_to_the_forward_conv():
         # the mapped layout gives the same numbers, transposed
         gw_mapped = O.conv_weight_grad(feats, g, (ks ** 3, c_in, c_out), rel)
         np.testing.assert_allclose(O.mapped_weight(gw), gw_mapped, rtol=1e-6)
+
+
+# -------------------------------------------------------------- pooling --
+
+
+@pytest.mark.parametrize('mode', ['sum', 'max', 'avg'])
+def test_pool_golden(mode):
+    g = golden('pool_local_line')
+    rel = O.kernel_relation(np.array(g['coords'], np.int32),
+                            kernel_size=g['kernel_size'], stride=g['stride'])
+    feats = np.array(g['feats'], np.float32)
+    assert O.pool_features(feats, rel, mode).tolist() == g[mode]
+    gg = golden('pool_grad_line')
+    feats = np.array(gg['feats'], np.float32)
+    pooled = O.pool_features(feats, rel, mode)
+    got = O.pool_grad(np.ones_like(pooled), feats, pooled, rel, mode)
+    np.testing.assert_allclose(got, gg[mode], rtol=1e-6)
+
+
+def test_pool_max_tie_policy_golden():
+    g = golden('pool_max_ties')
+    rel = O.kernel_relation(np.array(g['coords'], np.int32),
+                            kernel_size=g['kernel_size'])
+    feats = np.array(g['feats'], np.float32)
+    pooled = O.pool_features(feats, rel, 'max')
+    assert pooled.tolist() == g['pooled']
+    assert O.pool_grad(np.ones_like(pooled), feats, pooled, rel,
+                       'max').tolist() == g['grad']
+
+
+def test_pool_strided_golden():
+    g = golden('pool_strided_pointwise')
+    rel = O.kernel_relation(np.array(g['coords'], np.int32),
+                            kernel_size=g['kernel_size'], stride=g['stride'])
+    n = int(rel['counts'][1])
+    assert rel['out_coords'][:n].tolist() == g['out_coords']
+    got = O.pool_features(np.array(g['feats'], np.float32), rel, 'sum')
+    assert got[:n].tolist() == g['sum']
+
+
+def _pool_brute(coords, feats, ks, stride, mode):
+    """Brute force from the definition: every output cell's reduction over
+    the active inputs inside its kernel window."""
+    rel = O.kernel_relation(coords, kernel_size=ks, stride=stride)
+    n_out = int(rel['counts'][1])
+    outs = rel['out_coords'][:n_out]
+    index = {tuple(c): i for i, c in enumerate(coords.tolist())}
+    offs = O.kernel_offsets(ks)
+    res = np.full((n_out, feats.shape[1]), -np.inf if mode == 'max' else 0.0)
+    deg = np.zeros(n_out)
+    for o, (b, x, y, z) in enumerate(outs.tolist()):
+        for dx, dy, dz in offs.tolist():
+            i = index.get((b, x * stride + dx, y * stride + dy, z * stride + dz))
+            if i is None:
+                continue
+            deg[o] += 1
+            res[o] = np.maximum(res[o], feats[i]) if mode == 'max' else res[o] + feats[i]
+    if mode == 'avg':
+        res /= np.maximum(deg, 1)[:, None]
+    return rel, res
+
+
+@pytest.mark.parametrize('mode', ['sum', 'max', 'avg'])
+@pytest.mark.parametrize('ks,stride', [(3, 1), (2, 2)])
+def test_pool_brute_force(mode, ks, stride):
+    rng = np.random.default_rng(20 + ks)
+    coords = np.unique(rng.integers(0, 10, (400, 3)), axis=0)
+    coords = np.concatenate([rng.integers(0, 2, (len(coords), 1)), coords],
+                            1).astype(np.int32)
+    coords = coords[rng.permutation(len(coords))]
+    feats = rng.standard_normal((len(coords), 3)).astype(np.float32)
+    rel, ref = _pool_brute(coords, feats, ks, stride, mode)
+    got = O.pool_features(feats, rel, mode)
+    n_out = ref.shape[0]
+    np.testing.assert_allclose(got[:n_out], ref, rtol=1e-5, atol=1e-6)
+    # gradient of sum/avg pooling is the adjoint of the forward
+    if mode != 'max':
+        g = rng.standard_normal(got.shape).astype(np.float32)
+        g[n_out:] = 0
+        gin = O.pool_grad(g, feats, got, rel, mode)
+        lhs = float((got[:n_out].astype(np.float64) * g[:n_out]).sum())
+        assert abs(lhs - float((feats.astype(np.float64) * gin).sum())) < 1e-3 * (1 + abs(lhs))
