@@ -294,6 +294,39 @@ def backward_workload(feats, weight, coords, active, edges: int, steps: int,
     }
 
 
+def pooling_workload(coords, steps: int, warmup: int) -> dict:
+    """max_pool3d k=2 s=2 over the config-3 cloud with 64 fp32 channels
+    (pooling is float32 only, as in the reference): the pooling kernel on a
+    cached relation, against the HBM roofline of its algorithmic bytes
+    (each input row read once, each output row written once, plus the CSR
+    offsets and the edge rows)."""
+    import torch
+
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor
+
+    n, c = int(coords.shape[0]), 64
+    gen = torch.Generator(device=coords.device).manual_seed(11)
+    feats = torch.randn((n, c), generator=gen, device=coords.device)
+    x = SparseTensor(coords, feats)
+    out = ops.max_pool3d(x, kernel_size=2, stride=2)
+    torch.cuda.synchronize()
+    rel = x.coord_manager.kernel_relation(x.coord_key, kernel_size=2,
+                                          stride=2)
+    n_out = int(rel.counts[1].item())
+    e = int(rel.counts[0].item())
+    t = _timed(lambda: ops.max_pool3d(x, kernel_size=2, stride=2), steps,
+               warmup)
+    bytes_ = n * c * 4 + out.feats.shape[0] * c * 4 + 4 * (n_out + 1) + 4 * e
+    return {
+        'workload': 'max_pool3d k=2 s=2, fp32 64 channels, config-3 cloud '
+                    '(cached relation)',
+        'rows_in': n, 'rows_out': n_out, 'ms': round(t, 4),
+        'gbs': round(bytes_ / t / 1e6, 1),
+        'hbm_frac': round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -405,6 +438,7 @@ def main() -> int:
     }
     record['backward'] = backward_workload(feats, weight, coords, active,
                                            edges, args.steps, args.warmup)
+    record['pooling'] = pooling_workload(coords, args.steps, args.warmup)
     if not args.no_secondary:
         record['secondary'] = secondary_workloads()
     if not args.no_cpu_baseline:
