@@ -21,6 +21,8 @@
  *                                    relations.cpp:540-581, bindings/coords.cpp:414-449
  *   build_submanifold_kernel_relation relations.cpp:583-597, bindings/coords.cpp:480-507
  *   build_target_kernel_relation     relations.cpp:672-722, bindings/coords.cpp:550-589
+ *   build_generative_relation        relations.cpp:599-629, bindings/coords.cpp:451-479
+ *   build_transposed_kernel_relation relations.cpp:631-670, bindings/coords.cpp:509-548
  *   build_relation_implicit_gemm_view relations.cpp:498-538, bindings/coords.cpp:590-626
  *   sorted implicit-GEMM view        mlx_lattice/core/relations/views.py:467-510
  *   sparse_conv_features             native/features/convolution/api.cpp:119-246,
@@ -68,7 +70,8 @@ enum lattice_weight_layout {
 
 /* Bits of the device status word written by the relation builders. */
 enum lattice_relation_flags {
-    LATTICE_STATUS_COORD_RANGE = 1 /* an active coordinate does not fit the packed key */
+    LATTICE_STATUS_COORD_RANGE = 1,   /* an active coordinate does not fit the packed key */
+    LATTICE_STATUS_REPEATED_EDGE = 2  /* transposed relation: two edges share (out_row, kernel_id) */
 };
 
 /* Packed-key coordinate range: batch in [0, LATTICE_MAX_BATCH], spatial
@@ -137,6 +140,33 @@ int lattice_hip_build_target_kernel_relation(
     const int stride[3], const int padding[3], const int dilation[3],
     const lattice_relation_outputs* out, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Generative and transposed relations (relation_build_detail.h:82-196;
+ * native builders relations.cpp:599-670).  Every active input row expands
+ * into K candidates coord * stride + offset[k] - padding; output and edge
+ * capacities are rows * K, so out->out_coords holds rows * K rows and
+ * out->out_in_map / out->row_masks are not used (may be NULL).
+ *   generative: output row in*K + k per candidate (no padding, no
+ *     dilation), one edge per row (write_generative_relation :82-117);
+ *   transposed: the same layout when every stride exceeds the offsets'
+ *     extent (can_use_direct_transposed_relation, relations.cpp:107-127);
+ *     otherwise first-seen deduplicated output rows and edges in
+ *     (out_row, kernel_id, in_row) order (:119-196).  A repeated input
+ *     coordinate sets LATTICE_STATUS_REPEATED_EDGE in out->status.
+ * Candidate tables need the packed-key range (LATTICE_STATUS_COORD_RANGE). */
+size_t lattice_hip_expanded_relation_workspace_bytes(
+    int rows, const int kernel_size[3], const int stride[3],
+    const int dilation[3], int generative);
+int lattice_hip_build_generative_relation(
+    const int32_t* coords, int rows, const int32_t* active_rows,
+    const int kernel_size[3], const int stride[3],
+    const lattice_relation_outputs* out, void* workspace,
+    size_t workspace_bytes, void* stream);
+int lattice_hip_build_transposed_kernel_relation(
+    const int32_t* coords, int rows, const int32_t* active_rows,
+    const int kernel_size[3], const int stride[3], const int padding[3],
+    const int dilation[3], const lattice_relation_outputs* out,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grouped CSR views of a relation: write_relation_grouped_view
  * (relation_views_detail.h:84-120; relations.cpp:438-476).  Stable

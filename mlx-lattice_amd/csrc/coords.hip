@@ -1039,3 +1039,300 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
+
+// ---------------------------------------------------- expanded relations --
+//
+// Generative and transposed relations (relation_build_detail.h:82-196)
+// expand every active input row into K candidates
+//     cand(j) = (b, coord * stride + offset[k] - padding),  j = in * K + k,
+// and give every (row, offset) exactly one edge.  Capacities are rows * K
+// for both the output rows and the edges (relations.cpp:599-670).
+//   * generative, and transposed when the stride exceeds the offsets' extent
+//     on every axis (can_use_direct_transposed_relation, relations.cpp:
+//     107-127): output row j is cand(j), edge j = (in, j, k).  One lane per j.
+//   * other transposed relations: the output rows are the distinct
+//     candidates in first-seen j order (a candidate table keeps the minimum
+//     j; a flag, a scan and a scatter place the representatives), and the
+//     edges run in (out_row, kernel_id, in_row) order (write_map,
+//     relation_views_detail.h:52-82).  That order is a stable sort by
+//     out_row of the j's listed kernel-major (t = k * rows + in), which
+//     already runs in (kernel_id, in_row) order.  A repeated input coordinate
+//     gives a second edge for the same (out_row, kernel_id); the edge pass
+//     flags that in the status word, since the dense out_in_map view cannot
+//     hold it.
+
+namespace lattice {
+namespace {
+
+__device__ inline int4 candidate_of(const int32_t* coords, int in, int k, const KernelGeometry& g,
+                                    int64_t* x, int64_t* y, int64_t* z) {
+    const int4 c = load_coord(coords, in);
+    const Int3 off = offset_of(k, g);
+    *x = static_cast<int64_t>(c.y) * g.stride.x + off.x - g.padding.x;
+    *y = static_cast<int64_t>(c.z) * g.stride.y + off.y - g.padding.y;
+    *z = static_cast<int64_t>(c.w) * g.stride.z + off.z - g.padding.z;
+    return make_int4(c.x, static_cast<int>(*x), static_cast<int>(*y), static_cast<int>(*z));
+}
+
+__global__ void __launch_bounds__(kThreads)
+expand_direct(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
+              KernelGeometry g, lattice_relation_outputs out) {
+    const int K = g.volume;
+    const long long cap = static_cast<long long>(rows) * K;
+    const int total = min(max(*active_rows, 0), rows) * K;
+    int4* oc = reinterpret_cast<int4*>(out.out_coords);
+    for (long long j = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; j <= cap;
+         j += static_cast<long long>(gridDim.x) * kThreads) {
+        if (j == cap) {
+            out.row_offsets[cap] = total;
+            out.counts[0] = total;
+            out.counts[1] = total;
+            continue;
+        }
+        if (j < total) {
+            const int in = static_cast<int>(j / K);
+            const int k = static_cast<int>(j - static_cast<long long>(in) * K);
+            int64_t x, y, z;
+            oc[j] = candidate_of(coords, in, k, g, &x, &y, &z);
+            out.in_rows[j] = in;
+            out.out_rows[j] = static_cast<int32_t>(j);
+            out.kernel_ids[j] = k;
+            out.row_offsets[j] = static_cast<int32_t>(j);
+        } else {
+            oc[j] = make_int4(0, 0, 0, 0);
+            out.in_rows[j] = 0;
+            out.out_rows[j] = 0;
+            out.kernel_ids[j] = 0;
+            out.row_offsets[j] = total;
+        }
+    }
+}
+
+__device__ inline bool candidate_key(const int32_t* coords, int in, int k, const KernelGeometry& g,
+                                     uint64_t* key) {
+    int64_t x, y, z;
+    const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
+    return pack_key(c.x, x, y, z, key);
+}
+
+__global__ void __launch_bounds__(kThreads)
+insert_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
+                  const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* status) {
+    const int K = g.volume;
+    const int total = min(max(*active_rows, 0), rows) * K;
+    for (int j = blockIdx.x * kThreads + threadIdx.x; j < total; j += gridDim.x * kThreads) {
+        const int in = j / K;
+        uint64_t key;
+        if (!candidate_key(coords, in, j - in * K, g, &key)) {
+            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+            continue;
+        }
+        table.insert(key, j);
+    }
+}
+
+// flags[j] = 1 when candidate j is the first of its coordinate.
+__global__ void __launch_bounds__(kThreads)
+flag_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
+                const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* __restrict__ flags) {
+    const int K = g.volume;
+    const int cap = rows * K;
+    const int total = min(max(*active_rows, 0), rows) * K;
+    for (int j = blockIdx.x * kThreads + threadIdx.x; j < cap; j += gridDim.x * kThreads) {
+        int flag = 0;
+        if (j < total) {
+            const int in = j / K;
+            uint64_t key;
+            if (candidate_key(coords, in, j - in * K, g, &key)) flag = table.find(key) == j ? 1 : 0;
+        }
+        flags[j] = flag;
+    }
+}
+
+// Output coordinates of the representatives at their first-seen position,
+// zero tail; keys[t] (t = k * rows + in) = output row of candidate in*K+k,
+// -1 for inactive rows (sorted last).
+__global__ void __launch_bounds__(kThreads)
+place_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
+                 const int32_t* __restrict__ active_rows, KernelGeometry g, const int32_t* __restrict__ flags,
+                 const int32_t* __restrict__ positions, const int32_t* __restrict__ counts,
+                 int32_t* __restrict__ out_coords, int32_t* __restrict__ keys) {
+    const int K = g.volume;
+    const int cap = rows * K;
+    const int active = min(max(*active_rows, 0), rows);
+    const int n_out = counts[1];
+    int4* oc = reinterpret_cast<int4*>(out_coords);
+    for (int j = blockIdx.x * kThreads + threadIdx.x; j < cap; j += gridDim.x * kThreads) {
+        const int in = j / K;
+        const int k = j - in * K;
+        int out_row = -1;
+        if (in < active) {
+            int64_t x, y, z;
+            const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
+            uint64_t key;
+            if (pack_key(c.x, x, y, z, &key)) {
+                const int rep = table.find(key);
+                if (rep >= 0) out_row = positions[rep];
+            }
+            if (flags[j]) oc[positions[j]] = c;
+        }
+        if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
+        keys[static_cast<long long>(k) * rows + in] = out_row;
+    }
+}
+
+// Edge e of the sorted order: t = sorted_index[e] -> (in, k); flags a
+// repeated (out_row, kernel_id).
+__global__ void __launch_bounds__(kThreads)
+emit_sorted_edges(const int32_t* __restrict__ sorted_keys, const int32_t* __restrict__ sorted_index, int rows,
+                  int K, const int32_t* __restrict__ active_rows, lattice_relation_outputs out) {
+    const int cap = rows * K;
+    const int total = min(max(*active_rows, 0), rows) * K;
+    if (blockIdx.x == 0 && threadIdx.x == 0) out.counts[0] = total;
+    for (int e = blockIdx.x * kThreads + threadIdx.x; e < cap; e += gridDim.x * kThreads) {
+        if (e < total) {
+            const int t = sorted_index[e];
+            const int k = t / rows;
+            out.in_rows[e] = t - k * rows;
+            out.out_rows[e] = sorted_keys[e];
+            out.kernel_ids[e] = k;
+            if (e > 0 && sorted_keys[e - 1] == sorted_keys[e] && sorted_index[e - 1] / rows == k) {
+                atomicOr(out.status, LATTICE_STATUS_REPEATED_EDGE);
+            }
+        } else {
+            out.in_rows[e] = 0;
+            out.out_rows[e] = 0;
+            out.kernel_ids[e] = 0;
+        }
+    }
+}
+
+bool direct_expansion(const KernelGeometry& g) {
+    // Offset extent per axis: (size - 1) * dilation.
+    return g.stride.x > (g.size.x - 1) * g.dilation.x && g.stride.y > (g.size.y - 1) * g.dilation.y &&
+           g.stride.z > (g.size.z - 1) * g.dilation.z;
+}
+
+size_t expanded_relation_bytes(int rows, int K, bool direct) {
+    const long long cap = static_cast<long long>(std::max(rows, 0)) * K;
+    size_t bytes = group_view_bytes(static_cast<int>(cap)) + 4096;
+    if (direct) return bytes;
+    const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
+    bytes += table_bytes(static_cast<int>(cap)) + 5 * n + scan_workspace_bytes(cap);
+    bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
+    return bytes;
+}
+
+int check_expanded_outputs(const lattice_relation_outputs* out, long long cap) {
+    LATTICE_REQUIRE(out != nullptr, "relation outputs are required.");
+    LATTICE_REQUIRE(out->row_offsets && out->counts && out->status && out->out_coords,
+                    "relation output pointers must be non-null.");
+    LATTICE_REQUIRE(cap == 0 || (out->in_rows && out->out_rows && out->kernel_ids),
+                    "relation output pointers must be non-null.");
+    const bool views = out->in_edge_ids != nullptr || out->kernel_edge_ids != nullptr;
+    LATTICE_REQUIRE(!views || (out->in_edge_ids && out->kernel_edge_ids && out->in_row_offsets &&
+                               out->kernel_row_offsets),
+                    "grouped view outputs must be all set or all null.");
+    return LATTICE_OK;
+}
+
+__global__ void clear_status(int32_t* status) { status[0] = 0; }
+
+int build_expanded_relation(const int32_t* coords, int rows, const int32_t* active_rows, const KernelGeometry& g,
+                            bool direct, const lattice_relation_outputs* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    const int K = g.volume;
+    LATTICE_REQUIRE(rows >= 0, "coords must have shape (N, 4).");
+    LATTICE_REQUIRE(rows == 0 || coords != nullptr, "coords must be non-null.");
+    LATTICE_REQUIRE(active_rows != nullptr, "active_rows must be non-null.");
+    LATTICE_REQUIRE(static_cast<long long>(rows) * K < (1ll << 30), "relation capacity rows * K exceeds 2^30.");
+    int rc = check_expanded_outputs(out, static_cast<long long>(rows) * K);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(workspace_bytes >= expanded_relation_bytes(rows, K, direct), "relation workspace too small.");
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    const int cap = rows * K;
+    clear_status<<<1, 1, 0, stream>>>(out->status);
+    LATTICE_LAUNCH_CHECK();
+    if (direct) {
+        expand_direct<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 16), kThreads, 0, stream>>>(
+            coords, rows, active_rows, g, *out);
+        LATTICE_LAUNCH_CHECK();
+    } else if (cap == 0) {
+        rc = fill_i32(out->row_offsets, 1, 0, stream);
+        if (rc != LATTICE_OK) return rc;
+        rc = fill_i32(out->counts, 2, 0, stream);
+        if (rc != LATTICE_OK) return rc;
+    } else {
+        CoordTable table;
+        rc = make_table(cap, ws, &table);
+        if (rc != LATTICE_OK) return rc;
+        int32_t* flags = ws.take<int32_t>(cap);
+        int32_t* positions = ws.take<int32_t>(cap);
+        int32_t* keys = ws.take<int32_t>(cap);
+        int32_t* sorted_keys = ws.take<int32_t>(cap);
+        int32_t* sorted_index = ws.take<int32_t>(cap);
+        LATTICE_REQUIRE(flags && positions && keys && sorted_keys && sorted_index, "relation workspace too small.");
+        const int tcap = static_cast<int>(table.mask) + 1;
+        clear_table<<<grid_for(tcap, kThreads, 4096), kThreads, 0, stream>>>(table.keys, table.rows, tcap);
+        LATTICE_LAUNCH_CHECK();
+        const unsigned grid = grid_for(cap, kThreads, 1u << 14);
+        insert_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, out->status);
+        LATTICE_LAUNCH_CHECK();
+        flag_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, flags);
+        LATTICE_LAUNCH_CHECK();
+        rc = exclusive_scan(flags, positions, cap, out->counts + 1, ws, stream);
+        if (rc != LATTICE_OK) return rc;
+        place_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, flags, positions,
+                                                        out->counts, out->out_coords, keys);
+        LATTICE_LAUNCH_CHECK();
+        const SortKeys sk{keys, 1, nullptr, cap, false};
+        rc = radix_sort_indices(sk, cap, bit_width(cap), sorted_keys, sorted_index, ws, stream);
+        if (rc != LATTICE_OK) return rc;
+        emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out);
+        LATTICE_LAUNCH_CHECK();
+        group_offsets<<<grid_for(cap + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted_keys, cap, cap,
+                                                                                 out->row_offsets);
+        LATTICE_LAUNCH_CHECK();
+    }
+    if (out->in_edge_ids == nullptr) return LATTICE_OK;
+    Workspace views{static_cast<char*>(workspace), workspace_bytes};
+    return build_group_views(out->in_rows, out->kernel_ids, out->counts, cap, rows, K, out->in_row_offsets,
+                             out->in_edge_ids, out->kernel_row_offsets, out->kernel_edge_ids, views, stream);
+}
+
+}  // namespace
+}  // namespace lattice
+
+extern "C" size_t lattice_hip_expanded_relation_workspace_bytes(int rows, const int kernel_size[3],
+                                                                const int stride[3], const int dilation[3],
+                                                                int generative) {
+    const int zero[3] = {0, 0, 0};
+    if (validate_geometry(kernel_size, stride, zero, dilation) != LATTICE_OK) return 0;
+    const KernelGeometry g = make_geometry(kernel_size, stride, zero, dilation);
+    return expanded_relation_bytes(rows, g.volume, generative != 0 || direct_expansion(g));
+}
+
+extern "C" int lattice_hip_build_generative_relation(const int32_t* coords, int rows, const int32_t* active_rows,
+                                                     const int kernel_size[3], const int stride[3],
+                                                     const lattice_relation_outputs* out, void* workspace,
+                                                     size_t workspace_bytes, void* stream_ptr) {
+    const int zero[3] = {0, 0, 0};
+    const int one[3] = {1, 1, 1};
+    int rc = validate_geometry(kernel_size, stride, zero, one);
+    if (rc != LATTICE_OK) return rc;
+    return build_expanded_relation(coords, rows, active_rows, make_geometry(kernel_size, stride, zero, one), true,
+                                   out, workspace, workspace_bytes, as_stream(stream_ptr));
+}
+
+extern "C" int lattice_hip_build_transposed_kernel_relation(const int32_t* coords, int rows,
+                                                            const int32_t* active_rows, const int kernel_size[3],
+                                                            const int stride[3], const int padding[3],
+                                                            const int dilation[3],
+                                                            const lattice_relation_outputs* out, void* workspace,
+                                                            size_t workspace_bytes, void* stream_ptr) {
+    int rc = validate_geometry(kernel_size, stride, padding, dilation);
+    if (rc != LATTICE_OK) return rc;
+    const KernelGeometry g = make_geometry(kernel_size, stride, padding, dilation);
+    return build_expanded_relation(coords, rows, active_rows, g, direct_expansion(g), out, workspace,
+                                   workspace_bytes, as_stream(stream_ptr));
+}

@@ -152,6 +152,63 @@ def build_target_kernel_relation(
         stride=spec.stride, padding=spec.padding, kind='target')
 
 
+def build_generative_relation(coords: torch.Tensor,
+                              active_rows: torch.Tensor | None = None,
+                              kernel_size: int | Sequence[int] = 2,
+                              stride: int | Sequence[int] = 2
+                              ) -> KernelRelation:
+    """Generative transpose-convolution relation (builders.py:236-265):
+    output row ``in * K + k`` is ``coord * stride + offset[k]``, one edge
+    per output row; offsets without dilation."""
+    validate_coords(coords)
+    kernel = triple(kernel_size, name='kernel_size')
+    step = triple(stride, name='stride')
+    _require_positive(kernel, 'kernel_size')
+    _require_positive(step, 'stride')
+    offsets = kernel_offsets(kernel)
+    source_active = _active_rows(active_rows, coords)
+    native = _ext().build_generative_relation_lazy(
+        coords, source_active, list(kernel), list(step))
+    return _kernel_relation_from_native(
+        native[:10], offsets=offsets, in_capacity=int(coords.shape[0]),
+        source_coords=coords, source_active_rows=source_active, stride=step,
+        kind='generative', repeated_edges=False)
+
+
+def build_transposed_kernel_relation(coords: torch.Tensor,
+                                     active_rows: torch.Tensor | None = None,
+                                     kernel_size: int | Sequence[int] = 2,
+                                     stride: int | Sequence[int] = 2,
+                                     padding: int | Sequence[int] = 0,
+                                     dilation: int | Sequence[int] = 1
+                                     ) -> KernelRelation:
+    """Sparse transpose-convolution relation (builders.py:268-306): the
+    candidates ``coord * stride + offset - padding`` of every input row,
+    one output row each when the stride exceeds the offsets' extent,
+    otherwise deduplicated in first-seen order."""
+    validate_coords(coords)
+    kernel = triple(kernel_size, name='kernel_size')
+    step = triple(stride, name='stride')
+    pad = triple(padding, name='padding')
+    rate = triple(dilation, name='dilation')
+    _require_positive(kernel, 'kernel_size')
+    _require_positive(step, 'stride')
+    if any(value < 0 for value in pad):
+        raise ValueError('padding values must be non-negative.')
+    _require_positive(rate, 'dilation')
+    offsets = kernel_offsets(kernel, rate)
+    source_active = _active_rows(active_rows, coords)
+    native = _ext().build_transposed_kernel_relation_lazy(
+        coords, source_active, list(kernel), list(step), list(pad),
+        list(rate))
+    flags = int(native[10])
+    return _kernel_relation_from_native(
+        native[:10], offsets=offsets, in_capacity=int(coords.shape[0]),
+        source_coords=coords, source_active_rows=source_active, stride=step,
+        padding=pad, kind='transposed',
+        repeated_edges=None if flags < 0 else bool(flags & 2))
+
+
 def _kernel_relation_from_native(
         native, *, offsets: tuple[Triple, ...], in_capacity: int,
         out_coords: torch.Tensor | None = None,
@@ -159,7 +216,8 @@ def _kernel_relation_from_native(
         target_coords: torch.Tensor | None = None,
         target_active_rows: torch.Tensor | None = None,
         stride: Triple = (1, 1, 1), padding: Triple = (0, 0, 0),
-        kind: RelationKind = 'forward') -> KernelRelation:
+        kind: RelationKind = 'forward',
+        repeated_edges: bool | None = None) -> KernelRelation:
     (in_rows, out_rows, kernel_ids, row_offsets, native_out_coords, counts,
      in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids,
      *view) = native
@@ -185,7 +243,7 @@ def _kernel_relation_from_native(
         source_active_rows=source_active_rows, target_coords=target_coords,
         target_active_rows=target_active_rows, stride=stride,
         padding=padding, kind=kind, implicit_gemm=implicit,
-        grouped_views=grouped_views)
+        grouped_views=grouped_views, repeated_edges=repeated_edges)
 
 
 def _require_positive(values: Triple, name: str) -> None:

@@ -10,9 +10,11 @@ from itertools import count
 import torch
 
 from mlx_lattice_amd.core.coords.builders import (
+    build_generative_relation,
     build_kernel_relation,
     build_submanifold_kernel_relation,
     build_target_kernel_relation,
+    build_transposed_kernel_relation,
 )
 from mlx_lattice_amd.core.coords.validation import validate_coords
 from mlx_lattice_amd.core.relations import KernelRelation, KernelSpec
@@ -108,6 +110,38 @@ class CoordinateManager:
                 self.coords(key), active_rows=self.active_rows(key),
                 kernel_size=spec.size, stride=spec.stride,
                 padding=spec.padding, dilation=spec.dilation)
+        return self._kernel_relations[cache_key]
+
+    def generative_relation(self, key: CoordinateMapKey, *,
+                            kernel_size: int | Sequence[int] = 2,
+                            stride: int | Sequence[int] = 2) -> KernelRelation:
+        """Build or reuse a generative transpose-convolution relation
+        (manager.py:176-198)."""
+        spec = KernelSpec(size=kernel_size, stride=stride)
+        cache_key = (key, None, spec, 'generative')
+        if cache_key not in self._kernel_relations:
+            self._kernel_relations[cache_key] = build_generative_relation(
+                self.coords(key), active_rows=self.active_rows(key),
+                kernel_size=spec.size, stride=spec.stride)
+        return self._kernel_relations[cache_key]
+
+    def transposed_kernel_relation(self, key: CoordinateMapKey, *,
+                                   kernel_size: int | Sequence[int] = 2,
+                                   stride: int | Sequence[int] = 2,
+                                   padding: int | Sequence[int] = 0,
+                                   dilation: int | Sequence[int] = 1
+                                   ) -> KernelRelation:
+        """Build or reuse a transpose-convolution relation
+        (manager.py:231-264)."""
+        spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
+                          dilation=dilation)
+        cache_key = (key, None, spec, 'transpose')
+        if cache_key not in self._kernel_relations:
+            self._kernel_relations[cache_key] = (
+                build_transposed_kernel_relation(
+                    self.coords(key), active_rows=self.active_rows(key),
+                    kernel_size=spec.size, stride=spec.stride,
+                    padding=spec.padding, dilation=spec.dilation))
         return self._kernel_relations[cache_key]
 
     def submanifold_kernel_relation(

@@ -191,6 +191,10 @@ class KernelRelation:
     implicit_gemm: RelationImplicitGemmView | None = None
     sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
     transposed_sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
+    # Transposed relations only: whether two edges share (out_row, kernel_id)
+    # (a repeated input coordinate), as the builder's status word reported;
+    # None when not read back.
+    repeated_edges: bool | None = None
 
     def __init__(
         self,
@@ -219,6 +223,7 @@ class KernelRelation:
         implicit_gemm: RelationImplicitGemmView | None = None,
         sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None,
         grouped_views: Callable[[], tuple] | None = None,
+        repeated_edges: bool | None = None,
     ) -> None:
         """``grouped_views``, when given and the input/kernel CSR arrays are
         not, is called on first access of ``input_csr`` / ``kernel_csr`` and
@@ -284,6 +289,7 @@ class KernelRelation:
         object.__setattr__(self, 'implicit_gemm', implicit_gemm)
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
         object.__setattr__(self, 'transposed_sorted_implicit_gemm', None)
+        object.__setattr__(self, 'repeated_edges', repeated_edges)
 
     @property
     def input_csr(self) -> RelationCSRView:
@@ -383,6 +389,10 @@ class KernelRelation:
         """Return or lazily build the implicit-GEMM view (views.py:452-465)."""
         if self.implicit_gemm is not None:
             return self.implicit_gemm
+        if self.contract.kind in ('transposed', 'generative'):
+            view = self._expanded_implicit_gemm()
+            object.__setattr__(self, 'implicit_gemm', view)
+            return view
         from mlx_lattice_amd.core.coords.builders import (
             build_relation_implicit_gemm_view,
         )
@@ -390,6 +400,34 @@ class KernelRelation:
         view = build_relation_implicit_gemm_view(self)
         object.__setattr__(self, 'implicit_gemm', view)
         return view
+
+    @property
+    def dense_map_exact(self) -> bool:
+        """Whether the dense (out_row, offset) -> in_row map holds every edge:
+        at most one edge per (out_row, kernel_id).  Forward, submanifold and
+        generative relations hold it by construction (a target relation
+        too: each (target row, offset) has one candidate input, its first
+        row); a transposed relation does unless an input coordinate repeats."""
+        if self.contract.kind != 'transposed':
+            return True
+        if self.repeated_edges is None:
+            return False
+        return not self.repeated_edges
+
+    def _expanded_implicit_gemm(self) -> RelationImplicitGemmView:
+        """Dense map of a generative or transposed relation, scattered from
+        its edges: out_in_map[out][k] = in (the expanded relations carry no
+        source table to query)."""
+        if not self.dense_map_exact:
+            raise ValueError('the dense implicit-GEMM map cannot hold a '
+                             'relation with repeated (out_row, kernel_id) '
+                             'edges.')
+        from mlx_lattice_amd._native import ext
+
+        out_in_map, row_masks = ext.build_transposed_implicit_gemm_map(
+            self.edges.out_rows, self.edges.in_rows, self.edges.kernel_ids,
+            self.counts, int(self.n_out_capacity), int(self.n_kernels))
+        return RelationImplicitGemmView(out_in_map, row_masks=row_masks)
 
     def require_sorted_implicit_gemm(self) -> RelationSortedImplicitGemmView:
         """Return or lazily build the mask-sorted view (views.py:467-510):
@@ -418,13 +456,16 @@ class KernelRelation:
         row per offset), built on first use and cached: the matrix-core
         route of the input gradient runs the forward's implicit GEMM over
         it.  Forward and submanifold relations have at most one output row
-        per (input row, offset), so the transposed map is dense; target
-        relations (whose target may repeat a coordinate) are refused."""
+        per (input row, offset), and generative and transposed relations
+        exactly one, so the transposed map is dense; target relations (whose
+        target may repeat a coordinate) are refused."""
         if self.transposed_sorted_implicit_gemm is not None:
             return self.transposed_sorted_implicit_gemm
-        if self.contract.kind not in ('forward', 'submanifold'):
+        if self.contract.kind not in ('forward', 'submanifold', 'transposed',
+                                      'generative'):
             raise ValueError('the transposed implicit-GEMM view needs a '
-                             'forward or submanifold relation.')
+                             'forward, submanifold, transposed or generative '
+                             'relation.')
         if self.n_in_capacity is None or self.n_kernels is None:
             raise ValueError('kernel relation is missing static shape metadata.')
         if self.n_kernels > 32:

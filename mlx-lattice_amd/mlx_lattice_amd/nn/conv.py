@@ -12,9 +12,15 @@ import torch
 from torch import nn
 
 from mlx_lattice_amd.core import CoordinateMapKey, KernelSpec, SparseTensor
-from mlx_lattice_amd.ops import conv3d, subm_conv3d
+from mlx_lattice_amd.ops import (
+    conv3d,
+    conv_transpose3d,
+    generative_conv_transpose3d,
+    subm_conv3d,
+)
 
-__all__ = ['Conv3d', 'SubmConv3d']
+__all__ = ['Conv3d', 'ConvTranspose3d', 'GenerativeConvTranspose3d',
+           'SubmConv3d']
 
 
 class Conv3d(nn.Module):
@@ -75,6 +81,69 @@ class SubmConv3d(nn.Module):
         _validate_quantize_request(mode, quantize_input)
         return QuantizedSubmConv3d.from_conv(self, group_size=group_size,
                                              bits=4 if bits is None else bits)
+
+
+class ConvTranspose3d(nn.Module):
+    """Sparse transposed convolution delegating to
+    :func:`conv_transpose3d` (nn/conv.py:173-234)."""
+
+    def __init__(self, in_channels: int, out_channels: int, *,
+                 kernel_size: int | Sequence[int] = 2,
+                 stride: int | Sequence[int] = 2,
+                 padding: int | Sequence[int] = 0,
+                 dilation: int | Sequence[int] = 1, bias: bool = True,
+                 device=None, dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self.spec = KernelSpec(size=kernel_size, stride=stride,
+                               padding=padding, dilation=dilation)
+        _init_kernel_params(self, in_channels, out_channels, self.spec, bias,
+                            device, dtype)
+
+    def forward(self, x: SparseTensor) -> SparseTensor:
+        return conv_transpose3d(x, self.weight, self.bias,
+                                kernel_size=self.spec.size,
+                                stride=self.spec.stride,
+                                padding=self.spec.padding,
+                                dilation=self.spec.dilation)
+
+    def to_quantized(self, group_size: int | None = None,
+                     bits: int | None = None, *, mode: str = 'affine',
+                     quantize_input: bool = False):
+        from mlx_lattice_amd.nn.quantized_conv import QuantizedConvTranspose3d
+
+        _validate_quantize_request(mode, quantize_input)
+        return QuantizedConvTranspose3d.from_conv(
+            self, group_size=group_size, bits=4 if bits is None else bits)
+
+
+class GenerativeConvTranspose3d(nn.Module):
+    """Generative transposed convolution delegating to
+    :func:`generative_conv_transpose3d` (nn/conv.py:237-296)."""
+
+    def __init__(self, in_channels: int, out_channels: int, *,
+                 kernel_size: int | Sequence[int] = 2,
+                 stride: int | Sequence[int] = 2, bias: bool = True,
+                 device=None, dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self.spec = KernelSpec(size=kernel_size, stride=stride)
+        _init_kernel_params(self, in_channels, out_channels, self.spec, bias,
+                            device, dtype)
+
+    def forward(self, x: SparseTensor) -> SparseTensor:
+        return generative_conv_transpose3d(x, self.weight, self.bias,
+                                           kernel_size=self.spec.size,
+                                           stride=self.spec.stride)
+
+    def to_quantized(self, group_size: int | None = None,
+                     bits: int | None = None, *, mode: str = 'affine',
+                     quantize_input: bool = False):
+        from mlx_lattice_amd.nn.quantized_conv import (
+            QuantizedGenerativeConvTranspose3d,
+        )
+
+        _validate_quantize_request(mode, quantize_input)
+        return QuantizedGenerativeConvTranspose3d.from_conv(
+            self, group_size=group_size, bits=4 if bits is None else bits)
 
 
 def _init_kernel_params(module: nn.Module, in_channels: int,

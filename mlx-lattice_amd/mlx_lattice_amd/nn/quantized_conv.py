@@ -14,10 +14,21 @@ from mlx_lattice_amd.core import (
     SparseTensor,
     quantize_weight,
 )
-from mlx_lattice_amd.nn.conv import Conv3d, SubmConv3d
-from mlx_lattice_amd.ops import conv3d, subm_conv3d
+from mlx_lattice_amd.nn.conv import (
+    Conv3d,
+    ConvTranspose3d,
+    GenerativeConvTranspose3d,
+    SubmConv3d,
+)
+from mlx_lattice_amd.ops import (
+    conv3d,
+    conv_transpose3d,
+    generative_conv_transpose3d,
+    subm_conv3d,
+)
 
-__all__ = ['QuantizedConv3d', 'QuantizedSubmConv3d']
+__all__ = ['QuantizedConv3d', 'QuantizedConvTranspose3d',
+           'QuantizedGenerativeConvTranspose3d', 'QuantizedSubmConv3d']
 
 
 class _QuantizedConvBase(nn.Module):
@@ -101,6 +112,71 @@ class QuantizedSubmConv3d(_QuantizedConvBase):
     @classmethod
     def from_conv(cls, source: SubmConv3d, group_size: int | None = None,
                   bits: int = 4) -> QuantizedSubmConv3d:
+        out = cls.__new__(cls)
+        _QuantizedConvBase.__init__(out)
+        out._copy_from(source, group_size, bits)
+        return out
+
+
+class QuantizedConvTranspose3d(_QuantizedConvBase):
+    """Packed int4/int8 ``ConvTranspose3d`` (nn/quantized_conv.py:235-310)."""
+
+    def __init__(self, in_channels: int, out_channels: int, *,
+                 kernel_size: int | Sequence[int] = 2,
+                 stride: int | Sequence[int] = 2,
+                 padding: int | Sequence[int] = 0,
+                 dilation: int | Sequence[int] = 1, bias: bool = True,
+                 group_size: int | None = None, bits: int = 4, device=None,
+                 dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self._copy_from(ConvTranspose3d(in_channels, out_channels,
+                                        kernel_size=kernel_size,
+                                        stride=stride, padding=padding,
+                                        dilation=dilation, bias=bias,
+                                        device=device, dtype=dtype),
+                        group_size, bits)
+
+    def forward(self, x: SparseTensor) -> SparseTensor:
+        return conv_transpose3d(x, self._quantized_weight(), self.bias,
+                                kernel_size=self.spec.size,
+                                stride=self.spec.stride,
+                                padding=self.spec.padding,
+                                dilation=self.spec.dilation)
+
+    @classmethod
+    def from_conv(cls, source: ConvTranspose3d, group_size: int | None = None,
+                  bits: int = 4) -> QuantizedConvTranspose3d:
+        out = cls.__new__(cls)
+        _QuantizedConvBase.__init__(out)
+        out._copy_from(source, group_size, bits)
+        return out
+
+
+class QuantizedGenerativeConvTranspose3d(_QuantizedConvBase):
+    """Packed int4/int8 ``GenerativeConvTranspose3d``
+    (nn/quantized_conv.py:313-380)."""
+
+    def __init__(self, in_channels: int, out_channels: int, *,
+                 kernel_size: int | Sequence[int] = 2,
+                 stride: int | Sequence[int] = 2, bias: bool = True,
+                 group_size: int | None = None, bits: int = 4, device=None,
+                 dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self._copy_from(GenerativeConvTranspose3d(
+            in_channels, out_channels, kernel_size=kernel_size,
+            stride=stride, bias=bias, device=device, dtype=dtype),
+            group_size, bits)
+
+    def forward(self, x: SparseTensor) -> SparseTensor:
+        return generative_conv_transpose3d(x, self._quantized_weight(),
+                                           self.bias,
+                                           kernel_size=self.spec.size,
+                                           stride=self.spec.stride)
+
+    @classmethod
+    def from_conv(cls, source: GenerativeConvTranspose3d,
+                  group_size: int | None = None,
+                  bits: int = 4) -> QuantizedGenerativeConvTranspose3d:
         out = cls.__new__(cls)
         _QuantizedConvBase.__init__(out)
         out._copy_from(source, group_size, bits)

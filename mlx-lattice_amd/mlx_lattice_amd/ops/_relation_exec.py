@@ -4,8 +4,9 @@
 Route policy (this build's, the reference routes by Metal capability):
 fp16/bf16 features with ``C_in % 32 == 0``, ``C_out`` in {16, 32, 64, 128,
 256} and at most 32 kernel offsets run the matrix-core implicit GEMM over the
-mask-sorted view; everything else (fp32, small or odd channel counts) runs
-the CSR bandwidth kernel.  Both routes compute the same sum with an fp32
+mask-sorted view, for every relation kind whose edges fit the dense
+(out_row, offset) map; everything else (fp32, small or odd channel counts)
+runs the CSR bandwidth kernel.  Both routes compute the same sum with an fp32
 accumulator.
 """
 
@@ -36,8 +37,10 @@ def _require_static(relation: KernelRelation) -> None:
 def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
                           relation: KernelRelation, n_in: int = 0) -> bool:
     """Shapes the matrix-core kernel takes; its 32-bit gather offsets need
-    the feature table under 2 GiB."""
-    return (relation.contract.kind in ('forward', 'target', 'submanifold')
+    the feature table under 2 GiB.  The relation must fit the dense
+    (out_row, offset) map: a transposed relation with a repeated input
+    coordinate runs the CSR route."""
+    return (relation.dense_map_exact
             and dtype in (torch.float16, torch.bfloat16)
             and c_in % 32 == 0 and c_in <= 512
             and c_out in _MATRIX_CORE_C_OUT
@@ -93,7 +96,7 @@ def _input_grad_matrix_core_eligible(cot: torch.Tensor, weight: torch.Tensor,
     columns."""
     c_in = int(weight.shape[1] if weight.ndim == 3 else weight.shape[4])
     c_out = int(cot.shape[1])
-    return (relation.contract.kind in ('forward', 'submanifold')
+    return (relation.contract.kind != 'target'
             and cot.dtype in (torch.float16, torch.bfloat16)
             and c_out % 32 == 0 and c_out <= 512
             and c_in in _MATRIX_CORE_C_OUT

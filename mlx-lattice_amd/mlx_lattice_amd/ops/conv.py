@@ -1,10 +1,9 @@
 """Sparse convolution operators (mlx_lattice/ops/conv.py:34-493).
 
-``conv3d`` / ``subm_conv3d`` keep the reference signature, validation
+``conv3d`` / ``subm_conv3d`` / ``conv_transpose3d`` /
+``generative_conv_transpose3d`` keep the reference signatures, validation
 messages and coordinate-identity rules.  Relations come from the coordinate
-manager's cache and run on the gfx950 kernels.  Transposed and generative
-convolutions are outside this build's hot path and raise
-``NotImplementedError``.
+manager's cache and run on the gfx950 kernels.
 """
 
 from __future__ import annotations
@@ -86,24 +85,23 @@ def subm_conv3d(x: SparseTensor, weight: torch.Tensor | QuantizedWeight,
 
 def conv_transpose3d(x: SparseTensor, weight, bias=None, *, kernel_size=2,
                      stride=2, padding=0, dilation=1) -> SparseTensor:
-    """Transposed sparse convolution (ops/conv.py:153-186): not part of this
-    build's hot path."""
+    """Sparse transposed convolution over the transposed relation
+    (ops/conv.py:153-186).  The output stride is ``x.stride / stride``; each
+    component of ``stride`` must divide the input stride."""
     spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
                       dilation=dilation)
-    _div_stride(x.stride, spec.stride)
-    raise NotImplementedError(
-        'conv_transpose3d is outside the MI355X hot path of this build.')
+    return _relation_conv(x, weight, bias, spec, map_kind='transposed',
+                          output_stride=_div_stride(x.stride, spec.stride))
 
 
 def generative_conv_transpose3d(x: SparseTensor, weight, bias=None, *,
                                 kernel_size=2, stride=2) -> SparseTensor:
-    """Generative transposed convolution (ops/conv.py:189-214): not part of
-    this build's hot path."""
+    """Transposed convolution whose output support is generated from every
+    input row and offset (ops/conv.py:189-214): output row ``in * K + k``
+    at ``coord * stride + offset[k]``."""
     spec = KernelSpec(size=kernel_size, stride=stride)
-    _div_stride(x.stride, spec.stride)
-    raise NotImplementedError(
-        'generative_conv_transpose3d is outside the MI355X hot path of this '
-        'build.')
+    return _relation_conv(x, weight, bias, spec, map_kind='generative',
+                          output_stride=_div_stride(x.stride, spec.stride))
 
 
 # ------------------------------------------------------ execution policy --
@@ -148,13 +146,22 @@ def _kernel_relation(x: SparseTensor, spec: KernelSpec, map_kind: str, *,
     if map_kind == 'submanifold':
         return manager.submanifold_kernel_relation(
             x.coord_key, kernel_size=spec.size, dilation=spec.dilation)
+    if map_kind == 'transposed':
+        return manager.transposed_kernel_relation(
+            x.coord_key, kernel_size=spec.size, stride=spec.stride,
+            padding=spec.padding, dilation=spec.dilation)
+    if map_kind == 'generative':
+        return manager.generative_relation(
+            x.coord_key, kernel_size=spec.size, stride=spec.stride)
     if map_kind == 'target':
         if target_key is None:
             raise ValueError('target_key is required for target relations.')
         return manager.target_kernel_relation(
             x.coord_key, target_key, kernel_size=spec.size,
             stride=spec.stride, padding=spec.padding, dilation=spec.dilation)
-    raise ValueError("map_kind must be 'forward', 'submanifold', or 'target'.")
+    raise ValueError(
+        "map_kind must be 'forward', 'submanifold', 'transposed', "
+        "'generative', or 'target'.")
 
 
 def _target_key(x: SparseTensor, coordinates, output_stride: Triple,

@@ -106,6 +106,43 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
           py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
 
+    // Generative / transposed relations.  The *_lazy variants leave the
+    // grouped views to build_relation_grouped_views and append the status
+    // flags read by the range check (-1 when not checked).
+    auto expanded = [](bool generative, bool lazy) {
+        return [generative, lazy](const at::Tensor& coords, const at::Tensor& active_rows,
+                                  const std::vector<int>& kernel_size, const std::vector<int>& stride,
+                                  const std::vector<int>& padding, const std::vector<int>& dilation,
+                                  bool check_range) -> py::tuple {
+            auto r = ln::make_expanded_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
+                                                triple_from_values(stride, "stride"),
+                                                triple_from_values(padding, "padding"),
+                                                triple_from_values(dilation, "dilation"), generative, check_range,
+                                                !lazy);
+            if (!lazy) return relation_tuple(r);
+            return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
+                                  py::none(), py::none(), py::none(), py::none(), r.status_flags);
+        };
+    };
+    auto generative = [expanded](bool lazy) {
+        auto fn = expanded(true, lazy);
+        return [fn](const at::Tensor& coords, const at::Tensor& active_rows, const std::vector<int>& kernel_size,
+                    const std::vector<int>& stride, bool check_range) {
+            return fn(coords, active_rows, kernel_size, stride, {0}, {1}, check_range);
+        };
+    };
+    m.def("build_generative_relation", generative(false), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("stride"), py::kw_only(), py::arg("check_range") = true,
+          "Build a generative sparse kernel relation.");
+    m.def("build_generative_relation_lazy", generative(true), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("stride"), py::kw_only(), py::arg("check_range") = true);
+    m.def("build_transposed_kernel_relation", expanded(false, false), py::arg("coords"), py::arg("active_rows"),
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
+          py::arg("check_range") = true, "Build a transposed sparse kernel relation.");
+    m.def("build_transposed_kernel_relation_lazy", expanded(false, true), py::arg("coords"),
+          py::arg("active_rows"), py::arg("kernel_size"), py::arg("stride"), py::arg("padding"),
+          py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+
     m.def(
         "build_relation_grouped_views",
         [](const at::Tensor& in_rows, const at::Tensor& kernel_ids, const at::Tensor& counts, int in_capacity,

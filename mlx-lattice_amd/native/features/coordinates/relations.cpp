@@ -45,13 +45,14 @@ void validate_nonnegative(const Triple& v, const char* name) {
 
 // Raises when a builder flagged an active coordinate that does not fit the
 // packed key (reads one device word; the only host wait of a build).
-void check_coordinate_range(const at::Tensor& status) {
+int check_coordinate_range(const at::Tensor& status) {
     const int32_t flags = status.item<int32_t>();
     if (flags & LATTICE_STATUS_COORD_RANGE) {
         throw std::invalid_argument(
             "coordinates exceed the GPU packed-key range: batch must lie in [0, 1022] and x, y, z in "
             "[-131072, 131071].");
     }
+    return flags;
 }
 
 NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_capacity, int K, bool coords,
@@ -171,6 +172,71 @@ NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, co
         kernel_size.data(), stride.data(), padding.data(), dilation.data(), &o, ws.data_ptr(),
         static_cast<size_t>(ws.numel()), current_stream(coords)));
     if (check_range) check_coordinate_range(status);
+    return r;
+}
+
+NativeKernelRelation make_expanded_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
+                                            Triple kernel_size, Triple stride, Triple padding, Triple dilation,
+                                            bool generative, bool check_range, bool with_views) {
+    validate_coords(coords_in);
+    validate_active_rows(active_rows);
+    validate_positive(kernel_size, "kernel_size");
+    validate_positive(stride, "stride");
+    if (generative) {
+        padding = {0, 0, 0};
+        dilation = {1, 1, 1};
+    }
+    validate_nonnegative(padding, "padding");
+    validate_positive(dilation, "dilation");
+    require_on_device({{&coords_in, "coords"}, {&active_rows, "active_rows"}});
+    const at::Tensor coords = coords_in.contiguous();
+    const int rows = static_cast<int>(coords.size(0));
+    const int K = kernel_size[0] * kernel_size[1] * kernel_size[2];
+    if (static_cast<int64_t>(rows) * K >= (int64_t{1} << 30)) {
+        throw std::invalid_argument("relation capacity rows * K exceeds 2^30.");
+    }
+    const int cap = rows * K;
+    NativeKernelRelation r;
+    r.in_rows = empty_i32({cap}, coords);
+    r.out_rows = empty_i32({cap}, coords);
+    r.kernel_ids = empty_i32({cap}, coords);
+    r.output_row_offsets = empty_i32({cap + 1}, coords);
+    r.out_coords = empty_i32({cap, 4}, coords);
+    r.counts = empty_i32({2}, coords);
+    if (with_views) {
+        r.in_row_offsets = empty_i32({rows + 1}, coords);
+        r.in_edge_ids = empty_i32({cap}, coords);
+        r.kernel_row_offsets = empty_i32({K + 1}, coords);
+        r.kernel_edge_ids = empty_i32({cap}, coords);
+    }
+    at::Tensor status = empty_i32({1}, coords);
+    lattice_relation_outputs o{};
+    o.in_rows = i32(r.in_rows);
+    o.out_rows = i32(r.out_rows);
+    o.kernel_ids = i32(r.kernel_ids);
+    o.row_offsets = i32(r.output_row_offsets);
+    o.out_coords = i32(r.out_coords);
+    o.counts = i32(r.counts);
+    if (with_views) {
+        o.in_row_offsets = i32(r.in_row_offsets);
+        o.in_edge_ids = i32(r.in_edge_ids);
+        o.kernel_row_offsets = i32(r.kernel_row_offsets);
+        o.kernel_edge_ids = i32(r.kernel_edge_ids);
+    }
+    o.status = i32(status);
+    at::Tensor ws = workspace(lattice_hip_expanded_relation_workspace_bytes(rows, kernel_size.data(), stride.data(),
+                                                                           dilation.data(), generative ? 1 : 0),
+                              coords);
+    if (generative) {
+        check_status(lattice_hip_build_generative_relation(ci32(coords), rows, ci32(active_rows), kernel_size.data(),
+                                                           stride.data(), &o, ws.data_ptr(),
+                                                           static_cast<size_t>(ws.numel()), current_stream(coords)));
+    } else {
+        check_status(lattice_hip_build_transposed_kernel_relation(
+            ci32(coords), rows, ci32(active_rows), kernel_size.data(), stride.data(), padding.data(),
+            dilation.data(), &o, ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream(coords)));
+    }
+    if (check_range) r.status_flags = check_coordinate_range(status);
     return r;
 }
 

@@ -18,6 +18,13 @@
 //                                  brute force over small seeded clouds, E = N
 //                                  for k2s2, a self edge per submanifold row.
 //   oracle_target_kernel_relation  reference known answers, brute force.
+//   oracle_generative_relation     reference known answers (test_coordinate_
+//   oracle_transposed_kernel_      primitives.py:387-423, test_conv.py:674-700),
+//     relation                     brute force over seeded clouds, edge sets
+//                                  equal to the forward relation from the
+//                                  transposed output back to the input, and
+//                                  conv over them == torch conv_transpose3d
+//                                  on a fully occupied box.
 //   oracle_grouped_view            reference known answers (the 10-tuple's
 //                                  grouped CSR entries).
 //   oracle_implicit_gemm_view      reference known answers (forward, target,
@@ -309,6 +316,103 @@ void oracle_target_kernel_relation(
                    kernel_ids, row_offsets);
     counts[0] = static_cast<int32_t>(edges.size());
     counts[1] = t_active;
+}
+
+// write_generative_relation: relation_build_detail.h:82-117.  Output row
+// in*K + k is coord*stride + offset[k] (no padding, no deduplication); one
+// edge per output row.  Capacities rows*K (relations.cpp:599-629).
+void oracle_generative_relation(const int32_t* coords, int rows,
+                                int active_rows, const int32_t* offsets, int K,
+                                const int* stride, int32_t* in_rows,
+                                int32_t* out_rows, int32_t* kernel_ids,
+                                int32_t* row_offsets, int32_t* out_coords,
+                                int32_t* counts) {
+    auto values = read_coords(coords, rows);
+    values.resize(std::min(active_rows, rows));
+    std::vector<Edge> edges;
+    std::vector<Coord> out_values;
+    for (int in = 0; in < static_cast<int>(values.size()); ++in) {
+        for (int k = 0; k < K; ++k) {
+            const int o = static_cast<int>(out_values.size());
+            out_values.push_back({values[in][0],
+                                  values[in][1] * stride[0] + offsets[3 * k],
+                                  values[in][2] * stride[1] + offsets[3 * k + 1],
+                                  values[in][3] * stride[2] + offsets[3 * k + 2]});
+            edges.push_back({in, o, k});
+        }
+    }
+    write_map_rows(edges, rows * K, rows * K, in_rows, out_rows, kernel_ids,
+                   row_offsets);
+    write_coords(out_values, rows * K, out_coords);
+    counts[0] = static_cast<int32_t>(edges.size());
+    counts[1] = static_cast<int32_t>(out_values.size());
+}
+
+// can_use_direct_transposed_relation: relations.cpp:107-127.  The stride
+// exceeds the offsets' extent on every axis, so no two (row, offset)
+// candidates of distinct input coordinates coincide.
+int oracle_direct_transposed(const int32_t* offsets, int K, const int* stride) {
+    if (K <= 0) return 0;
+    for (int a = 0; a < 3; ++a) {
+        int lo = offsets[a], hi = offsets[a];
+        for (int k = 0; k < K; ++k) {
+            lo = std::min(lo, offsets[3 * k + a]);
+            hi = std::max(hi, offsets[3 * k + a]);
+        }
+        if (stride[a] <= hi - lo) return 0;
+    }
+    return 1;
+}
+
+// write_transposed_kernel_relation: relation_build_detail.h:119-196.
+// Candidates coord*stride + offset[k] - padding, enumerated input-row major.
+//   direct: output row in*K + k per candidate (as the generative relation);
+//   otherwise: first-seen deduplicated output rows, edges stably sorted by
+//   (out_row, kernel_id, in_row) (write_map, relation_views_detail.h:52-82).
+// Capacities rows*K (relations.cpp:631-670).
+void oracle_transposed_kernel_relation(
+    const int32_t* coords, int rows, int active_rows, const int32_t* offsets,
+    int K, const int* stride, const int* padding, int32_t* in_rows,
+    int32_t* out_rows, int32_t* kernel_ids, int32_t* row_offsets,
+    int32_t* out_coords, int32_t* counts) {
+    auto values = read_coords(coords, rows);
+    values.resize(std::min(active_rows, rows));
+    const bool direct = oracle_direct_transposed(offsets, K, stride) != 0;
+    std::vector<Edge> edges;
+    std::vector<Coord> out_values;
+    RowMap seen;
+    for (int in = 0; in < static_cast<int>(values.size()); ++in) {
+        for (int k = 0; k < K; ++k) {
+            Coord cand = {values[in][0],
+                          values[in][1] * stride[0] + offsets[3 * k] - padding[0],
+                          values[in][2] * stride[1] + offsets[3 * k + 1] - padding[1],
+                          values[in][3] * stride[2] + offsets[3 * k + 2] - padding[2]};
+            int o;
+            if (direct) {
+                o = in * K + k;
+                out_values.push_back(cand);
+            } else {
+                auto [it, inserted] =
+                    seen.emplace(cand, static_cast<int32_t>(out_values.size()));
+                if (inserted) out_values.push_back(cand);
+                o = it->second;
+            }
+            edges.push_back({in, o, k});
+        }
+    }
+    if (!direct) {
+        std::stable_sort(edges.begin(), edges.end(),
+                         [](const Edge& a, const Edge& b) {
+                             if (a[1] != b[1]) return a[1] < b[1];
+                             if (a[2] != b[2]) return a[2] < b[2];
+                             return a[0] < b[0];
+                         });
+    }
+    write_map_rows(edges, rows * K, rows * K, in_rows, out_rows, kernel_ids,
+                   row_offsets);
+    write_coords(out_values, rows * K, out_coords);
+    counts[0] = static_cast<int32_t>(edges.size());
+    counts[1] = static_cast<int32_t>(out_values.size());
 }
 
 // write_relation_grouped_view: relation_views_detail.h:84-120.  Stable

@@ -70,6 +70,14 @@ def lib() -> ctypes.CDLL:
         handle.oracle_target_kernel_relation.argtypes = [
             _i32p, _int, _int, _i32p, _int, _int, _i32p, _int, _i32p, _i32p,
             _i32p, _i32p, _i32p, _i32p, _i32p]
+        handle.oracle_generative_relation.argtypes = [
+            _i32p, _int, _int, _i32p, _int, _i32p,
+            _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]
+        handle.oracle_transposed_kernel_relation.argtypes = [
+            _i32p, _int, _int, _i32p, _int, _i32p, _i32p,
+            _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]
+        handle.oracle_direct_transposed.argtypes = [_i32p, _int, _i32p]
+        handle.oracle_direct_transposed.restype = _int
         handle.oracle_grouped_view.argtypes = [
             _i32p, _int, _int, _int, _i32p, _i32p]
         handle.oracle_implicit_gemm_view.argtypes = [
@@ -166,6 +174,52 @@ def target_kernel_relation(coords, target, active_rows=None,
         out['kernel_ids'], out['row_offsets'], out['counts'])
     _add_views(out, rows, k)
     return out
+
+
+def _expanded_relation(fn, coords, active_rows, kernel_size, stride,
+                       padding, dilation) -> dict:
+    coords = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+    rows = coords.shape[0]
+    active = rows if active_rows is None else int(active_rows)
+    offs = kernel_offsets(kernel_size, dilation)
+    k = offs.shape[0]
+    cap = rows * k
+    out = dict(
+        in_rows=np.zeros(cap, np.int32),
+        out_rows=np.zeros(cap, np.int32),
+        kernel_ids=np.zeros(cap, np.int32),
+        row_offsets=np.zeros(cap + 1, np.int32),
+        out_coords=np.zeros((cap, 4), np.int32),
+        counts=np.zeros(2, np.int32),
+    )
+    args = [coords, rows, active, offs, k, _triple(stride)]
+    if padding is not None:
+        args.append(_triple(padding))
+    fn(*args, out['in_rows'], out['out_rows'], out['kernel_ids'],
+       out['row_offsets'], out['out_coords'], out['counts'])
+    _add_views(out, rows, k)
+    return out
+
+
+def generative_relation(coords, active_rows=None, kernel_size=2,
+                        stride=2) -> dict:
+    """write_generative_relation (relation_build_detail.h:82-117)."""
+    return _expanded_relation(lib().oracle_generative_relation, coords,
+                              active_rows, kernel_size, stride, None, 1)
+
+
+def transposed_kernel_relation(coords, active_rows=None, kernel_size=2,
+                               stride=2, padding=0, dilation=1) -> dict:
+    """write_transposed_kernel_relation (relation_build_detail.h:119-196)."""
+    return _expanded_relation(lib().oracle_transposed_kernel_relation, coords,
+                              active_rows, kernel_size, stride, padding,
+                              dilation)
+
+
+def direct_transposed(kernel_size, stride, dilation=1) -> bool:
+    offs = kernel_offsets(kernel_size, dilation)
+    return bool(lib().oracle_direct_transposed(offs, offs.shape[0],
+                                               _triple(stride)))
 
 
 def grouped_view(group_ids: np.ndarray, edge_count: int, group_count: int):

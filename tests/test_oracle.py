@@ -524,3 +524,188 @@ def test_pool_brute_force(mode, ks, stride):
         gin = O.pool_grad(g, feats, got, rel, mode)
         lhs = float((got[:n_out].astype(np.float64) * g[:n_out]).sum())
         assert abs(lhs - float((feats.astype(np.float64) * gin).sum())) < 1e-3 * (1 + abs(lhs))
+
+
+# ------------------------------------- transposed / generative relations --
+
+
+def test_transposed_relation_policy_golden():
+    g = golden('transposed_relation_policy')
+    gen = O.generative_relation(g['coords'], kernel_size=g['kernel_size'],
+                                stride=g['stride'])
+    tr = O.transposed_kernel_relation(g['coords'],
+                                      kernel_size=g['kernel_size'],
+                                      stride=g['stride'])
+    assert gen['counts'].tolist() == g['generative_counts']
+    n = int(gen['counts'][1])
+    assert gen['out_coords'][:n].tolist() == g['generative_out_coords']
+    m = int(tr['counts'][1])
+    assert tr['out_coords'][:m].tolist() == g['transposed_out_coords']
+
+
+def test_conv_transpose_contract_golden():
+    g = golden('conv_transpose_contract')
+    feats = np.asarray(g['feats'], np.float32)
+    w = np.asarray(g['weight'], np.float32)
+    for rel in (O.generative_relation(g['coords'], kernel_size=g['kernel_size'],
+                                      stride=g['stride']),
+                O.transposed_kernel_relation(g['coords'],
+                                             kernel_size=g['kernel_size'],
+                                             stride=g['stride'])):
+        n = int(rel['counts'][1])
+        assert rel['out_coords'][:n].tolist() == g['out_coords']
+        assert O.conv_features(feats, w, rel)[:n].tolist() == g['out_feats']
+
+
+def test_conv_transpose_gradients_golden():
+    g = golden('grad_conv_transpose_line')
+    feats = np.asarray(g['feats'], np.float32)
+    w = np.asarray(g['weight'], np.float32)
+    for rel in (O.generative_relation(g['coords'], kernel_size=g['kernel_size'],
+                                      stride=g['stride']),
+                O.transposed_kernel_relation(g['coords'],
+                                             kernel_size=g['kernel_size'],
+                                             stride=g['stride'])):
+        n_out = rel['row_offsets'].shape[0] - 1
+        cot = np.zeros((n_out, 1), np.float32)
+        cot[:int(rel['counts'][1])] = 1.0
+        assert O.conv_input_grad(cot, w, rel, 1).tolist() == g['grad_feats']
+        assert O.conv_weight_grad(feats, cot, w.shape, rel).tolist() == \
+            g['grad_weight']
+
+
+def test_direct_transposed_rule():
+    """relations.cpp:107-127: direct when every stride exceeds the offsets'
+    extent on its axis."""
+    assert O.direct_transposed(2, 2)
+    assert O.direct_transposed(3, 3)
+    assert O.direct_transposed((2, 1, 3), (2, 1, 3))
+    assert not O.direct_transposed(3, 2)
+    assert not O.direct_transposed(2, 1)
+    assert not O.direct_transposed(2, 2, dilation=2)
+
+
+def _cloud_with_duplicates(rng, n, extent, batches=2):
+    coords = np.concatenate([rng.integers(0, batches, (n, 1)),
+                             rng.integers(-extent, extent, (n, 3))], 1)
+    coords[n // 2] = coords[3]          # a repeated coordinate
+    return coords.astype(np.int32)
+
+
+@pytest.mark.parametrize('ks,stride,pad,dil', [
+    (2, 2, 0, 1), (3, 2, 0, 1), (3, 1, 1, 1), (2, 1, 0, 1), (3, 2, 1, 2),
+    ((2, 3, 1), (2, 1, 1), (0, 1, 0), 1)])
+def test_transposed_relation_structure(ks, stride, pad, dil):
+    """Every (input row, offset) lands on the output row whose coordinate is
+    coord * stride + offset - padding; output rows are the distinct
+    candidates in first-seen order (or one per candidate when direct);
+    edges run in (out_row, kernel_id, in_row) order; the CSR rows cover
+    them."""
+    rng = np.random.default_rng(40)
+    coords = _cloud_with_duplicates(rng, 300, 6)
+    active = 290
+    rel = O.transposed_kernel_relation(coords, active, kernel_size=ks,
+                                       stride=stride, padding=pad,
+                                       dilation=dil)
+    offs = O.kernel_offsets(ks, dil).astype(np.int64)
+    s = np.asarray(stride if isinstance(stride, tuple) else (stride,) * 3)
+    p = np.asarray(pad if isinstance(pad, tuple) else (pad,) * 3)
+    K = len(offs)
+    E, n_out = int(rel['counts'][0]), int(rel['counts'][1])
+    assert E == active * K
+    c = coords[:active].astype(np.int64)
+    cand = np.concatenate([np.repeat(c[:, :1], K, 0),
+                           (c[:, None, 1:] * s + offs[None] - p).reshape(-1, 3)],
+                          1)  # candidate j = in*K + k
+    oc = rel['out_coords'][:n_out].astype(np.int64)
+    if O.direct_transposed(ks, stride, dil):
+        assert n_out == active * K
+        assert np.array_equal(oc, cand)
+    else:
+        _, first = np.unique(cand, axis=0, return_index=True)
+        assert np.array_equal(oc, cand[np.sort(first)])
+    in_r = rel['in_rows'][:E]
+    out_r = rel['out_rows'][:E]
+    k_r = rel['kernel_ids'][:E]
+    assert np.array_equal(oc[out_r], cand[in_r * K + k_r])
+    # every (in, k) exactly once
+    assert np.array_equal(np.sort(in_r.astype(np.int64) * K + k_r),
+                          np.arange(active * K))
+    order = np.lexsort((in_r, k_r, out_r))
+    assert np.array_equal(order, np.arange(E))
+    ro = rel['row_offsets']
+    assert ro[0] == 0 and np.all(np.diff(ro) >= 0) and ro[-1] == E
+    assert np.array_equal(np.diff(ro[:n_out + 1]),
+                          np.bincount(out_r, minlength=n_out))
+
+
+@pytest.mark.parametrize('ks,stride,pad', [(2, 2, 0), (3, 2, 1), (3, 1, 0)])
+def test_transposed_relation_is_the_forward_relation_reversed(ks, stride, pad):
+    """A target relation from the transposed relation's output coordinates
+    to its input coordinates (same kernel, stride, padding) holds exactly the
+    transposed edges with input and output swapped (unique coordinates)."""
+    rng = np.random.default_rng(41)
+    coords = np.unique(_cloud_with_duplicates(rng, 400, 5), axis=0)
+    coords = coords[rng.permutation(len(coords))]
+    tr = O.transposed_kernel_relation(coords, kernel_size=ks, stride=stride,
+                                      padding=pad)
+    n_out = int(tr['counts'][1])
+    fwd = O.target_kernel_relation(tr['out_coords'][:n_out], coords,
+                                   kernel_size=ks, stride=stride,
+                                   padding=pad)
+    E = int(tr['counts'][0])
+    assert int(fwd['counts'][0]) == E
+    a = set(zip(tr['in_rows'][:E].tolist(), tr['out_rows'][:E].tolist(),
+                tr['kernel_ids'][:E].tolist()))
+    b = set(zip(fwd['out_rows'][:E].tolist(), fwd['in_rows'][:E].tolist(),
+                fwd['kernel_ids'][:E].tolist()))
+    assert a == b
+
+
+def test_generative_relation_structure():
+    rng = np.random.default_rng(42)
+    coords = _cloud_with_duplicates(rng, 200, 6)
+    rel = O.generative_relation(coords, 150, kernel_size=3, stride=2)
+    offs = O.kernel_offsets(3).astype(np.int64)
+    K = len(offs)
+    assert rel['counts'].tolist() == [150 * K, 150 * K]
+    c = coords[:150].astype(np.int64)
+    oc = rel['out_coords'][:150 * K].reshape(150, K, 4)
+    assert np.array_equal(oc[..., 0], np.repeat(c[:, :1], K, 1))
+    assert np.array_equal(oc[..., 1:], c[:, None, 1:] * 2 + offs[None])
+    assert np.array_equal(rel['in_rows'][:150 * K], np.repeat(np.arange(150), K))
+    assert np.array_equal(rel['kernel_ids'][:150 * K], np.tile(np.arange(K), 150))
+    assert np.array_equal(rel['row_offsets'][:150 * K + 1], np.arange(150 * K + 1))
+    assert not rel['out_coords'][150 * K:].any()
+
+
+@pytest.mark.parametrize('ks,stride,pad,dil', [(2, 2, 0, 1), (3, 1, 0, 1),
+                                               (3, 2, 1, 1), (2, 1, 0, 2)])
+def test_conv_transpose_matches_dense_conv_transpose3d(ks, stride, pad, dil):
+    """On a fully occupied box the sparse transposed conv is torch's dense
+    conv_transpose3d, read at coordinate + centre offset + padding."""
+    torch = pytest.importorskip('torch')
+    rng = np.random.default_rng(43)
+    size, c_in, c_out = 4, 3, 2
+    coords = _box(size, rng)
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+    w = rng.standard_normal((c_out, ks, ks, ks, c_in)).astype(np.float32)
+    rel = O.transposed_kernel_relation(coords, kernel_size=ks, stride=stride,
+                                       padding=pad, dilation=dil)
+    got = O.conv_features(feats, w, rel)
+    n = int(rel['counts'][1])
+    dense = np.zeros((1, c_in, size, size, size), np.float64)
+    dense[0, :, coords[:, 1], coords[:, 2], coords[:, 3]] = feats
+    ref = torch.nn.functional.conv_transpose3d(
+        torch.from_numpy(dense),
+        torch.from_numpy(w.transpose(4, 0, 1, 2, 3).astype(np.float64)),
+        stride=stride, dilation=dil)[0].numpy()
+    shift = (ks // 2) * dil if ks % 2 else 0
+    idx = rel['out_coords'][:n, 1:] + shift + pad
+    assert (idx >= 0).all() and (idx < ref.shape[1]).all()
+    np.testing.assert_allclose(got[:n],
+                               ref[:, idx[:, 0], idx[:, 1], idx[:, 2]].T,
+                               rtol=1e-5, atol=1e-5)
+    # the sparse rows are exactly the dense positions that receive an edge
+    assert n == len(np.unique(idx, axis=0))
+    assert int((np.abs(ref).sum(0) > 0).sum()) == n
