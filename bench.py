@@ -327,6 +327,71 @@ def pooling_workload(coords, steps: int, warmup: int) -> dict:
     }
 
 
+def decoder_workload(coords, steps: int, warmup: int) -> dict:
+    """A decoder step on the config-3 cloud: the k=2 s=2 downsampled cloud
+    (the encoder's next level) upsampled again by conv_transpose3d k=2 s=2,
+    fp16 128 -> 128.  The transposed relation is direct (one output row per
+    (row, offset)), so E = 8 * N_coarse and every output row has one edge.
+    Reported: the relation build (HBM-bound: coords read, edges, offsets and
+    output coordinates written), its mask-sorted view, the conv on cached
+    views, and the build of the deduplicating k=3 s=2 transposed relation."""
+    import torch
+
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor
+    from mlx_lattice_amd._native import ext
+
+    fine = SparseTensor(coords, torch.zeros((coords.shape[0], 1),
+                                            device=coords.device))
+    down = fine.coord_manager.kernel_relation(fine.coord_key, kernel_size=2,
+                                              stride=2)
+    n = int(down.counts[1].item())
+    coarse = down.out_coords[:n].contiguous()
+    active = torch.tensor([n], dtype=torch.int32, device=coords.device)
+    c = 128
+    gen = torch.Generator(device=coords.device).manual_seed(13)
+    feats = torch.randn((n, c), generator=gen, device=coords.device
+                        ).to(torch.float16)
+    weight = (torch.randn((c, 2, 2, 2, c), generator=gen,
+                          device=coords.device) * (2.0 / (8 * c)) ** 0.5
+              ).to(torch.float16)
+    x = SparseTensor(coarse, feats, stride=2)
+    out = ops.conv_transpose3d(x, weight, kernel_size=2, stride=2)
+    torch.cuda.synchronize()
+    rel = x.coord_manager.transposed_kernel_relation(
+        x.coord_key, kernel_size=2, stride=2)
+    assert rel.sorted_implicit_gemm is not None, 'matrix-core route expected'
+    e = int(rel.counts[0].item())
+    t_build = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
+        coarse, active, [2, 2, 2], [2, 2, 2], [0, 0, 0], [1, 1, 1],
+        check_range=False), steps, warmup)
+    t_view = _timed(lambda: (object.__setattr__(
+        rel, 'sorted_implicit_gemm', None), object.__setattr__(
+        rel, 'implicit_gemm', None), rel.require_sorted_implicit_gemm()),
+        3, 1)
+    t_conv = _timed(lambda: ops.conv_transpose3d(x, weight, kernel_size=2,
+                                                 stride=2), steps, warmup)
+    t_k3 = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
+        coarse, active, [3, 3, 3], [2, 2, 2], [0, 0, 0], [1, 1, 1],
+        check_range=False), steps, warmup)
+    build_bytes = 16 * n + e * (12 + 4 + 16) + 4
+    flops = 2.0 * e * c * c
+    del out
+    return {
+        'workload': 'config-3 decoder: conv_transpose3d k=2 s=2 fp16 '
+                    '128->128 from the k2s2-downsampled cloud',
+        'rows_in': n, 'rows_out': e,
+        'relation_ms': round(t_build, 4),
+        'relation_hbm_frac': round(build_bytes / t_build / 1e6 / PEAK_HBM_GBS,
+                                   4),
+        'sorted_view_ms': round(t_view, 4),
+        'conv_ms': round(t_conv, 4),
+        'conv_tflops': round(flops / t_conv / 1e9, 2),
+        'conv_mfma_frac': round(flops / t_conv / 1e9 / PEAK_FP16_TFLOPS, 4),
+        'k3s2_relation_ms': round(t_k3, 4),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -439,6 +504,7 @@ def main() -> int:
     record['backward'] = backward_workload(feats, weight, coords, active,
                                            edges, args.steps, args.warmup)
     record['pooling'] = pooling_workload(coords, args.steps, args.warmup)
+    record['decoder'] = decoder_workload(coords, args.steps, args.warmup)
     if not args.no_secondary:
         record['secondary'] = secondary_workloads()
     if not args.no_cpu_baseline:

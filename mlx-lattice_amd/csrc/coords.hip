@@ -523,14 +523,48 @@ emit_edges(const int32_t* __restrict__ out_in_map, int out_capacity, int K,
 // `groups`, which sorts last), a stable radix sort of (key, edge id), and
 // the row offsets read off the sorted keys.
 
-// offsets[g] = number of sorted keys below g, for g in [0, groups].
+// offsets[g] = number of sorted keys below g, for g in [0, groups].  The
+// lane at position i writes the groups its key step (prev, cur] skips.  The
+// trailing run of empty groups (up to `groups`, past the last real key) can
+// be as long as the capacity, so no lane writes it: the lane at its start
+// records (first empty group, position) in tail[0..1] and fill_group_tail
+// spreads it over the grid.
 __global__ void __launch_bounds__(kThreads)
-group_offsets(const int32_t* __restrict__ sorted_keys, int capacity, int groups, int32_t* __restrict__ offsets) {
+group_offsets(const int32_t* __restrict__ sorted_keys, int capacity, int groups, int32_t* __restrict__ offsets,
+              int32_t* __restrict__ tail) {
     for (int i = blockIdx.x * kThreads + threadIdx.x; i <= capacity; i += gridDim.x * kThreads) {
-        const int prev = i > 0 ? sorted_keys[i - 1] : -1;
-        const int cur = i < capacity ? sorted_keys[i] : groups + 1;
-        for (int g = prev + 1; g <= min(cur, groups); ++g) offsets[g] = i;
+        const int prev = i > 0 ? min(sorted_keys[i - 1], groups) : -1;
+        const int cur = i < capacity ? min(sorted_keys[i], groups) : groups;
+        if (cur >= groups) {
+            if (prev < groups) {
+                tail[0] = prev + 1;
+                tail[1] = i;
+            }
+            continue;
+        }
+        for (int g = prev + 1; g <= cur; ++g) offsets[g] = i;
     }
+}
+
+__global__ void __launch_bounds__(kThreads)
+fill_group_tail(const int32_t* __restrict__ tail, int groups, int32_t* __restrict__ offsets) {
+    const int first = tail[0];
+    const int value = tail[1];
+    for (int g = blockIdx.x * kThreads + threadIdx.x; g <= groups; g += gridDim.x * kThreads) {
+        if (g >= first) offsets[g] = value;
+    }
+}
+
+// Row offsets of sorted group keys (sentinel `groups` for inactive slots).
+int launch_group_offsets(const int32_t* sorted_keys, int capacity, int groups, int32_t* offsets,
+                         int32_t* tail, hipStream_t stream) {
+    group_offsets<<<grid_for(static_cast<long long>(capacity) + 1, kThreads, 8192), kThreads, 0, stream>>>(
+        sorted_keys, capacity, groups, offsets, tail);
+    LATTICE_LAUNCH_CHECK();
+    fill_group_tail<<<grid_for(static_cast<long long>(groups) + 1, kThreads, 8192), kThreads, 0, stream>>>(
+        tail, groups, offsets);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
 }
 
 // ------------------------------------------------------------- helpers ----
@@ -610,7 +644,8 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
 
 size_t group_view_bytes(int edge_capacity) {
     const size_t n = static_cast<size_t>(std::max(edge_capacity, 1));
-    return aligned_bytes(n * sizeof(int32_t)) + radix_sort_workspace_bytes(edge_capacity, 32) + 1024;
+    return aligned_bytes(n * sizeof(int32_t)) + aligned_bytes(2 * sizeof(int32_t)) +
+           radix_sort_workspace_bytes(edge_capacity, 32) + 1024;
 }
 
 int bit_width(int v) {
@@ -624,14 +659,12 @@ int build_group_view(const int32_t* group_ids, const int32_t* counts, int edge_c
                      int32_t* offsets, int32_t* edge_ids, Workspace ws, hipStream_t stream) {
     if (edge_capacity <= 0) return fill_i32(offsets, groups + 1, 0, stream);
     int32_t* sorted = ws.take<int32_t>(edge_capacity);
-    LATTICE_REQUIRE(sorted, "grouped view workspace too small.");
+    int32_t* tail = ws.take<int32_t>(2);
+    LATTICE_REQUIRE(sorted && tail, "grouped view workspace too small.");
     const SortKeys keys{group_ids, 1, counts, groups, false};
     int rc = radix_sort_indices(keys, edge_capacity, bit_width(groups), sorted, edge_ids, ws, stream);
     if (rc != LATTICE_OK) return rc;
-    group_offsets<<<grid_for(edge_capacity + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted, edge_capacity,
-                                                                                       groups, offsets);
-    LATTICE_LAUNCH_CHECK();
-    return LATTICE_OK;
+    return launch_group_offsets(sorted, edge_capacity, groups, offsets, tail, stream);
 }
 
 int build_group_views(const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
@@ -1218,7 +1251,8 @@ size_t expanded_relation_bytes(int rows, int K, bool direct) {
     size_t bytes = group_view_bytes(static_cast<int>(cap)) + 4096;
     if (direct) return bytes;
     const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
-    bytes += table_bytes(static_cast<int>(cap)) + 5 * n + scan_workspace_bytes(cap);
+    bytes += table_bytes(static_cast<int>(cap)) + 5 * n + aligned_bytes(2 * sizeof(int32_t)) +
+             scan_workspace_bytes(cap);
     bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
     return bytes;
 }
@@ -1290,9 +1324,10 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         if (rc != LATTICE_OK) return rc;
         emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out);
         LATTICE_LAUNCH_CHECK();
-        group_offsets<<<grid_for(cap + 1, kThreads, 8192), kThreads, 0, stream>>>(sorted_keys, cap, cap,
-                                                                                 out->row_offsets);
-        LATTICE_LAUNCH_CHECK();
+        int32_t* tail = ws.take<int32_t>(2);
+        LATTICE_REQUIRE(tail, "relation workspace too small.");
+        rc = launch_group_offsets(sorted_keys, cap, cap, out->row_offsets, tail, stream);
+        if (rc != LATTICE_OK) return rc;
     }
     if (out->in_edge_ids == nullptr) return LATTICE_OK;
     Workspace views{static_cast<char*>(workspace), workspace_bytes};
