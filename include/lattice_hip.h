@@ -38,6 +38,11 @@
  *                                    pooling/cpu/algorithms.cpp:180-331,
  *                                    bindings/pooling.cpp:15-66
  *   global pools                     mlx_lattice/ops/pool.py:198-236
+ *   sparse_quantize, voxelize_features, build_point_voxel_map,
+ *   interpolate_point_features (+ vjps)
+ *                                    native/features/coordinates/quantization.cpp,
+ *                                    cpu/quantization_detail.h:66-391,
+ *                                    mlx_lattice/core/coords/quantization.py
  */
 #ifndef LATTICE_HIP_H_
 #define LATTICE_HIP_H_
@@ -167,6 +172,89 @@ int lattice_hip_build_transposed_kernel_relation(
     const int kernel_size[3], const int stride[3], const int padding[3],
     const int dilation[3], const lattice_relation_outputs* out,
     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Stable grouping of n int32 keys into `groups` groups (the counting sort
+ * of write_relation_grouped_view, relation_views_detail.h:84-120, for any
+ * key array): offsets[groups + 1] and ids[n], ids listing the positions of
+ * group 0, then group 1, ... each in increasing position order.  Keys
+ * outside [0, groups) and positions at or past *count (device, optional)
+ * are left out (sorted past offsets[groups]). */
+size_t lattice_hip_group_by_key_workspace_bytes(int n);
+int lattice_hip_group_by_key(const int32_t* keys, int n, const int32_t* count,
+                             int groups, int32_t* offsets, int32_t* ids,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---- point -> voxel quantization (core/coords/quantization.py;
+ * cpu/quantization_detail.h:66-391; native quantization.cpp) ----
+ * Points are float32 [rows, 3], batch indices int32 [rows]; voxel_size and
+ * origin are host float[3].  Float arithmetic is binary32 with one rounding
+ * per operation (no contracted multiply-adds). */
+
+/* sparse_quantize (quantization.py:92-118; write_sparse_quantization,
+ * quantization_detail.h:91-128): voxel (batch, floor((p - origin) /
+ * voxel_size)), first-seen point order.  Outputs (capacity = rows):
+ * coords int32 [rows, 4] (zero tail), voxel_count int32 [1], inverse_rows
+ * int32 [rows] (-1 for inactive points), counts int32 [rows] (zero tail).
+ * Voxel coordinates must fit the packed key (LATTICE_STATUS_COORD_RANGE). */
+size_t lattice_hip_sparse_quantize_workspace_bytes(int rows);
+int lattice_hip_sparse_quantize(
+    const float* points, const int32_t* batch_indices, int rows,
+    const int32_t* active_rows, const float voxel_size[3],
+    const float origin[3], int32_t* coords, int32_t* voxel_count,
+    int32_t* inverse_rows, int32_t* counts, int32_t* status, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* voxelize_features (quantization.py:121-149; write_voxel_features,
+ * quantization_detail.h:141-170): out[v] = sum over the points of voxel v,
+ * in point order, of feats[p] * scale (scale 1 for mode 0 = sum, 1 /
+ * max(counts[v], 1) for mode 1 = mean).  voxel_offsets / point_ids: the
+ * grouping of inverse_rows by voxel (lattice_hip_group_by_key, with the
+ * active point count).  feats and out are float32. */
+int lattice_hip_voxelize_features(int mode, const float* feats, int channels,
+                                  const int32_t* counts, int voxel_rows,
+                                  const int32_t* voxel_offsets,
+                                  const int32_t* point_ids, float* out,
+                                  void* stream);
+/* write_voxel_feature_grad (quantization_detail.h:172-200). */
+int lattice_hip_voxelize_features_grad(int mode, const float* cot,
+                                       int voxel_rows, int channels,
+                                       const int32_t* inverse_rows,
+                                       const int32_t* counts, int point_rows,
+                                       const int32_t* point_active,
+                                       float* grad, void* stream);
+
+/* build_point_voxel_map (quantization.py:152-195; write_point_voxel_map,
+ * quantization_detail.h:213-331): rows_out int32 [point_rows, 8] and
+ * weights_out float32 [point_rows, 8]; interpolation 0 = nearest (corner 0
+ * only, weight 1), 1 = linear (eight corners, trilinear weights); -1 / 0
+ * where no voxel is found.  Voxel coordinates map to their first row. */
+size_t lattice_hip_point_voxel_map_workspace_bytes(int voxel_rows);
+int lattice_hip_build_point_voxel_map(
+    const float* points, const int32_t* batch_indices, int point_rows,
+    const int32_t* point_active, const int32_t* voxel_coords, int voxel_rows,
+    const int32_t* voxel_active, const float voxel_size[3],
+    const float origin[3], int interpolation, int32_t* rows_out,
+    float* weights_out, int32_t* status, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* interpolate_point_features (quantization.py:198-213; write_point_features,
+ * quantization_detail.h:333-361) and its gradient (write_point_feature_grad,
+ * :363-391), the latter over the grouping of the map's (point, corner)
+ * entries by voxel row (lattice_hip_group_by_key over rows_out). */
+int lattice_hip_interpolate_point_features(const float* values,
+                                           int voxel_rows, int channels,
+                                           const int32_t* rows,
+                                           const float* weights,
+                                           int point_rows, float* out,
+                                           void* stream);
+int lattice_hip_interpolate_point_features_grad(const float* point_grad,
+                                                int channels,
+                                                const float* weights,
+                                                const int32_t* voxel_offsets,
+                                                const int32_t* entry_ids,
+                                                int voxel_rows, float* out,
+                                                void* stream);
 
 /* Grouped CSR views of a relation: write_relation_grouped_view
  * (relation_views_detail.h:84-120; relations.cpp:438-476).  Stable

@@ -28,11 +28,12 @@ NATIVE = HERE / 'native'
 INCLUDE = REPO / 'include'
 ARCH = 'gfx950'
 
-HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip', 'conv_grad.hip', 'pool.hip']
+HIP_SOURCES = ['scan.hip', 'sort.hip', 'coords.hip', 'conv.hip', 'conv_grad.hip', 'pool.hip', 'quantize.hip']
 HOST_SOURCES = [
     'native/features/coordinates/relations.cpp',
     'native/features/convolution/api.cpp',
     'native/features/pooling/pooling.cpp',
+    'native/features/quantization/quantization.cpp',
     'native/bindings/module.cpp',
 ]
 

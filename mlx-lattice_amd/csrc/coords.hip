@@ -1371,3 +1371,16 @@ extern "C" int lattice_hip_build_transposed_kernel_relation(const int32_t* coord
     return build_expanded_relation(coords, rows, active_rows, g, direct_expansion(g), out, workspace,
                                    workspace_bytes, as_stream(stream_ptr));
 }
+
+extern "C" size_t lattice_hip_group_by_key_workspace_bytes(int n) { return group_view_bytes(std::max(n, 0)); }
+
+extern "C" int lattice_hip_group_by_key(const int32_t* keys, int n, const int32_t* count, int groups,
+                                       int32_t* offsets, int32_t* ids, void* workspace, size_t workspace_bytes,
+                                       void* stream_ptr) {
+    LATTICE_REQUIRE(n >= 0 && groups >= 0, "group_by_key needs non-negative sizes.");
+    LATTICE_REQUIRE(offsets && (n == 0 || (keys && ids)), "group_by_key pointers must be non-null.");
+    LATTICE_REQUIRE(workspace_bytes >= lattice_hip_group_by_key_workspace_bytes(n),
+                    "group_by_key workspace too small.");
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    return build_group_view(keys, count, n, groups, offsets, ids, ws, as_stream(stream_ptr));
+}

@@ -1,0 +1,478 @@
+// Point -> voxel quantization and the point <-> voxel feature maps for gfx950
+// (mlx_lattice/core/coords/quantization.py; CPU routines
+// native/features/coordinates/cpu/quantization_detail.h:66-391).
+//
+//  * sparse_quantize: voxel = (batch, floor((p - origin) / voxel_size)) per
+//    point in binary32 with one rounding per operation.  The voxels are
+//    deduplicated in first-seen point order exactly as the forward
+//    relation's downsample is: a coordinate table keeps the minimum point
+//    row per voxel, a flag + scan places the representatives, every active
+//    point looks its voxel row up (inverse_rows) and counts it.
+//  * voxelize_features: one lane per (voxel, channel) sums its points in
+//    point order over a voxel -> points CSR (a stable grouping of the
+//    inverse rows), so the sum is deterministic and adds in the CPU
+//    routine's order.  Its gradient is a gather, one lane per (point,
+//    channel).
+//  * point_voxel_map: a coordinate table over the voxel coordinates (first
+//    row per coordinate); each point probes its nearest voxel or the eight
+//    corners of its cell, with trilinear weights (wx * wy) * wz.
+//  * interpolate_point_features: one lane per (point, channel) adds its
+//    eight corners in order; the gradient sums, per (voxel, channel), the
+//    (point, corner) entries that hit the voxel, in (point, corner) order,
+//    over a second stable grouping.
+// Floating-point contraction is off for this file: every product and sum
+// rounds once, in the CPU routine's order, so no multiply-add is fused.
+
+#include <algorithm>
+#include <climits>
+
+#include "lattice_common.h"
+#include "scan.h"
+
+#pragma clang fp contract(off)
+
+namespace lattice {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct VoxelGrid {
+    float size[3];
+    float origin[3];
+};
+
+__device__ inline float grid_position(float p, int axis, const VoxelGrid& g) {
+    return ((p - g.origin[axis]) / g.size[axis]);
+}
+
+// floor of a float as int64; values outside +-2^40 (and NaN) are reported
+// as out of range, which the packed key would reject anyway.
+__device__ inline bool floor_int(float v, int64_t* out) {
+    const float f = floorf(v);
+    if (!(fabsf(f) < 1099511627776.0f)) return false;
+    *out = static_cast<int64_t>(f);
+    return true;
+}
+
+int table_capacity_for(int rows) {
+    int cap = 1;
+    const long long want = std::max(2ll * rows, 1ll);
+    while (cap < want) cap <<= 1;
+    return cap;
+}
+
+size_t table_bytes_for(int rows) {
+    const size_t cap = static_cast<size_t>(table_capacity_for(rows));
+    return aligned_bytes(cap * sizeof(uint64_t)) + aligned_bytes(cap * sizeof(int32_t));
+}
+
+// Clears the table, zeroes `zero[0..zero_n)` and the status word.
+__global__ void __launch_bounds__(kThreads)
+clear_quant(uint64_t* keys, int32_t* rows, int capacity, int32_t* zero, int zero_n, int32_t* status) {
+    const int n = max(capacity, zero_n);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
+        if (i < capacity) {
+            keys[i] = kEmptyKey;
+            rows[i] = INT_MAX;
+        }
+        if (i < zero_n) zero[i] = 0;
+        if (i == 0 && status != nullptr) status[0] = 0;
+    }
+}
+
+// ------------------------------------------------------ sparse_quantize --
+
+// Voxel key of every point (kEmptyKey for inactive points), inserted with
+// the point row.
+__global__ void __launch_bounds__(kThreads)
+insert_points(CoordTable table, const float* __restrict__ points, const int32_t* __restrict__ batches, int rows,
+              const int32_t* __restrict__ active_rows, VoxelGrid g, uint64_t* __restrict__ keys, int32_t* status) {
+    const int active = min(max(*active_rows, 0), rows);
+    for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
+        uint64_t key = kEmptyKey;
+        if (p < active) {
+            const float* q = points + 3ll * p;
+            int64_t v[3];
+            bool ok = true;
+            for (int a = 0; a < 3; ++a) ok = floor_int(grid_position(q[a], a, g), &v[a]) && ok;
+            uint64_t k;
+            if (ok && pack_key(batches[p], v[0], v[1], v[2], &k)) {
+                key = k;
+                table.insert(k, p);
+            } else {
+                atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+            }
+        }
+        keys[p] = key;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+flag_points(CoordTable table, const uint64_t* __restrict__ keys, int rows, int32_t* __restrict__ flags) {
+    for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
+        const uint64_t k = keys[p];
+        flags[p] = (k != kEmptyKey && table.find(k) == p) ? 1 : 0;
+    }
+}
+
+__device__ inline int4 unpack_key(uint64_t k) {
+    return make_int4(static_cast<int>(k >> 54), static_cast<int>(((k >> 36) & (kAxisSpan - 1)) - kAxisBias),
+                     static_cast<int>(((k >> 18) & (kAxisSpan - 1)) - kAxisBias),
+                     static_cast<int>((k & (kAxisSpan - 1)) - kAxisBias));
+}
+
+__global__ void __launch_bounds__(kThreads)
+place_points(CoordTable table, const uint64_t* __restrict__ keys, int rows, const int32_t* __restrict__ flags,
+             const int32_t* __restrict__ positions, const int32_t* __restrict__ voxel_count,
+             int32_t* __restrict__ coords, int32_t* __restrict__ inverse_rows, int32_t* __restrict__ counts) {
+    const int n_vox = *voxel_count;
+    int4* out = reinterpret_cast<int4*>(coords);
+    for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
+        const uint64_t k = keys[p];
+        int inv = -1;
+        if (k != kEmptyKey) {
+            inv = positions[table.find(k)];
+            atomicAdd(counts + inv, 1);
+            if (flags[p]) out[positions[p]] = unpack_key(k);
+        }
+        if (p >= n_vox) out[p] = make_int4(0, 0, 0, 0);
+        inverse_rows[p] = inv;
+    }
+}
+
+// ---------------------------------------------------- voxel features --
+
+__device__ inline float mean_scale(int mode, const int32_t* counts, int v) {
+    return mode == 1 ? (1.0f / static_cast<float>(max(counts[v], 1))) : 1.0f;
+}
+
+__global__ void __launch_bounds__(kThreads)
+voxelize_csr(int mode, const float* __restrict__ feats, int channels, const int32_t* __restrict__ counts,
+             int voxel_rows, const int32_t* __restrict__ offsets, const int32_t* __restrict__ point_ids,
+             float* __restrict__ out) {
+    const long long total = static_cast<long long>(voxel_rows) * channels;
+    for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
+         t += static_cast<long long>(gridDim.x) * kThreads) {
+        const int v = static_cast<int>(t / channels);
+        const int c = static_cast<int>(t - static_cast<long long>(v) * channels);
+        const float scale = mean_scale(mode, counts, v);
+        float acc = 0.0f;
+        for (int i = offsets[v]; i < offsets[v + 1]; ++i) {
+            acc = (acc + (feats[static_cast<long long>(point_ids[i]) * channels + c] * scale));
+        }
+        out[t] = acc;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+voxelize_grad(int mode, const float* __restrict__ cot, int voxel_rows, int channels,
+              const int32_t* __restrict__ inverse_rows, const int32_t* __restrict__ counts, int point_rows,
+              const int32_t* __restrict__ point_active, float* __restrict__ grad) {
+    const int active = min(max(*point_active, 0), point_rows);
+    const long long total = static_cast<long long>(point_rows) * channels;
+    for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
+         t += static_cast<long long>(gridDim.x) * kThreads) {
+        const int p = static_cast<int>(t / channels);
+        const int c = static_cast<int>(t - static_cast<long long>(p) * channels);
+        float value = 0.0f;
+        if (p < active) {
+            const int v = inverse_rows[p];
+            if (v >= 0 && v < voxel_rows) {
+                value = (cot[static_cast<long long>(v) * channels + c] * mean_scale(mode, counts, v));
+            }
+        }
+        grad[t] = value;
+    }
+}
+
+// ---------------------------------------------------- point-voxel map --
+
+__global__ void __launch_bounds__(kThreads)
+insert_voxels(CoordTable table, const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
+              int32_t* status) {
+    const int active = min(max(*active_rows, 0), rows);
+    for (int v = blockIdx.x * kThreads + threadIdx.x; v < active; v += gridDim.x * kThreads) {
+        const int4 c = reinterpret_cast<const int4*>(coords)[v];
+        uint64_t key;
+        if (!pack_key(c.x, c.y, c.z, c.w, &key)) {
+            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+            continue;
+        }
+        table.insert(key, v);
+    }
+}
+
+__device__ inline int probe(const CoordTable& table, int b, int64_t x, int64_t y, int64_t z) {
+    uint64_t key;
+    if (!pack_key(b, x, y, z, &key)) return -1;
+    return table.find(key);
+}
+
+__global__ void __launch_bounds__(kThreads)
+map_points(CoordTable table, const float* __restrict__ points, const int32_t* __restrict__ batches, int point_rows,
+           const int32_t* __restrict__ point_active, VoxelGrid g, int linear, int32_t* __restrict__ rows_out,
+           float* __restrict__ weights_out) {
+    const int active = min(max(*point_active, 0), point_rows);
+    for (int p = blockIdx.x * kThreads + threadIdx.x; p < point_rows; p += gridDim.x * kThreads) {
+        int r[8];
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            r[i] = -1;
+            w[i] = 0.0f;
+        }
+        if (p < active) {
+            const float* q = points + 3ll * p;
+            const int b = batches[p];
+            float pos[3];
+            for (int a = 0; a < 3; ++a) pos[a] = grid_position(q[a], a, g);
+            if (!linear) {
+                int64_t n[3];
+                bool ok = true;
+                for (int a = 0; a < 3; ++a) ok = floor_int((pos[a] + 0.5f), &n[a]) && ok;
+                const int row = ok ? probe(table, b, n[0], n[1], n[2]) : -1;
+                if (row >= 0) {
+                    r[0] = row;
+                    w[0] = 1.0f;
+                }
+            } else {
+                int64_t lo[3];
+                float frac[3];
+                bool ok = true;
+                for (int a = 0; a < 3; ++a) {
+                    ok = floor_int(pos[a], &lo[a]) && ok;
+                    frac[a] = (pos[a] - static_cast<float>(lo[a]));
+                }
+                if (ok) {
+#pragma unroll
+                    for (int corner = 0; corner < 8; ++corner) {
+                        const int dx = corner & 1, dy = (corner >> 1) & 1, dz = (corner >> 2) & 1;
+                        const int row = probe(table, b, lo[0] + dx, lo[1] + dy, lo[2] + dz);
+                        if (row < 0) continue;
+                        const float wx = dx == 0 ? (1.0f - frac[0]) : frac[0];
+                        const float wy = dy == 0 ? (1.0f - frac[1]) : frac[1];
+                        const float wz = dz == 0 ? (1.0f - frac[2]) : frac[2];
+                        r[corner] = row;
+                        w[corner] = ((wx * wy) * wz);
+                    }
+                }
+            }
+        }
+        int4* ro = reinterpret_cast<int4*>(rows_out + 8ll * p);
+        float4* wo = reinterpret_cast<float4*>(weights_out + 8ll * p);
+        ro[0] = make_int4(r[0], r[1], r[2], r[3]);
+        ro[1] = make_int4(r[4], r[5], r[6], r[7]);
+        wo[0] = make_float4(w[0], w[1], w[2], w[3]);
+        wo[1] = make_float4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+interpolate(const float* __restrict__ values, int voxel_rows, int channels, const int32_t* __restrict__ rows,
+            const float* __restrict__ weights, int point_rows, float* __restrict__ out) {
+    const long long total = static_cast<long long>(point_rows) * channels;
+    for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
+         t += static_cast<long long>(gridDim.x) * kThreads) {
+        const int p = static_cast<int>(t / channels);
+        const int c = static_cast<int>(t - static_cast<long long>(p) * channels);
+        float acc = 0.0f;
+#pragma unroll
+        for (int corner = 0; corner < 8; ++corner) {
+            const int v = rows[8ll * p + corner];
+            if (v < 0 || v >= voxel_rows) continue;
+            acc = (acc + (values[static_cast<long long>(v) * channels + c] * weights[8ll * p + corner]));
+        }
+        out[t] = acc;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+interpolate_grad(const float* __restrict__ point_grad, int channels, const float* __restrict__ weights,
+                 const int32_t* __restrict__ offsets, const int32_t* __restrict__ entries, int voxel_rows,
+                 float* __restrict__ out) {
+    const long long total = static_cast<long long>(voxel_rows) * channels;
+    for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
+         t += static_cast<long long>(gridDim.x) * kThreads) {
+        const int v = static_cast<int>(t / channels);
+        const int c = static_cast<int>(t - static_cast<long long>(v) * channels);
+        float acc = 0.0f;
+        for (int i = offsets[v]; i < offsets[v + 1]; ++i) {
+            const int e = entries[i];
+            acc = (acc + (point_grad[static_cast<long long>(e >> 3) * channels + c] * weights[e]));
+        }
+        out[t] = acc;
+    }
+}
+
+int check_grid(const float* size, const float* origin) {
+    LATTICE_REQUIRE(size != nullptr && origin != nullptr, "voxel_size and origin must be non-null.");
+    for (int a = 0; a < 3; ++a) LATTICE_REQUIRE(size[a] > 0.0f, "voxel_size values must be positive.");
+    return LATTICE_OK;
+}
+
+VoxelGrid make_grid(const float* size, const float* origin) {
+    VoxelGrid g;
+    for (int a = 0; a < 3; ++a) {
+        g.size[a] = size[a];
+        g.origin[a] = origin[a];
+    }
+    return g;
+}
+
+}  // namespace
+}  // namespace lattice
+
+using namespace lattice;
+
+extern "C" size_t lattice_hip_sparse_quantize_workspace_bytes(int rows) {
+    const size_t n = static_cast<size_t>(std::max(rows, 1));
+    return table_bytes_for(std::max(rows, 0)) + aligned_bytes(n * sizeof(uint64_t)) +
+           2 * aligned_bytes(n * sizeof(int32_t)) + scan_workspace_bytes(std::max(rows, 0)) + 1024;
+}
+
+extern "C" int lattice_hip_sparse_quantize(const float* points, const int32_t* batch_indices, int rows,
+                                           const int32_t* active_rows, const float voxel_size[3],
+                                           const float origin[3], int32_t* coords, int32_t* voxel_count,
+                                           int32_t* inverse_rows, int32_t* counts, int32_t* status,
+                                           void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    int rc = check_grid(voxel_size, origin);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(rows >= 0, "points must have shape (N, 3).");
+    LATTICE_REQUIRE(active_rows && voxel_count && status && (rows == 0 || (points && batch_indices && coords &&
+                                                                           inverse_rows && counts)),
+                    "sparse_quantize pointers must be non-null.");
+    LATTICE_REQUIRE(workspace_bytes >= lattice_hip_sparse_quantize_workspace_bytes(rows),
+                    "sparse_quantize workspace too small.");
+    hipStream_t stream = as_stream(stream_ptr);
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    const int cap = table_capacity_for(rows);
+    CoordTable table;
+    table.keys = ws.take<uint64_t>(cap);
+    table.rows = ws.take<int32_t>(cap);
+    table.mask = static_cast<uint32_t>(cap - 1);
+    uint64_t* keys = ws.take<uint64_t>(std::max(rows, 1));
+    int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
+    int32_t* positions = ws.take<int32_t>(std::max(rows, 1));
+    LATTICE_REQUIRE(table.keys && table.rows && keys && flags && positions, "sparse_quantize workspace too small.");
+    clear_quant<<<grid_for(std::max(cap, rows), kThreads, 8192), kThreads, 0, stream>>>(table.keys, table.rows, cap,
+                                                                                      counts, rows, status);
+    LATTICE_LAUNCH_CHECK();
+    if (rows == 0) return fill_i32(voxel_count, 1, 0, stream);
+    const VoxelGrid g = make_grid(voxel_size, origin);
+    const unsigned grid = grid_for(rows, kThreads, 1u << 14);
+    insert_points<<<grid, kThreads, 0, stream>>>(table, points, batch_indices, rows, active_rows, g, keys, status);
+    LATTICE_LAUNCH_CHECK();
+    flag_points<<<grid, kThreads, 0, stream>>>(table, keys, rows, flags);
+    LATTICE_LAUNCH_CHECK();
+    rc = exclusive_scan(flags, positions, rows, voxel_count, ws, stream);
+    if (rc != LATTICE_OK) return rc;
+    place_points<<<grid, kThreads, 0, stream>>>(table, keys, rows, flags, positions, voxel_count, coords,
+                                               inverse_rows, counts);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_voxelize_features(int mode, const float* feats, int channels, const int32_t* counts,
+                                             int voxel_rows, const int32_t* voxel_offsets,
+                                             const int32_t* point_ids, float* out, void* stream_ptr) {
+    LATTICE_REQUIRE(mode == 0 || mode == 1, "reduction must be 'sum' or 'mean'.");
+    LATTICE_REQUIRE(channels > 0 && voxel_rows >= 0, "voxelize shapes must be positive.");
+    if (voxel_rows == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(feats && counts && voxel_offsets && point_ids && out, "voxelize pointers must be non-null.");
+    const long long total = static_cast<long long>(voxel_rows) * channels;
+    voxelize_csr<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
+        mode, feats, channels, counts, voxel_rows, voxel_offsets, point_ids, out);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_voxelize_features_grad(int mode, const float* cot, int voxel_rows, int channels,
+                                                  const int32_t* inverse_rows, const int32_t* counts,
+                                                  int point_rows, const int32_t* point_active, float* grad,
+                                                  void* stream_ptr) {
+    LATTICE_REQUIRE(mode == 0 || mode == 1, "reduction must be 'sum' or 'mean'.");
+    LATTICE_REQUIRE(channels > 0 && voxel_rows >= 0 && point_rows >= 0, "voxelize shapes must be positive.");
+    if (point_rows == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(grad && inverse_rows && point_active && (voxel_rows == 0 || (cot && counts)),
+                    "voxelize gradient pointers must be non-null.");
+    const long long total = static_cast<long long>(point_rows) * channels;
+    voxelize_grad<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
+        mode, cot, voxel_rows, channels, inverse_rows, counts, point_rows, point_active, grad);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" size_t lattice_hip_point_voxel_map_workspace_bytes(int voxel_rows) {
+    return table_bytes_for(std::max(voxel_rows, 0)) + 1024;
+}
+
+extern "C" int lattice_hip_build_point_voxel_map(const float* points, const int32_t* batch_indices, int point_rows,
+                                                 const int32_t* point_active, const int32_t* voxel_coords,
+                                                 int voxel_rows, const int32_t* voxel_active,
+                                                 const float voxel_size[3], const float origin[3],
+                                                 int interpolation, int32_t* rows_out, float* weights_out,
+                                                 int32_t* status, void* workspace, size_t workspace_bytes,
+                                                 void* stream_ptr) {
+    int rc = check_grid(voxel_size, origin);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(interpolation == 0 || interpolation == 1, "interpolation must be 'nearest' or 'linear'.");
+    LATTICE_REQUIRE(point_rows >= 0 && voxel_rows >= 0, "point and voxel rows must be non-negative.");
+    LATTICE_REQUIRE(point_active && voxel_active && status &&
+                        (point_rows == 0 || (points && batch_indices && rows_out && weights_out)) &&
+                        (voxel_rows == 0 || voxel_coords),
+                    "point-voxel map pointers must be non-null.");
+    LATTICE_REQUIRE(workspace_bytes >= lattice_hip_point_voxel_map_workspace_bytes(voxel_rows),
+                    "point-voxel map workspace too small.");
+    hipStream_t stream = as_stream(stream_ptr);
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    const int cap = table_capacity_for(voxel_rows);
+    CoordTable table;
+    table.keys = ws.take<uint64_t>(cap);
+    table.rows = ws.take<int32_t>(cap);
+    table.mask = static_cast<uint32_t>(cap - 1);
+    LATTICE_REQUIRE(table.keys && table.rows, "point-voxel map workspace too small.");
+    clear_quant<<<grid_for(cap, kThreads, 8192), kThreads, 0, stream>>>(table.keys, table.rows, cap, nullptr, 0,
+                                                                      status);
+    LATTICE_LAUNCH_CHECK();
+    if (voxel_rows > 0) {
+        insert_voxels<<<grid_for(voxel_rows, kThreads, 1u << 14), kThreads, 0, stream>>>(table, voxel_coords,
+                                                                                        voxel_rows, voxel_active,
+                                                                                        status);
+        LATTICE_LAUNCH_CHECK();
+    }
+    if (point_rows == 0) return LATTICE_OK;
+    map_points<<<grid_for(point_rows, kThreads, 1u << 14), kThreads, 0, stream>>>(
+        table, points, batch_indices, point_rows, point_active, make_grid(voxel_size, origin), interpolation,
+        rows_out, weights_out);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_interpolate_point_features(const float* values, int voxel_rows, int channels,
+                                                      const int32_t* rows, const float* weights, int point_rows,
+                                                      float* out, void* stream_ptr) {
+    LATTICE_REQUIRE(channels > 0 && voxel_rows >= 0 && point_rows >= 0, "interpolation shapes must be positive.");
+    if (point_rows == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(rows && weights && out && (voxel_rows == 0 || values),
+                    "interpolation pointers must be non-null.");
+    const long long total = static_cast<long long>(point_rows) * channels;
+    interpolate<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
+        values, voxel_rows, channels, rows, weights, point_rows, out);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_interpolate_point_features_grad(const float* point_grad, int channels,
+                                                           const float* weights, const int32_t* voxel_offsets,
+                                                           const int32_t* entry_ids, int voxel_rows, float* out,
+                                                           void* stream_ptr) {
+    LATTICE_REQUIRE(channels > 0 && voxel_rows >= 0, "interpolation shapes must be positive.");
+    if (voxel_rows == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(point_grad && weights && voxel_offsets && entry_ids && out,
+                    "interpolation gradient pointers must be non-null.");
+    const long long total = static_cast<long long>(voxel_rows) * channels;
+    interpolate_grad<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
+        point_grad, channels, weights, voxel_offsets, entry_ids, voxel_rows, out);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}

@@ -1,4 +1,8 @@
 from mlx_lattice_amd.core.coords import CoordinateManager, CoordinateMapKey
+from mlx_lattice_amd.core.coords.quantization import (
+    PointVoxelMap,
+    SparseQuantization,
+)
 from mlx_lattice_amd.core.quantized import (
     QuantizedWeight,
     dequantize_weight,
@@ -20,11 +24,13 @@ __all__ = [
     'CoordinateMapKey',
     'KernelRelation',
     'KernelSpec',
+    'PointVoxelMap',
     'QuantizedWeight',
     'RelationCSRView',
     'RelationEdges',
     'RelationImplicitGemmView',
     'RelationSortedImplicitGemmView',
+    'SparseQuantization',
     'SparseRelationContract',
     'SparseTensor',
     'dequantize_weight',

@@ -11,6 +11,7 @@
 
 #include "features/convolution/api.h"
 #include "features/pooling/api.h"
+#include "features/quantization/api.h"
 #include "features/coordinates/relations.h"
 #include "foundation/runtime.h"
 #include "lattice_hip.h"
@@ -235,6 +236,23 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("pooled"), py::arg("in_rows"), py::arg("out_rows"), py::arg("row_offsets"), py::arg("counts"),
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("reduce"),
           "Gradient of sparse pooling with respect to the input features.");
+    m.def("sparse_quantize", &ln::sparse_quantize, py::arg("points"), py::arg("batch_indices"),
+          py::arg("active_rows"), py::arg("voxel_size"), py::arg("origin"),
+          "Voxelize points: (coords, active_rows, inverse_rows, counts).");
+    m.def("group_by_key", &ln::group_by_key, py::arg("keys"), py::arg("count"), py::arg("groups"));
+    m.def("voxelize_features", &ln::voxelize_features, py::arg("feats"), py::arg("inverse_rows"),
+          py::arg("counts"), py::arg("active_rows"), py::arg("reduction"));
+    m.def("voxelize_features_grouped", &ln::voxelize_features_grouped, py::arg("feats"), py::arg("counts"),
+          py::arg("voxel_offsets"), py::arg("point_ids"), py::arg("reduction"));
+    m.def("voxelize_features_grad", &ln::voxelize_features_grad, py::arg("cotangent"), py::arg("inverse_rows"),
+          py::arg("counts"), py::arg("active_rows"), py::arg("point_rows"), py::arg("reduction"));
+    m.def("build_point_voxel_map", &ln::build_point_voxel_map, py::arg("points"), py::arg("batch_indices"),
+          py::arg("point_active_rows"), py::arg("voxel_coords"), py::arg("voxel_active_rows"),
+          py::arg("voxel_size"), py::arg("origin"), py::arg("interpolation"));
+    m.def("interpolate_point_features", &ln::interpolate_point_features, py::arg("voxel_feats"), py::arg("rows"),
+          py::arg("weights"));
+    m.def("interpolate_point_features_grad", &ln::interpolate_point_features_grad, py::arg("point_grad"),
+          py::arg("weights"), py::arg("voxel_offsets"), py::arg("entry_ids"), py::arg("voxel_rows"));
     m.def("global_pool", &ln::global_pool, py::arg("feats"), py::arg("batch_counts"), py::arg("mode"),
           "Per-batch global pooling: (B, C).");
 }

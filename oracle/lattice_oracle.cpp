@@ -41,6 +41,12 @@
 //   oracle_pool_features           reference known answers (tests/ops/
 //   oracle_pool_grad               test_pool.py:32-117), a numpy brute force,
 //                                  sum pooling == conv with all-ones weights.
+//   oracle_sparse_quantize,        reference known answers (tests/ops/
+//   oracle_voxelize_features(_grad), test_quantization.py:39-335), brute
+//   oracle_point_voxel_map,        force with numpy (np.unique first-seen
+//   oracle_point_features(_grad)   order, bincount), trilinear weights
+//                                  reproduce affine fields exactly and sum
+//                                  to one, gradients adjoint to the forward.
 //   oracle_quantized_conv_features unpack formula on hand-built words, equal
 //   oracle_dequantize_mapped       to the float route on dequantized weights.
 // Not restated here, hence parity unpinned: the reference's quantizer
@@ -51,6 +57,7 @@
 
 #include <algorithm>
 #include <array>
+#include <cmath>
 #include <chrono>
 #include <cstdint>
 #include <cstring>
@@ -781,6 +788,169 @@ void oracle_dequantize_mapped(const uint32_t* weights, const float* scales,
 // Round trip through IEEE binary16 with round-to-nearest-even.
 void oracle_round_half(const float* in, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = float_to_half(in[i]);
+}
+
+// ------------------------------------------------- point quantization --
+// Float arithmetic below is plain IEEE binary32 with one rounding per
+// operation (the Makefile builds with -ffp-contract=off).
+
+// voxel_coord_for_point: quantization_detail.h:66-89.
+static Coord voxel_of(const float* points, const int32_t* batches, int row,
+                      const float* size, const float* origin) {
+    const float* p = points + static_cast<size_t>(row) * 3;
+    return {batches[row],
+            static_cast<int64_t>(std::floor((p[0] - origin[0]) / size[0])),
+            static_cast<int64_t>(std::floor((p[1] - origin[1]) / size[1])),
+            static_cast<int64_t>(std::floor((p[2] - origin[2]) / size[2]))};
+}
+
+// write_sparse_quantization: quantization_detail.h:91-128.  Voxels in
+// first-seen point order; inverse_rows -1 for inactive points; counts per
+// voxel, zero tail; coords zero tail.  Returns the voxel count.
+int oracle_sparse_quantize(const float* points, const int32_t* batches,
+                           int rows, int active_rows, const float* size,
+                           const float* origin, int32_t* coords,
+                           int32_t* inverse_rows, int32_t* counts) {
+    const int n = std::min(active_rows, rows);
+    RowMap seen;
+    std::vector<Coord> out;
+    std::fill(inverse_rows, inverse_rows + rows, -1);
+    std::fill(counts, counts + rows, 0);
+    for (int p = 0; p < n; ++p) {
+        Coord c = voxel_of(points, batches, p, size, origin);
+        auto [it, inserted] = seen.emplace(c, static_cast<int32_t>(out.size()));
+        if (inserted) out.push_back(c);
+        inverse_rows[p] = it->second;
+        counts[it->second] += 1;
+    }
+    write_coords(out, rows, coords);
+    return static_cast<int>(out.size());
+}
+
+// write_voxel_features (quantization_detail.h:141-170) and
+// write_voxel_feature_grad (:172-200).  mode 0 = sum, 1 = mean.
+void oracle_voxelize_features(int mode, const float* feats, int point_rows,
+                              int active_rows, int channels,
+                              const int32_t* inverse_rows,
+                              const int32_t* counts, int voxel_rows,
+                              float* out) {
+    const int n = std::min(active_rows, point_rows);
+    std::fill(out, out + static_cast<size_t>(voxel_rows) * channels, 0.0f);
+    for (int p = 0; p < n; ++p) {
+        const int v = inverse_rows[p];
+        if (v < 0 || v >= voxel_rows) continue;
+        const float scale =
+            mode == 1 ? 1.0f / static_cast<float>(std::max(counts[v], 1)) : 1.0f;
+        for (int c = 0; c < channels; ++c) {
+            out[static_cast<size_t>(v) * channels + c] +=
+                feats[static_cast<size_t>(p) * channels + c] * scale;
+        }
+    }
+}
+
+void oracle_voxelize_features_grad(int mode, const float* cot, int point_rows,
+                                   int active_rows, int channels,
+                                   const int32_t* inverse_rows,
+                                   const int32_t* counts, int voxel_rows,
+                                   float* grad) {
+    const int n = std::min(active_rows, point_rows);
+    std::fill(grad, grad + static_cast<size_t>(point_rows) * channels, 0.0f);
+    for (int p = 0; p < n; ++p) {
+        const int v = inverse_rows[p];
+        if (v < 0 || v >= voxel_rows) continue;
+        const float scale =
+            mode == 1 ? 1.0f / static_cast<float>(std::max(counts[v], 1)) : 1.0f;
+        for (int c = 0; c < channels; ++c) {
+            grad[static_cast<size_t>(p) * channels + c] =
+                cot[static_cast<size_t>(v) * channels + c] * scale;
+        }
+    }
+}
+
+// write_nearest_point_voxel_map (quantization_detail.h:213-257) and
+// write_linear_point_voxel_map (:259-318).  mode 0 = nearest, 1 = linear.
+// rows/weights are (point_rows, 8): -1 / 0 where no voxel is found.
+void oracle_point_voxel_map(const float* points, const int32_t* batches,
+                            int point_rows, int point_active,
+                            const int32_t* voxel_coords, int voxel_rows,
+                            int voxel_active, const float* size,
+                            const float* origin, int mode, int32_t* rows,
+                            float* weights) {
+    const int n = std::min(point_active, point_rows);
+    std::fill(rows, rows + static_cast<size_t>(point_rows) * 8, -1);
+    std::fill(weights, weights + static_cast<size_t>(point_rows) * 8, 0.0f);
+    auto voxels = read_coords(voxel_coords, voxel_rows);
+    voxels.resize(std::min(voxel_active, voxel_rows));
+    auto map = first_row_map(voxels);
+    for (int p = 0; p < n; ++p) {
+        float pos[3];
+        for (int a = 0; a < 3; ++a) {
+            pos[a] = (points[static_cast<size_t>(p) * 3 + a] - origin[a]) / size[a];
+        }
+        const size_t base = static_cast<size_t>(p) * 8;
+        if (mode == 0) {
+            Coord q = {batches[p], static_cast<int64_t>(std::floor(pos[0] + 0.5f)),
+                       static_cast<int64_t>(std::floor(pos[1] + 0.5f)),
+                       static_cast<int64_t>(std::floor(pos[2] + 0.5f))};
+            auto it = map.find(q);
+            if (it == map.end()) continue;
+            rows[base] = it->second;
+            weights[base] = 1.0f;
+            continue;
+        }
+        int64_t lo[3];
+        float frac[3];
+        for (int a = 0; a < 3; ++a) {
+            lo[a] = static_cast<int64_t>(std::floor(pos[a]));
+            frac[a] = pos[a] - static_cast<float>(lo[a]);
+        }
+        for (int corner = 0; corner < 8; ++corner) {
+            const int dx = corner & 1, dy = (corner >> 1) & 1, dz = (corner >> 2) & 1;
+            Coord q = {batches[p], lo[0] + dx, lo[1] + dy, lo[2] + dz};
+            auto it = map.find(q);
+            if (it == map.end()) continue;
+            const float wx = dx == 0 ? 1.0f - frac[0] : frac[0];
+            const float wy = dy == 0 ? 1.0f - frac[1] : frac[1];
+            const float wz = dz == 0 ? 1.0f - frac[2] : frac[2];
+            rows[base + corner] = it->second;
+            weights[base + corner] = wx * wy * wz;
+        }
+    }
+}
+
+// write_point_features (quantization_detail.h:333-361) and
+// write_point_feature_grad (:363-391).
+void oracle_point_features(const float* values, int voxel_rows, int channels,
+                           const int32_t* rows, const float* weights,
+                           int point_rows, float* out) {
+    std::fill(out, out + static_cast<size_t>(point_rows) * channels, 0.0f);
+    for (int p = 0; p < point_rows; ++p)
+        for (int corner = 0; corner < 8; ++corner) {
+            const int v = rows[static_cast<size_t>(p) * 8 + corner];
+            if (v < 0 || v >= voxel_rows) continue;
+            const float w = weights[static_cast<size_t>(p) * 8 + corner];
+            for (int c = 0; c < channels; ++c) {
+                out[static_cast<size_t>(p) * channels + c] +=
+                    values[static_cast<size_t>(v) * channels + c] * w;
+            }
+        }
+}
+
+void oracle_point_features_grad(const float* point_grad, int voxel_rows,
+                                int channels, const int32_t* rows,
+                                const float* weights, int point_rows,
+                                float* out) {
+    std::fill(out, out + static_cast<size_t>(voxel_rows) * channels, 0.0f);
+    for (int p = 0; p < point_rows; ++p)
+        for (int corner = 0; corner < 8; ++corner) {
+            const int v = rows[static_cast<size_t>(p) * 8 + corner];
+            if (v < 0 || v >= voxel_rows) continue;
+            const float w = weights[static_cast<size_t>(p) * 8 + corner];
+            for (int c = 0; c < channels; ++c) {
+                out[static_cast<size_t>(v) * channels + c] +=
+                    point_grad[static_cast<size_t>(p) * channels + c] * w;
+            }
+        }
 }
 
 int oracle_hardware_concurrency(void) { return hardware_threads(0); }

@@ -102,6 +102,20 @@ def lib() -> ctypes.CDLL:
             _i32p, _i32p, _i32p, _int, _i32p, _int, _vp, _int]
         handle.oracle_dequantize_mapped.argtypes = [
             _u32p, _f32p, _f32p, _int, _int, _int, _int, _int, _int, _f32p]
+        handle.oracle_sparse_quantize.argtypes = [
+            _f32p, _i32p, _int, _int, _f32p, _f32p, _i32p, _i32p, _i32p]
+        handle.oracle_sparse_quantize.restype = _int
+        handle.oracle_voxelize_features.argtypes = [
+            _int, _f32p, _int, _int, _int, _i32p, _i32p, _int, _f32p]
+        handle.oracle_voxelize_features_grad.argtypes = [
+            _int, _f32p, _int, _int, _int, _i32p, _i32p, _int, _f32p]
+        handle.oracle_point_voxel_map.argtypes = [
+            _f32p, _i32p, _int, _int, _i32p, _int, _int, _f32p, _f32p, _int,
+            _i32p, _f32p]
+        handle.oracle_point_features.argtypes = [
+            _f32p, _int, _int, _i32p, _f32p, _int, _f32p]
+        handle.oracle_point_features_grad.argtypes = [
+            _f32p, _int, _int, _i32p, _f32p, _int, _f32p]
         handle.oracle_hardware_concurrency.restype = _int
         _lib = handle
     return _lib
@@ -440,3 +454,103 @@ def mapped_weight(weight: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(
         weight.transpose(1, 2, 3, 4, 0).reshape(-1, c_in, c_out))
 
+
+
+# ------------------------------------------------- point quantization ----
+
+
+def _ftriple(v) -> np.ndarray:
+    if isinstance(v, (int, float)):
+        v = (v, v, v)
+    return np.ascontiguousarray(v, dtype=np.float32)
+
+
+def _batches(batch_indices, rows):
+    if batch_indices is None:
+        return np.zeros(rows, np.int32)
+    return np.ascontiguousarray(batch_indices, dtype=np.int32)
+
+
+def sparse_quantize(points, voxel_size=1.0, batch_indices=None, origin=0.0,
+                    active_rows=None) -> dict:
+    """write_sparse_quantization (quantization_detail.h:91-128)."""
+    pts = np.ascontiguousarray(points, dtype=np.float32).reshape(-1, 3)
+    rows = pts.shape[0]
+    active = rows if active_rows is None else int(active_rows)
+    out = dict(coords=np.zeros((rows, 4), np.int32),
+               inverse_rows=np.zeros(rows, np.int32),
+               counts=np.zeros(rows, np.int32))
+    n = lib().oracle_sparse_quantize(
+        pts, _batches(batch_indices, rows), rows, active,
+        _ftriple(voxel_size), _ftriple(origin), out['coords'],
+        out['inverse_rows'], out['counts'])
+    out['active_rows'] = np.array([n], np.int32)
+    return out
+
+
+_VOXEL_MODES = {'sum': 0, 'mean': 1}
+
+
+def voxelize_features(feats, inverse_rows, counts, reduction='mean',
+                      active_rows=None) -> np.ndarray:
+    f = np.ascontiguousarray(feats, dtype=np.float32)
+    rows, channels = f.shape
+    active = rows if active_rows is None else int(active_rows)
+    counts = np.ascontiguousarray(counts, dtype=np.int32)
+    out = np.zeros((counts.shape[0], channels), np.float32)
+    lib().oracle_voxelize_features(
+        _VOXEL_MODES[reduction], f, rows, active, channels,
+        np.ascontiguousarray(inverse_rows, dtype=np.int32), counts,
+        counts.shape[0], out)
+    return out
+
+
+def voxelize_features_grad(cot, inverse_rows, counts, point_rows,
+                           reduction='mean', active_rows=None) -> np.ndarray:
+    g = np.ascontiguousarray(cot, dtype=np.float32)
+    channels = g.shape[1]
+    active = point_rows if active_rows is None else int(active_rows)
+    out = np.zeros((point_rows, channels), np.float32)
+    lib().oracle_voxelize_features_grad(
+        _VOXEL_MODES[reduction], g, point_rows, active, channels,
+        np.ascontiguousarray(inverse_rows, dtype=np.int32),
+        np.ascontiguousarray(counts, dtype=np.int32), g.shape[0], out)
+    return out
+
+
+def point_voxel_map(points, voxel_coords, voxel_active=None, voxel_size=1.0,
+                    batch_indices=None, point_active=None, origin=0.0,
+                    interpolation='linear'):
+    """write_point_voxel_map (quantization_detail.h:213-331)."""
+    pts = np.ascontiguousarray(points, dtype=np.float32).reshape(-1, 3)
+    vox = np.ascontiguousarray(voxel_coords, dtype=np.int32).reshape(-1, 4)
+    n = pts.shape[0]
+    rows = np.zeros((n, 8), np.int32)
+    weights = np.zeros((n, 8), np.float32)
+    lib().oracle_point_voxel_map(
+        pts, _batches(batch_indices, n), n,
+        n if point_active is None else int(point_active), vox, vox.shape[0],
+        vox.shape[0] if voxel_active is None else int(voxel_active),
+        _ftriple(voxel_size), _ftriple(origin),
+        {'nearest': 0, 'linear': 1}[interpolation], rows, weights)
+    return rows, weights
+
+
+def point_features(values, rows, weights) -> np.ndarray:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    out = np.zeros((rows.shape[0], v.shape[1]), np.float32)
+    lib().oracle_point_features(v, v.shape[0], v.shape[1], rows,
+                                np.ascontiguousarray(weights, np.float32),
+                                rows.shape[0], out)
+    return out
+
+
+def point_features_grad(point_grad, rows, weights, voxel_rows) -> np.ndarray:
+    g = np.ascontiguousarray(point_grad, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    out = np.zeros((voxel_rows, g.shape[1]), np.float32)
+    lib().oracle_point_features_grad(g, voxel_rows, g.shape[1], rows,
+                                     np.ascontiguousarray(weights, np.float32),
+                                     rows.shape[0], out)
+    return out

@@ -709,3 +709,190 @@ def test_conv_transpose_matches_dense_conv_transpose3d(ks, stride, pad, dil):
     # the sparse rows are exactly the dense positions that receive an edge
     assert n == len(np.unique(idx, axis=0))
     assert int((np.abs(ref).sum(0) > 0).sum()) == n
+
+
+# ------------------------------------------------- point quantization ----
+
+
+def test_sparse_quantize_golden():
+    g = golden('quantize_ordered_metadata')
+    q = O.sparse_quantize(g['points'], g['voxel_size'],
+                          batch_indices=g['batch_indices'])
+    n = int(q['active_rows'][0])
+    assert q['coords'].shape[0] == g['capacity']
+    assert q['active_rows'].tolist() == g['active_rows']
+    assert q['coords'][:n].tolist() == g['coords']
+    assert q['inverse_rows'].tolist() == g['inverse_rows']
+    assert q['counts'][:n].tolist() == g['counts']
+    g = golden('quantize_origin_active_rows')
+    q = O.sparse_quantize(g['points'], g['voxel_size'], origin=g['origin'],
+                          active_rows=g['active_rows_in'][0])
+    n = int(q['active_rows'][0])
+    assert q['active_rows'].tolist() == g['active_rows']
+    assert q['coords'][:n].tolist() == g['coords']
+    assert q['inverse_rows'].tolist() == g['inverse_rows']
+    assert q['counts'].tolist() == g['counts_full']
+
+
+def test_voxelize_golden():
+    g = golden('voxelize_mean_sum')
+    q = O.sparse_quantize(g['points'], g['voxel_size'])
+    n = int(q['active_rows'][0])
+    assert q['coords'][:n].tolist() == g['coords']
+    for mode in ('mean', 'sum'):
+        out = O.voxelize_features(g['feats'], q['inverse_rows'], q['counts'],
+                                  mode)
+        np.testing.assert_allclose(out[:n], g[mode], rtol=1e-6)
+    g = golden('voxelize_grad')
+    q = O.sparse_quantize(g['points'])
+    n = int(q['active_rows'][0])
+    out = O.voxelize_features(g['feats'], q['inverse_rows'], q['counts'],
+                              g['reduction'])
+    np.testing.assert_allclose(out[:n], g['features'], rtol=1e-6)
+    cot = np.zeros_like(out)
+    cot[:n] = 1.0
+    grad = O.voxelize_features_grad(cot, q['inverse_rows'], q['counts'], 3,
+                                    g['reduction'])
+    np.testing.assert_allclose(grad, g['grad'], rtol=1e-6)
+    # the forward is linear, so its jvp is the forward of the tangent
+    jvp = O.voxelize_features(g['tangent'], q['inverse_rows'], q['counts'],
+                              g['reduction'])
+    np.testing.assert_allclose(jvp[:n], g['jvp'], rtol=1e-6)
+
+
+def test_point_voxel_map_golden():
+    g = golden('devoxelize_nearest')
+    rows, w = O.point_voxel_map(g['points'], g['coords'],
+                                interpolation='nearest')
+    np.testing.assert_allclose(O.point_features(g['feats'], rows, w),
+                               g['sampled'], rtol=1e-6)
+    g = golden('devoxelize_linear')
+    rows, w = O.point_voxel_map(g['points'], g['coords'],
+                                interpolation='linear')
+    np.testing.assert_allclose(O.point_features(g['feats'], rows, w),
+                               g['sampled'], rtol=1e-6)
+    g = golden('point_voxel_map_reuse')
+    rows, w = O.point_voxel_map(g['points'], g['coords'],
+                                g['voxel_active_rows'][0],
+                                point_active=g['point_active_rows'][0],
+                                interpolation=g['interpolation'])
+    assert rows.shape[0] == g['point_count']
+    np.testing.assert_allclose(O.point_features(g['feats'], rows, w),
+                               g['sampled'], rtol=1e-6)
+    g = golden('devoxelize_grad')
+    rows, w = O.point_voxel_map(g['points'], g['coords'],
+                                g['voxel_active_rows'][0],
+                                interpolation=g['interpolation'])
+    np.testing.assert_allclose(O.point_features(g['feats'], rows, w),
+                               g['features'], rtol=1e-6)
+    grad = O.point_features_grad(np.ones((1, 1), np.float32), rows, w, 2)
+    np.testing.assert_allclose(grad, g['grad'], rtol=1e-6)
+    np.testing.assert_allclose(O.point_features(g['tangent'], rows, w),
+                               g['jvp'], rtol=1e-6)
+
+
+def _points(rng, n, batches=2):
+    pts = (rng.standard_normal((n, 3)) * 3.0).astype(np.float32)
+    pts[n // 2] = pts[3]                          # a repeated point
+    return pts, rng.integers(0, batches, n).astype(np.int32)
+
+
+@pytest.mark.parametrize('size,origin', [(0.5, 0.0), ((0.3, 0.7, 0.25),
+                                                      (0.1, -0.2, 0.05))])
+def test_sparse_quantize_brute_force(size, origin):
+    """numpy restatement from the definition: voxel = floor((p - o) / s) in
+    float32, voxels in first-seen order (np.unique's first index, sorted),
+    inverse by lookup, counts by bincount."""
+    rng = np.random.default_rng(90)
+    pts, b = _points(rng, 3000)
+    active = 2900
+    q = O.sparse_quantize(pts, size, batch_indices=b, origin=origin,
+                          active_rows=active)
+    s = np.asarray(size if isinstance(size, tuple) else (size,) * 3,
+                   np.float32)
+    o = np.asarray(origin if isinstance(origin, tuple) else (origin,) * 3,
+                   np.float32)
+    vox = np.floor((pts[:active] - o) / s).astype(np.int64)
+    keys = np.concatenate([b[:active, None].astype(np.int64), vox], 1)
+    uniq, first, inv = np.unique(keys, axis=0, return_index=True,
+                                 return_inverse=True)
+    order = np.argsort(first)
+    rank = np.empty_like(order)
+    rank[order] = np.arange(len(order))
+    n = int(q['active_rows'][0])
+    assert n == len(uniq)
+    assert np.array_equal(q['coords'][:n], uniq[order])
+    assert not q['coords'][n:].any()
+    assert np.array_equal(q['inverse_rows'][:active], rank[inv.ravel()])
+    assert (q['inverse_rows'][active:] == -1).all()
+    assert np.array_equal(q['counts'][:n],
+                          np.bincount(rank[inv.ravel()], minlength=n))
+    assert not q['counts'][n:].any()
+
+
+def test_voxelize_brute_force_and_adjoint():
+    rng = np.random.default_rng(91)
+    pts, b = _points(rng, 2000)
+    feats = rng.standard_normal((2000, 5)).astype(np.float32)
+    q = O.sparse_quantize(pts, 0.4, batch_indices=b)
+    n = int(q['active_rows'][0])
+    inv = q['inverse_rows']
+    sums = np.zeros((2000, 5))
+    np.add.at(sums, inv, feats.astype(np.float64))
+    for mode in ('sum', 'mean'):
+        out = O.voxelize_features(feats, inv, q['counts'], mode)
+        ref = sums if mode == 'sum' else (
+            sums / np.maximum(q['counts'], 1)[:, None])
+        np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+        cot = rng.standard_normal(out.shape).astype(np.float32)
+        grad = O.voxelize_features_grad(cot, inv, q['counts'], 2000, mode)
+        lhs = float((out[:n].astype(np.float64) * cot[:n]).sum())
+        rhs = float((feats.astype(np.float64) * grad).sum())
+        assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
+
+
+def test_linear_map_reproduces_affine_fields():
+    """Trilinear weights sum to one and reproduce an affine function of the
+    voxel centres exactly wherever all eight corners exist."""
+    rng = np.random.default_rng(92)
+    grid = np.stack(np.meshgrid(np.arange(6), np.arange(6), np.arange(6),
+                                indexing='ij'), -1).reshape(-1, 3)
+    coords = np.concatenate([np.zeros((len(grid), 1), np.int64), grid], 1
+                            ).astype(np.int32)
+    coords = coords[rng.permutation(len(coords))]
+    size, origin = 0.5, (0.25, -0.5, 1.0)
+    pts = (rng.uniform(0.0, 5.0, (400, 3)) * size
+           + np.asarray(origin)).astype(np.float32)
+    rows, w = O.point_voxel_map(pts, coords, voxel_size=size, origin=origin)
+    assert (rows >= 0).all()
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    a = np.array([0.3, -1.2, 2.0])
+    field = (coords[:, 1:] @ a + 0.7).astype(np.float32)[:, None]
+    got = O.point_features(field, rows, w)[:, 0]
+    pos = (pts.astype(np.float64) - origin) / size
+    np.testing.assert_allclose(got, pos @ a + 0.7, rtol=1e-5, atol=1e-5)
+    # nearest == the voxel containing the rounded position
+    rows_n, w_n = O.point_voxel_map(pts, coords, voxel_size=size,
+                                    origin=origin, interpolation='nearest')
+    near = np.floor(((pts - np.float32(origin)) / np.float32(size))
+                    + np.float32(0.5)).astype(np.int64)
+    lookup = {tuple(c[1:]): i for i, c in enumerate(coords)}
+    expect = [lookup.get(tuple(v), -1) for v in near]
+    assert rows_n[:, 0].tolist() == expect
+    assert (rows_n[:, 1:] == -1).all() and (w_n[:, 1:] == 0).all()
+
+
+def test_point_features_adjoint():
+    rng = np.random.default_rng(93)
+    pts, b = _points(rng, 1500)
+    q = O.sparse_quantize(pts, 0.6, batch_indices=b)
+    n = int(q['active_rows'][0])
+    rows, w = O.point_voxel_map(pts, q['coords'], n, voxel_size=0.6,
+                                batch_indices=b)
+    vals = rng.standard_normal((len(pts), 3)).astype(np.float32)
+    out = O.point_features(vals, rows, w)
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    grad = O.point_features_grad(g, rows, w, len(pts))
+    lhs = float((out.astype(np.float64) * g).sum())
+    rhs = float((vals.astype(np.float64) * grad).sum())
+    assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
