@@ -392,6 +392,75 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
     }
 
 
+def quantization_workload(coords, steps: int, warmup: int) -> dict:
+    """Point -> voxel quantization at the config-3 scale: 1M float32 points
+    drawn inside the voxels of the config-3 cloud (2.5 points per voxel on
+    average, unit voxels), then voxelize (mean, 64 fp32 channels) and
+    devoxelize (trilinear map + interpolation, 64 channels).  All HBM-bound;
+    each line reports its algorithmic bytes against 8 TB/s:
+      quantize: points 12 B + batch 4 B read, keys 8 B written and read
+        twice, inverse 4 B, counts 4 B per point; coords 16 B per voxel;
+      voxelize: feats read, output written, the grouping read (4 B per
+        point, 4 B per voxel);
+      interpolate: 8 rows + 8 weights per point read, the feature row of
+        every corner found read once per (point, corner), output written."""
+    import torch
+
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd._native import ext
+
+    dev = coords.device
+    gen = torch.Generator(device=dev).manual_seed(17)
+    n_vox = int(coords.shape[0])
+    n = 1000000
+    pick = torch.randint(0, n_vox, (n,), generator=gen, device=dev)
+    base = coords[pick]
+    pts = (base[:, 1:].float() + torch.rand((n, 3), generator=gen,
+                                            device=dev)).contiguous()
+    batches = base[:, 0].contiguous()
+    active = torch.tensor([n], dtype=torch.int32, device=dev)
+    q = ops.sparse_quantize(pts, 1.0, batch_indices=batches)
+    v = int(q.active_rows.item())
+    t_q = _timed(lambda: ext.sparse_quantize(pts, batches, active, [1.0],
+                                             [0.0], check_range=False),
+                 steps, warmup)
+    c = 64
+    feats = torch.randn((n, c), generator=gen, device=dev)
+    offsets, ids = q.voxel_groups(None)
+    t_vox = _timed(lambda: ext.voxelize_features_grouped(
+        feats, q.counts, offsets, ids, 'mean'), steps, warmup)
+    t_group = _timed(lambda: ext.group_by_key(q.inverse_rows, None, n),
+                     steps, warmup)
+    vfeats = torch.randn((n, c), generator=gen, device=dev)
+    pmap = ops.build_point_voxel_map(pts, q.coords, q.active_rows, 1.0,
+                                     batch_indices=batches)
+    t_map = _timed(lambda: ext.build_point_voxel_map(
+        pts, batches, active, q.coords, q.active_rows, [1.0], [0.0],
+        'linear', check_range=False), steps, warmup)
+    t_int = _timed(lambda: ext.interpolate_point_features(
+        vfeats, pmap.rows, pmap.weights), steps, warmup)
+    hbm = PEAK_HBM_GBS * 1e6
+    b_q = n * (12 + 4 + 8 * 3 + 4 + 4) + v * 16
+    b_vox = n * c * 4 + v * c * 4 + 4 * n + 4 * v
+    corners = int((pmap.rows >= 0).sum().item())
+    b_int = n * (32 + 32) + n * c * 4 + corners * c * 4
+    return {
+        'workload': '1M points in the config-3 voxels (unit voxel): '
+                    'sparse_quantize, voxelize mean 64 ch, trilinear '
+                    'devoxelize 64 ch',
+        'points': n, 'voxels': v,
+        'quantize_ms': round(t_q, 4),
+        'quantize_hbm_frac': round(b_q / t_q / hbm, 4),
+        'group_ms': round(t_group, 4),
+        'voxelize_ms': round(t_vox, 4),
+        'voxelize_hbm_frac': round(b_vox / t_vox / hbm, 4),
+        'corners_found': corners,
+        'point_map_ms': round(t_map, 4),
+        'interpolate_ms': round(t_int, 4),
+        'interpolate_hbm_frac': round(b_int / t_int / hbm, 4),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -505,6 +574,8 @@ def main() -> int:
                                            edges, args.steps, args.warmup)
     record['pooling'] = pooling_workload(coords, args.steps, args.warmup)
     record['decoder'] = decoder_workload(coords, args.steps, args.warmup)
+    record['quantization'] = quantization_workload(coords, args.steps,
+                                                   args.warmup)
     if not args.no_secondary:
         record['secondary'] = secondary_workloads()
     if not args.no_cpu_baseline:

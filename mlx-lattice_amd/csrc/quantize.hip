@@ -146,42 +146,80 @@ __device__ inline float mean_scale(int mode, const int32_t* counts, int v) {
     return mode == 1 ? (1.0f / static_cast<float>(max(counts[v], 1))) : 1.0f;
 }
 
+// Feature kernels run one lane per (row, V-channel chunk): V = 4 (16-byte
+// loads and stores) when the channel count allows, else 1.  Each channel is
+// still accumulated in the same order with the same roundings.
+template <int V> struct Vec;
+template <> struct Vec<1> {
+    float v[1];
+    __device__ static Vec load(const float* p) { return {{p[0]}}; }
+    __device__ void store(float* p) const { p[0] = v[0]; }
+};
+template <> struct Vec<4> {
+    float v[4];
+    __device__ static Vec load(const float* p) {
+        const float4 f = *reinterpret_cast<const float4*>(p);
+        return {{f.x, f.y, f.z, f.w}};
+    }
+    __device__ void store(float* p) const { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+};
+
+template <int V>
+__device__ inline void add_scaled(Vec<V>& acc, const Vec<V>& x, float s) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc.v[j] = acc.v[j] + x.v[j] * s;
+}
+
+template <int V>
 __global__ void __launch_bounds__(kThreads)
 voxelize_csr(int mode, const float* __restrict__ feats, int channels, const int32_t* __restrict__ counts,
              int voxel_rows, const int32_t* __restrict__ offsets, const int32_t* __restrict__ point_ids,
              float* __restrict__ out) {
-    const long long total = static_cast<long long>(voxel_rows) * channels;
+    const int chunks = channels / V;
+    const long long total = static_cast<long long>(voxel_rows) * chunks;
     for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
          t += static_cast<long long>(gridDim.x) * kThreads) {
-        const int v = static_cast<int>(t / channels);
-        const int c = static_cast<int>(t - static_cast<long long>(v) * channels);
+        const int v = static_cast<int>(t / chunks);
+        const int c = static_cast<int>(t - static_cast<long long>(v) * chunks) * V;
         const float scale = mean_scale(mode, counts, v);
-        float acc = 0.0f;
-        for (int i = offsets[v]; i < offsets[v + 1]; ++i) {
-            acc = (acc + (feats[static_cast<long long>(point_ids[i]) * channels + c] * scale));
+        Vec<V> acc{};
+        const int lo = offsets[v];
+        const int hi = offsets[v + 1];
+        int i = lo;
+        for (; i + 1 < hi; i += 2) {  // two gathers in flight
+            const Vec<V> a = Vec<V>::load(feats + static_cast<long long>(point_ids[i]) * channels + c);
+            const Vec<V> b = Vec<V>::load(feats + static_cast<long long>(point_ids[i + 1]) * channels + c);
+            add_scaled(acc, a, scale);
+            add_scaled(acc, b, scale);
         }
-        out[t] = acc;
+        if (i < hi) add_scaled(acc, Vec<V>::load(feats + static_cast<long long>(point_ids[i]) * channels + c), scale);
+        acc.store(out + static_cast<long long>(v) * channels + c);
     }
 }
 
+template <int V>
 __global__ void __launch_bounds__(kThreads)
 voxelize_grad(int mode, const float* __restrict__ cot, int voxel_rows, int channels,
               const int32_t* __restrict__ inverse_rows, const int32_t* __restrict__ counts, int point_rows,
               const int32_t* __restrict__ point_active, float* __restrict__ grad) {
     const int active = min(max(*point_active, 0), point_rows);
-    const long long total = static_cast<long long>(point_rows) * channels;
+    const int chunks = channels / V;
+    const long long total = static_cast<long long>(point_rows) * chunks;
     for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
          t += static_cast<long long>(gridDim.x) * kThreads) {
-        const int p = static_cast<int>(t / channels);
-        const int c = static_cast<int>(t - static_cast<long long>(p) * channels);
-        float value = 0.0f;
+        const int p = static_cast<int>(t / chunks);
+        const int c = static_cast<int>(t - static_cast<long long>(p) * chunks) * V;
+        Vec<V> value{};
         if (p < active) {
             const int v = inverse_rows[p];
             if (v >= 0 && v < voxel_rows) {
-                value = (cot[static_cast<long long>(v) * channels + c] * mean_scale(mode, counts, v));
+                const float s = mean_scale(mode, counts, v);
+                const Vec<V> x = Vec<V>::load(cot + static_cast<long long>(v) * channels + c);
+#pragma unroll
+                for (int j = 0; j < V; ++j) value.v[j] = x.v[j] * s;
             }
         }
-        grad[t] = value;
+        value.store(grad + static_cast<long long>(p) * channels + c);
     }
 }
 
@@ -267,42 +305,69 @@ map_points(CoordTable table, const float* __restrict__ points, const int32_t* __
     }
 }
 
+template <int V>
 __global__ void __launch_bounds__(kThreads)
 interpolate(const float* __restrict__ values, int voxel_rows, int channels, const int32_t* __restrict__ rows,
             const float* __restrict__ weights, int point_rows, float* __restrict__ out) {
-    const long long total = static_cast<long long>(point_rows) * channels;
+    const int chunks = channels / V;
+    const long long total = static_cast<long long>(point_rows) * chunks;
     for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
          t += static_cast<long long>(gridDim.x) * kThreads) {
-        const int p = static_cast<int>(t / channels);
-        const int c = static_cast<int>(t - static_cast<long long>(p) * channels);
-        float acc = 0.0f;
+        const int p = static_cast<int>(t / chunks);
+        const int c = static_cast<int>(t - static_cast<long long>(p) * chunks) * V;
+        const int4* r4 = reinterpret_cast<const int4*>(rows + 8ll * p);
+        const float4* w4 = reinterpret_cast<const float4*>(weights + 8ll * p);
+        const int4 ra = r4[0], rb = r4[1];
+        const float4 wa = w4[0], wb = w4[1];
+        const int r[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+        const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        Vec<V> x[8];
+#pragma unroll
+        for (int corner = 0; corner < 8; ++corner) {  // all gathers in flight
+            x[corner] = (r[corner] >= 0 && r[corner] < voxel_rows)
+                            ? Vec<V>::load(values + static_cast<long long>(r[corner]) * channels + c)
+                            : Vec<V>{};
+        }
+        Vec<V> acc{};
 #pragma unroll
         for (int corner = 0; corner < 8; ++corner) {
-            const int v = rows[8ll * p + corner];
-            if (v < 0 || v >= voxel_rows) continue;
-            acc = (acc + (values[static_cast<long long>(v) * channels + c] * weights[8ll * p + corner]));
+            if (r[corner] >= 0 && r[corner] < voxel_rows) add_scaled(acc, x[corner], w[corner]);
         }
-        out[t] = acc;
+        acc.store(out + static_cast<long long>(p) * channels + c);
     }
 }
 
+template <int V>
 __global__ void __launch_bounds__(kThreads)
 interpolate_grad(const float* __restrict__ point_grad, int channels, const float* __restrict__ weights,
                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ entries, int voxel_rows,
                  float* __restrict__ out) {
-    const long long total = static_cast<long long>(voxel_rows) * channels;
+    const int chunks = channels / V;
+    const long long total = static_cast<long long>(voxel_rows) * chunks;
     for (long long t = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; t < total;
          t += static_cast<long long>(gridDim.x) * kThreads) {
-        const int v = static_cast<int>(t / channels);
-        const int c = static_cast<int>(t - static_cast<long long>(v) * channels);
-        float acc = 0.0f;
+        const int v = static_cast<int>(t / chunks);
+        const int c = static_cast<int>(t - static_cast<long long>(v) * chunks) * V;
+        Vec<V> acc{};
         for (int i = offsets[v]; i < offsets[v + 1]; ++i) {
             const int e = entries[i];
-            acc = (acc + (point_grad[static_cast<long long>(e >> 3) * channels + c] * weights[e]));
+            add_scaled(acc, Vec<V>::load(point_grad + static_cast<long long>(e >> 3) * channels + c), weights[e]);
         }
-        out[t] = acc;
+        acc.store(out + static_cast<long long>(v) * channels + c);
     }
 }
+
+// Launches kernel<4> when the channels split into 16-byte chunks, else <1>.
+#define LATTICE_LAUNCH_VEC(kernel, channels, rows, stream, ...)                                             \
+    do {                                                                                                    \
+        if ((channels) % 4 == 0) {                                                                          \
+            const long long work_ = static_cast<long long>(rows) * ((channels) / 4);                        \
+            kernel<4><<<grid_for(work_, kThreads, 1u << 16), kThreads, 0, stream>>>(__VA_ARGS__);           \
+        } else {                                                                                            \
+            const long long work_ = static_cast<long long>(rows) * (channels);                              \
+            kernel<1><<<grid_for(work_, kThreads, 1u << 16), kThreads, 0, stream>>>(__VA_ARGS__);           \
+        }                                                                                                   \
+    } while (0)
 
 int check_grid(const float* size, const float* origin) {
     LATTICE_REQUIRE(size != nullptr && origin != nullptr, "voxel_size and origin must be non-null.");
@@ -379,9 +444,8 @@ extern "C" int lattice_hip_voxelize_features(int mode, const float* feats, int c
     LATTICE_REQUIRE(channels > 0 && voxel_rows >= 0, "voxelize shapes must be positive.");
     if (voxel_rows == 0) return LATTICE_OK;
     LATTICE_REQUIRE(feats && counts && voxel_offsets && point_ids && out, "voxelize pointers must be non-null.");
-    const long long total = static_cast<long long>(voxel_rows) * channels;
-    voxelize_csr<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
-        mode, feats, channels, counts, voxel_rows, voxel_offsets, point_ids, out);
+    LATTICE_LAUNCH_VEC(voxelize_csr, channels, voxel_rows, as_stream(stream_ptr), mode, feats, channels, counts,
+                       voxel_rows, voxel_offsets, point_ids, out);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -395,9 +459,8 @@ extern "C" int lattice_hip_voxelize_features_grad(int mode, const float* cot, in
     if (point_rows == 0) return LATTICE_OK;
     LATTICE_REQUIRE(grad && inverse_rows && point_active && (voxel_rows == 0 || (cot && counts)),
                     "voxelize gradient pointers must be non-null.");
-    const long long total = static_cast<long long>(point_rows) * channels;
-    voxelize_grad<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
-        mode, cot, voxel_rows, channels, inverse_rows, counts, point_rows, point_active, grad);
+    LATTICE_LAUNCH_VEC(voxelize_grad, channels, point_rows, as_stream(stream_ptr), mode, cot, voxel_rows, channels,
+                       inverse_rows, counts, point_rows, point_active, grad);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -455,9 +518,8 @@ extern "C" int lattice_hip_interpolate_point_features(const float* values, int v
     if (point_rows == 0) return LATTICE_OK;
     LATTICE_REQUIRE(rows && weights && out && (voxel_rows == 0 || values),
                     "interpolation pointers must be non-null.");
-    const long long total = static_cast<long long>(point_rows) * channels;
-    interpolate<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
-        values, voxel_rows, channels, rows, weights, point_rows, out);
+    LATTICE_LAUNCH_VEC(interpolate, channels, point_rows, as_stream(stream_ptr), values, voxel_rows, channels, rows,
+                       weights, point_rows, out);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -470,9 +532,8 @@ extern "C" int lattice_hip_interpolate_point_features_grad(const float* point_gr
     if (voxel_rows == 0) return LATTICE_OK;
     LATTICE_REQUIRE(point_grad && weights && voxel_offsets && entry_ids && out,
                     "interpolation gradient pointers must be non-null.");
-    const long long total = static_cast<long long>(voxel_rows) * channels;
-    interpolate_grad<<<grid_for(total, kThreads, 1u << 16), kThreads, 0, as_stream(stream_ptr)>>>(
-        point_grad, channels, weights, voxel_offsets, entry_ids, voxel_rows, out);
+    LATTICE_LAUNCH_VEC(interpolate_grad, channels, voxel_rows, as_stream(stream_ptr), point_grad, channels, weights,
+                       voxel_offsets, entry_ids, voxel_rows, out);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }

@@ -237,8 +237,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("reduce"),
           "Gradient of sparse pooling with respect to the input features.");
     m.def("sparse_quantize", &ln::sparse_quantize, py::arg("points"), py::arg("batch_indices"),
-          py::arg("active_rows"), py::arg("voxel_size"), py::arg("origin"),
-          "Voxelize points: (coords, active_rows, inverse_rows, counts).");
+          py::arg("active_rows"), py::arg("voxel_size"), py::arg("origin"), py::kw_only(),
+          py::arg("check_range") = true, "Voxelize points: (coords, active_rows, inverse_rows, counts).");
     m.def("group_by_key", &ln::group_by_key, py::arg("keys"), py::arg("count"), py::arg("groups"));
     m.def("voxelize_features", &ln::voxelize_features, py::arg("feats"), py::arg("inverse_rows"),
           py::arg("counts"), py::arg("active_rows"), py::arg("reduction"));
@@ -248,7 +248,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("counts"), py::arg("active_rows"), py::arg("point_rows"), py::arg("reduction"));
     m.def("build_point_voxel_map", &ln::build_point_voxel_map, py::arg("points"), py::arg("batch_indices"),
           py::arg("point_active_rows"), py::arg("voxel_coords"), py::arg("voxel_active_rows"),
-          py::arg("voxel_size"), py::arg("origin"), py::arg("interpolation"));
+          py::arg("voxel_size"), py::arg("origin"), py::arg("interpolation"), py::kw_only(),
+          py::arg("check_range") = true);
     m.def("interpolate_point_features", &ln::interpolate_point_features, py::arg("voxel_feats"), py::arg("rows"),
           py::arg("weights"));
     m.def("interpolate_point_features_grad", &ln::interpolate_point_features_grad, py::arg("point_grad"),
