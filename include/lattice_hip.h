@@ -295,12 +295,19 @@ int lattice_hip_build_sorted_implicit_gemm_view(
 /* Float sparse conv over the output CSR (cpu/algorithms.cpp:180-302):
  * out[o] = sum_{e in CSR(o)} feats[in_rows[e]] @ W[kernel_ids[e]] with an
  * fp32 accumulator; rows >= counts[1] are zero.  feats [n_in, c_in];
- * out [out_capacity, c_out], both in `dtype`. */
+ * out [out_capacity, c_out], both in `dtype`.
+ * bias (optional, [c_out] in `dtype`, NULL = none) fuses the operator's
+ * `feats + bias` (ops/conv.py:460-469) into the store: the conv result is
+ * rounded to `dtype`, then the bias is added and the sum rounded again, so
+ * the output equals the separate add bit for bit, on every row (rows
+ * without edges hold the bias).  The same holds for the two entries
+ * below. */
 int lattice_hip_sparse_conv_features(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out, const int32_t* in_rows,
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
-    const int32_t* row_offsets, int out_capacity, void* out, void* stream);
+    const int32_t* row_offsets, int out_capacity, void* out, const void* bias,
+    void* stream);
 
 /* Implicit-GEMM conv over the sorted view (the reference's sorted plan):
  * row i of the mask-sorted order gathers feats[sorted_kv_out_in_map[k, i]]
@@ -320,8 +327,8 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out,
     const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
-    const int32_t* reorder_rows, int out_capacity, void* out, void* workspace,
-    size_t workspace_bytes, void* stream);
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Tuning knob with no counterpart in the reference: rows of the sorted
  * order owned by one wavefront in the implicit-GEMM route (32 or 64).
@@ -345,7 +352,8 @@ int lattice_hip_sparse_quantized_conv_features(
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
     const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
-    void* out, void* workspace, size_t workspace_bytes, void* stream);
+    void* out, const void* bias, void* workspace, size_t workspace_bytes,
+    void* stream);
 
 /* Input gradient of the float conv (SparseConvFeaturesInputGrad,
  * primitive.cpp:192-260, 597-639; cpu/algorithms.cpp:355-410):

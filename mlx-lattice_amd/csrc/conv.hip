@@ -50,6 +50,20 @@ template <> struct Elem<__bf16> {
     __device__ static void store(__bf16* p, long long i, float v) { p[i] = static_cast<__bf16>(v); }
 };
 
+// Output value with the optional bias added as a separate operation: the
+// conv result is rounded to T first, then bias is added and the sum rounded
+// again, exactly as `feats + bias` over the stored output computes it
+// (ops/conv.py:460-469).
+template <typename T>
+__device__ inline void store_out(T* out, long long i, float acc, const T* bias, int co) {
+    if (bias == nullptr) {
+        Elem<T>::store(out, i, acc);
+        return;
+    }
+    const float rounded = static_cast<float>(static_cast<T>(acc));
+    Elem<T>::store(out, i, rounded + Elem<T>::load(bias, co));
+}
+
 // ------------------------------------------------------------- CSR route --
 
 struct WeightIndex {
@@ -73,7 +87,7 @@ __global__ void __launch_bounds__(256)
 conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, WeightIndex widx,
          const int32_t* __restrict__ in_rows, const int32_t* __restrict__ kernel_ids,
          const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ row_offsets,
-         int out_capacity, T* __restrict__ out, bool staged) {
+         int out_capacity, T* __restrict__ out, const T* __restrict__ bias, bool staged) {
     extern __shared__ float wlds[];
     const int c_out = widx.c_out;
     if (staged) {
@@ -111,7 +125,7 @@ conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, W
                 }
             }
         }
-        Elem<T>::store(out, t, acc);
+        store_out(out, t, acc, bias, co);
     }
 }
 
@@ -135,7 +149,8 @@ __global__ void __launch_bounds__(256)
 quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights, const T* __restrict__ scales,
                const T* __restrict__ biases, QuantIndex q, const int32_t* __restrict__ in_rows,
                const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
-               const int32_t* __restrict__ row_offsets, int out_capacity, T* __restrict__ out, bool staged) {
+               const int32_t* __restrict__ row_offsets, int out_capacity, T* __restrict__ out,
+               const T* __restrict__ bias, bool staged) {
     extern __shared__ float wlds[];
     if (staged) {
         const int nw = q.K * q.c_in * q.c_out;
@@ -172,7 +187,7 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
                 }
             }
         }
-        Elem<T>::store(out, t, acc);
+        store_out(out, t, acc, bias, co);
     }
 }
 
@@ -579,7 +594,7 @@ template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
-           const int32_t* __restrict__ block_order, T* __restrict__ out) {
+           const int32_t* __restrict__ block_order, T* __restrict__ out, const T* __restrict__ bias) {
     using V = typename MfmaOps<T>::vec;
     constexpr int WAVES = S::WAVES;
     constexpr int WAVE_ROWS = S::WAVE_ROWS;
@@ -708,6 +723,13 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     // Epilogue: stage this wave's tile in LDS (pieces swizzled by row), then
     // write whole rows with 16-byte stores to out[reorder_rows[row]].
     T* stage = lds + wave * WAVE_ROWS * S::EROW;
+    // Optional bias, added after the conv result is rounded (as a separate
+    // `feats + bias` would): one value per column this lane writes.
+    float bcol[S::CB];
+#pragma unroll
+    for (int cb = 0; cb < S::CB; ++cb) {
+        bcol[cb] = bias != nullptr ? static_cast<float>(bias[wc * S::WAVE_COLS + cb * 16 + lr]) : 0.0f;
+    }
 #pragma unroll
     for (int rb = 0; rb < S::RB; ++rb) {
 #pragma unroll
@@ -717,7 +739,9 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
                 const int r = rb * 16 + (lane >> 4) * 4 + q;
                 const int piece = (cb * 16 + lr) / 8;
                 const int slot = piece ^ (r % S::EPIECES);
-                stage[r * S::EROW + slot * 8 + (lr & 7)] = static_cast<T>(acc[rb][cb][q]);
+                T v = static_cast<T>(acc[rb][cb][q]);
+                if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + bcol[cb]);
+                stage[r * S::EROW + slot * 8 + (lr & 7)] = v;
             }
         }
     }
@@ -785,7 +809,7 @@ schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, in
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
-                       T* out, hipStream_t stream) {
+                       T* out, const T* bias, hipStream_t stream) {
     const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
     if (blocks > kMaxScheduledTiles) schedule = nullptr;
     if (schedule != nullptr) {
@@ -793,7 +817,7 @@ int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, con
         LATTICE_LAUNCH_CHECK();
     }
     conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks), S::THREADS, 0, stream>>>(
-        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out);
+        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, bias);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -809,11 +833,11 @@ extern "C" void lattice_hip_sweep_variant(int v) { g_igemm_sweep = v; }
 template <typename T, typename BSource>
 int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
                  const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, T* out,
-                 hipStream_t stream) {
+                 const T* bias, hipStream_t stream) {
     if (rows <= 0) return LATTICE_OK;
 #define LATTICE_IGEMM_LAUNCH(...) \
     launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, \
-                                                   schedule, out, stream)
+                                                   schedule, out, bias, stream)
 #ifdef LATTICE_IGEMM_SWEEP
     if (c_out == 128 && g_igemm_sweep >= 0) {
         switch (g_igemm_sweep) {
@@ -904,7 +928,7 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
                                                 int c_out, const int32_t* in_rows, const int32_t* kernel_ids,
                                                 const int32_t* counts, int edge_capacity,
                                                 const int32_t* row_offsets, int out_capacity, void* out,
-                                                void* stream_ptr) {
+                                                const void* bias, void* stream_ptr) {
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(n_in >= 0 && c_in > 0 && c_out > 0, "feats must have shape (N, C_in).");
@@ -925,17 +949,19 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
         conv_csr<float><<<grid, 256, lds, stream>>>(static_cast<const float*>(feats), c_in,
                                                   static_cast<const float*>(weights), widx, in_rows, kernel_ids,
                                                   counts, edge_capacity, row_offsets, out_capacity,
-                                                  static_cast<float*>(out), staged);
+                                                  static_cast<float*>(out), static_cast<const float*>(bias), staged);
     } else if (dtype == LATTICE_F16) {
         conv_csr<_Float16><<<grid, 256, lds, stream>>>(static_cast<const _Float16*>(feats), c_in,
                                                      static_cast<const _Float16*>(weights), widx, in_rows,
                                                      kernel_ids, counts, edge_capacity, row_offsets, out_capacity,
-                                                     static_cast<_Float16*>(out), staged);
+                                                     static_cast<_Float16*>(out),
+                                                     static_cast<const _Float16*>(bias), staged);
     } else {
         conv_csr<__bf16><<<grid, 256, lds, stream>>>(static_cast<const __bf16*>(feats), c_in,
                                                    static_cast<const __bf16*>(weights), widx, in_rows, kernel_ids,
                                                    counts, edge_capacity, row_offsets, out_capacity,
-                                                   static_cast<__bf16*>(out), staged);
+                                                   static_cast<__bf16*>(out), static_cast<const __bf16*>(bias),
+                                                   staged);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
@@ -944,7 +970,7 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
 extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights, int weight_layout, int kernel_count,
     int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
-    int out_capacity, void* out, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    int out_capacity, void* out, const void* bias, void* workspace, size_t workspace_bytes, void* stream_ptr) {
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(dtype != LATTICE_F32, "the implicit GEMM route runs on fp16/bf16 matrix cores.");
@@ -968,11 +994,12 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         FloatB<_Float16> b{static_cast<const _Float16*>(weights), s_co, s_k};
         return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                       tile_masks, reorder_rows, out_capacity, schedule,
-                                      static_cast<_Float16*>(out), stream);
+                                      static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
     }
     FloatB<__bf16> b{static_cast<const __bf16*>(weights), s_co, s_k};
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out), stream);
+                                tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
+                                static_cast<const __bf16*>(bias), stream);
 }
 
 extern "C" int lattice_hip_sparse_quantized_conv_features(
@@ -980,8 +1007,8 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const void* biases, int kernel_count, int c_out, int storage_c_in, int group_size, int bits,
     const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
-    const int32_t* reorder_rows, int out_capacity, void* out, void* workspace, size_t workspace_bytes,
-    void* stream_ptr) {
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias, void* workspace,
+    size_t workspace_bytes, void* stream_ptr) {
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized convolution bits must be 4 or 8.");
@@ -1006,13 +1033,13 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
                                 packed_words, groups, group_size, c_out, bits};
             return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                           tile_masks, reorder_rows, out_capacity, schedule,
-                                          static_cast<_Float16*>(out), stream);
+                                          static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
         }
         PackedB<__bf16> b{weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases),
                           packed_words, groups, group_size, c_out, bits};
         return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                     tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
-                                    stream);
+                                    static_cast<const __bf16*>(bias), stream);
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");
     QuantIndex q{kernel_count, c_in, c_out, packed_words, groups, group_size, bits};
@@ -1025,17 +1052,17 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
         quant_conv_csr<float><<<grid, 256, lds, stream>>>(
             static_cast<const float*>(feats), weights, static_cast<const float*>(scales),
             static_cast<const float*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<float*>(out), staged);
+            out_capacity, static_cast<float*>(out), static_cast<const float*>(bias), staged);
     } else if (dtype == LATTICE_F16) {
         quant_conv_csr<_Float16><<<grid, 256, lds, stream>>>(
             static_cast<const _Float16*>(feats), weights, static_cast<const _Float16*>(scales),
             static_cast<const _Float16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<_Float16*>(out), staged);
+            out_capacity, static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), staged);
     } else {
         quant_conv_csr<__bf16><<<grid, 256, lds, stream>>>(
             static_cast<const __bf16*>(feats), weights, static_cast<const __bf16*>(scales),
             static_cast<const __bf16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<__bf16*>(out), staged);
+            out_capacity, static_cast<__bf16*>(out), static_cast<const __bf16*>(bias), staged);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;

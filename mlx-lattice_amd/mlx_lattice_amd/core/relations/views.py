@@ -10,7 +10,7 @@ relation's device; counts stay on the device.
 from __future__ import annotations
 
 from collections.abc import Callable
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Literal
 
 import torch
@@ -130,9 +130,16 @@ class SparseRelationContract:
     stride: Triple = (1, 1, 1)
     padding: Triple = (0, 0, 0)
     kind: RelationKind = 'forward'
+    # One view object per count: a strided output tensor is keyed in its
+    # coordinate manager by the identity of its active-row array, so handing
+    # out the same view lets repeated calls reuse the output's relations.
+    _edge_count: torch.Tensor = field(init=False, repr=False, compare=False)
+    _out_count: torch.Tensor = field(init=False, repr=False, compare=False)
 
     def __post_init__(self) -> None:
         _validate_counts(self.counts)
+        object.__setattr__(self, '_edge_count', self.counts[:1])
+        object.__setattr__(self, '_out_count', self.counts[1:2])
         for name in ('out_coords', 'source_coords', 'target_coords'):
             value = getattr(self, name)
             if value is not None:
@@ -171,11 +178,11 @@ class SparseRelationContract:
 
     @property
     def edge_count(self) -> torch.Tensor:
-        return self.counts[:1]
+        return self._edge_count
 
     @property
     def out_count(self) -> torch.Tensor:
-        return self.counts[1:2]
+        return self._out_count
 
 
 @dataclass(frozen=True, slots=True, init=False)

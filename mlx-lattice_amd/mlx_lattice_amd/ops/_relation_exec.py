@@ -51,6 +51,7 @@ def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
 def sparse_conv_features_from_relation(feats: torch.Tensor,
                                        weight: torch.Tensor,
                                        relation: KernelRelation,
+                                       bias: torch.Tensor | None = None,
                                        ) -> torch.Tensor:
     """Execute sparse convolution over a prebuilt relation
     (_relation_exec.py:84-116).  Differentiable in ``feats`` and ``weight``:
@@ -58,9 +59,22 @@ def sparse_conv_features_from_relation(feats: torch.Tensor,
     (native/features/convolution/primitive.cpp:137-176)."""
     _require_static(relation)
     if torch.is_grad_enabled() and (feats.requires_grad
-                                    or weight.requires_grad):
-        return _SparseConvFeatures.apply(feats, weight, relation)
-    return _conv_features(feats, weight, relation)
+                                    or weight.requires_grad
+                                    or (bias is not None
+                                        and bias.requires_grad)):
+        out = _SparseConvFeatures.apply(feats, weight, relation)
+        return out if bias is None else _add_bias(out, bias)
+    return _conv_features(feats, weight, relation, bias)
+
+
+def _add_bias(feats: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    if bias.ndim != 1:
+        raise ValueError('bias must have shape (C_out,).')
+    if bias.shape[0] != feats.shape[1]:
+        raise ValueError('bias channels must match output channels.')
+    if bias.dtype != feats.dtype:
+        raise ValueError('bias dtype must match output features.')
+    return feats + bias
 
 
 class _SparseConvFeatures(torch.autograd.Function):
@@ -152,29 +166,28 @@ def sparse_conv_weight_grad_from_relation(feats: torch.Tensor,
 
 
 def _conv_features(feats: torch.Tensor, weight: torch.Tensor,
-                   relation: KernelRelation) -> torch.Tensor:
+                   relation: KernelRelation,
+                   bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Forward features on the matrix-core or the CSR route; ``bias``
+    (optional) is added in the kernels' store, after the conv result is
+    rounded, exactly as a separate ``feats + bias``."""
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
     if feats.ndim == 2 and _matrix_core_eligible(
             feats.dtype, int(feats.shape[1]), c_out, relation,
             int(feats.shape[0])):
         return sparse_conv_features_sorted_from_relation(feats, weight,
-                                                         relation)
-    input_csr = relation.input_csr
-    kernel_csr = relation.kernel_csr
-    if input_csr.edge_ids is None or kernel_csr.edge_ids is None:
-        raise ValueError('kernel relation is missing grouped CSR views.')
-    return ext.sparse_conv_features(
-        feats, weight, relation.edges.in_rows, relation.edges.out_rows,
-        relation.edges.kernel_ids, relation.counts,
-        relation.output_csr.row_offsets, input_csr.row_offsets,
-        input_csr.edge_ids, kernel_csr.row_offsets, kernel_csr.edge_ids,
-        relation.n_out_capacity, relation.n_kernels)
+                                                         relation, bias=bias)
+    return ext.sparse_conv_features_csr(
+        feats, weight, relation.edges.in_rows, relation.edges.kernel_ids,
+        relation.counts, relation.output_csr.row_offsets,
+        relation.n_out_capacity, relation.n_kernels, bias=bias)
 
 
 def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
                                               weight: torch.Tensor,
                                               relation: KernelRelation, *,
                                               store_sorted: bool = False,
+                                              bias: torch.Tensor | None = None,
                                               ) -> torch.Tensor:
     """Matrix-core implicit GEMM over the sorted view
     (_relation_exec.py:119-156)."""
@@ -193,12 +206,13 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
         relation.edges.kernel_ids, relation.counts,
         relation.output_csr.row_offsets, None, None, None, None,
         relation.n_out_capacity, relation.n_kernels,
-        store_sorted=store_sorted)
+        store_sorted=store_sorted, bias=bias)
 
 
 def sparse_quantized_conv_features_from_relation(
         feats: torch.Tensor, weight: QuantizedWeight,
-        relation: KernelRelation) -> torch.Tensor:
+        relation: KernelRelation,
+        bias: torch.Tensor | None = None) -> torch.Tensor:
     """Quantized sparse convolution over a prebuilt relation
     (_relation_exec.py:19-61); the sorted plan is passed when the matrix-core
     route applies."""
@@ -221,7 +235,7 @@ def sparse_quantized_conv_features_from_relation(
         relation.output_csr.row_offsets, kv, reorder, tiles,
         relation.n_out_capacity, relation.n_kernels, weight.in_channels,
         weight.out_channels, weight.storage_in_channels, weight.group_size,
-        weight.bits)
+        weight.bits, bias=bias)
 
 
 def sparse_pool_features_from_relation(feats: torch.Tensor,

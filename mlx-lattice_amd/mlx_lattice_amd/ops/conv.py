@@ -117,21 +117,29 @@ def _relation_conv(x: SparseTensor, weight, bias, spec: KernelSpec, *,
     relation = _kernel_relation(x, spec, map_kind, target_key=target_key)
     if relation.n_out_capacity is None or relation.n_kernels is None:
         raise ValueError('kernel relation is missing static shape metadata.')
+    # The bias is added in the conv kernels' store (after rounding, as a
+    # separate add would) unless autograd must see the add.
+    fuse = bias is not None and not (
+        torch.is_grad_enabled() and bias.requires_grad)
+    fused = bias if fuse else None
     feats = (sparse_quantized_conv_features_from_relation(x.feats, weight,
-                                                          relation)
+                                                          relation, fused)
              if isinstance(weight, QuantizedWeight)
-             else sparse_conv_features_from_relation(x.feats, weight, relation))
+             else sparse_conv_features_from_relation(x.feats, weight, relation,
+                                                     fused))
+    if not fuse:
+        feats = _with_bias(feats, bias)
     if reuse_input_coords:
-        return x.replace(feats=_with_bias(feats, bias))
+        return x.replace(feats=feats)
     if relation.out_coords is None:
         raise ValueError('kernel relation is missing output coordinates.')
     if target_key is not None and map_kind == 'target':
         return SparseTensor(
-            x.coord_manager.coords(target_key), _with_bias(feats, bias),
+            x.coord_manager.coords(target_key), feats,
             stride=output_stride, coord_key=target_key,
             coord_manager=x.coord_manager,
             active_rows=x.coord_manager.active_rows(target_key))
-    return SparseTensor(relation.out_coords, _with_bias(feats, bias),
+    return SparseTensor(relation.out_coords, feats,
                         stride=output_stride, coord_manager=x.coord_manager,
                         active_rows=relation.out_count)
 

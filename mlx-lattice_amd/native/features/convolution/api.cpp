@@ -23,6 +23,21 @@ void require_i32_vector(const at::Tensor& t, const char* message) {
     if (t.dim() != 1 || t.scalar_type() != at::kInt) throw std::invalid_argument(message);
 }
 
+// Optional fused bias: (C_out,) in the feature dtype on the same device, as
+// the operator's _with_bias validates it (ops/conv.py:460-469).
+const void* bias_ptr(const std::optional<at::Tensor>& bias, const at::Tensor& feats, int64_t c_out,
+                     at::Tensor* keep) {
+    if (!bias.has_value() || !bias->defined()) return nullptr;
+    if (bias->dim() != 1) throw std::invalid_argument("bias must have shape (C_out,).");
+    if (bias->size(0) != c_out) throw std::invalid_argument("bias channels must match output channels.");
+    if (bias->scalar_type() != feats.scalar_type()) {
+        throw std::invalid_argument("bias dtype must match output features.");
+    }
+    require_device(*bias, "bias");
+    *keep = bias->contiguous();
+    return keep->data_ptr();
+}
+
 void validate_weights(const at::Tensor& feats, const at::Tensor& weights, int n_kernels, const char* op) {
     if (feats.dim() != 2) throw std::invalid_argument("feats must have shape (N, C_in).");
     if (weights.dim() != 3 && weights.dim() != 5) {
@@ -55,7 +70,8 @@ at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& we
                                 const at::Tensor& out_rows, const at::Tensor& kernel_ids, const at::Tensor& counts,
                                 const at::Tensor& row_offsets, const at::Tensor& in_row_offsets,
                                 const at::Tensor& in_edge_ids, const at::Tensor& kernel_row_offsets,
-                                const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels) {
+                                const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels,
+                                const std::optional<at::Tensor>& bias) {
     const char* op = "sparse_conv_features";
     if (out_capacity < 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
@@ -100,10 +116,48 @@ at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& we
     const int64_t c_out = out_channels_of(weights);
     at::Tensor out = at::empty({out_capacity, c_out}, feats.options());
     const int layout = weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D;
+    at::Tensor bias_keep;
+    const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
     check_status(lattice_hip_sparse_conv_features(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
-        ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(),
+        ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(), b,
+        current_stream(feats)));
+    return out;
+}
+
+at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor& weights_in, const at::Tensor& in_rows,
+                                    const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                    const at::Tensor& row_offsets, int out_capacity, int n_kernels,
+                                    const std::optional<at::Tensor>& bias) {
+    const char* op = "sparse_conv_features";
+    if (out_capacity < 0) {
+        throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
+    }
+    validate_weights(feats_in, weights_in, n_kernels, op);
+    require_i32_vector(in_rows, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    require_i32_vector(kernel_ids, "relation rows and kernel_ids must be one-dimensional int32 arrays.");
+    if (in_rows.size(0) != kernel_ids.size(0)) {
+        throw std::invalid_argument("relation row arrays and kernel_ids must have equal capacity.");
+    }
+    if (counts.dim() != 1 || counts.size(0) != 2 || counts.scalar_type() != at::kInt) {
+        throw std::invalid_argument("counts must have shape (2,) and int32 dtype.");
+    }
+    require_i32_vector(row_offsets, "row_offsets must be a one-dimensional int32 array.");
+    if (row_offsets.size(0) != out_capacity + 1) {
+        throw std::invalid_argument("row_offsets length must match out_capacity + 1.");
+    }
+    const at::Tensor feats = feats_in.contiguous();
+    const at::Tensor weights = weights_in.contiguous();
+    const int64_t c_out = out_channels_of(weights);
+    at::Tensor out = at::empty({out_capacity, c_out}, feats.options());
+    const int layout = weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D;
+    at::Tensor bias_keep;
+    const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
+    check_status(lattice_hip_sparse_conv_features(
+        dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
+        weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
+        ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(), b,
         current_stream(feats)));
     return out;
 }
@@ -112,7 +166,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
                                                      const at::Tensor& sorted_out_in_map,
                                                      const at::Tensor& sorted_kv_out_in_map,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
-                                                     int out_capacity, int n_kernels, bool store_sorted) {
+                                                     int out_capacity, int n_kernels, bool store_sorted,
+                                                     const std::optional<at::Tensor>& bias) {
     const char* op = "sparse_conv_features_sorted_implicit_gemm";
     if (sorted_out_in_map.dim() != 2 || sorted_out_in_map.scalar_type() != at::kInt) {
         throw std::invalid_argument("sorted_out_in_map must have shape (N_out, K) and int32 dtype.");
@@ -146,10 +201,12 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     const at::Tensor order = reorder_rows.contiguous();
     const size_t ws_bytes = lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity));
     at::Tensor ws = workspace(ws_bytes, feats);
+    at::Tensor bias_keep;
+    const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(kv), ci32(tiles),
-        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), ws.data_ptr(), ws_bytes,
+        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), b, ws.data_ptr(), ws_bytes,
         current_stream(feats)));
     return out;
 }
@@ -161,7 +218,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
                                           const at::Tensor& row_offsets, const at::Tensor& sorted_kv_out_in_map,
                                           const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
-                                          int storage_in_channels, int group_size, int bits) {
+                                          int storage_in_channels, int group_size, int bits,
+                                          const std::optional<at::Tensor>& bias) {
     if (out_capacity < 0 || n_kernels <= 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
     }
@@ -233,12 +291,14 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
     at::Tensor out = at::empty({out_capacity, out_channels}, feats.options());
     const size_t ws_bytes = has_plan ? lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity)) : 0;
     at::Tensor ws = workspace(ws_bytes, feats);
+    at::Tensor bias_keep;
+    const void* b = bias_ptr(bias, feats, out_channels, &bias_keep);
     check_status(lattice_hip_sparse_quantized_conv_features(
         dtype_code(feats, "quantized sparse convolution"), feats.data_ptr(), static_cast<int>(feats.size(0)),
         in_channels, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(),
         n_kernels, out_channels, storage_in_channels, group_size, bits, ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), has_plan ? ci32(kv) : nullptr,
-        has_plan ? ci32(tiles) : nullptr, has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(),
+        has_plan ? ci32(tiles) : nullptr, has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(), b,
         has_plan ? ws.data_ptr() : nullptr, ws_bytes, current_stream(feats)));
     return out;
 }

@@ -6,19 +6,30 @@
 
 #include <torch/extension.h>
 
+#include <optional>
+
 namespace lattice_native {
 
 at::Tensor sparse_conv_features(const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& in_rows,
                                 const at::Tensor& out_rows, const at::Tensor& kernel_ids, const at::Tensor& counts,
                                 const at::Tensor& row_offsets, const at::Tensor& in_row_offsets,
                                 const at::Tensor& in_edge_ids, const at::Tensor& kernel_row_offsets,
-                                const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels);
+                                const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels,
+                                const std::optional<at::Tensor>& bias = std::nullopt);
+
+// The CSR conv without the grouped plan views the reference signature
+// carries for its gradient (the forward reads only the output CSR).
+at::Tensor sparse_conv_features_csr(const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& in_rows,
+                                    const at::Tensor& kernel_ids, const at::Tensor& counts,
+                                    const at::Tensor& row_offsets, int out_capacity, int n_kernels,
+                                    const std::optional<at::Tensor>& bias = std::nullopt);
 
 at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, const at::Tensor& weights,
                                                      const at::Tensor& sorted_out_in_map,
                                                      const at::Tensor& sorted_kv_out_in_map,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
-                                                     int out_capacity, int n_kernels, bool store_sorted);
+                                                     int out_capacity, int n_kernels, bool store_sorted,
+                                                     const std::optional<at::Tensor>& bias = std::nullopt);
 
 at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Tensor& weights,
                                           const at::Tensor& scales, const at::Tensor& biases,
@@ -27,7 +38,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           const at::Tensor& row_offsets, const at::Tensor& sorted_kv_out_in_map,
                                           const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
-                                          int storage_in_channels, int group_size, int bits);
+                                          int storage_in_channels, int group_size, int bits,
+                                          const std::optional<at::Tensor>& bias = std::nullopt);
 
 // Gradients (the reference conv primitive's vjp, primitive.cpp:137-176):
 // input gradient over the input-grouped CSR, (in_capacity, C_in) in the

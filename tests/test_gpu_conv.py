@@ -332,11 +332,11 @@ def test_tile_schedule_does_not_change_results():
     lib.lattice_hip_conv_workspace_bytes.restype = ctypes.c_size_t
     P, I = ctypes.c_void_p, ctypes.c_int
     sorted_conv = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm
-    sorted_conv.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P,
+    sorted_conv.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P, P,
                             ctypes.c_size_t, P]
     quant_conv = lib.lattice_hip_sparse_quantized_conv_features
     quant_conv.argtypes = [I, P, I, I, P, P, P, I, I, I, I, I, P, P, P, I, P,
-                           P, P, P, I, P, P, ctypes.c_size_t, P]
+                           P, P, P, I, P, P, P, ctypes.c_size_t, P]
     coords, rng = _shell(30000, 128, 31)
     n = len(coords)
     c = torch.as_tensor(coords, dtype=torch.int32).to(DEV)
@@ -358,7 +358,7 @@ def test_tile_schedule_does_not_change_results():
             out = torch.empty((n, c_out), dtype=torch.float16, device=DEV)
             assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1,
                                27, c_out, kv.data_ptr(), tiles.data_ptr(),
-                               reorder.data_ptr(), n, out.data_ptr(),
+                               reorder.data_ptr(), n, out.data_ptr(), None,
                                workspace, nbytes, stream) == 0
             outs.append(out)
         torch.cuda.synchronize()
@@ -374,7 +374,7 @@ def test_tile_schedule_does_not_change_results():
                               rel[5].data_ptr(), int(rel[0].shape[0]),
                               rel[3].data_ptr(), kv.data_ptr(),
                               tiles.data_ptr(), reorder.data_ptr(), n,
-                              out.data_ptr(), workspace, nbytes,
+                              out.data_ptr(), None, workspace, nbytes,
                               stream) == 0
             qouts.append(out)
         torch.cuda.synchronize()
@@ -383,4 +383,46 @@ def test_tile_schedule_does_not_change_results():
     out = torch.empty((n, 128), dtype=torch.float16, device=DEV)
     assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27, 128,
                        kv.data_ptr(), tiles.data_ptr(), reorder.data_ptr(), n,
-                       out.data_ptr(), ws.data_ptr(), 4, stream) == 1
+                       out.data_ptr(), None, ws.data_ptr(), 4, stream) == 1
+
+
+# -------------------------------------------------------- fused bias ----
+
+
+@pytest.mark.parametrize('dtype,c_in,c_out,quant,kind', [
+    (torch.float16, 64, 64, None, 'subm'),       # matrix cores
+    (torch.bfloat16, 128, 256, None, 'subm'),    # 8-wave C_out = 256 shape
+    (torch.float16, 32, 16, None, 'subm'),       # C_out = 16 shape
+    (torch.float16, 64, 128, None, 'down'),      # k2s2: bias on rows past the active count too
+    (torch.float32, 16, 32, None, 'subm'),       # CSR fp32
+    (torch.float16, 24, 40, None, 'subm'),       # CSR fp16
+    (torch.float16, 64, 64, 8, 'subm'),          # quantized, matrix cores
+    (torch.float16, 4, 32, 8, 'subm'),           # quantized CSR (staged weights)
+])
+def test_fused_bias_equals_separate_add(dtype, c_in, c_out, quant, kind):
+    """The bias added in the conv store equals conv + bias done as a
+    separate torch add, bit for bit, on every capacity row."""
+    from mlx_lattice_amd import quantize_weight
+
+    ops, _ = _imports()
+    coords, rng = _shell(20000, 128, 41 + c_in + c_out)
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+    ks = 3 if kind == 'subm' else 2
+    w = (rng.standard_normal((c_out, ks, ks, ks, c_in))
+         / np.sqrt(ks ** 3 * c_in)).astype(np.float32)
+    b = torch.as_tensor(rng.standard_normal(c_out).astype(np.float32)).to(
+        DEV, dtype)
+    x = _tensor(coords, feats).astype(dtype)
+    wt = torch.as_tensor(w).to(DEV, dtype)
+    if quant:
+        wt = quantize_weight(wt, group_size=32, bits=quant)
+    print(f'fused bias {dtype} {c_in}->{c_out} quant={quant} {kind}',
+          flush=True)
+    if kind == 'subm':
+        fused = ops.subm_conv3d(x, wt, b, kernel_size=3)
+        plain = ops.subm_conv3d(x, wt, kernel_size=3)
+    else:
+        fused = ops.conv3d(x, wt, b, kernel_size=2, stride=2)
+        plain = ops.conv3d(x, wt, kernel_size=2, stride=2)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.feats, plain.feats + b)
