@@ -333,13 +333,19 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
     fp16 128 -> 128.  The transposed relation is direct (one output row per
     (row, offset)), so E = 8 * N_coarse and every output row has one edge.
     Reported: the relation build (HBM-bound: coords read, edges, offsets and
-    output coordinates written), its mask-sorted view, the conv on cached
-    views, and the build of the deduplicating k=3 s=2 transposed relation."""
+    output coordinates written); the conv on the dense expansion kernel,
+    against the HBM roofline of its bytes (input rows read once, output
+    written, weight); the generic matrix-core route over the same relation
+    with its sorted view, for comparison; and the build of the
+    deduplicating k=3 s=2 transposed relation."""
     import torch
 
     import mlx_lattice_amd.ops as ops
     from mlx_lattice_amd import SparseTensor
     from mlx_lattice_amd._native import ext
+    from mlx_lattice_amd.ops._relation_exec import (
+        sparse_conv_features_sorted_from_relation,
+    )
 
     fine = SparseTensor(coords, torch.zeros((coords.shape[0], 1),
                                             device=coords.device))
@@ -360,21 +366,26 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     rel = x.coord_manager.transposed_kernel_relation(
         x.coord_key, kernel_size=2, stride=2)
-    assert rel.sorted_implicit_gemm is not None, 'matrix-core route expected'
+    assert rel.direct_expansion and rel.sorted_implicit_gemm is None, \
+        'the direct expansion route is expected'
     e = int(rel.counts[0].item())
     t_build = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
         coarse, active, [2, 2, 2], [2, 2, 2], [0, 0, 0], [1, 1, 1],
         check_range=False), steps, warmup)
+    t_conv = _timed(lambda: ops.conv_transpose3d(x, weight, kernel_size=2,
+                                                 stride=2), steps, warmup)
+    # the generic matrix-core route over the same relation, for comparison
     t_view = _timed(lambda: (object.__setattr__(
         rel, 'sorted_implicit_gemm', None), object.__setattr__(
         rel, 'implicit_gemm', None), rel.require_sorted_implicit_gemm()),
         3, 1)
-    t_conv = _timed(lambda: ops.conv_transpose3d(x, weight, kernel_size=2,
-                                                 stride=2), steps, warmup)
+    t_generic = _timed(lambda: sparse_conv_features_sorted_from_relation(
+        feats, weight, rel), steps, warmup)
     t_k3 = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
         coarse, active, [3, 3, 3], [2, 2, 2], [0, 0, 0], [1, 1, 1],
         check_range=False), steps, warmup)
     build_bytes = 16 * n + e * (12 + 4 + 16) + 4
+    conv_bytes = n * c * 2 + e * c * 2 + 8 * c * c * 2
     flops = 2.0 * e * c * c
     del out
     return {
@@ -384,10 +395,11 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
         'relation_ms': round(t_build, 4),
         'relation_hbm_frac': round(build_bytes / t_build / 1e6 / PEAK_HBM_GBS,
                                    4),
-        'sorted_view_ms': round(t_view, 4),
         'conv_ms': round(t_conv, 4),
         'conv_tflops': round(flops / t_conv / 1e9, 2),
-        'conv_mfma_frac': round(flops / t_conv / 1e9 / PEAK_FP16_TFLOPS, 4),
+        'conv_hbm_frac': round(conv_bytes / t_conv / 1e6 / PEAK_HBM_GBS, 4),
+        'generic_route_conv_ms': round(t_generic, 4),
+        'generic_route_sorted_view_ms': round(t_view, 4),
         'k3s2_relation_ms': round(t_k3, 4),
     }
 

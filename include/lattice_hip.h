@@ -330,6 +330,19 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Conv over a direct generative / transposed relation (output row
+ * in * K + k holds the single edge (in, k); lattice_hip_build_generative_relation
+ * and the direct case of lattice_hip_build_transposed_kernel_relation):
+ * out[in * K + k] = feats[in] @ W[k] for in < *active_rows, zero rows (plus
+ * bias) for the others.  The same sum as the CSR and sorted routes over
+ * that relation, as a dense matrix-core GEMM with no gather.  fp16/bf16,
+ * c_in, c_out in {32, 64, 128, 256} with c_in * c_out <= 16384; weights (C_out,
+ * Kx, Ky, Kz, C_in); out [n_in * K, c_out]; bias optional as above. */
+int lattice_hip_sparse_conv_features_expand(
+    int dtype, const void* feats, int n_in, const int32_t* active_rows,
+    int c_in, const void* weights, int kernel_count, int c_out, void* out,
+    const void* bias, void* stream);
+
 /* Tuning knob with no counterpart in the reference: rows of the sorted
  * order owned by one wavefront in the implicit-GEMM route (32 or 64).
  * 64 doubles the reuse of each staged weight fragment; 32 (the default)

@@ -758,6 +758,165 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     }
 }
 
+// ------------------------------------------------- direct expansion ----
+//
+// Conv over a direct generative / transposed relation (output row
+// in * K + k has the single edge (in, k)): out[in*K + k] = feats[in] @ W[k],
+// a dense GEMM of the input rows against the K weight slices, with no
+// gather.  A block owns 128 consecutive input rows (32 per wave) and keeps
+// their MFMA A fragments in registers for all K offsets.  Per offset k:
+//   * the block's threads hold W[:, k+1, :] in registers (loaded while k
+//     computes) and store it to LDS after a barrier, so the weight crosses
+//     the vector-memory path once per block instead of once per wave;
+//   * B fragments are read from LDS (16-byte pieces XOR-swizzled by row);
+//   * each wave stages its 32 x C_OUT tile in its own LDS area and writes
+//     whole 16-byte row pieces to out[in * K + k].
+// Input rows at or past the active count give zero rows (plus bias), as
+// the relation has no edges for them.
+template <typename T, int KSTEPS, int CB>
+__global__ void __launch_bounds__(256, 2)
+conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ active_rows,
+            const T* __restrict__ weights, int K, T* __restrict__ out, const T* __restrict__ bias) {
+    using V = typename MfmaOps<T>::vec;
+    constexpr int C_IN = KSTEPS * 32;
+    constexpr int C_OUT = CB * 16;
+    constexpr int PIECES = C_OUT / 8;       // 16-byte pieces per output row
+    constexpr int SROW = C_OUT + 8;         // padded stage row
+    constexpr int WPIECES = C_IN / 8;       // 16-byte pieces per weight row (one output channel)
+    constexpr int WTOTAL = C_OUT * WPIECES;  // pieces of one W[:, k, :]
+    constexpr int WPER = (WTOTAL + 255) / 256;
+    __shared__ __align__(16) T wbuf[C_OUT * C_IN];
+    __shared__ __align__(16) T stage[4][32 * SROW];
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int active = min(max(*active_rows, 0), n_in);
+    const int in0 = blockIdx.x * 128 + wave * 32;
+    V a[2][KSTEPS];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int row = in0 + rb * 16 + lr;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            a[rb][ks] = row < active
+                            ? *reinterpret_cast<const V*>(feats + static_cast<long long>(row) * C_IN + ks * 32 + lg * 8)
+                            : V{};
+        }
+    }
+    float bcol[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) bcol[cb] = bias != nullptr ? static_cast<float>(bias[cb * 16 + lr]) : 0.0f;
+    // piece p of W[co, k, :] sits at wbuf[co * C_IN + ((p ^ (co % WPIECES)) * 8)]
+    V wreg[WPER];
+    auto load_w = [&](int k) {
+#pragma unroll
+        for (int j = 0; j < WPER; ++j) {
+            const int i = j * 256 + threadIdx.x;
+            if (i < WTOTAL) {
+                const int co = i / WPIECES;
+                const int p = i - co * WPIECES;
+                wreg[j] = *reinterpret_cast<const V*>(weights + (static_cast<long long>(co) * K + k) * C_IN + p * 8);
+            }
+        }
+    };
+    auto store_w = [&]() {
+#pragma unroll
+        for (int j = 0; j < WPER; ++j) {
+            const int i = j * 256 + threadIdx.x;
+            if (i < WTOTAL) {
+                const int co = i / WPIECES;
+                const int p = i - co * WPIECES;
+                *reinterpret_cast<V*>(wbuf + co * C_IN + ((p ^ (co % WPIECES)) * 8)) = wreg[j];
+            }
+        }
+    };
+    load_w(0);
+    store_w();
+    __syncthreads();
+    T* st = stage[wave];
+    for (int k = 0; k < K; ++k) {
+        if (k + 1 < K) load_w(k + 1);  // in flight during this offset's MFMAs
+        float4_t acc[2][CB];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            V b[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int co = cb * 16 + lr;
+                const int p = ks * 4 + lg;
+                b[cb] = *reinterpret_cast<const V*>(wbuf + co * C_IN + ((p ^ (co % WPIECES)) * 8));
+            }
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = MfmaOps<T>::mfma(a[rb][ks], b[cb], acc[rb][cb]);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    T v = static_cast<T>(acc[rb][cb][q]);
+                    if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + bcol[cb]);
+                    st[(rb * 16 + lg * 4 + q) * SROW + cb * 16 + lr] = v;
+                }
+        __syncthreads();  // every wave has read W[:, k, :] and staged its tile
+        for (int p = lane; p < 32 * PIECES; p += kWave) {
+            const int r = p / PIECES;
+            const int piece = p - r * PIECES;
+            const int in = in0 + r;
+            if (in < n_in) {
+                *reinterpret_cast<V*>(out + (static_cast<long long>(in) * K + k) * C_OUT + piece * 8) =
+                    *reinterpret_cast<const V*>(st + r * SROW + piece * 8);
+            }
+        }
+        if (k + 1 < K) store_w();
+        __syncthreads();  // W[:, k+1, :] in LDS; the stage is free again
+    }
+}
+
+// Launches conv_expand for c_in * c_out <= 16384 (the weight slice of one
+// offset fits a 32 KB LDS buffer next to the four 32-row output stages).
+template <typename T, int KSTEPS, int CB>
+int launch_expand_shape(const T* feats, int n_in, const int32_t* active, const T* w, int K, T* out, const T* bias,
+                        hipStream_t stream) {
+    static_assert(KSTEPS * 32 * CB * 16 <= 16384, "the weight slice must fit its LDS buffer");
+    const unsigned blocks = static_cast<unsigned>((n_in + 127) / 128);
+    conv_expand<T, KSTEPS, CB><<<blocks, 256, 0, stream>>>(feats, n_in, active, w, K, out, bias);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+template <typename T>
+int launch_expand(const T* feats, int n_in, const int32_t* active, int c_in, const T* w, int K, int c_out, T* out,
+                  const T* bias, hipStream_t stream) {
+    if (n_in <= 0) return LATTICE_OK;
+#define LATTICE_EXPAND(CI, CO) \
+    if (c_in == CI && c_out == CO) return launch_expand_shape<T, CI / 32, CO / 16>(feats, n_in, active, w, K, out, bias, stream)
+    LATTICE_EXPAND(32, 32);
+    LATTICE_EXPAND(32, 64);
+    LATTICE_EXPAND(32, 128);
+    LATTICE_EXPAND(32, 256);
+    LATTICE_EXPAND(64, 32);
+    LATTICE_EXPAND(64, 64);
+    LATTICE_EXPAND(64, 128);
+    LATTICE_EXPAND(64, 256);
+    LATTICE_EXPAND(128, 32);
+    LATTICE_EXPAND(128, 64);
+    LATTICE_EXPAND(128, 128);
+    LATTICE_EXPAND(256, 32);
+    LATTICE_EXPAND(256, 64);
+#undef LATTICE_EXPAND
+    set_error("the expansion conv supports c_in, c_out in {32, 64, 128, 256} with c_in * c_out <= 16384.");
+    return LATTICE_ERROR_UNSUPPORTED;
+}
+
 // Longest-first order of the row tiles of one launch: the cost of a tile is
 // the number of offsets its rows use (stages it runs); a counting sort by
 // descending cost fills `order`.  One workgroup: costs are read with 16-byte
@@ -1066,4 +1225,26 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_sparse_conv_features_expand(int dtype, const void* feats, int n_in,
+                                                       const int32_t* active_rows, int c_in, const void* weights,
+                                                       int kernel_count, int c_out, void* out, const void* bias,
+                                                       void* stream_ptr) {
+    int rc = check_dtype(dtype);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(dtype != LATTICE_F32, "the expansion conv runs on fp16/bf16 matrix cores.");
+    LATTICE_REQUIRE(n_in >= 0 && kernel_count > 0, "feats must have shape (N, C_in) and n_kernels be positive.");
+    LATTICE_REQUIRE(static_cast<long long>(n_in) * kernel_count < (1ll << 31), "expanded rows exceed int32.");
+    if (n_in == 0) return LATTICE_OK;
+    LATTICE_REQUIRE(feats && weights && out && active_rows, "conv pointers must be non-null.");
+    hipStream_t stream = as_stream(stream_ptr);
+    if (dtype == LATTICE_F16) {
+        return launch_expand<_Float16>(static_cast<const _Float16*>(feats), n_in, active_rows, c_in,
+                                       static_cast<const _Float16*>(weights), kernel_count, c_out,
+                                       static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
+    }
+    return launch_expand<__bf16>(static_cast<const __bf16*>(feats), n_in, active_rows, c_in,
+                                 static_cast<const __bf16*>(weights), kernel_count, c_out,
+                                 static_cast<__bf16*>(out), static_cast<const __bf16*>(bias), stream);
 }

@@ -172,7 +172,7 @@ def build_generative_relation(coords: torch.Tensor,
     return _kernel_relation_from_native(
         native[:10], offsets=offsets, in_capacity=int(coords.shape[0]),
         source_coords=coords, source_active_rows=source_active, stride=step,
-        kind='generative', repeated_edges=False)
+        kind='generative', repeated_edges=False, direct_expansion=True)
 
 
 def build_transposed_kernel_relation(coords: torch.Tensor,
@@ -202,11 +202,15 @@ def build_transposed_kernel_relation(coords: torch.Tensor,
         coords, source_active, list(kernel), list(step), list(pad),
         list(rate))
     flags = int(native[10])
+    # can_use_direct_transposed_relation (relations.cpp:107-127)
+    direct = all(step[a] > max(o[a] for o in offsets) - min(o[a] for o in offsets)
+                 for a in range(3))
     return _kernel_relation_from_native(
         native[:10], offsets=offsets, in_capacity=int(coords.shape[0]),
         source_coords=coords, source_active_rows=source_active, stride=step,
         padding=pad, kind='transposed',
-        repeated_edges=None if flags < 0 else bool(flags & 2))
+        repeated_edges=None if flags < 0 else bool(flags & 2),
+        direct_expansion=direct)
 
 
 def _kernel_relation_from_native(
@@ -217,7 +221,8 @@ def _kernel_relation_from_native(
         target_active_rows: torch.Tensor | None = None,
         stride: Triple = (1, 1, 1), padding: Triple = (0, 0, 0),
         kind: RelationKind = 'forward',
-        repeated_edges: bool | None = None) -> KernelRelation:
+        repeated_edges: bool | None = None,
+        direct_expansion: bool = False) -> KernelRelation:
     (in_rows, out_rows, kernel_ids, row_offsets, native_out_coords, counts,
      in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids,
      *view) = native
@@ -243,7 +248,8 @@ def _kernel_relation_from_native(
         source_active_rows=source_active_rows, target_coords=target_coords,
         target_active_rows=target_active_rows, stride=stride,
         padding=padding, kind=kind, implicit_gemm=implicit,
-        grouped_views=grouped_views, repeated_edges=repeated_edges)
+        grouped_views=grouped_views, repeated_edges=repeated_edges,
+        direct_expansion=direct_expansion)
 
 
 def _require_positive(values: Triple, name: str) -> None:

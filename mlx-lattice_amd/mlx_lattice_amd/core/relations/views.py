@@ -202,6 +202,9 @@ class KernelRelation:
     # (a repeated input coordinate), as the builder's status word reported;
     # None when not read back.
     repeated_edges: bool | None = None
+    # Generative, and transposed relations whose stride exceeds the offsets'
+    # extent: output row in * K + k holds the single edge (in, k).
+    direct_expansion: bool = False
 
     def __init__(
         self,
@@ -231,6 +234,7 @@ class KernelRelation:
         sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None,
         grouped_views: Callable[[], tuple] | None = None,
         repeated_edges: bool | None = None,
+        direct_expansion: bool = False,
     ) -> None:
         """``grouped_views``, when given and the input/kernel CSR arrays are
         not, is called on first access of ``input_csr`` / ``kernel_csr`` and
@@ -297,6 +301,7 @@ class KernelRelation:
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
         object.__setattr__(self, 'transposed_sorted_implicit_gemm', None)
         object.__setattr__(self, 'repeated_edges', repeated_edges)
+        object.__setattr__(self, 'direct_expansion', bool(direct_expansion))
 
     @property
     def input_csr(self) -> RelationCSRView:

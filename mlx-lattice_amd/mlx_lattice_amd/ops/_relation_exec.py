@@ -48,6 +48,24 @@ def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
             and n_in * c_in * 2 < 2 ** 31)
 
 
+_EXPAND_CHANNELS = (32, 64, 128, 256)
+
+
+def _expand_eligible(feats: torch.Tensor, c_out: int,
+                     relation: KernelRelation) -> bool:
+    """A direct expanded relation (output row in * K + k = the single edge
+    (in, k)) runs as a dense matrix-core GEMM without gathers."""
+    return (relation.direct_expansion
+            and relation.contract.source_active_rows is not None
+            and feats.dtype in (torch.float16, torch.bfloat16)
+            and int(feats.shape[1]) in _EXPAND_CHANNELS
+            and c_out in _EXPAND_CHANNELS
+            and int(feats.shape[1]) * c_out <= 16384
+            and relation.n_in_capacity == int(feats.shape[0])
+            and relation.n_out_capacity
+            == int(feats.shape[0]) * int(relation.n_kernels))
+
+
 def sparse_conv_features_from_relation(feats: torch.Tensor,
                                        weight: torch.Tensor,
                                        relation: KernelRelation,
@@ -172,6 +190,10 @@ def _conv_features(feats: torch.Tensor, weight: torch.Tensor,
     (optional) is added in the kernels' store, after the conv result is
     rounded, exactly as a separate ``feats + bias``."""
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
+    if feats.ndim == 2 and _expand_eligible(feats, c_out, relation):
+        return ext.sparse_conv_features_expand(
+            feats, weight, relation.contract.source_active_rows,
+            relation.n_kernels, bias=bias)
     if feats.ndim == 2 and _matrix_core_eligible(
             feats.dtype, int(feats.shape[1]), c_out, relation,
             int(feats.shape[0])):

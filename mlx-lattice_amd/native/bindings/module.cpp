@@ -184,6 +184,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("kernel_row_offsets"),
           py::arg("kernel_edge_ids"), py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(),
           py::arg("bias") = py::none());
+    m.def("sparse_conv_features_expand", &ln::sparse_conv_features_expand, py::arg("feats"), py::arg("weights"),
+          py::arg("active_rows"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none());
     m.def("sparse_conv_features_csr", &ln::sparse_conv_features_csr, py::arg("feats"), py::arg("weights"),
           py::arg("in_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
           py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none());

@@ -162,6 +162,30 @@ at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor
     return out;
 }
 
+at::Tensor sparse_conv_features_expand(const at::Tensor& feats_in, const at::Tensor& weights_in,
+                                       const at::Tensor& active_rows, int n_kernels,
+                                       const std::optional<at::Tensor>& bias) {
+    const char* op = "sparse_conv_features_expand";
+    validate_weights(feats_in, weights_in, n_kernels, op);
+    if (active_rows.dim() != 1 || active_rows.size(0) != 1 || active_rows.scalar_type() != at::kInt) {
+        throw std::invalid_argument("active_rows must have shape (1,) and int32 dtype.");
+    }
+    require_device(active_rows, "active_rows");
+    const at::Tensor feats = feats_in.contiguous();
+    const at::Tensor weights =
+        weights_in.dim() == 5 ? weights_in.contiguous() : weights_in.permute({2, 0, 1}).contiguous();
+    const int64_t c_out = out_channels_of(weights_in);
+    const int64_t rows = feats.size(0);
+    at::Tensor out = at::empty({rows * n_kernels, c_out}, feats.options());
+    at::Tensor bias_keep;
+    const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
+    check_status(lattice_hip_sparse_conv_features_expand(
+        dtype_code(feats, op), feats.data_ptr(), static_cast<int>(rows), ci32(active_rows),
+        static_cast<int>(feats.size(1)), weights.data_ptr(), n_kernels, static_cast<int>(c_out), out.data_ptr(), b,
+        current_stream(feats)));
+    return out;
+}
+
 at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in, const at::Tensor& weights_in,
                                                      const at::Tensor& sorted_out_in_map,
                                                      const at::Tensor& sorted_kv_out_in_map,

@@ -24,6 +24,12 @@ at::Tensor sparse_conv_features_csr(const at::Tensor& feats, const at::Tensor& w
                                     const at::Tensor& row_offsets, int out_capacity, int n_kernels,
                                     const std::optional<at::Tensor>& bias = std::nullopt);
 
+// Dense expansion conv over a direct generative / transposed relation:
+// (rows * K, C_out), output row in * K + k = feats[in] @ W[k].
+at::Tensor sparse_conv_features_expand(const at::Tensor& feats, const at::Tensor& weights,
+                                       const at::Tensor& active_rows, int n_kernels,
+                                       const std::optional<at::Tensor>& bias = std::nullopt);
+
 at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, const at::Tensor& weights,
                                                      const at::Tensor& sorted_out_in_map,
                                                      const at::Tensor& sorted_kv_out_in_map,

@@ -278,7 +278,14 @@ def test_conv_transpose_matches_oracle(op, ks, stride, c_in, c_out, dtype,
         if op == 'conv_transpose3d' else
         x.coord_manager.generative_relation(x.coord_key, kernel_size=ks,
                                             stride=stride))
-    mfma = dtype != torch.float32 and (op != 'conv_transpose3d' or not dup)
+    direct = op == 'generative_conv_transpose3d' or O.direct_transposed(
+        ks, stride)
+    expand = (direct and dtype != torch.float32
+              and c_in in (32, 64, 128, 256) and c_out in (32, 64, 128, 256)
+              and c_in * c_out <= 16384)
+    mfma = (dtype != torch.float32 and not expand
+            and (op != 'conv_transpose3d' or not dup))
+    assert relation.direct_expansion == direct
     assert (relation.sorted_implicit_gemm is not None) == mfma
 
 
@@ -353,3 +360,48 @@ def test_modules_and_quantized_transpose():
         n = int(ref.active_rows.item())
         _close(to_np(qout.feats[:n].float()), to_np(ref.feats[:n].float()),
                2e-2, 1e-2, f'{cls.__name__} int8')
+
+
+@pytest.mark.parametrize('c_in,c_out,dtype', [
+    (128, 128, torch.float16), (64, 256, torch.bfloat16), (32, 32, torch.float16),
+    (256, 64, torch.float16)])
+def test_expansion_conv_matches_sorted_route_and_oracle(c_in, c_out, dtype):
+    """The dense expansion kernel of a direct relation against the generic
+    matrix-core route over the same relation (same fp32 MFMA sums) and the
+    oracle; rows past the active count hold the bias."""
+    ops, _ = _ops()
+    from mlx_lattice_amd.ops._relation_exec import (
+        sparse_conv_features_sorted_from_relation,
+    )
+    from mlx_lattice_amd.synthetic import sphere_shell_cloud
+
+    rng = np.random.default_rng(90 + c_in + c_out)
+    coords = sphere_shell_cloud(5000, 128, rng=rng)
+    n = len(coords)
+    active = n - 37
+    feats_np = rng.standard_normal((n, c_in)).astype(np.float32)
+    w_np = (rng.standard_normal((c_out, 2, 2, 2, c_in))
+            / np.sqrt(8 * c_in)).astype(np.float32)
+    feats = torch.as_tensor(feats_np).to(DEV, dtype)
+    w = torch.as_tensor(w_np).to(DEV, dtype)
+    bias = torch.as_tensor(rng.standard_normal(c_out).astype(np.float32)
+                           ).to(DEV, dtype)
+    from mlx_lattice_amd import SparseTensor
+    x = SparseTensor(_t(coords), feats, stride=2, active_rows=_active(active))
+    print(f'expand {c_in}->{c_out} {dtype}', flush=True)
+    out = ops.conv_transpose3d(x, w, bias, kernel_size=2, stride=2)
+    rel = x.coord_manager.transposed_kernel_relation(x.coord_key,
+                                                     kernel_size=2, stride=2)
+    assert rel.direct_expansion and rel.sorted_implicit_gemm is None
+    generic = sparse_conv_features_sorted_from_relation(feats, w, rel)
+    torch.cuda.synchronize()
+    assert torch.equal(out.feats, generic + bias)
+    ref_rel = O.transposed_kernel_relation(coords, active, kernel_size=2,
+                                           stride=2)
+    f32 = lambda t: to_np(t.float())  # noqa: E731
+    ref = O.conv_features_fp64(f32(feats).astype(np.float64),
+                               O.mapped_weight(f32(w).astype(np.float64)),
+                               ref_rel)
+    _close(f32(generic), ref, 2e-2, 1e-2, 'expansion vs oracle')
+    assert torch.equal(out.feats[active * 8:],
+                       bias.expand(n * 8 - active * 8, c_out))
