@@ -1259,9 +1259,8 @@ size_t expanded_relation_bytes(int rows, int K, bool direct) {
 
 int check_expanded_outputs(const lattice_relation_outputs* out, long long cap) {
     LATTICE_REQUIRE(out != nullptr, "relation outputs are required.");
-    LATTICE_REQUIRE(out->row_offsets && out->counts && out->status && out->out_coords,
-                    "relation output pointers must be non-null.");
-    LATTICE_REQUIRE(cap == 0 || (out->in_rows && out->out_rows && out->kernel_ids),
+    LATTICE_REQUIRE(out->row_offsets && out->counts && out->status, "relation output pointers must be non-null.");
+    LATTICE_REQUIRE(cap == 0 || (out->in_rows && out->out_rows && out->kernel_ids && out->out_coords),
                     "relation output pointers must be non-null.");
     const bool views = out->in_edge_ids != nullptr || out->kernel_edge_ids != nullptr;
     LATTICE_REQUIRE(!views || (out->in_edge_ids && out->kernel_edge_ids && out->in_row_offsets &&
