@@ -182,23 +182,27 @@ sort_scan(uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_tota
     }
 }
 
-// Stable ranks of a tile's items per digit, then the scatter.  The last
-// pass writes the caller's arrays (keys restored to their signed form).
+// Stable ranks of a tile's items per digit, then the scatter.  Wave w
+// holds the tile's items w * 512 .. w * 512 + 511 (round r, lane l: item
+// w * 512 + r * 64 + l), so index order is (wave, round, lane): each wave
+// ranks its rounds in order against its own per-digit running counts (no
+// block barrier between rounds; LDS accesses of one wave execute in
+// order), then one exclusive scan over the four waves' counts places the
+// waves.  The last pass writes the caller's arrays (keys restored to their
+// signed form).
 __global__ void __launch_bounds__(kSortThreads)
 sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __restrict__ offsets, bool final,
              uint32_t* __restrict__ keys_out, int32_t* __restrict__ idx_out, int32_t* __restrict__ final_keys) {
-    __shared__ uint32_t wave_count[kSortWaves][kDigits];
-    __shared__ uint32_t running[kDigits];
+    __shared__ uint32_t wave_run[kSortWaves][kDigits];
     __shared__ uint32_t offset[kDigits];
     const int t = threadIdx.x;
     const int wave = t / kWave;
     const int lane = lane_id();
     const int tile = blockIdx.x;
     for (int d = t; d < kDigits; d += kSortThreads) {
-        running[d] = 0;
         offset[d] = offsets[static_cast<long long>(d) * padded_tiles(tiles) + tile];
 #pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) wave_count[w][d] = 0;
+        for (int w = 0; w < kSortWaves; ++w) wave_run[w][d] = 0;
     }
     __syncthreads();
     const int valid_src = valid_items(in, n);
@@ -208,18 +212,17 @@ sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __re
     uint32_t rank[kSortItems];
     int digit[kSortItems];
     const uint32_t digit_mask = (1u << plan.bits) - 1u;
+    const int base = tile * kSortTile + wave * (kSortItems * kWave);
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        const int i = tile * kSortTile + r * kSortThreads + t;
+        const int i = base + r * kWave + lane;
         digit[r] = -1;
         if (i < n) {
             load_item(in, i, valid_src, key[r], index[r]);
             digit[r] = static_cast<int>((key[r] >> plan.shift) & digit_mask);
         }
     }
-    // Stable ranks: rounds in index order; within a round, lanes of a wave
-    // in lane order, waves in wave order.  Lanes with equal digits are found
-    // with one ballot per digit bit.
+    uint32_t* run = wave_run[wave];
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const bool has = digit[r] >= 0;
@@ -230,29 +233,24 @@ sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __re
             peers &= bit ? ones : ~ones;
         }
         const uint64_t below = peers & ((1ull << lane) - 1ull);
-        if (has && below == 0) wave_count[wave][digit[r]] = static_cast<uint32_t>(__popcll(peers));
-        __syncthreads();
-        if (has) {
-            uint32_t before = running[digit[r]];
-            for (int w = 0; w < wave; ++w) before += wave_count[w][digit[r]];
-            rank[r] = before + static_cast<uint32_t>(__popcll(below));
-        }
-        __syncthreads();
-        for (int d = t; d < kDigits; d += kSortThreads) {
-            uint32_t sum = 0;
-#pragma unroll
-            for (int w = 0; w < kSortWaves; ++w) {
-                sum += wave_count[w][d];
-                wave_count[w][d] = 0;
-            }
-            running[d] += sum;
-        }
-        __syncthreads();
+        if (has) rank[r] = run[digit[r]] + static_cast<uint32_t>(__popcll(below));
+        if (has && below == 0) run[digit[r]] += static_cast<uint32_t>(__popcll(peers));
     }
+    __syncthreads();
+    for (int d = t; d < kDigits; d += kSortThreads) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) {
+            const uint32_t c = wave_run[w][d];
+            wave_run[w][d] = sum;
+            sum += c;
+        }
+    }
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         if (digit[r] < 0) continue;
-        const uint32_t pos = offset[digit[r]] + rank[r];
+        const uint32_t pos = offset[digit[r]] + run[digit[r]] + rank[r];
         idx_out[pos] = index[r];
         if (!final) {
             keys_out[pos] = key[r];
