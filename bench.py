@@ -473,6 +473,32 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
     }
 
 
+def map_build_roofline(n: int, edges: int, relation_ms: float) -> dict:
+    """Algorithmic HBM bytes of the submanifold kernel-map build (hash build
+    + map: query, dense map, masks, edges, row offsets, counts) against
+    8 TB/s, with the per-unit figures of the hot-path survey:
+      hash: 16 B coords read + 12 B per insert + 8 B per table slot cleared
+        (capacity next_pow2(2N));
+      map: 16 B coords + 12 B per probe (K per row) + 4 B per dense-map
+        entry + 12 B per edge + 4 B per row offset + 8 B of counts.
+    The sorted view is not part of this figure (its own kernels are listed
+    in the profile)."""
+    cap = 1
+    while cap < 2 * n:
+        cap <<= 1
+    k = 27
+    b_hash = 16 * n + 12 * n + 8 * cap
+    b_map = 16 * n + 12 * k * n + 4 * k * n + 12 * edges + 4 * (n + 1) + 8
+    gbs = (b_hash + b_map) / (relation_ms * 1e-3) / 1e9
+    return {
+        'bytes': b_hash + b_map,
+        'ms': round(relation_ms, 4),
+        'gbs': round(gbs, 1),
+        'peak_gbs': PEAK_HBM_GBS,
+        'frac': round(gbs / PEAK_HBM_GBS, 4),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -569,6 +595,7 @@ def main() -> int:
         },
         'mvoxels_per_s': round(n_out / (conv_ms * 1e-3) / 1e6, 3),
         'kernel_map_build_ms': round(map_ms, 4),
+        'kernel_map_hbm': map_build_roofline(n_out, edges, rel_ms),
         'relation_ms': round(rel_ms, 4),
         'sorted_view_ms': round(view_ms, 4),
         'conv_ms': round(conv_ms, 4),
