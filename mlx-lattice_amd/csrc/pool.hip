@@ -26,17 +26,40 @@ constexpr int kPoolSum = 0;
 constexpr int kPoolMax = 1;
 constexpr int kPoolAvg = 2;
 
+// One lane per (output row, V-channel chunk): V = 4 (16-byte loads and
+// stores) when the channel count allows, else 1; each channel reduces its
+// edges in CSR order either way.
+template <int V> struct PoolVec;
+template <> struct PoolVec<1> {
+    float v[1];
+    __device__ static PoolVec load(const float* p) { return {{p[0]}}; }
+    __device__ void store(float* p) const { p[0] = v[0]; }
+};
+template <> struct PoolVec<4> {
+    float v[4];
+    __device__ static PoolVec load(const float* p) {
+        const float4 f = *reinterpret_cast<const float4*>(p);
+        return {{f.x, f.y, f.z, f.w}};
+    }
+    __device__ void store(float* p) const { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+};
+
+template <int V>
 __global__ void __launch_bounds__(256)
 pool_forward(int mode, const float* __restrict__ feats, int n_in, int channels, const int32_t* __restrict__ in_rows,
              int edge_capacity, const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ counts,
              int out_capacity, float* __restrict__ out) {
     const int out_count = min(counts[1], out_capacity);
-    const long long total = static_cast<long long>(out_capacity) * channels;
+    const int chunks = channels / V;
+    const long long total = static_cast<long long>(out_capacity) * chunks;
+    const float identity = mode == kPoolMax ? -INFINITY : 0.0f;
     for (long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
          t += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const int row = static_cast<int>(t / channels);
-        const int c = static_cast<int>(t - static_cast<long long>(row) * channels);
-        float acc = mode == kPoolMax ? -INFINITY : 0.0f;
+        const int row = static_cast<int>(t / chunks);
+        const int c = static_cast<int>(t - static_cast<long long>(row) * chunks) * V;
+        PoolVec<V> acc;
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc.v[j] = identity;
         if (row < out_count) {
             const int lo = row_offsets[row];
             const int hi = row_offsets[row + 1];
@@ -44,12 +67,17 @@ pool_forward(int mode, const float* __restrict__ feats, int n_in, int channels, 
                 if (e < 0 || e >= edge_capacity) continue;
                 const int in = in_rows[e];
                 if (in < 0 || in >= n_in) continue;
-                const float v = feats[static_cast<long long>(in) * channels + c];
-                acc = mode == kPoolMax ? fmaxf(acc, v) : acc + v;
+                const PoolVec<V> x = PoolVec<V>::load(feats + static_cast<long long>(in) * channels + c);
+#pragma unroll
+                for (int j = 0; j < V; ++j) acc.v[j] = mode == kPoolMax ? fmaxf(acc.v[j], x.v[j]) : acc.v[j] + x.v[j];
             }
-            if (mode == kPoolAvg) acc *= 1.0f / static_cast<float>(max(hi - lo, 1));
+            if (mode == kPoolAvg) {
+                const float scale = 1.0f / static_cast<float>(max(hi - lo, 1));
+#pragma unroll
+                for (int j = 0; j < V; ++j) acc.v[j] *= scale;
+            }
         }
-        out[t] = acc;
+        acc.store(out + static_cast<long long>(row) * channels + c);
     }
 }
 
@@ -136,9 +164,15 @@ extern "C" int lattice_hip_sparse_pool_features(int mode, const float* feats, in
     if (out_capacity == 0) return LATTICE_OK;
     LATTICE_REQUIRE(out && row_offsets && counts && (edge_capacity == 0 || in_rows) && (feats || n_in == 0),
                     "pooling pointers must be non-null.");
-    const long long total = static_cast<long long>(out_capacity) * channels;
-    pool_forward<<<grid_for(total, 256, 1u << 16), 256, 0, as_stream(stream_ptr)>>>(
-        mode, feats, n_in, channels, in_rows, edge_capacity, row_offsets, counts, out_capacity, out);
+    if (channels % 4 == 0) {
+        const long long total = static_cast<long long>(out_capacity) * (channels / 4);
+        pool_forward<4><<<grid_for(total, 256, 1u << 16), 256, 0, as_stream(stream_ptr)>>>(
+            mode, feats, n_in, channels, in_rows, edge_capacity, row_offsets, counts, out_capacity, out);
+    } else {
+        const long long total = static_cast<long long>(out_capacity) * channels;
+        pool_forward<1><<<grid_for(total, 256, 1u << 16), 256, 0, as_stream(stream_ptr)>>>(
+            mode, feats, n_in, channels, in_rows, edge_capacity, row_offsets, counts, out_capacity, out);
+    }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
