@@ -191,6 +191,84 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
     }
 }
 
+// Row-per-lane CSR conv for tiny channel counts (c_in <= 16, c_out 16 or
+// 32, weights staged in LDS, e.g. a 4 -> 32 stem): one lane walks one
+// output row's edges once and accumulates all c_out channels in registers,
+// so the dependent loads of an edge (row offsets, edge row and offset,
+// feature row) are paid once per row instead of once per (row, channel).
+// Each channel still sums its edges in CSR order and its input channels in
+// order with an fp32 accumulator, as the per-channel kernels do.
+// QUANT: the staged weight is dequantised from the packed layout.
+template <typename T, int CO, bool QUANT>
+__global__ void __launch_bounds__(256)
+conv_csr_rows(const T* __restrict__ feats, int c_in, const T* __restrict__ fweights, WeightIndex widx,
+              const uint32_t* __restrict__ qweights, const T* __restrict__ scales, const T* __restrict__ qbiases,
+              QuantIndex q, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ kernel_ids,
+              const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ row_offsets,
+              int out_capacity, T* __restrict__ out, const T* __restrict__ bias) {
+    // (k, ci, co) with co fastest; each offset's slice is padded by 4 floats
+    // so the lanes of a wave, which read different offsets, spread over the
+    // LDS banks (16-byte reads).
+    extern __shared__ float wlds[];
+    const int K = QUANT ? q.K : widx.K;
+    const int kstride = c_in * CO + 4;
+    const int nw = K * c_in * CO;
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+        const int co = i % CO;
+        const int kc = i / CO;
+        const int k = kc / c_in;
+        const int ci = kc - k * c_in;
+        wlds[k * kstride + ci * CO + co] = QUANT ? dequant(qweights, scales, qbiases, q, k, ci, co)
+                                                 : Elem<T>::load(fweights, widx(k, ci, co));
+    }
+    __syncthreads();
+    const int E = min(counts[0], edge_capacity);
+    const int n_out = min(counts[1], out_capacity);
+    for (int row = blockIdx.x * blockDim.x + threadIdx.x; row < out_capacity; row += gridDim.x * blockDim.x) {
+        float acc[CO];
+#pragma unroll
+        for (int co = 0; co < CO; ++co) acc[co] = 0.0f;
+        if (row < n_out) {
+            const int e_end = row_offsets[row + 1];
+            for (int e = row_offsets[row]; e < e_end; ++e) {
+                if (e < 0 || e >= E) continue;
+                const int in = in_rows[e];
+                const int k = kernel_ids[e];
+                if (in < 0 || k < 0 || k >= K) continue;
+                const T* f = feats + static_cast<long long>(in) * c_in;
+                const float4* wk = reinterpret_cast<const float4*>(wlds + k * kstride);
+                for (int ci = 0; ci < c_in; ++ci) {
+                    const float x = Elem<T>::load(f, ci);
+#pragma unroll
+                    for (int c4 = 0; c4 < CO / 4; ++c4) {
+                        const float4 w = wk[ci * (CO / 4) + c4];
+                        acc[4 * c4 + 0] += x * w.x;
+                        acc[4 * c4 + 1] += x * w.y;
+                        acc[4 * c4 + 2] += x * w.z;
+                        acc[4 * c4 + 3] += x * w.w;
+                    }
+                }
+            }
+        }
+        // the row's CO outputs as whole 16-byte stores
+        T vals[CO];
+#pragma unroll
+        for (int co = 0; co < CO; ++co) {
+            T v = static_cast<T>(acc[co]);
+            if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + Elem<T>::load(bias, co));
+            vals[co] = v;
+        }
+        uint4* dst = reinterpret_cast<uint4*>(out + static_cast<long long>(row) * CO);
+#pragma unroll
+        for (int j = 0; j < static_cast<int>(CO * sizeof(T) / 16); ++j) dst[j] = reinterpret_cast<const uint4*>(vals)[j];
+    }
+}
+
+// Whether the row-per-lane kernel takes the shape (weights staged).
+inline bool csr_rows_ok(int c_in, int c_out, long long nw) {
+    return nw <= kCsrLdsFloats && c_in <= 16 && (c_out == 16 || c_out == 32);
+}
+
 // ------------------------------------------------------ implicit GEMM ----
 //
 // Block = WAVES waves.  Each wave owns WAVE_ROWS consecutive rows of the
@@ -1101,6 +1179,26 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
     WeightIndex widx{weight_layout, kernel_count, c_in, c_out};
     const long long total = static_cast<long long>(out_capacity) * c_out;
     const long long nw = static_cast<long long>(kernel_count) * c_in * c_out;
+    if (csr_rows_ok(c_in, c_out, nw)) {
+        const QuantIndex none{};
+        const unsigned rgrid = grid_for(out_capacity, 256, 1u << 16);
+        const size_t rlds = static_cast<size_t>(nw + 4 * kernel_count) * sizeof(float);
+#define LATTICE_CSR_ROWS(T, CO)                                                                                   \
+    conv_csr_rows<T, CO, false><<<rgrid, 256, rlds, stream>>>(                                                    \
+        static_cast<const T*>(feats), c_in, static_cast<const T*>(weights), widx, nullptr, nullptr, nullptr, none, \
+        in_rows, kernel_ids, counts, edge_capacity, row_offsets, out_capacity, static_cast<T*>(out),             \
+        static_cast<const T*>(bias))
+        if (dtype == LATTICE_F32) {
+            if (c_out == 16) LATTICE_CSR_ROWS(float, 16); else LATTICE_CSR_ROWS(float, 32);
+        } else if (dtype == LATTICE_F16) {
+            if (c_out == 16) LATTICE_CSR_ROWS(_Float16, 16); else LATTICE_CSR_ROWS(_Float16, 32);
+        } else {
+            if (c_out == 16) LATTICE_CSR_ROWS(__bf16, 16); else LATTICE_CSR_ROWS(__bf16, 32);
+        }
+#undef LATTICE_CSR_ROWS
+        LATTICE_LAUNCH_CHECK();
+        return LATTICE_OK;
+    }
     const bool staged = nw <= kCsrLdsFloats;
     const unsigned grid = grid_for(total, 256, staged ? kCsrStagedBlocks : 1u << 16);
     const size_t lds = staged ? static_cast<size_t>(nw) * sizeof(float) : 0;
@@ -1203,6 +1301,26 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");
     QuantIndex q{kernel_count, c_in, c_out, packed_words, groups, group_size, bits};
     const long long nw = static_cast<long long>(kernel_count) * c_in * c_out;
+    if (csr_rows_ok(c_in, c_out, nw)) {
+        const WeightIndex none{};
+        const unsigned rgrid = grid_for(out_capacity, 256, 1u << 16);
+        const size_t rlds = static_cast<size_t>(nw + 4 * kernel_count) * sizeof(float);
+#define LATTICE_QCSR_ROWS(T, CO)                                                                                 \
+    conv_csr_rows<T, CO, true><<<rgrid, 256, rlds, stream>>>(                                                    \
+        static_cast<const T*>(feats), c_in, nullptr, none, weights, static_cast<const T*>(scales),              \
+        static_cast<const T*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets, out_capacity, \
+        static_cast<T*>(out), static_cast<const T*>(bias))
+        if (dtype == LATTICE_F32) {
+            if (c_out == 16) LATTICE_QCSR_ROWS(float, 16); else LATTICE_QCSR_ROWS(float, 32);
+        } else if (dtype == LATTICE_F16) {
+            if (c_out == 16) LATTICE_QCSR_ROWS(_Float16, 16); else LATTICE_QCSR_ROWS(_Float16, 32);
+        } else {
+            if (c_out == 16) LATTICE_QCSR_ROWS(__bf16, 16); else LATTICE_QCSR_ROWS(__bf16, 32);
+        }
+#undef LATTICE_QCSR_ROWS
+        LATTICE_LAUNCH_CHECK();
+        return LATTICE_OK;
+    }
     const bool staged = nw <= kCsrLdsFloats;
     const unsigned grid =
         grid_for(static_cast<long long>(out_capacity) * c_out, 256, staged ? kCsrStagedBlocks : 1u << 16);
