@@ -672,7 +672,7 @@ template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
-           const int32_t* __restrict__ block_order, T* __restrict__ out, const T* __restrict__ bias) {
+           const int32_t* __restrict__ block_order, T* __restrict__ out, const T* __restrict__ bias, int out_ld) {
     using V = typename MfmaOps<T>::vec;
     constexpr int WAVES = S::WAVES;
     constexpr int WAVE_ROWS = S::WAVE_ROWS;
@@ -830,7 +830,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         const int sr = row0 + r;
         if (sr < rows) {
             const long long orow = reorder_rows != nullptr ? reorder_rows[sr] : sr;
-            *reinterpret_cast<V*>(out + orow * C_OUT + wc * S::WAVE_COLS + piece * 8) =
+            *reinterpret_cast<V*>(out + orow * out_ld + wc * S::WAVE_COLS + piece * 8) =
                 *reinterpret_cast<const V*>(stage + r * S::EROW + (piece ^ (r % S::EPIECES)) * 8);
         }
     }
@@ -1046,17 +1046,31 @@ schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, in
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
-                       T* out, const T* bias, hipStream_t stream) {
+                       T* out, const T* bias, hipStream_t stream, int out_ld = S::C_OUT, bool scheduled = false) {
     const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
     if (blocks > kMaxScheduledTiles) schedule = nullptr;
-    if (schedule != nullptr) {
+    if (schedule != nullptr && !scheduled) {
         schedule_tiles<S::BLOCK_ROWS / 16><<<1, kScheduleThreads, 0, stream>>>(tile_masks, rows, blocks, schedule);
         LATTICE_LAUNCH_CHECK();
     }
     conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks), S::THREADS, 0, stream>>>(
-        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, bias);
+        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, bias, out_ld);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
+}
+
+// A column half of the weight: output channels co_base .. co_base + 127.
+template <typename T> FloatB<T> column_half(const FloatB<T>& b, int co_base) {
+    FloatB<T> h = b;
+    h.w += co_base * b.s_co;
+    return h;
+}
+template <typename T> PackedB<T> column_half(const PackedB<T>& b, int co_base) {
+    PackedB<T> h = b;  // c_out stays the row stride of the packed arrays
+    h.w += co_base;
+    h.scales += co_base;
+    h.biases += co_base;
+    return h;
 }
 
 // Wave tile rows: 64 doubles the reuse of each B fragment read from LDS;
@@ -1110,9 +1124,21 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
         LATTICE_IGEMM_CASE(32)
         LATTICE_IGEMM_CASE(64)
         LATTICE_IGEMM_CASE(128)
-    case 256:
+    case 256: {
         if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(256, 64, 4);
-        return LATTICE_IGEMM_LAUNCH(256, 32, 8, 64);
+        // Two launches of the 128-column kernel, each writing its half of
+        // every output row (row stride 256): its occupancy and B tile beat
+        // the 8-wave 256-column shape, at the cost of gathering A twice.
+        using S128 = IgemmShape<128, 32, 4, 64, 1, false, kAldsOcc, 128, false, true>;
+        for (int h = 0; h < 2; ++h) {
+            const int rc = launch_igemm_shape<T, S128>(feats, n_in, c_in, column_half(b, h * 128), kv_map,
+                                                      tile_masks, reorder_rows, rows, schedule, out + h * 128,
+                                                      bias != nullptr ? bias + h * 128 : nullptr, stream, 256,
+                                                      h == 1);
+            if (rc != LATTICE_OK) return rc;
+        }
+        return LATTICE_OK;
+    }
 #undef LATTICE_IGEMM_CASE
 #undef LATTICE_IGEMM_LAUNCH
     default:
