@@ -379,6 +379,7 @@ __device__ inline int swizzle_piece(int piece, int row) { return piece ^ (row & 
 // B operand sources.  `load(k, co, ci0)` returns 8 consecutive input
 // channels ci0..ci0+7 of W[k][:, co] as one 16-byte vector.
 template <typename T> struct FloatB {
+    static constexpr bool kCoFastest = false;  // C_in is contiguous: 8 lanes read one row's 128 bytes
     const T* w;
     long long s_co, s_k;  // element strides; C_in is contiguous
     __device__ inline typename MfmaOps<T>::vec load(int k, int co, int ci0) const {
@@ -386,8 +387,24 @@ template <typename T> struct FloatB {
     }
 };
 
+// fp16 dequantisation of packed codes with packed half math: a code c
+// (0..255) placed in the low byte of the half 0x6400 reads as 1024 + c, so
+// subtracting 1024 recovers c exactly; then one fused c * scale + bias per
+// half pair (one rounding, to fp16, the MFMA operand's type).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ inline half2_t code_pair(uint32_t bits) {
+    const half2_t biased = __builtin_bit_cast(half2_t, bits | 0x64006400u);
+    return biased - half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+}
+
+__device__ inline half2_t affine_pair(half2_t c, half2_t s, half2_t b) { return __builtin_elementwise_fma(c, s, b); }
+
 // Packed affine codes: w = q * scale + bias, dequantised while staging B.
 template <typename T> struct PackedB {
+    // C_out is contiguous in the packed words, scales and biases: lanes take
+    // consecutive output channels so each of their loads is one coalesced run.
+    static constexpr bool kCoFastest = true;
     const uint32_t* w;
     const T* scales;
     const T* biases;
@@ -395,25 +412,122 @@ template <typename T> struct PackedB {
     __device__ inline typename MfmaOps<T>::vec load(int k, int co, int ci0) const {
         typename MfmaOps<T>::vec out;
         const long long s = (static_cast<long long>(k) * groups + ci0 / group_size) * c_out + co;
-        const float sc = Elem<T>::load(scales, s);
-        const float bi = Elem<T>::load(biases, s);
         const long long wbase = static_cast<long long>(k) * packed_words * c_out + co;
-        if (bits == 4) {
-            const uint32_t word = w[wbase + static_cast<long long>(ci0 >> 3) * c_out];
+        if constexpr (std::is_same<T, _Float16>::value) {
+            const half2_t sc = {scales[s], scales[s]};
+            const half2_t bi = {biases[s], biases[s]};
+            if (bits == 4) {
+                // nibble j of the word is code j: pairs (j, j + 4)
+                const uint32_t word = w[wbase + static_cast<long long>(ci0 >> 3) * c_out];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                out[j] = static_cast<T>(static_cast<float>((word >> (4 * j)) & 15u) * sc + bi);
+                for (int j = 0; j < 4; ++j) {
+                    const half2_t r = affine_pair(code_pair((word >> (4 * j)) & 0x000F000Fu), sc, bi);
+                    out[j] = r[0];
+                    out[j + 4] = r[1];
+                }
+            } else {
+                // byte j of word i is code 4i + j: pairs (4i + j, 4i + j + 2)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t word = w[wbase + static_cast<long long>((ci0 >> 2) + i) * c_out];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const half2_t r = affine_pair(code_pair((word >> (8 * j)) & 0x00FF00FFu), sc, bi);
+                        out[4 * i + j] = r[0];
+                        out[4 * i + j + 2] = r[1];
+                    }
+                }
+            }
+            return out;
+        } else {
+            const float sc = Elem<T>::load(scales, s);
+            const float bi = Elem<T>::load(biases, s);
+            if (bits == 4) {
+                const uint32_t word = w[wbase + static_cast<long long>(ci0 >> 3) * c_out];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    out[j] = static_cast<T>(static_cast<float>((word >> (4 * j)) & 15u) * sc + bi);
+                }
+            } else {
+                const uint32_t w0 = w[wbase + static_cast<long long>(ci0 >> 2) * c_out];
+                const uint32_t w1 = w[wbase + static_cast<long long>((ci0 >> 2) + 1) * c_out];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    out[j] = static_cast<T>(static_cast<float>((w0 >> (8 * j)) & 255u) * sc + bi);
+                    out[4 + j] = static_cast<T>(static_cast<float>((w1 >> (8 * j)) & 255u) * sc + bi);
+                }
+            }
+            return out;
+        }
+    }
+
+    // Pieces of output channels co .. co + N - 1 (co a multiple of N) for
+    // input channels ci0 .. ci0 + 7: one N-word load per word row and N-half
+    // loads of the scales and biases.
+    template <int N>
+    __device__ inline void load_n(int k, int co, int ci0, typename MfmaOps<T>::vec (&out)[N]) const {
+        static_assert(N == 2 || N == 4, "two or four output channels per thread");
+        using W = typename std::conditional<N == 4, uint4, uint2>::type;
+        using H = typename std::conditional<N == 4, uint2, uint32_t>::type;
+        const long long s = (static_cast<long long>(k) * groups + ci0 / group_size) * c_out + co;
+        const long long wbase = static_cast<long long>(k) * packed_words * c_out + co;
+        const H sraw = *reinterpret_cast<const H*>(scales + s);
+        const H braw = *reinterpret_cast<const H*>(biases + s);
+        const T* sv = reinterpret_cast<const T*>(&sraw);
+        const T* bv = reinterpret_cast<const T*>(&braw);
+        if (bits == 4) {
+            const W wv = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(ci0 >> 3) * c_out);
+            const uint32_t* words = reinterpret_cast<const uint32_t*>(&wv);
+#pragma unroll
+            for (int c = 0; c < N; ++c) {
+                if constexpr (std::is_same<T, _Float16>::value) {
+                    const half2_t sc = {sv[c], sv[c]};
+                    const half2_t bi = {bv[c], bv[c]};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const half2_t r = affine_pair(code_pair((words[c] >> (4 * j)) & 0x000F000Fu), sc, bi);
+                        out[c][j] = r[0];
+                        out[c][j + 4] = r[1];
+                    }
+                } else {
+                    const float sc = static_cast<float>(sv[c]);
+                    const float bi = static_cast<float>(bv[c]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        out[c][j] = static_cast<T>(static_cast<float>((words[c] >> (4 * j)) & 15u) * sc + bi);
+                    }
+                }
             }
         } else {
-            const uint32_t w0 = w[wbase + static_cast<long long>(ci0 >> 2) * c_out];
-            const uint32_t w1 = w[wbase + static_cast<long long>((ci0 >> 2) + 1) * c_out];
+            const W w0 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(ci0 >> 2) * c_out);
+            const W w1 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>((ci0 >> 2) + 1) * c_out);
+            const uint32_t* lo = reinterpret_cast<const uint32_t*>(&w0);
+            const uint32_t* hi = reinterpret_cast<const uint32_t*>(&w1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                out[j] = static_cast<T>(static_cast<float>((w0 >> (8 * j)) & 255u) * sc + bi);
-                out[4 + j] = static_cast<T>(static_cast<float>((w1 >> (8 * j)) & 255u) * sc + bi);
+            for (int c = 0; c < N; ++c) {
+                if constexpr (std::is_same<T, _Float16>::value) {
+                    const half2_t sc = {sv[c], sv[c]};
+                    const half2_t bi = {bv[c], bv[c]};
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const half2_t a = affine_pair(code_pair((lo[c] >> (8 * j)) & 0x00FF00FFu), sc, bi);
+                        const half2_t b = affine_pair(code_pair((hi[c] >> (8 * j)) & 0x00FF00FFu), sc, bi);
+                        out[c][j] = a[0];
+                        out[c][j + 2] = a[1];
+                        out[c][4 + j] = b[0];
+                        out[c][4 + j + 2] = b[1];
+                    }
+                } else {
+                    const float sc = static_cast<float>(sv[c]);
+                    const float bi = static_cast<float>(bv[c]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        out[c][j] = static_cast<T>(static_cast<float>((lo[c] >> (8 * j)) & 255u) * sc + bi);
+                        out[c][4 + j] = static_cast<T>(static_cast<float>((hi[c] >> (8 * j)) & 255u) * sc + bi);
+                    }
+                }
             }
         }
-        return out;
     }
 };
 
@@ -461,31 +575,70 @@ __device__ inline void load_a(V (&a)[RB][ST], const int (&idx)[RB], __amdgpu_buf
     }
 }
 
-// Register staging of one B tile: thread t holds pieces t + i*THREADS
-// (row co = piece / 16), four consecutive rows per wave per load.
+// Register staging of one B tile: thread t holds pieces t + i*THREADS.
+// Float weights (C_in contiguous) map a piece to row co = p / PIECES, so a
+// wave reads whole rows; packed weights (C_out contiguous) map consecutive
+// threads to consecutive output channels.
+template <typename S, bool CO_FASTEST>
+__device__ inline void b_piece(int p, int& co, int& piece) {
+    if (CO_FASTEST) {
+        piece = p / S::C_OUT;
+        co = p - piece * S::C_OUT;
+    } else {
+        co = p / S::PIECES;
+        piece = p - co * S::PIECES;
+    }
+}
+
+// Packed weights whose tile gives every thread two or four pieces: thread
+// t takes the N consecutive output channels N * (t % (C_OUT / N)) .. + N - 1
+// at piece t / (C_OUT / N) and loads them with one N-word load per word row
+// (load_n).
+template <typename S, typename BSource>
+struct MultiB {
+    static constexpr int N = S::B_PIECES;
+    static constexpr bool value = BSource::kCoFastest && (N == 2 || N == 4) && S::C_OUT % N == 0 &&
+                                  S::C_OUT * S::PIECES == N * S::THREADS;
+};
+
 template <typename T, typename S, typename BSource, typename V>
 __device__ inline void stage_b_load(const BSource& bsrc, int k, int ci0, int cw, V (&breg)[S::B_PIECES]) {
+    if constexpr (MultiB<S, BSource>::value) {
+        constexpr int N = MultiB<S, BSource>::N;
+        const int co = N * (threadIdx.x % (S::C_OUT / N));
+        const int piece = threadIdx.x / (S::C_OUT / N);
+        bsrc.template load_n<N>(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0), breg);
+    } else {
 #pragma unroll
-    for (int i = 0; i < S::B_PIECES; ++i) {
-        const int p = threadIdx.x + i * S::THREADS;
-        const int co = p / S::PIECES;
-        const int piece = p - co * S::PIECES;
-        breg[i] = bsrc.load(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0));
+        for (int i = 0; i < S::B_PIECES; ++i) {
+            int co, piece;
+            b_piece<S, BSource::kCoFastest>(threadIdx.x + i * S::THREADS, co, piece);
+            breg[i] = bsrc.load(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0));
+        }
     }
 }
 
-template <typename T, typename S, typename V>
+template <typename T, typename S, typename BSource, typename V>
 __device__ inline void stage_b_store(T* dst, const V (&breg)[S::B_PIECES]) {
+    if constexpr (MultiB<S, BSource>::value) {
+        constexpr int N = MultiB<S, BSource>::N;
+        const int co0 = N * (threadIdx.x % (S::C_OUT / N));
+        const int piece = threadIdx.x / (S::C_OUT / N);
 #pragma unroll
-    for (int i = 0; i < S::B_PIECES; ++i) {
-        const int p = threadIdx.x + i * S::THREADS;
-        const int co = p / S::PIECES;
-        const int piece = p - co * S::PIECES;
-        *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = breg[i];
+        for (int c = 0; c < N; ++c) {
+            const int co = co0 + c;
+            *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = breg[c];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::B_PIECES; ++i) {
+            int co, piece;
+            b_piece<S, BSource::kCoFastest>(threadIdx.x + i * S::THREADS, co, piece);
+            *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = breg[i];
+        }
     }
 }
 
-// B fragments of 32-channel step `st` for the wave's CB column blocks.
 template <typename T, typename S, typename V>
 __device__ inline void read_b_step(V (&b)[S::CB], const T* brow, int st, int lane, int lr) {
     const T* bp = brow + swizzle_piece<S::PIECES>(st * 4 + (lane >> 4), lr) * 8;
@@ -562,7 +715,7 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
             }
         }
     }
-    stage_b_store<T, S>(bnext, breg);
+    stage_b_store<T, S, BSource>(bnext, breg);
     __syncthreads();
 }
 
@@ -663,7 +816,7 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
             }
         }
     }
-    stage_b_store<T, S>(bnext, breg);
+    stage_b_store<T, S, BSource>(bnext, breg);
     if (need_a) store_a_coal<T, V, S::RB>(abuf, areg, c.lane);
     __syncthreads();
 }
@@ -743,7 +896,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
                 stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
                 V areg[S::RB][2];
                 load_a_coal<T, V, S::RB>(areg, idx[0], rows_rsrc, c_in, 0, min(S::CHUNK, c_in), lane);
-                stage_b_store<T, S>(bbuf0, breg);
+                stage_b_store<T, S, BSource>(bbuf0, breg);
                 store_a_coal<T, V, S::RB>(abuf, areg, lane);
             }
             __syncthreads();
@@ -772,7 +925,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         {
             V breg[S::B_PIECES];
             stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
-            stage_b_store<T, S>(bbuf0, breg);
+            stage_b_store<T, S, BSource>(bbuf0, breg);
         }
 #pragma unroll
         for (int j = 0; j < S::DEPTH; ++j) {
@@ -1110,9 +1263,9 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 // eight waves, so each thread stages four B pieces instead of eight (with
 // eight, the packed-weight variant spills to scratch).
 // c_out 32..128 gather A in whole lines through LDS (ALDS), three blocks
-// per CU for float weights; packed weights need the registers of their
-// dequantisation and run two.
-    constexpr int kAldsOcc = std::is_same<BSource, FloatB<T>>::value ? 3 : 2;
+// per CU (float and packed weights alike: the packed tile's dequantisation
+// from vector loads of consecutive output channels fits the registers).
+    constexpr int kAldsOcc = 3;
 #define LATTICE_IGEMM_CASE(C)                                                  \
     case C:                                                                    \
         if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(C, 64, 4);   \
