@@ -531,7 +531,8 @@ emit_edges(const int32_t* __restrict__ out_in_map, int out_capacity, int K,
 // spreads it over the grid.
 __global__ void __launch_bounds__(kThreads)
 group_offsets(const int32_t* __restrict__ sorted_keys, int capacity, int groups, int32_t* __restrict__ offsets,
-              int32_t* __restrict__ tail) {
+              int32_t* __restrict__ tail, const int32_t* run_if) {
+    if (run_if != nullptr && *run_if == 0) return;
     for (int i = blockIdx.x * kThreads + threadIdx.x; i <= capacity; i += gridDim.x * kThreads) {
         const int prev = i > 0 ? min(sorted_keys[i - 1], groups) : -1;
         const int cur = i < capacity ? min(sorted_keys[i], groups) : groups;
@@ -547,7 +548,8 @@ group_offsets(const int32_t* __restrict__ sorted_keys, int capacity, int groups,
 }
 
 __global__ void __launch_bounds__(kThreads)
-fill_group_tail(const int32_t* __restrict__ tail, int groups, int32_t* __restrict__ offsets) {
+fill_group_tail(const int32_t* __restrict__ tail, int groups, int32_t* __restrict__ offsets, const int32_t* run_if) {
+    if (run_if != nullptr && *run_if == 0) return;
     const int first = tail[0];
     const int value = tail[1];
     for (int g = blockIdx.x * kThreads + threadIdx.x; g <= groups; g += gridDim.x * kThreads) {
@@ -555,14 +557,15 @@ fill_group_tail(const int32_t* __restrict__ tail, int groups, int32_t* __restric
     }
 }
 
-// Row offsets of sorted group keys (sentinel `groups` for inactive slots).
+// Row offsets of sorted group keys (sentinel `groups` for inactive slots);
+// skipped on the device when run_if is non-null and *run_if == 0.
 int launch_group_offsets(const int32_t* sorted_keys, int capacity, int groups, int32_t* offsets,
-                         int32_t* tail, hipStream_t stream) {
+                         int32_t* tail, hipStream_t stream, const int32_t* run_if = nullptr) {
     group_offsets<<<grid_for(static_cast<long long>(capacity) + 1, kThreads, 8192), kThreads, 0, stream>>>(
-        sorted_keys, capacity, groups, offsets, tail);
+        sorted_keys, capacity, groups, offsets, tail, run_if);
     LATTICE_LAUNCH_CHECK();
     fill_group_tail<<<grid_for(static_cast<long long>(groups) + 1, kThreads, 8192), kThreads, 0, stream>>>(
-        tail, groups, offsets);
+        tail, groups, offsets, run_if);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -1084,10 +1087,16 @@ extern "C" int lattice_hip_build_sorted_implicit_gemm_view(const int32_t* out_in
 //     on every axis (can_use_direct_transposed_relation, relations.cpp:
 //     107-127): output row j is cand(j), edge j = (in, j, k).  One lane per j.
 //   * other transposed relations: the output rows are the distinct
-//     candidates in first-seen j order (a candidate table keeps the minimum
-//     j; a flag, a scan and a scatter place the representatives), and the
+//     candidates in first-seen j order, and the
 //     edges run in (out_row, kernel_id, in_row) order (write_map,
-//     relation_views_detail.h:52-82).  That order is a stable sort by
+//     relation_views_detail.h:52-82).  The first j of a candidate is found
+//     without a candidate table: cand(in, k) = cand(in', k') exactly when
+//     offset[k] - offset[k'] is a multiple of the stride on every axis and
+//     coord(in') = coord(in) + (offset[k] - offset[k']) / stride, so its
+//     representative is the minimum of first_row(coord') * K + k' over those
+//     k' (k itself included), looked up in the input rows' block table.  A
+//     flag, a scan and a scatter then place the representatives.  That
+//     edge order is a stable sort by
 //     out_row of the j's listed kernel-major (t = k * rows + in), which
 //     already runs in (kernel_id, in_row) order.  A repeated input coordinate
 //     gives a second edge for the same (out_row, kernel_id); the edge pass
@@ -1141,76 +1150,219 @@ expand_direct(const int32_t* __restrict__ coords, int rows, const int32_t* __res
     }
 }
 
-__device__ inline bool candidate_key(const int32_t* coords, int in, int k, const KernelGeometry& g,
-                                     uint64_t* key) {
-    int64_t x, y, z;
-    const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
-    return pack_key(c.x, x, y, z, key);
+__device__ inline int axis_offset(int i, int size, int dilation) {
+    return (i - ((size & 1) ? size / 2 : 0)) * dilation;
 }
 
-__global__ void __launch_bounds__(kThreads)
-insert_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
-                  const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* status) {
-    const int K = g.volume;
-    const int total = min(max(*active_rows, 0), rows) * K;
-    for (int j = blockIdx.x * kThreads + threadIdx.x; j < total; j += gridDim.x * kThreads) {
-        const int in = j / K;
-        uint64_t key;
-        if (!candidate_key(coords, in, j - in * K, g, &key)) {
-            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-            continue;
-        }
-        table.insert(key, j);
-    }
+// First input row of a coordinate, or -1 (absent or outside the key range).
+__device__ inline int first_row(const BlockTable& table, int b, int64_t x, int64_t y, int64_t z) {
+    uint64_t block_key;
+    int octant;
+    if (!block_of(b, x, y, z, &block_key, &octant)) return -1;
+    return table.find(block_key, octant);
 }
 
-// flags[j] = 1 when candidate j is the first of its coordinate.
+// reps[j] = first candidate index j' with cand(j') == cand(j) (-1 for
+// inactive rows and candidates outside the key range); flags[j] = reps[j]
+// == j.  Lanes of one input row share its neighbourhood's bucket lines.
 __global__ void __launch_bounds__(kThreads)
-flag_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
-                const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* __restrict__ flags) {
+resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int rows,
+                   const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* status,
+                   int32_t* __restrict__ reps, int32_t* __restrict__ flags) {
     const int K = g.volume;
     const int cap = rows * K;
     const int total = min(max(*active_rows, 0), rows) * K;
+    const int yz = g.size.y * g.size.z;
     for (int j = blockIdx.x * kThreads + threadIdx.x; j < cap; j += gridDim.x * kThreads) {
-        int flag = 0;
+        int rep = -1;
         if (j < total) {
             const int in = j / K;
+            const int k = j - in * K;
+            int64_t x, y, z;
+            const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
             uint64_t key;
-            if (candidate_key(coords, in, j - in * K, g, &key)) flag = table.find(key) == j ? 1 : 0;
+            if (!pack_key(c.x, x, y, z, &key)) {
+                atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+            } else {
+                const int4 src = load_coord(coords, in);
+                const int ix = k / yz;
+                const int iy = (k - ix * yz) / g.size.z;
+                const int iz = k - ix * yz - iy * g.size.z;
+                const int ox = axis_offset(ix, g.size.x, g.dilation.x);
+                const int oy = axis_offset(iy, g.size.y, g.dilation.y);
+                const int oz = axis_offset(iz, g.size.z, g.dilation.z);
+                rep = j;
+                for (int ax = 0; ax < g.size.x; ++ax) {
+                    const int dx = ox - axis_offset(ax, g.size.x, g.dilation.x);
+                    if (dx % g.stride.x != 0) continue;
+                    for (int ay = 0; ay < g.size.y; ++ay) {
+                        const int dy = oy - axis_offset(ay, g.size.y, g.dilation.y);
+                        if (dy % g.stride.y != 0) continue;
+                        for (int az = 0; az < g.size.z; ++az) {
+                            const int dz = oz - axis_offset(az, g.size.z, g.dilation.z);
+                            if (dz % g.stride.z != 0) continue;
+                            const int r = first_row(table, src.x, static_cast<int64_t>(src.y) + dx / g.stride.x,
+                                                    static_cast<int64_t>(src.z) + dy / g.stride.y,
+                                                    static_cast<int64_t>(src.w) + dz / g.stride.z);
+                            if (r >= 0) rep = min(rep, r * K + ax * yz + ay * g.size.z + az);
+                        }
+                    }
+                }
+            }
         }
-        flags[j] = flag;
+        reps[j] = rep;
+        flags[j] = rep == j ? 1 : 0;
+    }
+}
+
+// resolve_candidates for a tile of kResolveRows input rows at a time: the
+// block first looks up every input coordinate a candidate of the tile can
+// coincide with, coord(in) + d for d in [-R, R] per axis (R = floor(offset
+// extent / stride)), into LDS, one lane per (row, d), so a wave's lanes probe
+// neighbouring lines; then each (row, k) lane takes the minimum over its
+// preimages from LDS.  Used when the neighbourhood has at most
+// kResolveCells cells.
+constexpr int kResolveRows = 64;
+constexpr int kResolveCells = 64;
+
+__global__ void __launch_bounds__(kThreads)
+resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, int rows,
+                         const int32_t* __restrict__ active_rows, KernelGeometry g, Int3 reach, int32_t* status,
+                         int32_t* __restrict__ reps, int32_t* __restrict__ flags, int32_t* __restrict__ sizes,
+                         int32_t* __restrict__ ranks) {
+    __shared__ int32_t found[kResolveRows * kResolveCells];
+    const int K = g.volume;
+    const int active = min(max(*active_rows, 0), rows);
+    const int dx_n = 2 * reach.x + 1, dy_n = 2 * reach.y + 1, dz_n = 2 * reach.z + 1;
+    const int cells = dx_n * dy_n * dz_n;
+    const int yz = g.size.y * g.size.z;
+    const int tiles = (rows + kResolveRows - 1) / kResolveRows;
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int r0 = tile * kResolveRows;
+        const int tile_rows = min(kResolveRows, rows - r0);
+        for (int i = threadIdx.x; i < tile_rows * cells; i += kThreads) {
+            const int row = r0 + i / cells;
+            const int d = i - (i / cells) * cells;
+            int r = -1;
+            if (row < active) {
+                const int ix = d / (dy_n * dz_n);
+                const int iy = (d - ix * dy_n * dz_n) / dz_n;
+                const int iz = d - ix * dy_n * dz_n - iy * dz_n;
+                const int4 c = load_coord(coords, row);
+                r = first_row(table, c.x, static_cast<int64_t>(c.y) + ix - reach.x,
+                              static_cast<int64_t>(c.z) + iy - reach.y, static_cast<int64_t>(c.w) + iz - reach.z);
+                // A later row with the coordinate of an earlier one gives a
+                // second edge for some (out_row, kernel_id).
+                if (ix == reach.x && iy == reach.y && iz == reach.z && r >= 0 && r != row) {
+                    atomicOr(status, LATTICE_STATUS_REPEATED_EDGE);
+                }
+            }
+            found[i] = r;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < tile_rows * K; i += kThreads) {
+            const int in = r0 + i / K;
+            const int k = i - (i / K) * K;
+            const int j = in * K + k;
+            int rep = -1;
+            int members = 0;  // candidates equal to this one
+            int before = 0;   // of those, with a smaller kernel id
+            if (in < active) {
+                int64_t x, y, z;
+                const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
+                uint64_t key;
+                if (!pack_key(c.x, x, y, z, &key)) {
+                    atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+                } else {
+                    const int32_t* f = found + (in - r0) * cells;
+                    const int ix = k / yz;
+                    const int iy = (k - ix * yz) / g.size.z;
+                    const int iz = k - ix * yz - iy * g.size.z;
+                    const int ox = axis_offset(ix, g.size.x, g.dilation.x);
+                    const int oy = axis_offset(iy, g.size.y, g.dilation.y);
+                    const int oz = axis_offset(iz, g.size.z, g.dilation.z);
+                    rep = j;
+                    for (int ax = 0; ax < g.size.x; ++ax) {
+                        const int dx = ox - axis_offset(ax, g.size.x, g.dilation.x);
+                        if (dx % g.stride.x != 0) continue;
+                        const int cx = dx / g.stride.x + reach.x;
+                        for (int ay = 0; ay < g.size.y; ++ay) {
+                            const int dy = oy - axis_offset(ay, g.size.y, g.dilation.y);
+                            if (dy % g.stride.y != 0) continue;
+                            const int cy = dy / g.stride.y + reach.y;
+                            for (int az = 0; az < g.size.z; ++az) {
+                                const int dz = oz - axis_offset(az, g.size.z, g.dilation.z);
+                                if (dz % g.stride.z != 0) continue;
+                                const int r = f[(cx * dy_n + cy) * dz_n + dz / g.stride.z + reach.z];
+                                const int kk = ax * yz + ay * g.size.z + az;
+                                if (r >= 0) {
+                                    rep = min(rep, r * K + kk);
+                                    ++members;
+                                    before += kk < k ? 1 : 0;
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+            reps[j] = rep;
+            flags[j] = rep == j ? 1 : 0;
+            sizes[j] = rep == j ? members : 0;
+            ranks[j] = before;
+        }
+        __syncthreads();
     }
 }
 
 // Output coordinates of the representatives at their first-seen position,
 // zero tail; keys[t] (t = k * rows + in) = output row of candidate in*K+k,
-// -1 for inactive rows (sorted last).
+// -1 for inactive rows (sorted last).  With edge_offsets (the exclusive scan
+// of the representatives' group sizes) and ranks, and while the status word
+// is clear (every candidate in range, no repeated input coordinate), the
+// edges are written in their final (out_row, kernel_id, in_row) order here:
+// candidate j is edge edge_offsets[rep] + ranks[j] and out row positions[j]
+// of a representative starts at edge_offsets[j].
 __global__ void __launch_bounds__(kThreads)
-place_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
-                 const int32_t* __restrict__ active_rows, KernelGeometry g, const int32_t* __restrict__ flags,
-                 const int32_t* __restrict__ positions, const int32_t* __restrict__ counts,
-                 int32_t* __restrict__ out_coords, int32_t* __restrict__ keys) {
+place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
+                 KernelGeometry g, const int32_t* __restrict__ reps, const int32_t* __restrict__ flags,
+                 const int32_t* __restrict__ positions, const int32_t* __restrict__ edge_offsets,
+                 const int32_t* __restrict__ ranks, lattice_relation_outputs out, int32_t* __restrict__ keys) {
     const int K = g.volume;
     const int cap = rows * K;
-    const int active = min(max(*active_rows, 0), rows);
-    const int n_out = counts[1];
-    int4* oc = reinterpret_cast<int4*>(out_coords);
-    for (int j = blockIdx.x * kThreads + threadIdx.x; j < cap; j += gridDim.x * kThreads) {
+    const int total = min(max(*active_rows, 0), rows) * K;
+    const int n_out = out.counts[1];
+    const bool emit = edge_offsets != nullptr && *out.status == 0;
+    int4* oc = reinterpret_cast<int4*>(out.out_coords);
+    if (emit && blockIdx.x == 0 && threadIdx.x == 0) out.counts[0] = total;
+    for (int j = blockIdx.x * kThreads + threadIdx.x; j <= cap; j += gridDim.x * kThreads) {
+        if (j == cap) {
+            if (emit) out.row_offsets[cap] = total;
+            continue;
+        }
         const int in = j / K;
         const int k = j - in * K;
-        int out_row = -1;
-        if (in < active) {
+        const int rep = reps[j];
+        const bool first = flags[j] != 0;
+        if (first) {
             int64_t x, y, z;
-            const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
-            uint64_t key;
-            if (pack_key(c.x, x, y, z, &key)) {
-                const int rep = table.find(key);
-                if (rep >= 0) out_row = positions[rep];
-            }
-            if (flags[j]) oc[positions[j]] = c;
+            oc[positions[j]] = candidate_of(coords, in, k, g, &x, &y, &z);
         }
         if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
-        keys[static_cast<long long>(k) * rows + in] = out_row;
+        keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
+        if (emit) {
+            if (j < total) {
+                const int e = edge_offsets[rep] + ranks[j];
+                out.in_rows[e] = in;
+                out.out_rows[e] = positions[rep];
+                out.kernel_ids[e] = k;
+                if (first) out.row_offsets[positions[j]] = edge_offsets[j];
+            } else {
+                out.in_rows[j] = 0;
+                out.out_rows[j] = 0;
+                out.kernel_ids[j] = 0;
+            }
+            if (j >= n_out) out.row_offsets[j] = total;
+        }
     }
 }
 
@@ -1218,7 +1370,9 @@ place_candidates(CoordTable table, const int32_t* __restrict__ coords, int rows,
 // repeated (out_row, kernel_id).
 __global__ void __launch_bounds__(kThreads)
 emit_sorted_edges(const int32_t* __restrict__ sorted_keys, const int32_t* __restrict__ sorted_index, int rows,
-                  int K, const int32_t* __restrict__ active_rows, lattice_relation_outputs out) {
+                  int K, const int32_t* __restrict__ active_rows, lattice_relation_outputs out,
+                  const int32_t* run_if) {
+    if (run_if != nullptr && *run_if == 0) return;
     const int cap = rows * K;
     const int total = min(max(*active_rows, 0), rows) * K;
     if (blockIdx.x == 0 && threadIdx.x == 0) out.counts[0] = total;
@@ -1251,8 +1405,8 @@ size_t expanded_relation_bytes(int rows, int K, bool direct) {
     size_t bytes = group_view_bytes(static_cast<int>(cap)) + 4096;
     if (direct) return bytes;
     const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
-    bytes += table_bytes(static_cast<int>(cap)) + 5 * n + aligned_bytes(2 * sizeof(int32_t)) +
-             scan_workspace_bytes(cap);
+    bytes += block_table_bytes(std::max(rows, 0)) + 9 * n + aligned_bytes(2 * sizeof(int32_t)) +
+             2 * scan_workspace_bytes(cap);
     bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
     return bytes;
 }
@@ -1296,36 +1450,60 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         rc = fill_i32(out->counts, 2, 0, stream);
         if (rc != LATTICE_OK) return rc;
     } else {
-        CoordTable table;
-        rc = make_table(cap, ws, &table);
+        const Prologue prologue{out->status, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr};
+        BlockTable table;
+        rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
         if (rc != LATTICE_OK) return rc;
+        int32_t* reps = ws.take<int32_t>(cap);
         int32_t* flags = ws.take<int32_t>(cap);
         int32_t* positions = ws.take<int32_t>(cap);
         int32_t* keys = ws.take<int32_t>(cap);
         int32_t* sorted_keys = ws.take<int32_t>(cap);
         int32_t* sorted_index = ws.take<int32_t>(cap);
-        LATTICE_REQUIRE(flags && positions && keys && sorted_keys && sorted_index, "relation workspace too small.");
-        const int tcap = static_cast<int>(table.mask) + 1;
-        clear_table<<<grid_for(tcap, kThreads, 4096), kThreads, 0, stream>>>(table.keys, table.rows, tcap);
-        LATTICE_LAUNCH_CHECK();
+        int32_t* sizes = ws.take<int32_t>(cap);
+        int32_t* ranks = ws.take<int32_t>(cap);
+        int32_t* edge_offsets = ws.take<int32_t>(cap);
+        LATTICE_REQUIRE(reps && flags && positions && keys && sorted_keys && sorted_index && sizes && ranks &&
+                            edge_offsets,
+                        "relation workspace too small.");
         const unsigned grid = grid_for(cap, kThreads, 1u << 14);
-        insert_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, out->status);
-        LATTICE_LAUNCH_CHECK();
-        flag_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, flags);
+        const Int3 reach{(g.size.x - 1) * g.dilation.x / g.stride.x, (g.size.y - 1) * g.dilation.y / g.stride.y,
+                         (g.size.z - 1) * g.dilation.z / g.stride.z};
+        const long long cells = (2ll * reach.x + 1) * (2ll * reach.y + 1) * (2ll * reach.z + 1);
+        // The tiled resolve also ranks every candidate inside its output
+        // row, so the edges are placed directly; the stable sort then runs
+        // only when the status word reports a candidate out of range or a
+        // repeated input coordinate.  The general resolve always sorts.
+        const bool tiled = cells <= kResolveCells;
+        if (tiled) {
+            const int tiles = (rows + kResolveRows - 1) / kResolveRows;
+            resolve_candidates_tiled<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
+                table, coords, rows, active_rows, g, reach, out->status, reps, flags, sizes, ranks);
+        } else {
+            resolve_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, out->status, reps,
+                                                              flags);
+        }
         LATTICE_LAUNCH_CHECK();
         rc = exclusive_scan(flags, positions, cap, out->counts + 1, ws, stream);
         if (rc != LATTICE_OK) return rc;
-        place_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, flags, positions,
-                                                        out->counts, out->out_coords, keys);
+        if (tiled) {
+            rc = exclusive_scan(sizes, edge_offsets, cap, nullptr, ws, stream);
+            if (rc != LATTICE_OK) return rc;
+        }
+        place_candidates<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
+            coords, rows, active_rows, g, reps, flags, positions, tiled ? edge_offsets : nullptr, ranks, *out, keys);
         LATTICE_LAUNCH_CHECK();
-        const SortKeys sk{keys, 1, nullptr, cap, false};
+        const int32_t* run_if = tiled ? out->status : nullptr;
+        SortKeys sk{keys, 1, nullptr, cap, false};
+        sk.run_if = run_if;
         rc = radix_sort_indices(sk, cap, bit_width(cap), sorted_keys, sorted_index, ws, stream);
         if (rc != LATTICE_OK) return rc;
-        emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out);
+        emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out,
+                                                         run_if);
         LATTICE_LAUNCH_CHECK();
         int32_t* tail = ws.take<int32_t>(2);
         LATTICE_REQUIRE(tail, "relation workspace too small.");
-        rc = launch_group_offsets(sorted_keys, cap, cap, out->row_offsets, tail, stream);
+        rc = launch_group_offsets(sorted_keys, cap, cap, out->row_offsets, tail, stream, run_if);
         if (rc != LATTICE_OK) return rc;
     }
     if (out->in_edge_ids == nullptr) return LATTICE_OK;

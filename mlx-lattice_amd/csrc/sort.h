@@ -17,6 +17,9 @@ struct SortKeys {
     const int32_t* count;
     int groups;
     bool flip_sign;
+    // When non-null, the sort runs only if *run_if != 0 (read on the
+    // device, so a caller can skip it without a host synchronisation).
+    const int32_t* run_if = nullptr;
 };
 
 size_t radix_sort_workspace_bytes(int n, int end_bit);

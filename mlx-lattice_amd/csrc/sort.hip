@@ -69,6 +69,7 @@ __host__ __device__ inline int padded_tiles(int tiles) { return (tiles + 3) & ~3
 __global__ void __launch_bounds__(kSortThreads)
 sort_count(PassInput in, int n, PassPlan plan, int tiles, uint32_t* __restrict__ counts,
            uint32_t* __restrict__ digit_totals) {
+    if (in.src.run_if != nullptr && *in.src.run_if == 0) return;
     __shared__ uint32_t hist[kDigits];
     for (int d = threadIdx.x; d < kDigits; d += kSortThreads) hist[d] = 0;
     __syncthreads();
@@ -118,7 +119,9 @@ __device__ inline uint32_t wave_inclusive_scan(uint32_t v, int lane) {
 }
 
 __global__ void __launch_bounds__(kScanBlockThreads)
-sort_scan(uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_totals, int tiles) {
+sort_scan(uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_totals, int tiles,
+          const int32_t* run_if) {
+    if (run_if != nullptr && *run_if == 0) return;
     __shared__ uint32_t base[kDigits];
     __shared__ uint32_t wave_sum[kScanWaves];
     const int lane = lane_id();
@@ -193,6 +196,7 @@ sort_scan(uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_tota
 __global__ void __launch_bounds__(kSortThreads)
 sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __restrict__ offsets, bool final,
              uint32_t* __restrict__ keys_out, int32_t* __restrict__ idx_out, int32_t* __restrict__ final_keys) {
+    if (in.src.run_if != nullptr && *in.src.run_if == 0) return;
     __shared__ uint32_t wave_run[kSortWaves][kDigits];
     __shared__ uint32_t offset[kDigits];
     const int t = threadIdx.x;
@@ -298,7 +302,7 @@ int radix_sort_indices(const SortKeys& keys, int n, int end_bit, int32_t* sorted
         uint32_t* pass_totals = totals + static_cast<size_t>(p) * kDigits;
         sort_count<<<tiles, kSortThreads, 0, stream>>>(input, n, plan, tiles, counts, pass_totals);
         LATTICE_LAUNCH_CHECK();
-        sort_scan<<<kDigits / kScanRows, kScanBlockThreads, 0, stream>>>(counts, pass_totals, tiles);
+        sort_scan<<<kDigits / kScanRows, kScanBlockThreads, 0, stream>>>(counts, pass_totals, tiles, keys.run_if);
         LATTICE_LAUNCH_CHECK();
         sort_scatter<<<tiles, kSortThreads, 0, stream>>>(input, n, plan, tiles, counts, final,
                                                           final ? nullptr : key_buf[out],
