@@ -1215,6 +1215,92 @@ resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int row
     }
 }
 
+constexpr int kResolveRows = 64;
+constexpr int kResolveCells = 64;
+
+// Exclusive scan of an (x, y) pair over the block's threads; the block
+// total comes back through `total`.  Every thread of the block calls it.
+__device__ inline int2 block_scan_pair(int2 v, int2* total) {
+    __shared__ int2 wave_sums[kThreads / kWave];
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    int2 incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int ux = __shfl_up(incl.x, d, kWave);
+        const int uy = __shfl_up(incl.y, d, kWave);
+        if (lane >= d) {
+            incl.x += ux;
+            incl.y += uy;
+        }
+    }
+    if (lane == kWave - 1) wave_sums[wave] = incl;
+    __syncthreads();
+    int2 base = make_int2(0, 0), tot = make_int2(0, 0);
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) {
+        const int2 ws = wave_sums[w];
+        if (w < wave) {
+            base.x += ws.x;
+            base.y += ws.y;
+        }
+        tot.x += ws.x;
+        tot.y += ws.y;
+    }
+    __syncthreads();
+    *total = tot;
+    return make_int2(base.x + incl.x - v.x, base.y + incl.y - v.y);
+}
+
+// Exclusive scan of the per-tile (representatives, edges) totals in one
+// block; counts[1] receives the number of representatives.
+__global__ void __launch_bounds__(kThreads)
+scan_tile_pairs(int32_t* __restrict__ tile_firsts, int32_t* __restrict__ tile_edges, int tiles,
+                int32_t* __restrict__ counts) {
+    int2 carry = make_int2(0, 0);
+    for (int c = 0; c < tiles; c += kThreads) {
+        const int i = c + threadIdx.x;
+        const int2 v = i < tiles ? make_int2(tile_firsts[i], tile_edges[i]) : make_int2(0, 0);
+        int2 tot;
+        const int2 pre = block_scan_pair(v, &tot);
+        if (i < tiles) {
+            tile_firsts[i] = carry.x + pre.x;
+            tile_edges[i] = carry.y + pre.y;
+        }
+        carry.x += tot.x;
+        carry.y += tot.y;
+    }
+    if (threadIdx.x == 0) counts[1] = carry.x;
+}
+
+// positions[j] (output row of a representative) and edge_offsets[j] (its
+// first edge): the tile's scanned base plus the in-tile exclusive prefix
+// of flags and sizes, in j order.
+__global__ void __launch_bounds__(kThreads)
+finalize_tiles(const int32_t* __restrict__ flags, const int32_t* __restrict__ sizes,
+               const int32_t* __restrict__ tile_firsts, const int32_t* __restrict__ tile_edges, int rows, int K,
+               int32_t* __restrict__ positions, int32_t* __restrict__ edge_offsets) {
+    const int tiles = (rows + kResolveRows - 1) / kResolveRows;
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int j0 = tile * kResolveRows * K;
+        const int n = min(kResolveRows, rows - tile * kResolveRows) * K;
+        int2 base = make_int2(tile_firsts[tile], tile_edges[tile]);
+        for (int c = 0; c < n; c += kThreads) {
+            const int i = c + threadIdx.x;
+            const int2 v = i < n ? make_int2(flags[j0 + i], sizes[j0 + i]) : make_int2(0, 0);
+            int2 tot;
+            const int2 pre = block_scan_pair(v, &tot);
+            if (i < n) {
+                positions[j0 + i] = base.x + pre.x;
+                edge_offsets[j0 + i] = base.y + pre.y;
+            }
+            base.x += tot.x;
+            base.y += tot.y;
+        }
+    }
+}
+
+
 // resolve_candidates for a tile of kResolveRows input rows at a time: the
 // block first looks up every input coordinate a candidate of the tile can
 // coincide with, coord(in) + d for d in [-R, R] per axis (R = floor(offset
@@ -1222,14 +1308,13 @@ resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int row
 // neighbouring lines; then each (row, k) lane takes the minimum over its
 // preimages from LDS.  Used when the neighbourhood has at most
 // kResolveCells cells.
-constexpr int kResolveRows = 64;
-constexpr int kResolveCells = 64;
-
 __global__ void __launch_bounds__(kThreads)
 resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, int rows,
-                         const int32_t* __restrict__ active_rows, KernelGeometry g, Int3 reach, int32_t* status,
+                         const int32_t* __restrict__ active_rows, KernelGeometry g, Int3 reach, Int3 period,
+                         Int3 step, int32_t* status,
                          int32_t* __restrict__ reps, int32_t* __restrict__ flags, int32_t* __restrict__ sizes,
-                         int32_t* __restrict__ ranks) {
+                         int32_t* __restrict__ ranks, int32_t* __restrict__ tile_firsts,
+                         int32_t* __restrict__ tile_edges) {
     __shared__ int32_t found[kResolveRows * kResolveCells];
     const int K = g.volume;
     const int active = min(max(*active_rows, 0), rows);
@@ -1260,6 +1345,7 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
             found[i] = r;
         }
         __syncthreads();
+        int2 mine = make_int2(0, 0);
         for (int i = threadIdx.x; i < tile_rows * K; i += kThreads) {
             const int in = r0 + i / K;
             const int k = i - (i / K) * K;
@@ -1278,22 +1364,18 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
                     const int ix = k / yz;
                     const int iy = (k - ix * yz) / g.size.z;
                     const int iz = k - ix * yz - iy * g.size.z;
-                    const int ox = axis_offset(ix, g.size.x, g.dilation.x);
-                    const int oy = axis_offset(iy, g.size.y, g.dilation.y);
-                    const int oz = axis_offset(iz, g.size.z, g.dilation.z);
+                    // Offsets i' of one axis meet offset i exactly when
+                    // i - i' is a multiple of the period; the input cell
+                    // then moves by (i - i') / period * step.
+                    const int ax0 = ix % period.x, ay0 = iy % period.y, az0 = iz % period.z;
+                    const int tx0 = (ix - ax0) / period.x, ty0 = (iy - ay0) / period.y, tz0 = (iz - az0) / period.z;
                     rep = j;
-                    for (int ax = 0; ax < g.size.x; ++ax) {
-                        const int dx = ox - axis_offset(ax, g.size.x, g.dilation.x);
-                        if (dx % g.stride.x != 0) continue;
-                        const int cx = dx / g.stride.x + reach.x;
-                        for (int ay = 0; ay < g.size.y; ++ay) {
-                            const int dy = oy - axis_offset(ay, g.size.y, g.dilation.y);
-                            if (dy % g.stride.y != 0) continue;
-                            const int cy = dy / g.stride.y + reach.y;
-                            for (int az = 0; az < g.size.z; ++az) {
-                                const int dz = oz - axis_offset(az, g.size.z, g.dilation.z);
-                                if (dz % g.stride.z != 0) continue;
-                                const int r = f[(cx * dy_n + cy) * dz_n + dz / g.stride.z + reach.z];
+                    for (int ax = ax0, tx = tx0; ax < g.size.x; ax += period.x, --tx) {
+                        const int cx = tx * step.x + reach.x;
+                        for (int ay = ay0, ty = ty0; ay < g.size.y; ay += period.y, --ty) {
+                            const int cy = ty * step.y + reach.y;
+                            for (int az = az0, tz = tz0; az < g.size.z; az += period.z, --tz) {
+                                const int r = f[(cx * dy_n + cy) * dz_n + tz * step.z + reach.z];
                                 const int kk = ax * yz + ay * g.size.z + az;
                                 if (r >= 0) {
                                     rep = min(rep, r * K + kk);
@@ -1309,8 +1391,17 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
             flags[j] = rep == j ? 1 : 0;
             sizes[j] = rep == j ? members : 0;
             ranks[j] = before;
+            if (rep == j) {
+                mine.x += 1;
+                mine.y += members;
+            }
         }
-        __syncthreads();
+        int2 tot;
+        block_scan_pair(mine, &tot);
+        if (threadIdx.x == 0) {
+            tile_firsts[tile] = tot.x;
+            tile_edges[tile] = tot.y;
+        }
     }
 }
 
@@ -1348,7 +1439,7 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
             oc[positions[j]] = candidate_of(coords, in, k, g, &x, &y, &z);
         }
         if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
-        keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
+        if (!emit) keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
         if (emit) {
             if (j < total) {
                 const int e = edge_offsets[rep] + ranks[j];
@@ -1405,8 +1496,9 @@ size_t expanded_relation_bytes(int rows, int K, bool direct) {
     size_t bytes = group_view_bytes(static_cast<int>(cap)) + 4096;
     if (direct) return bytes;
     const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
-    bytes += block_table_bytes(std::max(rows, 0)) + 9 * n + aligned_bytes(2 * sizeof(int32_t)) +
-             2 * scan_workspace_bytes(cap);
+    const size_t tiles = static_cast<size_t>(std::max(rows, 0)) / kResolveRows + 1;
+    bytes += block_table_bytes(std::max(rows, 0)) + 9 * n + 2 * aligned_bytes(tiles * sizeof(int32_t)) +
+             aligned_bytes(2 * sizeof(int32_t)) + scan_workspace_bytes(cap);
     bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
     return bytes;
 }
@@ -1463,8 +1555,11 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         int32_t* sizes = ws.take<int32_t>(cap);
         int32_t* ranks = ws.take<int32_t>(cap);
         int32_t* edge_offsets = ws.take<int32_t>(cap);
+        const int resolve_tiles = (rows + kResolveRows - 1) / kResolveRows;
+        int32_t* tile_firsts = ws.take<int32_t>(resolve_tiles);
+        int32_t* tile_edges = ws.take<int32_t>(resolve_tiles);
         LATTICE_REQUIRE(reps && flags && positions && keys && sorted_keys && sorted_index && sizes && ranks &&
-                            edge_offsets,
+                            edge_offsets && tile_firsts && tile_edges,
                         "relation workspace too small.");
         const unsigned grid = grid_for(cap, kThreads, 1u << 14);
         const Int3 reach{(g.size.x - 1) * g.dilation.x / g.stride.x, (g.size.y - 1) * g.dilation.y / g.stride.y,
@@ -1475,19 +1570,37 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         // only when the status word reports a candidate out of range or a
         // repeated input coordinate.  The general resolve always sorts.
         const bool tiled = cells <= kResolveCells;
+        const auto gcd = [](int a, int b) {
+            while (b != 0) {
+                const int t = a % b;
+                a = b;
+                b = t;
+            }
+            return a;
+        };
+        const Int3 period{g.stride.x / gcd(g.stride.x, g.dilation.x), g.stride.y / gcd(g.stride.y, g.dilation.y),
+                          g.stride.z / gcd(g.stride.z, g.dilation.z)};
+        const Int3 step{g.dilation.x / gcd(g.stride.x, g.dilation.x), g.dilation.y / gcd(g.stride.y, g.dilation.y),
+                        g.dilation.z / gcd(g.stride.z, g.dilation.z)};
         if (tiled) {
             const int tiles = (rows + kResolveRows - 1) / kResolveRows;
             resolve_candidates_tiled<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
-                table, coords, rows, active_rows, g, reach, out->status, reps, flags, sizes, ranks);
+                table, coords, rows, active_rows, g, reach, period, step, out->status, reps, flags, sizes, ranks,
+                tile_firsts, tile_edges);
         } else {
             resolve_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, out->status, reps,
                                                               flags);
         }
         LATTICE_LAUNCH_CHECK();
-        rc = exclusive_scan(flags, positions, cap, out->counts + 1, ws, stream);
-        if (rc != LATTICE_OK) return rc;
         if (tiled) {
-            rc = exclusive_scan(sizes, edge_offsets, cap, nullptr, ws, stream);
+            const int tiles = (rows + kResolveRows - 1) / kResolveRows;
+            scan_tile_pairs<<<1, kThreads, 0, stream>>>(tile_firsts, tile_edges, tiles, out->counts);
+            LATTICE_LAUNCH_CHECK();
+            finalize_tiles<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
+                flags, sizes, tile_firsts, tile_edges, rows, K, positions, edge_offsets);
+            LATTICE_LAUNCH_CHECK();
+        } else {
+            rc = exclusive_scan(flags, positions, cap, out->counts + 1, ws, stream);
             if (rc != LATTICE_OK) return rc;
         }
         place_candidates<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
