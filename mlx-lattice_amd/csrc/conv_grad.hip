@@ -150,6 +150,7 @@ template <> struct GradMfma<__bf16> {
     }
 };
 
+constexpr int kXcds = 8;       // XCDs of an MI355X, each with its own L2
 constexpr int kWgEdges = 64;   // edges per staged step (two 32-edge MFMA steps)
 constexpr int kWgRow = 72;     // LDS row stride in elements (64 edges + 8 pad)
 
@@ -158,11 +159,26 @@ constexpr int kWgRow = 72;     // LDS row stride in elements (64 edges + 8 pad)
 // pieces) and the fragment reads (16 rows, one chunk) spread over the banks.
 __device__ inline int wg_slot(int r, int j) { return r * kWgRow + (((j >> 3) ^ ((r >> 3) & 7)) << 3) + (j & 7); }
 
+// Channel rows r0 .. r0 + 7 at columns (col, col + 1): element c of `lo`
+// and of `hi` (8 x 16 bits each) as one 32-bit word per row.
+template <typename T>
+__device__ inline void store_pairs(T* lds, int r0, int col, uint4 lo, uint4 hi) {
+    const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w};
+    const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        // low halves (element 2d) and high halves (element 2d + 1)
+        *reinterpret_cast<uint32_t*>(lds + wg_slot(r0 + 2 * d, col)) = __builtin_amdgcn_perm(h[d], l[d], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(lds + wg_slot(r0 + 2 * d + 1, col)) =
+            __builtin_amdgcn_perm(h[d], l[d], 0x07060302u);
+    }
+}
+
 // Block (tile_ci * tiles_co + tile_co, k, split): channel tile TCI x TCO,
 // four waves of (TCI/2) x (TCO/2).  Per step of 32 edges the block stages
 // both operands transposed into channel-major LDS rows (64 edges per step).
 template <typename T, int TCI, int TCO>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 3)
 weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ cot, int n_out, int c_out,
                  const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                  const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
@@ -172,11 +188,23 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     constexpr int NB = TCO / 32;  // 16-column blocks per wave
     __shared__ __align__(16) T a_t[TCI * kWgRow];
     __shared__ __align__(16) T b_t[TCO * kWgRow];
+    // Blocks are dealt to the 8 XCDs round-robin in launch order.  The
+    // logical order (tile, then k, then split) is cut into 8 contiguous
+    // chunks, one per XCD, so the K offsets of a split, which gather the
+    // same neighbourhood of rows, share one XCD's L2.
     const int K = gridDim.y;
-    const int k = blockIdx.y;
-    const int s = blockIdx.z;
-    const int ci0 = (blockIdx.x / tiles_co) * TCI;
-    const int co0 = (blockIdx.x % tiles_co) * TCO;
+    const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+    const int launch = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int per = n_blocks / kXcds;
+    const int extra = n_blocks % kXcds;
+    const int xcd = launch % kXcds;
+    const int slot = launch / kXcds;
+    const int logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + slot;
+    const int tile = logical % gridDim.x;
+    const int k = (logical / gridDim.x) % K;
+    const int s = logical / (gridDim.x * K);
+    const int ci0 = (tile / tiles_co) * TCI;
+    const int co0 = (tile % tiles_co) * TCO;
     const int E = min(counts[0], edge_capacity);
     const int lo_k = koff[k];
     const int n_k = koff[k + 1] - lo_k;
@@ -203,49 +231,76 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     const int j = threadIdx.x >> 3;
     const int p = threadIdx.x & 7;
     V av[2][PA], bv[2][PB];
-    // Rows of step `base`: edges base + j + 32h, zeros past the split's end.
-    auto gather = [&](int base) {
+    // Three-stage pipeline over the steps: the edge ids of step s+3 and the
+    // row indices of step s+2 are loaded while the rows of step s+1 are
+    // gathered, so no step waits on a dependent index load.  Edges past the
+    // split's end or outside the relation read as zeros (row -1).
+    auto fetch_edges = [&](int base, int (&ev)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int cur = base + j + 32 * h;
+            ev[h] = cur < hi ? kedges[cur] : -1;
+        }
+    };
+    auto fetch_rows = [&](const int (&ev)[2], int (&ri)[2], int (&ro)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            ri[h] = -1;
+            ro[h] = -1;
+            const int e = ev[h];
+            if (e < 0 || e >= E) continue;
+            const int in = in_rows[e];
+            const int o = out_rows[e];
+            if (in < 0 || in >= n_in || o < 0 || o >= n_out) continue;
+            ri[h] = in;
+            ro[h] = o;
+        }
+    };
+    auto gather = [&](const int (&ri)[2], const int (&ro)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int i = 0; i < PA; ++i) av[h][i] = V{};
 #pragma unroll
             for (int i = 0; i < PB; ++i) bv[h][i] = V{};
-            const int cur = base + j + 32 * h;
-            if (cur >= hi) continue;
-            const int e = kedges[cur];
-            if (e < 0 || e >= E) continue;
-            const int in = in_rows[e];
-            const int o = out_rows[e];
-            if (in < 0 || in >= n_in || o < 0 || o >= n_out) continue;
+            if (ri[h] < 0) continue;
 #pragma unroll
             for (int i = 0; i < PA; ++i) {
                 const int c = ci0 + 8 * (p + 8 * i);
-                if (c < c_in) av[h][i] = *reinterpret_cast<const V*>(feats + static_cast<long long>(in) * c_in + c);
+                if (c < c_in) av[h][i] = *reinterpret_cast<const V*>(feats + static_cast<long long>(ri[h]) * c_in + c);
             }
 #pragma unroll
             for (int i = 0; i < PB; ++i) {
                 const int c = co0 + 8 * (p + 8 * i);
-                if (c < c_out) bv[h][i] = *reinterpret_cast<const V*>(cot + static_cast<long long>(o) * c_out + c);
+                if (c < c_out) bv[h][i] = *reinterpret_cast<const V*>(cot + static_cast<long long>(ro[h]) * c_out + c);
             }
         }
     };
-    // The gathers of step s+1 are issued before the MFMAs of step s.
-    gather(lo);
+    int ev[2], ri[2], ro[2];
+    fetch_edges(lo, ev);
+    fetch_rows(ev, ri, ro);
+    gather(ri, ro);
+    fetch_edges(lo + kWgEdges, ev);
+    fetch_rows(ev, ri, ro);
+    fetch_edges(lo + 2 * kWgEdges, ev);
     for (int base = lo; base < hi; base += kWgEdges) {
+        // The thread's two edges take adjacent columns 2j and 2j + 1 (the
+        // order of edges inside a step is free: the sum over them is in
+        // fp32), so each channel is one 32-bit store of the pair.
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int i = 0; i < PA; ++i) {
+            store_pairs(a_t, 8 * (p + 8 * i), 2 * j, __builtin_bit_cast(uint4, av[0][i]),
+                        __builtin_bit_cast(uint4, av[1][i]));
+        }
 #pragma unroll
-            for (int i = 0; i < PA; ++i)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) a_t[wg_slot(8 * (p + 8 * i) + c, j + 32 * h)] = av[h][i][c];
-#pragma unroll
-            for (int i = 0; i < PB; ++i)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) b_t[wg_slot(8 * (p + 8 * i) + c, j + 32 * h)] = bv[h][i][c];
+        for (int i = 0; i < PB; ++i) {
+            store_pairs(b_t, 8 * (p + 8 * i), 2 * j, __builtin_bit_cast(uint4, bv[0][i]),
+                        __builtin_bit_cast(uint4, bv[1][i]));
         }
         __syncthreads();
-        gather(base + kWgEdges);
+        gather(ri, ro);
+        fetch_rows(ev, ri, ro);
+        fetch_edges(base + 3 * kWgEdges, ev);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             V af[MB], bf[NB];
