@@ -225,29 +225,54 @@ voxelize_grad(int mode, const float* __restrict__ cot, int voxel_rows, int chann
 
 // ---------------------------------------------------- point-voxel map --
 
+// Block-bucketed table of the voxel rows for the point-voxel map: a 2x2x2
+// block of voxels per 64-byte bucket, so a point's 8 trilinear corners
+// touch at most 8 lines (one when the corners share a block) and each probe
+// reads its key and row from one line.
+int block_capacity_for(int rows) {
+    int cap = 1;
+    const long long want = std::max(static_cast<long long>(rows) + rows / 2 + 1, 1ll);
+    while (cap < want) cap <<= 1;
+    return cap;
+}
+
+// Clears the block table (one thread per 16-byte quarter of a bucket) and
+// the status word.
 __global__ void __launch_bounds__(kThreads)
-insert_voxels(CoordTable table, const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
-              int32_t* status) {
-    const int active = min(max(*active_rows, 0), rows);
-    for (int v = blockIdx.x * kThreads + threadIdx.x; v < active; v += gridDim.x * kThreads) {
-        const int4 c = reinterpret_cast<const int4*>(coords)[v];
-        uint64_t key;
-        if (!pack_key(c.x, c.y, c.z, c.w, &key)) {
-            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-            continue;
-        }
-        table.insert(key, v);
+clear_voxel_blocks(BlockBucket* buckets, long long quarters, int32_t* status) {
+    int4* q = reinterpret_cast<int4*>(buckets);
+    for (long long i = blockIdx.x * static_cast<long long>(kThreads) + threadIdx.x; i < quarters;
+         i += static_cast<long long>(gridDim.x) * kThreads) {
+        q[i] = (i & 3) == 0 ? make_int4(-1, -1, 0, 0) : make_int4(0, 0, 0, 0);
+        if (i == 0) status[0] = 0;
     }
 }
 
-__device__ inline int probe(const CoordTable& table, int b, int64_t x, int64_t y, int64_t z) {
-    uint64_t key;
-    if (!pack_key(b, x, y, z, &key)) return -1;
-    return table.find(key);
+__global__ void __launch_bounds__(kThreads)
+insert_voxel_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
+                    const int32_t* __restrict__ active_rows, int32_t* status) {
+    const int active = min(max(*active_rows, 0), rows);
+    for (int v = blockIdx.x * kThreads + threadIdx.x; v < active; v += gridDim.x * kThreads) {
+        const int4 c = reinterpret_cast<const int4*>(coords)[v];
+        uint64_t block_key;
+        int octant;
+        if (!block_of(c.x, c.y, c.z, c.w, &block_key, &octant)) {
+            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
+            continue;
+        }
+        table.insert(block_key, octant, v);
+    }
+}
+
+__device__ inline int probe(const BlockTable& table, int b, int64_t x, int64_t y, int64_t z) {
+    uint64_t block_key;
+    int octant;
+    if (!block_of(b, x, y, z, &block_key, &octant)) return -1;
+    return table.find(block_key, octant);
 }
 
 __global__ void __launch_bounds__(kThreads)
-map_points(CoordTable table, const float* __restrict__ points, const int32_t* __restrict__ batches, int point_rows,
+map_points(BlockTable table, const float* __restrict__ points, const int32_t* __restrict__ batches, int point_rows,
            const int32_t* __restrict__ point_active, VoxelGrid g, int linear, int32_t* __restrict__ rows_out,
            float* __restrict__ weights_out) {
     const int active = min(max(*point_active, 0), point_rows);
@@ -466,7 +491,8 @@ extern "C" int lattice_hip_voxelize_features_grad(int mode, const float* cot, in
 }
 
 extern "C" size_t lattice_hip_point_voxel_map_workspace_bytes(int voxel_rows) {
-    return table_bytes_for(std::max(voxel_rows, 0)) + 1024;
+    return aligned_bytes(static_cast<size_t>(block_capacity_for(std::max(voxel_rows, 0))) * sizeof(BlockBucket)) +
+           1024;
 }
 
 extern "C" int lattice_hip_build_point_voxel_map(const float* points, const int32_t* batch_indices, int point_rows,
@@ -488,19 +514,17 @@ extern "C" int lattice_hip_build_point_voxel_map(const float* points, const int3
                     "point-voxel map workspace too small.");
     hipStream_t stream = as_stream(stream_ptr);
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
-    const int cap = table_capacity_for(voxel_rows);
-    CoordTable table;
-    table.keys = ws.take<uint64_t>(cap);
-    table.rows = ws.take<int32_t>(cap);
+    const int cap = block_capacity_for(voxel_rows);
+    BlockTable table;
+    table.buckets = ws.take<BlockBucket>(cap);
     table.mask = static_cast<uint32_t>(cap - 1);
-    LATTICE_REQUIRE(table.keys && table.rows, "point-voxel map workspace too small.");
-    clear_quant<<<grid_for(cap, kThreads, 8192), kThreads, 0, stream>>>(table.keys, table.rows, cap, nullptr, 0,
-                                                                      status);
+    LATTICE_REQUIRE(table.buckets, "point-voxel map workspace too small.");
+    clear_voxel_blocks<<<grid_for(4ll * cap, kThreads, 8192), kThreads, 0, stream>>>(table.buckets, 4ll * cap,
+                                                                                   status);
     LATTICE_LAUNCH_CHECK();
     if (voxel_rows > 0) {
-        insert_voxels<<<grid_for(voxel_rows, kThreads, 1u << 14), kThreads, 0, stream>>>(table, voxel_coords,
-                                                                                        voxel_rows, voxel_active,
-                                                                                        status);
+        insert_voxel_blocks<<<grid_for(voxel_rows, kThreads, 1u << 14), kThreads, 0, stream>>>(
+            table, voxel_coords, voxel_rows, voxel_active, status);
         LATTICE_LAUNCH_CHECK();
     }
     if (point_rows == 0) return LATTICE_OK;
