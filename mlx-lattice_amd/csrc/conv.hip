@@ -1003,9 +1003,11 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
 //   * each wave stages its 32 x C_OUT tile in its own LDS area and writes
 //     whole 16-byte row pieces to out[in * K + k].
 // Input rows at or past the active count give zero rows (plus bias), as
-// the relation has no edges for them.
+// the relation has no edges for them.  Two blocks share a CU, except at
+// C_out = 256, whose per-wave staging (4 x 32 x 264 halves) leaves LDS for
+// one.
 template <typename T, int KSTEPS, int CB>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, CB == 16 ? 1 : 2)
 conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ active_rows,
             const T* __restrict__ weights, int K, T* __restrict__ out, const T* __restrict__ bias) {
     using V = typename MfmaOps<T>::vec;
