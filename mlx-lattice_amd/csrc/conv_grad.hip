@@ -120,17 +120,31 @@ transposed_map(const int32_t* __restrict__ in_rows, const int32_t* __restrict__ 
     }
 }
 
-// Offset bits of each input row, from its row of the transposed map.
+// Offset bits of each input row, from its row of the transposed map.  A
+// block takes `rows_per_block` consecutive rows, copies their contiguous
+// map rows into LDS with coalesced loads, and one lane per row then reads
+// its row from LDS (a lane-per-row read of global memory would touch a
+// different line per lane for each offset).
 __global__ void __launch_bounds__(256)
-transposed_masks(const int32_t* __restrict__ in_out_map, int in_capacity, int K, int words,
+transposed_masks(const int32_t* __restrict__ in_out_map, int in_capacity, int K, int words, int rows_per_block,
                  int32_t* __restrict__ row_masks) {
-    for (int row = blockIdx.x * blockDim.x + threadIdx.x; row < in_capacity; row += gridDim.x * blockDim.x) {
-        const int32_t* m = in_out_map + static_cast<long long>(row) * K;
-        for (int w = 0; w < words; ++w) {
-            uint32_t bits = 0;
-            for (int k = 32 * w; k < min(K, 32 * w + 32); ++k) bits |= (m[k] >= 0 ? 1u : 0u) << (k & 31);
-            row_masks[static_cast<long long>(row) * words + w] = static_cast<int32_t>(bits);
+    extern __shared__ int32_t map_rows[];
+    const int blocks = (in_capacity + rows_per_block - 1) / rows_per_block;
+    for (int blk = blockIdx.x; blk < blocks; blk += gridDim.x) {
+        const int r0 = blk * rows_per_block;
+        const int n = min(rows_per_block, in_capacity - r0);
+        const int32_t* src = in_out_map + static_cast<long long>(r0) * K;
+        for (int i = threadIdx.x; i < n * K; i += blockDim.x) map_rows[i] = src[i];
+        __syncthreads();
+        for (int r = threadIdx.x; r < n; r += blockDim.x) {
+            const int32_t* m = map_rows + r * K;
+            for (int w = 0; w < words; ++w) {
+                uint32_t bits = 0;
+                for (int k = 32 * w; k < min(K, 32 * w + 32); ++k) bits |= (m[k] >= 0 ? 1u : 0u) << (k & 31);
+                row_masks[static_cast<long long>(r0 + r) * words + w] = static_cast<int32_t>(bits);
+            }
         }
+        __syncthreads();
     }
 }
 
@@ -510,8 +524,12 @@ extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_
             in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, in_out_map);
         LATTICE_LAUNCH_CHECK();
     }
-    transposed_masks<<<grid_for(in_capacity, 256, 1u << 16), 256, 0, stream>>>(in_out_map, in_capacity,
-                                                                              kernel_count, words, row_masks);
+    // At most 64 KB of map rows per block, and at most one row per lane.
+    const int rows_per_block = std::max(1, std::min(256, 16384 / kernel_count));
+    const size_t lds = static_cast<size_t>(rows_per_block) * kernel_count * sizeof(int32_t);
+    LATTICE_REQUIRE(lds <= 65536, "kernel count too large for the transposed masks.");
+    transposed_masks<<<grid_for(in_capacity, rows_per_block, 1u << 16), 256, lds, stream>>>(
+        in_out_map, in_capacity, kernel_count, words, rows_per_block, row_masks);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
