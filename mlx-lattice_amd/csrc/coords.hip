@@ -67,10 +67,9 @@ __device__ inline int4 load_coord(const int32_t* coords, long long row) {
 // ------------------------------------------------------------- tables ----
 
 __global__ void __launch_bounds__(kThreads)
-clear_table(uint64_t* keys, int32_t* rows, int capacity) {
+clear_table(CoordSlot* slots, int capacity) {
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < capacity; i += gridDim.x * kThreads) {
-        keys[i] = kEmptyKey;
-        rows[i] = INT_MAX;
+        reinterpret_cast<int4*>(slots)[i] = empty_coord_slot();
     }
 }
 
@@ -581,15 +580,14 @@ int table_capacity(int rows) {
 
 size_t table_bytes(int rows) {
     const size_t cap = static_cast<size_t>(table_capacity(rows));
-    return aligned_bytes(cap * sizeof(uint64_t)) + aligned_bytes(cap * sizeof(int32_t));
+    return aligned_bytes(cap * sizeof(CoordSlot));
 }
 
 int make_table(int rows, Workspace& ws, CoordTable* table) {
     const int cap = table_capacity(rows);
-    table->keys = ws.take<uint64_t>(cap);
-    table->rows = ws.take<int32_t>(cap);
+    table->slots = ws.take<CoordSlot>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
-    if (table->keys == nullptr || table->rows == nullptr) {
+    if (table->slots == nullptr) {
         set_error("relation workspace too small for the coordinate table");
         return LATTICE_ERROR_INVALID_ARGUMENT;
     }
@@ -601,7 +599,7 @@ int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int
     int rc = make_table(rows, ws, table);
     if (rc != LATTICE_OK) return rc;
     const int cap = static_cast<int>(table->mask) + 1;
-    clear_table<<<grid_for(cap, kThreads, 4096), kThreads, 0, stream>>>(table->keys, table->rows, cap);
+    clear_table<<<grid_for(cap, kThreads, 4096), kThreads, 0, stream>>>(table->slots, cap);
     LATTICE_LAUNCH_CHECK();
     if (rows > 0) {
         insert_rows<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(

@@ -111,23 +111,32 @@ __host__ __device__ inline uint64_t mix64(uint64_t k) {
     return k;
 }
 
-// Open-addressing table: `keys` (uint64) and `rows` (int32), power-of-two
+// Open-addressing table of 16-byte slots (key, first row), power-of-two
 // capacity, linear probing.  A stored row is the minimum input row that
-// inserted the key, i.e. its first occurrence.
+// inserted the key, i.e. its first occurrence.  Key and row share one slot,
+// so an insert's compare-and-swap and its atomic min, and a lookup's key
+// and row, touch one line.
+struct alignas(16) CoordSlot {
+    unsigned long long key;
+    int32_t row;
+    int32_t pad;
+};
+static_assert(sizeof(CoordSlot) == 16, "one 16-byte slot per key");
+
+// Cleared slot: empty key, row INT_MAX (as one 16-byte store).
+__host__ __device__ inline int4 empty_coord_slot() { return int4{-1, -1, 0x7fffffff, 0}; }
+
 struct CoordTable {
-    uint64_t* keys;
-    int32_t* rows;
+    CoordSlot* slots;
     uint32_t mask;  // capacity - 1
 
     __device__ inline void insert(uint64_t key, int32_t row) const {
         uint32_t slot = static_cast<uint32_t>(mix64(key)) & mask;
         while (true) {
-            unsigned long long prev = atomicCAS(
-                reinterpret_cast<unsigned long long*>(keys + slot),
-                static_cast<unsigned long long>(kEmptyKey),
-                static_cast<unsigned long long>(key));
+            unsigned long long prev = atomicCAS(&slots[slot].key, static_cast<unsigned long long>(kEmptyKey),
+                                                static_cast<unsigned long long>(key));
             if (prev == kEmptyKey || prev == key) {
-                atomicMin(rows + slot, row);
+                atomicMin(&slots[slot].row, row);
                 return;
             }
             slot = (slot + 1) & mask;
@@ -137,8 +146,10 @@ struct CoordTable {
     __device__ inline int32_t find(uint64_t key) const {
         uint32_t slot = static_cast<uint32_t>(mix64(key)) & mask;
         while (true) {
-            uint64_t k = keys[slot];
-            if (k == key) return rows[slot];
+            const int4 v = *reinterpret_cast<const int4*>(slots + slot);
+            const uint64_t k = static_cast<uint64_t>(static_cast<uint32_t>(v.x)) |
+                               (static_cast<uint64_t>(static_cast<uint32_t>(v.y)) << 32);
+            if (k == key) return v.z;
             if (k == kEmptyKey) return -1;
             slot = (slot + 1) & mask;
         }

@@ -63,18 +63,15 @@ int table_capacity_for(int rows) {
 
 size_t table_bytes_for(int rows) {
     const size_t cap = static_cast<size_t>(table_capacity_for(rows));
-    return aligned_bytes(cap * sizeof(uint64_t)) + aligned_bytes(cap * sizeof(int32_t));
+    return aligned_bytes(cap * sizeof(CoordSlot));
 }
 
 // Clears the table, zeroes `zero[0..zero_n)` and the status word.
 __global__ void __launch_bounds__(kThreads)
-clear_quant(uint64_t* keys, int32_t* rows, int capacity, int32_t* zero, int zero_n, int32_t* status) {
+clear_quant(CoordSlot* slots, int capacity, int32_t* zero, int zero_n, int32_t* status) {
     const int n = max(capacity, zero_n);
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-        if (i < capacity) {
-            keys[i] = kEmptyKey;
-            rows[i] = INT_MAX;
-        }
+        if (i < capacity) reinterpret_cast<int4*>(slots)[i] = empty_coord_slot();
         if (i < zero_n) zero[i] = 0;
         if (i == 0 && status != nullptr) status[0] = 0;
     }
@@ -437,14 +434,13 @@ extern "C" int lattice_hip_sparse_quantize(const float* points, const int32_t* b
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const int cap = table_capacity_for(rows);
     CoordTable table;
-    table.keys = ws.take<uint64_t>(cap);
-    table.rows = ws.take<int32_t>(cap);
+    table.slots = ws.take<CoordSlot>(cap);
     table.mask = static_cast<uint32_t>(cap - 1);
     uint64_t* keys = ws.take<uint64_t>(std::max(rows, 1));
     int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
     int32_t* positions = ws.take<int32_t>(std::max(rows, 1));
-    LATTICE_REQUIRE(table.keys && table.rows && keys && flags && positions, "sparse_quantize workspace too small.");
-    clear_quant<<<grid_for(std::max(cap, rows), kThreads, 8192), kThreads, 0, stream>>>(table.keys, table.rows, cap,
+    LATTICE_REQUIRE(table.slots && keys && flags && positions, "sparse_quantize workspace too small.");
+    clear_quant<<<grid_for(std::max(cap, rows), kThreads, 8192), kThreads, 0, stream>>>(table.slots, cap,
                                                                                       counts, rows, status);
     LATTICE_LAUNCH_CHECK();
     if (rows == 0) return fill_i32(voxel_count, 1, 0, stream);
