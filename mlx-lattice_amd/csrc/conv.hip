@@ -1261,9 +1261,7 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
-// c_out = 256 splits the columns over two waves per row group and uses
-// eight waves, so each thread stages four B pieces instead of eight (with
-// eight, the packed-weight variant spills to scratch).
+// c_out = 256 runs the 128-column shape twice (below).
 // c_out 32..128 gather A in whole lines through LDS (ALDS), three blocks
 // per CU (float and packed weights alike: the packed tile's dequantisation
 // from vector loads of consecutive output channels fits the registers).
