@@ -143,7 +143,10 @@ GEOMS = [
     (3, 2, 0, 1),          # overlapping candidates
     (3, 1, 1, 1),
     (2, 1, 0, 1),
-    (3, 2, 1, 2),          # dilated
+    (3, 2, 1, 2),          # dilated (neighbourhood of 125 cells: per-candidate lookups)
+    (3, 4, 0, 2),          # dilated, offset period 2 (tiled neighbourhood)
+    ((5, 3, 2), (3, 2, 1), (1, 0, 0), 1),  # anisotropic 3x3x3 neighbourhood
+    (4, 2, 0, 1),          # even kernel, two preimages per axis
 ]
 
 
