@@ -52,24 +52,7 @@ def parse_args():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-secondary', action='store_true',
                    help='skip the timings of configs 2, 4 and 5')
-    p.add_argument('--copy-probe-mib', type=int, default=0,
-                   help='only run a plain device copy of this many MiB '
-                        '(5 launches) and exit: the reference kernel that '
-                        'scales the FETCH_SIZE / WRITE_SIZE counters')
     return p.parse_args()
-
-
-def copy_probe(mib: int) -> int:
-    import torch
-
-    n = mib * (1 << 20)
-    src = torch.ones(n, dtype=torch.uint8, device='cuda:0')
-    dst = torch.empty_like(src)
-    for _ in range(5):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({'copy_probe_bytes': n, 'launches': 5}), flush=True)
-    return 0
 
 
 def make_workload():
@@ -370,8 +353,7 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
         'the direct expansion route is expected'
     e = int(rel.counts[0].item())
     t_build = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
-        coarse, active, [2, 2, 2], [2, 2, 2], [0, 0, 0], [1, 1, 1],
-        check_range=False), steps, warmup)
+        coarse, active, [2, 2, 2], [2, 2, 2], [0, 0, 0], [1, 1, 1]), steps, warmup)
     t_conv = _timed(lambda: ops.conv_transpose3d(x, weight, kernel_size=2,
                                                  stride=2), steps, warmup)
     # the generic matrix-core route over the same relation, for comparison
@@ -382,8 +364,7 @@ def decoder_workload(coords, steps: int, warmup: int) -> dict:
     t_generic = _timed(lambda: sparse_conv_features_sorted_from_relation(
         feats, weight, rel), steps, warmup)
     t_k3 = _timed(lambda: ext.build_transposed_kernel_relation_lazy(
-        coarse, active, [3, 3, 3], [2, 2, 2], [0, 0, 0], [1, 1, 1],
-        check_range=False), steps, warmup)
+        coarse, active, [3, 3, 3], [2, 2, 2], [0, 0, 0], [1, 1, 1]), steps, warmup)
     build_bytes = 16 * n + e * (12 + 4 + 16) + 4
     conv_bytes = n * c * 2 + e * c * 2 + 8 * c * c * 2
     flops = 2.0 * e * c * c
@@ -434,7 +415,7 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
     q = ops.sparse_quantize(pts, 1.0, batch_indices=batches)
     v = int(q.active_rows.item())
     t_q = _timed(lambda: ext.sparse_quantize(pts, batches, active, [1.0],
-                                             [0.0], check_range=False),
+                                             [0.0]),
                  steps, warmup)
     c = 64
     feats = torch.randn((n, c), generator=gen, device=dev)
@@ -448,7 +429,7 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
                                      batch_indices=batches)
     t_map = _timed(lambda: ext.build_point_voxel_map(
         pts, batches, active, q.coords, q.active_rows, [1.0], [0.0],
-        'linear', check_range=False), steps, warmup)
+        'linear'), steps, warmup)
     t_int = _timed(lambda: ext.interpolate_point_features(
         vfeats, pmap.rows, pmap.weights), steps, warmup)
     hbm = PEAK_HBM_GBS * 1e6
@@ -507,8 +488,6 @@ def main() -> int:
               'exchange (see DESIGN.md), so run one process per GPU.',
               file=sys.stderr)
         return 2
-    if args.copy_probe_mib:
-        return copy_probe(args.copy_probe_mib)
     import torch
 
     from mlx_lattice_amd._native import ext
@@ -523,7 +502,7 @@ def main() -> int:
 
     def map_build():
         native = ext.build_submanifold_kernel_relation_with_view(
-            coords, active, [3, 3, 3], [1, 1, 1], check_range=False)
+            coords, active, [3, 3, 3], [1, 1, 1])
         return native
 
     def sorted_view(native):
@@ -536,9 +515,6 @@ def main() -> int:
             native[2], native[5], native[3], native[6], native[7], native[8],
             native[9], n_out, 27)
 
-    # One checked build validates the coordinate range once.
-    native = ext.build_submanifold_kernel_relation_with_view(
-        coords, active, [3, 3, 3], [1, 1, 1])
     for _ in range(args.warmup):
         native = map_build()
         view = sorted_view(native)

@@ -73,14 +73,20 @@ enum lattice_weight_layout {
     LATTICE_WEIGHT_DENSE_5D = 1      /* (C_out, Kx, Ky, Kz, C_in) contiguous */
 };
 
-/* Bits of the device status word written by the relation builders. */
+/* Bits of the device status word written by the relation builders.  Every
+ * int32 coordinate is accepted (as by the reference's CoordHash over all
+ * four words, cpu/common_detail.h:68-77); LATTICE_STATUS_COORD_RANGE is
+ * kept for ABI stability and is never set. */
 enum lattice_relation_flags {
-    LATTICE_STATUS_COORD_RANGE = 1,   /* an active coordinate does not fit the packed key */
+    LATTICE_STATUS_COORD_RANGE = 1,   /* unused: no coordinate is out of range */
     LATTICE_STATUS_REPEATED_EDGE = 2  /* transposed relation: two edges share (out_row, kernel_id) */
 };
 
-/* Packed-key coordinate range: batch in [0, LATTICE_MAX_BATCH], spatial
- * axes in [LATTICE_MIN_COORD, LATTICE_MAX_COORD]. */
+/* Packed-key range: a key with batch in [0, LATTICE_MAX_BATCH] and axes in
+ * [LATTICE_MIN_COORD, LATTICE_MAX_COORD] (a 2x2x2 block key: the block
+ * coordinates) takes the one-compare packed form; every other key takes
+ * the wide form, compared in full against the table's source rows.  Both
+ * give the same results; only the speed of a lookup differs. */
 #define LATTICE_MAX_BATCH 1022
 #define LATTICE_MIN_COORD (-131072)
 #define LATTICE_MAX_COORD 131071
@@ -157,8 +163,7 @@ int lattice_hip_build_target_kernel_relation(
  *     extent (can_use_direct_transposed_relation, relations.cpp:107-127);
  *     otherwise first-seen deduplicated output rows and edges in
  *     (out_row, kernel_id, in_row) order (:119-196).  A repeated input
- *     coordinate sets LATTICE_STATUS_REPEATED_EDGE in out->status.
- * Candidate tables need the packed-key range (LATTICE_STATUS_COORD_RANGE). */
+ *     coordinate sets LATTICE_STATUS_REPEATED_EDGE in out->status. */
 size_t lattice_hip_expanded_relation_workspace_bytes(
     int rows, const int kernel_size[3], const int stride[3],
     const int dilation[3], int generative);
@@ -196,7 +201,8 @@ int lattice_hip_group_by_key(const int32_t* keys, int n, const int32_t* count,
  * voxel_size)), first-seen point order.  Outputs (capacity = rows):
  * coords int32 [rows, 4] (zero tail), voxel_count int32 [1], inverse_rows
  * int32 [rows] (-1 for inactive points), counts int32 [rows] (zero tail).
- * Voxel coordinates must fit the packed key (LATTICE_STATUS_COORD_RANGE). */
+ * Voxels are deduplicated on their int64 value and written as int32 (low
+ * 32 bits); `status` is zeroed. */
 size_t lattice_hip_sparse_quantize_workspace_bytes(int rows);
 int lattice_hip_sparse_quantize(
     const float* points, const int32_t* batch_indices, int rows,
@@ -342,13 +348,6 @@ int lattice_hip_sparse_conv_features_expand(
     int dtype, const void* feats, int n_in, const int32_t* active_rows,
     int c_in, const void* weights, int kernel_count, int c_out, void* out,
     const void* bias, void* stream);
-
-/* Tuning knob with no counterpart in the reference: rows of the sorted
- * order owned by one wavefront in the implicit-GEMM route (32 or 64).
- * 64 doubles the reuse of each staged weight fragment; 32 (the default)
- * keeps the register footprint low enough for three blocks per CU.
- * Process-wide. */
-int lattice_hip_set_conv_tile_rows(int rows);
 
 /* Quantized conv (cpu/quantized.cpp:64-141): weights uint32
  * [K, storage_c_in*bits/32, c_out] with codes LSB-first along C_in,

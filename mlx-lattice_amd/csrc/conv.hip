@@ -1228,14 +1228,6 @@ template <typename T> PackedB<T> column_half(const PackedB<T>& b, int co_base) {
     return h;
 }
 
-// Wave tile rows: 64 doubles the reuse of each B fragment read from LDS;
-// 32 (the default) keeps registers low enough for three blocks per CU.
-int g_igemm_wave_rows = 32;
-#ifdef LATTICE_IGEMM_SWEEP
-int g_igemm_sweep = -1;
-extern "C" void lattice_hip_sweep_variant(int v) { g_igemm_sweep = v; }
-#endif
-
 template <typename T, typename BSource>
 int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
                  const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, T* out,
@@ -1244,20 +1236,6 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 #define LATTICE_IGEMM_LAUNCH(...) \
     launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, \
                                                    schedule, out, bias, stream)
-#ifdef LATTICE_IGEMM_SWEEP
-    if (c_out == 128 && g_igemm_sweep >= 0) {
-        switch (g_igemm_sweep) {
-            // the shape before line-coalesced A
-            case 0: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64);
-            // line-coalesced A, skipping the offsets the wave does not use
-            case 1: return LATTICE_IGEMM_LAUNCH(128, 32, 4, 64, 1, false, 3, 128, true, true);
-            // line-coalesced A with 256-row tiles
-            case 2: return LATTICE_IGEMM_LAUNCH(128, 32, 8, 64, 1, false, 4, 128, false, true);
-            case 3: return LATTICE_IGEMM_LAUNCH(128, 64, 4, 64, 1, false, 2, 128, false, true);
-            default: break;
-        }
-    }
-#endif
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
@@ -1268,17 +1246,14 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
     constexpr int kAldsOcc = 3;
 #define LATTICE_IGEMM_CASE(C)                                                  \
     case C:                                                                    \
-        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(C, 64, 4);   \
         return LATTICE_IGEMM_LAUNCH(C, 32, 4, 64, 1, false, kAldsOcc, 128, false, true);
     switch (c_out) {
     case 16:
-        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(16, 64, 4);
         return LATTICE_IGEMM_LAUNCH(16, 32, 4, 128);
         LATTICE_IGEMM_CASE(32)
         LATTICE_IGEMM_CASE(64)
         LATTICE_IGEMM_CASE(128)
     case 256: {
-        if (g_igemm_wave_rows == 64) return LATTICE_IGEMM_LAUNCH(256, 64, 4);
         // Two launches of the 128-column kernel, each writing its half of
         // every output row (row stride 256): its occupancy and B tile beat
         // the 8-wave 256-column shape, at the cost of gathering A twice.
@@ -1332,12 +1307,6 @@ int check_dtype(int dtype) {
 using namespace lattice;
 
 extern "C" size_t lattice_hip_conv_workspace_bytes(int out_capacity) { return conv_schedule_bytes(out_capacity); }
-
-extern "C" int lattice_hip_set_conv_tile_rows(int rows) {
-    LATTICE_REQUIRE(rows == 32 || rows == 64, "conv tile rows must be 32 or 64.");
-    g_igemm_wave_rows = rows;
-    return LATTICE_OK;
-}
 
 extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, int n_in, int c_in,
                                                 const void* weights, int weight_layout, int kernel_count,

@@ -112,44 +112,44 @@ clear_blocks(BlockBucket* buckets, long long quarters, Prologue p) {
     }
 }
 
-// Inserts the active rows into the block table; flags coordinates outside
-// the packed-key range.
+// Inserts the active rows into the block table.  Every int32 coordinate
+// has a key: packed when it fits, wide otherwise.
 __global__ void __launch_bounds__(kThreads)
 insert_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
-              const int32_t* __restrict__ active_rows, int32_t* status) {
+              const int32_t* __restrict__ active_rows) {
     const int active = min(max(*active_rows, 0), rows);
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < active; i += gridDim.x * kThreads) {
         const int4 c = load_coord(coords, i);
-        uint64_t block_key;
+        TableKey block_key;
         int octant;
-        if (!block_of(c.x, c.y, c.z, c.w, &block_key, &octant)) {
-            status[0] = LATTICE_STATUS_COORD_RANGE;
-            continue;
-        }
+        block_of(c.x, c.y, c.z, c.w, &block_key, &octant);
         table.insert(block_key, octant, i);
     }
 }
 
-// Inserts active rows keyed by their coordinate (cell_stride == 1) or by the
-// floor-divided cell (cell_stride > 1 on an axis).
+// The floor-divided cell of an input row (downsample_values,
+// quantization_detail.h:12-31): the key source of the cell table.
+struct CellSource {
+    const int32_t* coords;
+    Int3 cell;
+    __device__ inline FullKey key_of(int32_t row) const {
+        const int4 c = load_coord(coords, row);
+        return {c.x, floor_div_pos(c.y, cell.x), floor_div_pos(c.z, cell.y), floor_div_pos(c.w, cell.z)};
+    }
+    __device__ inline TableKey table_key_of(int32_t row) const {
+        const FullKey k = key_of(row);
+        return table_key(k.b, k.x, k.y, k.z);
+    }
+};
+
+// Inserts active rows keyed by their floor-divided cell.
 __global__ void __launch_bounds__(kThreads)
 insert_rows(CoordTable table, const int32_t* __restrict__ coords, int rows,
-            const int32_t* __restrict__ active_rows, Int3 cell, int32_t* status) {
+            const int32_t* __restrict__ active_rows, Int3 cell) {
     const int active = min(max(*active_rows, 0), rows);
+    const CellSource src{coords, cell};
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < active; i += gridDim.x * kThreads) {
-        int4 c = load_coord(coords, i);
-        int64_t x = c.y, y = c.z, z = c.w;
-        if (cell.x != 1 || cell.y != 1 || cell.z != 1) {
-            x = floor_div_pos(x, cell.x);
-            y = floor_div_pos(y, cell.y);
-            z = floor_div_pos(z, cell.z);
-        }
-        uint64_t key;
-        if (!pack_key(c.x, x, y, z, &key)) {
-            status[0] = LATTICE_STATUS_COORD_RANGE;
-            continue;
-        }
-        table.insert(key, i);
+        table.insert(src.table_key_of(i), i, src);
     }
 }
 
@@ -161,17 +161,9 @@ flag_cell_representatives(CoordTable cells, const int32_t* __restrict__ coords, 
                           const int32_t* __restrict__ active_rows, Int3 cell,
                           int32_t* __restrict__ flags) {
     const int active = min(max(*active_rows, 0), rows);
+    const CellSource src{coords, cell};
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        int flag = 0;
-        if (i < active) {
-            int4 c = load_coord(coords, i);
-            uint64_t key;
-            if (pack_key(c.x, floor_div_pos(c.y, cell.x), floor_div_pos(c.z, cell.y),
-                         floor_div_pos(c.w, cell.z), &key)) {
-                flag = cells.find(key) == i ? 1 : 0;
-            }
-        }
-        flags[i] = flag;
+        flags[i] = i < active && cells.find(src.table_key_of(i), src) == i ? 1 : 0;
     }
 }
 
@@ -254,7 +246,7 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
                 int64_t x = static_cast<int64_t>(oc.y) * a.geom.stride.x + off.x - a.geom.padding.x;
                 int64_t y = static_cast<int64_t>(oc.z) * a.geom.stride.y + off.y - a.geom.padding.y;
                 int64_t z = static_cast<int64_t>(oc.w) * a.geom.stride.z + off.z - a.geom.padding.z;
-                uint64_t block_key;
+                TableKey block_key;
                 int octant;
                 if (block_of(oc.x, x, y, z, &block_key, &octant)) found = a.table.find(block_key, octant);
             }
@@ -307,20 +299,46 @@ __device__ inline int query_rows_k3(const QueryArgs& a, long long row0, int lane
     const bool row_ok = row < a.out_capacity;
     const bool active = row < n_active;
     const int4 c = active ? load_coord(a.out_coords, row) : make_int4(0, 0, 0, 0);
-    const int bx = (c.y - 1) >> 1, by = (c.z - 1) >> 1, bz = (c.w - 1) >> 1;  // floor division
+    // The window's blocks floor((v - 1) / 2) .. floor((v + 1) / 2) per axis
+    // have packed keys when v lies in [-2^18 + 1, 2^18 - 2] and the batch in
+    // [0, 1022]; int32 arithmetic is exact there.
+    const auto window_packs = [](int v) { return v >= -(1 << 18) + 1 && v <= (1 << 18) - 2; };
+    const bool packed = c.x >= 0 && c.x <= LATTICE_MAX_BATCH && window_packs(c.y) && window_packs(c.z) &&
+                        window_packs(c.w);
     uint64_t keys[8];
     bool key_ok[8];
     uint32_t slot[8];
     uint4 lo[8], mid[8];
     uint2 hi[8];
+    if (packed || !active) {
+        const int bx = (c.y - 1) >> 1, by = (c.z - 1) >> 1, bz = (c.w - 1) >> 1;  // floor division
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        key_ok[j] = active && pack_key(c.x, bx + (j >> 2), by + ((j >> 1) & 1), bz + (j & 1), &keys[j]);
-        slot[j] = static_cast<uint32_t>(mix64(keys[j])) & a.table.mask;
-        const uint4* bucket = reinterpret_cast<const uint4*>(a.table.buckets + slot[j]);
-        lo[j] = bucket[0];   // key, rows 0..1
-        mid[j] = bucket[1];  // rows 2..5
-        hi[j] = *reinterpret_cast<const uint2*>(bucket + 2);  // rows 6..7
+        for (int j = 0; j < 8; ++j) {
+            pack_key(c.x, bx + (j >> 2), by + ((j >> 1) & 1), bz + (j & 1), &keys[j]);
+            key_ok[j] = active;
+            slot[j] = static_cast<uint32_t>(mix64(keys[j])) & a.table.mask;
+            const uint4* bucket = reinterpret_cast<const uint4*>(a.table.buckets + slot[j]);
+            lo[j] = bucket[0];   // key, rows 0..1
+            mid[j] = bucket[1];  // rows 2..5
+            hi[j] = *reinterpret_cast<const uint2*>(bucket + 2);  // rows 6..7
+        }
+    } else {
+        // Rare: some block key is wide.  Each block is found through the
+        // table, which compares wide keys in full (int64: v - 1 leaves int32
+        // at INT_MIN); the probe below then stops at once.
+        const int64_t bx = (static_cast<int64_t>(c.y) - 1) >> 1;
+        const int64_t by = (static_cast<int64_t>(c.z) - 1) >> 1;
+        const int64_t bz = (static_cast<int64_t>(c.w) - 1) >> 1;
+        for (int j = 0; j < 8; ++j) {
+            const int32_t b = a.table.find_bucket(table_key(c.x, bx + (j >> 2), by + ((j >> 1) & 1), bz + (j & 1)));
+            slot[j] = b < 0 ? 0u : static_cast<uint32_t>(b);
+            const uint4* bucket = reinterpret_cast<const uint4*>(a.table.buckets + slot[j]);
+            lo[j] = bucket[0];
+            mid[j] = bucket[1];
+            hi[j] = *reinterpret_cast<const uint2*>(bucket + 2);
+            key_ok[j] = b >= 0;
+            keys[j] = (static_cast<uint64_t>(lo[j].y) << 32) | lo[j].x;
+        }
     }
     uint32_t rows[8][8];
 #pragma unroll
@@ -595,7 +613,7 @@ int make_table(int rows, Workspace& ws, CoordTable* table) {
 }
 
 int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int3 cell,
-                int32_t* status, Workspace& ws, hipStream_t stream, CoordTable* table) {
+                Workspace& ws, hipStream_t stream, CoordTable* table) {
     int rc = make_table(rows, ws, table);
     if (rc != LATTICE_OK) return rc;
     const int cap = static_cast<int>(table->mask) + 1;
@@ -603,7 +621,7 @@ int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int
     LATTICE_LAUNCH_CHECK();
     if (rows > 0) {
         insert_rows<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
-            *table, coords, rows, active_rows, cell, status);
+            *table, coords, rows, active_rows, cell);
         LATTICE_LAUNCH_CHECK();
     }
     return LATTICE_OK;
@@ -622,11 +640,12 @@ size_t block_table_bytes(int rows) {
     return aligned_bytes(static_cast<size_t>(block_capacity(rows)) * sizeof(BlockBucket));
 }
 
-int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows, int32_t* status,
+int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows,
                       const Prologue& prologue, Workspace& ws, hipStream_t stream, BlockTable* table) {
     const int cap = block_capacity(rows);
     table->buckets = ws.take<BlockBucket>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
+    table->src = BlockSource{coords};
     if (table->buckets == nullptr) {
         set_error("relation workspace too small for the coordinate table");
         return LATTICE_ERROR_INVALID_ARGUMENT;
@@ -636,8 +655,7 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
         table->buckets, quarters, prologue);
     LATTICE_LAUNCH_CHECK();
     if (rows > 0) {
-        insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows,
-                                                                              status);
+        insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows);
         LATTICE_LAUNCH_CHECK();
     }
     return LATTICE_OK;
@@ -856,7 +874,7 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
         prologue.copy_dst = out->out_coords;
     }
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
+    rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
 
     QueryArgs q{};
@@ -873,7 +891,7 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     } else {
         const Int3 cell{stride[0], stride[1], stride[2]};
         CoordTable cells;
-        rc = build_table(coords, rows, active_rows, cell, out->status, ws, stream, &cells);
+        rc = build_table(coords, rows, active_rows, cell, ws, stream, &cells);
         if (rc != LATTICE_OK) return rc;
         int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
         int32_t* positions = ws.take<int32_t>(std::max(rows, 1));
@@ -916,7 +934,7 @@ extern "C" int lattice_hip_build_target_kernel_relation(
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const Prologue prologue{out->status, target_active_rows, target_rows, out->counts, nullptr, nullptr, 0, nullptr};
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
+    rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
     QueryArgs q{};
     q.out_coords = target_coords;
@@ -976,7 +994,7 @@ extern "C" int lattice_hip_build_relation_implicit_gemm_view(
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const Prologue prologue{status, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr};
     BlockTable table;
-    int rc = build_block_table(source_coords, source_rows, source_active_rows, status, prologue, ws, stream, &table);
+    int rc = build_block_table(source_coords, source_rows, source_active_rows, prologue, ws, stream, &table);
     if (rc != LATTICE_OK) return rc;
     QueryArgs q{};
     q.out_coords = output_coords;
@@ -1152,20 +1170,20 @@ __device__ inline int axis_offset(int i, int size, int dilation) {
     return (i - ((size & 1) ? size / 2 : 0)) * dilation;
 }
 
-// First input row of a coordinate, or -1 (absent or outside the key range).
+// First input row of a coordinate, or -1.
 __device__ inline int first_row(const BlockTable& table, int b, int64_t x, int64_t y, int64_t z) {
-    uint64_t block_key;
+    TableKey block_key;
     int octant;
     if (!block_of(b, x, y, z, &block_key, &octant)) return -1;
     return table.find(block_key, octant);
 }
 
 // reps[j] = first candidate index j' with cand(j') == cand(j) (-1 for
-// inactive rows and candidates outside the key range); flags[j] = reps[j]
+// inactive rows); flags[j] = reps[j]
 // == j.  Lanes of one input row share its neighbourhood's bucket lines.
 __global__ void __launch_bounds__(kThreads)
 resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int rows,
-                   const int32_t* __restrict__ active_rows, KernelGeometry g, int32_t* status,
+                   const int32_t* __restrict__ active_rows, KernelGeometry g,
                    int32_t* __restrict__ reps, int32_t* __restrict__ flags) {
     const int K = g.volume;
     const int cap = rows * K;
@@ -1176,12 +1194,7 @@ resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int row
         if (j < total) {
             const int in = j / K;
             const int k = j - in * K;
-            int64_t x, y, z;
-            const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
-            uint64_t key;
-            if (!pack_key(c.x, x, y, z, &key)) {
-                atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-            } else {
+            {
                 const int4 src = load_coord(coords, in);
                 const int ix = k / yz;
                 const int iy = (k - ix * yz) / g.size.z;
@@ -1352,12 +1365,7 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
             int members = 0;  // candidates equal to this one
             int before = 0;   // of those, with a smaller kernel id
             if (in < active) {
-                int64_t x, y, z;
-                const int4 c = candidate_of(coords, in, k, g, &x, &y, &z);
-                uint64_t key;
-                if (!pack_key(c.x, x, y, z, &key)) {
-                    atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-                } else {
+                {
                     const int32_t* f = found + (in - r0) * cells;
                     const int ix = k / yz;
                     const int iy = (k - ix * yz) / g.size.z;
@@ -1407,7 +1415,7 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
 // zero tail; keys[t] (t = k * rows + in) = output row of candidate in*K+k,
 // -1 for inactive rows (sorted last).  With edge_offsets (the exclusive scan
 // of the representatives' group sizes) and ranks, and while the status word
-// is clear (every candidate in range, no repeated input coordinate), the
+// is clear (no repeated input coordinate), the
 // edges are written in their final (out_row, kernel_id, in_row) order here:
 // candidate j is edge edge_offsets[rep] + ranks[j] and out row positions[j]
 // of a representative starts at edge_offsets[j].
@@ -1542,7 +1550,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
     } else {
         const Prologue prologue{out->status, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr};
         BlockTable table;
-        rc = build_block_table(coords, rows, active_rows, out->status, prologue, ws, stream, &table);
+        rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table);
         if (rc != LATTICE_OK) return rc;
         int32_t* reps = ws.take<int32_t>(cap);
         int32_t* flags = ws.take<int32_t>(cap);
@@ -1565,8 +1573,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         const long long cells = (2ll * reach.x + 1) * (2ll * reach.y + 1) * (2ll * reach.z + 1);
         // The tiled resolve also ranks every candidate inside its output
         // row, so the edges are placed directly; the stable sort then runs
-        // only when the status word reports a candidate out of range or a
-        // repeated input coordinate.  The general resolve always sorts.
+        // only when the status word reports a repeated input coordinate.  The general resolve always sorts.
         const bool tiled = cells <= kResolveCells;
         const auto gcd = [](int a, int b) {
             while (b != 0) {
@@ -1586,7 +1593,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
                 table, coords, rows, active_rows, g, reach, period, step, out->status, reps, flags, sizes, ranks,
                 tile_firsts, tile_edges);
         } else {
-            resolve_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, out->status, reps,
+            resolve_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, reps,
                                                               flags);
         }
         LATTICE_LAUNCH_CHECK();

@@ -45,14 +45,37 @@ __device__ inline float grid_position(float p, int axis, const VoxelGrid& g) {
     return ((p - g.origin[axis]) / g.size[axis]);
 }
 
-// floor of a float as int64; values outside +-2^40 (and NaN) are reported
-// as out of range, which the packed key would reject anyway.
+// floor of a float as int64; false outside +-2^40 (and for NaN), where no
+// int32 voxel coordinate can match.
 __device__ inline bool floor_int(float v, int64_t* out) {
     const float f = floorf(v);
     if (!(fabsf(f) < 1099511627776.0f)) return false;
     *out = static_cast<int64_t>(f);
     return true;
 }
+
+// floor of a float as int64 (static_cast<int64_t>(std::floor(v)), exact
+// below 2^63 in magnitude).  The reference's conversion is undefined beyond
+// that and for NaN; here they saturate, NaN to INT64_MIN.
+__device__ inline int64_t floor_i64(float v) {
+    const float f = floorf(v);
+    if (!(f >= -9223372036854775808.0f)) return INT64_MIN;
+    if (f >= 9223372036854775808.0f) return INT64_MAX;
+    return static_cast<int64_t>(f);
+}
+
+// The voxel of a point (batch, floor((p - origin) / voxel_size)): the key
+// source of the voxel table.
+struct PointSource {
+    const float* points;
+    const int32_t* batches;
+    VoxelGrid g;
+    __device__ inline FullKey key_of(int32_t p) const {
+        const float* q = points + 3ll * p;
+        return {batches[p], floor_i64(grid_position(q[0], 0, g)), floor_i64(grid_position(q[1], 1, g)),
+                floor_i64(grid_position(q[2], 2, g))};
+    }
+};
 
 int table_capacity_for(int rows) {
     int cap = 1;
@@ -79,58 +102,50 @@ clear_quant(CoordSlot* slots, int capacity, int32_t* zero, int zero_n, int32_t* 
 
 // ------------------------------------------------------ sparse_quantize --
 
-// Voxel key of every point (kEmptyKey for inactive points), inserted with
-// the point row.
+// Inserts the voxel of every active point with the point row; slots[p] =
+// the voxel's table slot (-1 for inactive points).
 __global__ void __launch_bounds__(kThreads)
-insert_points(CoordTable table, const float* __restrict__ points, const int32_t* __restrict__ batches, int rows,
-              const int32_t* __restrict__ active_rows, VoxelGrid g, uint64_t* __restrict__ keys, int32_t* status) {
+insert_points(CoordTable table, PointSource src, int rows, const int32_t* __restrict__ active_rows,
+              int32_t* __restrict__ slots) {
     const int active = min(max(*active_rows, 0), rows);
     for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
-        uint64_t key = kEmptyKey;
+        int32_t slot = -1;
         if (p < active) {
-            const float* q = points + 3ll * p;
-            int64_t v[3];
-            bool ok = true;
-            for (int a = 0; a < 3; ++a) ok = floor_int(grid_position(q[a], a, g), &v[a]) && ok;
-            uint64_t k;
-            if (ok && pack_key(batches[p], v[0], v[1], v[2], &k)) {
-                key = k;
-                table.insert(k, p);
-            } else {
-                atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-            }
+            const FullKey v = src.key_of(p);
+            slot = static_cast<int32_t>(table.insert(table_key(v.b, v.x, v.y, v.z), p, src));
         }
-        keys[p] = key;
+        slots[p] = slot;
     }
 }
 
 __global__ void __launch_bounds__(kThreads)
-flag_points(CoordTable table, const uint64_t* __restrict__ keys, int rows, int32_t* __restrict__ flags) {
+flag_points(CoordTable table, const int32_t* __restrict__ slots, int rows, int32_t* __restrict__ flags) {
     for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
-        const uint64_t k = keys[p];
-        flags[p] = (k != kEmptyKey && table.find(k) == p) ? 1 : 0;
+        const int32_t s = slots[p];
+        flags[p] = (s >= 0 && table.slots[s].row == p) ? 1 : 0;
     }
 }
 
-__device__ inline int4 unpack_key(uint64_t k) {
-    return make_int4(static_cast<int>(k >> 54), static_cast<int>(((k >> 36) & (kAxisSpan - 1)) - kAxisBias),
-                     static_cast<int>(((k >> 18) & (kAxisSpan - 1)) - kAxisBias),
-                     static_cast<int>((k & (kAxisSpan - 1)) - kAxisBias));
-}
-
+// Output voxel coordinates are written as int32 (write_coords); an axis
+// value outside int32 keeps its low 32 bits.
 __global__ void __launch_bounds__(kThreads)
-place_points(CoordTable table, const uint64_t* __restrict__ keys, int rows, const int32_t* __restrict__ flags,
-             const int32_t* __restrict__ positions, const int32_t* __restrict__ voxel_count,
-             int32_t* __restrict__ coords, int32_t* __restrict__ inverse_rows, int32_t* __restrict__ counts) {
+place_points(CoordTable table, PointSource src, const int32_t* __restrict__ slots, int rows,
+             const int32_t* __restrict__ flags, const int32_t* __restrict__ positions,
+             const int32_t* __restrict__ voxel_count, int32_t* __restrict__ coords,
+             int32_t* __restrict__ inverse_rows, int32_t* __restrict__ counts) {
     const int n_vox = *voxel_count;
     int4* out = reinterpret_cast<int4*>(coords);
     for (int p = blockIdx.x * kThreads + threadIdx.x; p < rows; p += gridDim.x * kThreads) {
-        const uint64_t k = keys[p];
+        const int32_t s = slots[p];
         int inv = -1;
-        if (k != kEmptyKey) {
-            inv = positions[table.find(k)];
+        if (s >= 0) {
+            inv = positions[table.slots[s].row];
             atomicAdd(counts + inv, 1);
-            if (flags[p]) out[positions[p]] = unpack_key(k);
+            if (flags[p]) {
+                const FullKey v = src.key_of(p);
+                out[positions[p]] = make_int4(static_cast<int32_t>(v.b), static_cast<int32_t>(v.x),
+                                              static_cast<int32_t>(v.y), static_cast<int32_t>(v.z));
+            }
         }
         if (p >= n_vox) out[p] = make_int4(0, 0, 0, 0);
         inverse_rows[p] = inv;
@@ -247,22 +262,19 @@ clear_voxel_blocks(BlockBucket* buckets, long long quarters, int32_t* status) {
 
 __global__ void __launch_bounds__(kThreads)
 insert_voxel_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
-                    const int32_t* __restrict__ active_rows, int32_t* status) {
+                    const int32_t* __restrict__ active_rows) {
     const int active = min(max(*active_rows, 0), rows);
     for (int v = blockIdx.x * kThreads + threadIdx.x; v < active; v += gridDim.x * kThreads) {
         const int4 c = reinterpret_cast<const int4*>(coords)[v];
-        uint64_t block_key;
+        TableKey block_key;
         int octant;
-        if (!block_of(c.x, c.y, c.z, c.w, &block_key, &octant)) {
-            atomicOr(status, LATTICE_STATUS_COORD_RANGE);
-            continue;
-        }
+        block_of(c.x, c.y, c.z, c.w, &block_key, &octant);
         table.insert(block_key, octant, v);
     }
 }
 
 __device__ inline int probe(const BlockTable& table, int b, int64_t x, int64_t y, int64_t z) {
-    uint64_t block_key;
+    TableKey block_key;
     int octant;
     if (!block_of(b, x, y, z, &block_key, &octant)) return -1;
     return table.find(block_key, octant);
@@ -413,7 +425,7 @@ using namespace lattice;
 
 extern "C" size_t lattice_hip_sparse_quantize_workspace_bytes(int rows) {
     const size_t n = static_cast<size_t>(std::max(rows, 1));
-    return table_bytes_for(std::max(rows, 0)) + aligned_bytes(n * sizeof(uint64_t)) +
+    return table_bytes_for(std::max(rows, 0)) + aligned_bytes(n * sizeof(int32_t)) +
            2 * aligned_bytes(n * sizeof(int32_t)) + scan_workspace_bytes(std::max(rows, 0)) + 1024;
 }
 
@@ -436,23 +448,23 @@ extern "C" int lattice_hip_sparse_quantize(const float* points, const int32_t* b
     CoordTable table;
     table.slots = ws.take<CoordSlot>(cap);
     table.mask = static_cast<uint32_t>(cap - 1);
-    uint64_t* keys = ws.take<uint64_t>(std::max(rows, 1));
+    int32_t* slots = ws.take<int32_t>(std::max(rows, 1));
     int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
     int32_t* positions = ws.take<int32_t>(std::max(rows, 1));
-    LATTICE_REQUIRE(table.slots && keys && flags && positions, "sparse_quantize workspace too small.");
+    LATTICE_REQUIRE(table.slots && slots && flags && positions, "sparse_quantize workspace too small.");
     clear_quant<<<grid_for(std::max(cap, rows), kThreads, 8192), kThreads, 0, stream>>>(table.slots, cap,
                                                                                       counts, rows, status);
     LATTICE_LAUNCH_CHECK();
     if (rows == 0) return fill_i32(voxel_count, 1, 0, stream);
-    const VoxelGrid g = make_grid(voxel_size, origin);
+    const PointSource src{points, batch_indices, make_grid(voxel_size, origin)};
     const unsigned grid = grid_for(rows, kThreads, 1u << 14);
-    insert_points<<<grid, kThreads, 0, stream>>>(table, points, batch_indices, rows, active_rows, g, keys, status);
+    insert_points<<<grid, kThreads, 0, stream>>>(table, src, rows, active_rows, slots);
     LATTICE_LAUNCH_CHECK();
-    flag_points<<<grid, kThreads, 0, stream>>>(table, keys, rows, flags);
+    flag_points<<<grid, kThreads, 0, stream>>>(table, slots, rows, flags);
     LATTICE_LAUNCH_CHECK();
     rc = exclusive_scan(flags, positions, rows, voxel_count, ws, stream);
     if (rc != LATTICE_OK) return rc;
-    place_points<<<grid, kThreads, 0, stream>>>(table, keys, rows, flags, positions, voxel_count, coords,
+    place_points<<<grid, kThreads, 0, stream>>>(table, src, slots, rows, flags, positions, voxel_count, coords,
                                                inverse_rows, counts);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
@@ -514,13 +526,14 @@ extern "C" int lattice_hip_build_point_voxel_map(const float* points, const int3
     BlockTable table;
     table.buckets = ws.take<BlockBucket>(cap);
     table.mask = static_cast<uint32_t>(cap - 1);
+    table.src = BlockSource{voxel_coords};
     LATTICE_REQUIRE(table.buckets, "point-voxel map workspace too small.");
     clear_voxel_blocks<<<grid_for(4ll * cap, kThreads, 8192), kThreads, 0, stream>>>(table.buckets, 4ll * cap,
                                                                                    status);
     LATTICE_LAUNCH_CHECK();
     if (voxel_rows > 0) {
         insert_voxel_blocks<<<grid_for(voxel_rows, kThreads, 1u << 14), kThreads, 0, stream>>>(
-            table, voxel_coords, voxel_rows, voxel_active, status);
+            table, voxel_coords, voxel_rows, voxel_active);
         LATTICE_LAUNCH_CHECK();
     }
     if (point_rows == 0) return LATTICE_OK;

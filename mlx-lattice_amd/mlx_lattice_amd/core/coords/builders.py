@@ -201,7 +201,7 @@ def build_transposed_kernel_relation(coords: torch.Tensor,
     native = _ext().build_transposed_kernel_relation_lazy(
         coords, source_active, list(kernel), list(step), list(pad),
         list(rate))
-    flags = int(native[10])
+    status = native[10]
     # can_use_direct_transposed_relation (relations.cpp:107-127)
     direct = all(step[a] > max(o[a] for o in offsets) - min(o[a] for o in offsets)
                  for a in range(3))
@@ -209,7 +209,7 @@ def build_transposed_kernel_relation(coords: torch.Tensor,
         native[:10], offsets=offsets, in_capacity=int(coords.shape[0]),
         source_coords=coords, source_active_rows=source_active, stride=step,
         padding=pad, kind='transposed',
-        repeated_edges=None if flags < 0 else bool(flags & 2),
+        repeated_edges=False if direct else status,
         direct_expansion=direct)
 
 
@@ -221,7 +221,7 @@ def _kernel_relation_from_native(
         target_active_rows: torch.Tensor | None = None,
         stride: Triple = (1, 1, 1), padding: Triple = (0, 0, 0),
         kind: RelationKind = 'forward',
-        repeated_edges: bool | None = None,
+        repeated_edges: bool | torch.Tensor | None = None,
         direct_expansion: bool = False) -> KernelRelation:
     (in_rows, out_rows, kernel_ids, row_offsets, native_out_coords, counts,
      in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids,
@@ -264,5 +264,5 @@ def _active_rows(value: torch.Tensor | None,
             raise ValueError(
                 'active_rows must have shape (1,) and int32 dtype.')
         return value
-    return torch.tensor([coords.shape[0]], dtype=torch.int32,
-                        device=coords.device)
+    return torch.full((1,), coords.shape[0], dtype=torch.int32,
+                      device=coords.device)

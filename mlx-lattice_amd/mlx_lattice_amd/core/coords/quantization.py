@@ -187,8 +187,8 @@ class _VoxelizeFeatures(torch.autograd.Function):
         q = ctx.quantization
         rows = ctx.rows
         if rows is None:
-            rows = torch.tensor([ctx.point_rows], dtype=torch.int32,
-                                device=grad_out.device)
+            rows = torch.full((1,), ctx.point_rows, dtype=torch.int32,
+                              device=grad_out.device)
         grad = _ext().voxelize_features_grad(
             grad_out.contiguous(), q.inverse_rows, q.counts, rows,
             ctx.point_rows, ctx.reduction)
@@ -280,8 +280,8 @@ def _batch_indices(value: torch.Tensor | None,
 def _active_rows(value: torch.Tensor | None,
                  like: torch.Tensor) -> torch.Tensor:
     if value is None:
-        return torch.tensor([like.shape[0]], dtype=torch.int32,
-                            device=like.device)
+        return torch.full((1,), like.shape[0], dtype=torch.int32,
+                          device=like.device)
     if tuple(value.shape) != (1,) or value.dtype != torch.int32:
         raise ValueError('active_rows must have shape (1,) and int32 dtype.')
     return value

@@ -199,9 +199,10 @@ class KernelRelation:
     sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
     transposed_sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
     # Transposed relations only: whether two edges share (out_row, kernel_id)
-    # (a repeated input coordinate), as the builder's status word reported;
-    # None when not read back.
-    repeated_edges: bool | None = None
+    # (a repeated input coordinate).  The builder hands over its device
+    # status word; it is read on the first question (dense_map_exact), so
+    # building the relation never waits for the device.  None: unknown.
+    repeated_edges: bool | torch.Tensor | None = None
     # Generative, and transposed relations whose stride exceeds the offsets'
     # extent: output row in * K + k holds the single edge (in, k).
     direct_expansion: bool = False
@@ -233,7 +234,7 @@ class KernelRelation:
         implicit_gemm: RelationImplicitGemmView | None = None,
         sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None,
         grouped_views: Callable[[], tuple] | None = None,
-        repeated_edges: bool | None = None,
+        repeated_edges: bool | torch.Tensor | None = None,
         direct_expansion: bool = False,
     ) -> None:
         """``grouped_views``, when given and the input/kernel CSR arrays are
@@ -422,6 +423,10 @@ class KernelRelation:
         row); a transposed relation does unless an input coordinate repeats."""
         if self.contract.kind != 'transposed':
             return True
+        if isinstance(self.repeated_edges, torch.Tensor):
+            # lattice_relation_flags: bit 2 = repeated (out_row, kernel_id)
+            flags = int(self.repeated_edges.item())
+            object.__setattr__(self, 'repeated_edges', bool(flags & 2))
         if self.repeated_edges is None:
             return False
         return not self.repeated_edges

@@ -56,93 +56,89 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     auto forward = [](bool with_view) {
         return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,
                            const std::vector<int>& kernel_size, const std::vector<int>& stride,
-                           const std::vector<int>& padding, const std::vector<int>& dilation, bool check_range) {
+                           const std::vector<int>& padding, const std::vector<int>& dilation) {
             auto r = ln::make_kernel_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
                                               triple_from_values(stride, "stride"),
                                               triple_from_values(padding, "padding"),
-                                              triple_from_values(dilation, "dilation"), check_range, !with_view);
+                                              triple_from_values(dilation, "dilation"), !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
     m.def("build_kernel_relation", forward(false), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
-          py::arg("check_range") = true, "Build a forward sparse kernel relation.");
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"),
+          "Build a forward sparse kernel relation.");
     m.def("build_kernel_relation_with_view", forward(true), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
-          py::arg("check_range") = true);
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"));
 
     auto subm = [](bool with_view) {
         return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,
-                           const std::vector<int>& kernel_size, const std::vector<int>& dilation, bool check_range) {
+                           const std::vector<int>& kernel_size, const std::vector<int>& dilation) {
             auto r = ln::make_submanifold_kernel_relation(coords, active_rows,
                                                           triple_from_values(kernel_size, "kernel_size"),
-                                                          triple_from_values(dilation, "dilation"), check_range, !with_view);
+                                                          triple_from_values(dilation, "dilation"), !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
     m.def("build_submanifold_kernel_relation", subm(false), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true,
+          py::arg("kernel_size"), py::arg("dilation"),
           "Build a submanifold sparse kernel relation.");
     m.def("build_submanifold_kernel_relation_with_view", subm(true), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+          py::arg("kernel_size"), py::arg("dilation"));
 
     auto target = [](bool with_view) {
         return [with_view](const at::Tensor& coords, const at::Tensor& active_rows, const at::Tensor& target_coords,
                            const at::Tensor& target_active_rows, const std::vector<int>& kernel_size,
                            const std::vector<int>& stride, const std::vector<int>& padding,
-                           const std::vector<int>& dilation, bool check_range) {
+                           const std::vector<int>& dilation) {
             auto r = ln::make_target_kernel_relation(
                 coords, active_rows, target_coords, target_active_rows,
                 triple_from_values(kernel_size, "kernel_size"), triple_from_values(stride, "stride"),
-                triple_from_values(padding, "padding"), triple_from_values(dilation, "dilation"), check_range,
-                !with_view);
+                triple_from_values(padding, "padding"), triple_from_values(dilation, "dilation"), !with_view);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
     m.def("build_target_kernel_relation", target(false), py::arg("coords"), py::arg("active_rows"),
           py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
-          py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true,
+          py::arg("padding"), py::arg("dilation"),
           "Build a target-aligned sparse kernel relation.");
     m.def("build_target_kernel_relation_with_view", target(true), py::arg("coords"), py::arg("active_rows"),
           py::arg("target_coords"), py::arg("target_active_rows"), py::arg("kernel_size"), py::arg("stride"),
-          py::arg("padding"), py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+          py::arg("padding"), py::arg("dilation"));
 
     // Generative / transposed relations.  The *_lazy variants leave the
-    // grouped views to build_relation_grouped_views and append the status
-    // flags read by the range check (-1 when not checked).
+    // grouped views to build_relation_grouped_views and append the build's
+    // device status word (int32 (1,), lattice_relation_flags).
     auto expanded = [](bool generative, bool lazy) {
         return [generative, lazy](const at::Tensor& coords, const at::Tensor& active_rows,
                                   const std::vector<int>& kernel_size, const std::vector<int>& stride,
-                                  const std::vector<int>& padding, const std::vector<int>& dilation,
-                                  bool check_range) -> py::tuple {
+                                  const std::vector<int>& padding, const std::vector<int>& dilation) -> py::tuple {
             auto r = ln::make_expanded_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
                                                 triple_from_values(stride, "stride"),
                                                 triple_from_values(padding, "padding"),
-                                                triple_from_values(dilation, "dilation"), generative, check_range,
-                                                !lazy);
+                                                triple_from_values(dilation, "dilation"), generative, !lazy);
             if (!lazy) return relation_tuple(r);
             return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
-                                  py::none(), py::none(), py::none(), py::none(), r.status_flags);
+                                  py::none(), py::none(), py::none(), py::none(), r.status);
         };
     };
     auto generative = [expanded](bool lazy) {
         auto fn = expanded(true, lazy);
         return [fn](const at::Tensor& coords, const at::Tensor& active_rows, const std::vector<int>& kernel_size,
-                    const std::vector<int>& stride, bool check_range) {
-            return fn(coords, active_rows, kernel_size, stride, {0}, {1}, check_range);
+                    const std::vector<int>& stride) {
+            return fn(coords, active_rows, kernel_size, stride, {0}, {1});
         };
     };
     m.def("build_generative_relation", generative(false), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::kw_only(), py::arg("check_range") = true,
+          py::arg("kernel_size"), py::arg("stride"),
           "Build a generative sparse kernel relation.");
     m.def("build_generative_relation_lazy", generative(true), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::kw_only(), py::arg("check_range") = true);
+          py::arg("kernel_size"), py::arg("stride"));
     m.def("build_transposed_kernel_relation", expanded(false, false), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
-          py::arg("check_range") = true, "Build a transposed sparse kernel relation.");
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"),
+          "Build a transposed sparse kernel relation.");
     m.def("build_transposed_kernel_relation_lazy", expanded(false, true), py::arg("coords"),
           py::arg("active_rows"), py::arg("kernel_size"), py::arg("stride"), py::arg("padding"),
-          py::arg("dilation"), py::kw_only(), py::arg("check_range") = true);
+          py::arg("dilation"));
 
     m.def(
         "build_relation_grouped_views",
@@ -176,9 +172,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("out_in_map"), py::arg("row_masks"),
         "Return (reorder_rows, sorted_out_in_map, sorted_kv_out_in_map, tile_masks).");
 
-    m.def(
-        "set_conv_tile_rows", [](int rows) { lattice_native::check_status(lattice_hip_set_conv_tile_rows(rows)); },
-        py::arg("rows"), "Rows of the sorted order per wavefront in the implicit-GEMM conv (32 or 64).");
     m.def("sparse_conv_features", &ln::sparse_conv_features, py::arg("feats"), py::arg("weights"),
           py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("kernel_row_offsets"),
@@ -208,7 +201,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("in_rows"), py::arg("out_rows"),
         py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("in_row_offsets"),
         py::arg("in_edge_ids"), py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("out_capacity"),
-        py::arg("n_kernels"), py::kw_only(), py::arg("store_sorted") = false, py::arg("bias") = py::none());
+        py::arg("n_kernels"), py::arg("store_sorted") = false, py::kw_only(), py::arg("bias") = py::none());
     m.def("sparse_quantized_conv_features", &ln::sparse_quantized_conv_features, py::arg("feats"),
           py::arg("weights"), py::arg("scales"), py::arg("biases"), py::arg("in_rows"), py::arg("out_rows"),
           py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("sorted_kv_out_in_map"),
@@ -244,8 +237,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("reduce"),
           "Gradient of sparse pooling with respect to the input features.");
     m.def("sparse_quantize", &ln::sparse_quantize, py::arg("points"), py::arg("batch_indices"),
-          py::arg("active_rows"), py::arg("voxel_size"), py::arg("origin"), py::kw_only(),
-          py::arg("check_range") = true, "Voxelize points: (coords, active_rows, inverse_rows, counts).");
+          py::arg("active_rows"), py::arg("voxel_size"), py::arg("origin"),
+          "Voxelize points: (coords, active_rows, inverse_rows, counts).");
     m.def("group_by_key", &ln::group_by_key, py::arg("keys"), py::arg("count"), py::arg("groups"));
     m.def("voxelize_features", &ln::voxelize_features, py::arg("feats"), py::arg("inverse_rows"),
           py::arg("counts"), py::arg("active_rows"), py::arg("reduction"));
@@ -255,8 +248,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("counts"), py::arg("active_rows"), py::arg("point_rows"), py::arg("reduction"));
     m.def("build_point_voxel_map", &ln::build_point_voxel_map, py::arg("points"), py::arg("batch_indices"),
           py::arg("point_active_rows"), py::arg("voxel_coords"), py::arg("voxel_active_rows"),
-          py::arg("voxel_size"), py::arg("origin"), py::arg("interpolation"), py::kw_only(),
-          py::arg("check_range") = true);
+          py::arg("voxel_size"), py::arg("origin"), py::arg("interpolation"));
     m.def("interpolate_point_features", &ln::interpolate_point_features, py::arg("voxel_feats"), py::arg("rows"),
           py::arg("weights"));
     m.def("interpolate_point_features_grad", &ln::interpolate_point_features_grad, py::arg("point_grad"),

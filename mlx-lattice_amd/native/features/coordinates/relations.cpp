@@ -43,18 +43,6 @@ void validate_nonnegative(const Triple& v, const char* name) {
     }
 }
 
-// Raises when a builder flagged an active coordinate that does not fit the
-// packed key (reads one device word; the only host wait of a build).
-int check_coordinate_range(const at::Tensor& status) {
-    const int32_t flags = status.item<int32_t>();
-    if (flags & LATTICE_STATUS_COORD_RANGE) {
-        throw std::invalid_argument(
-            "coordinates exceed the GPU packed-key range: batch must lie in [0, 1022] and x, y, z in "
-            "[-131072, 131071].");
-    }
-    return flags;
-}
-
 NativeKernelRelation allocate(const at::Tensor& like, int out_capacity, int in_capacity, int K, bool coords,
                               bool views) {
     const int64_t edges = static_cast<int64_t>(out_capacity) * K;
@@ -110,7 +98,7 @@ std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation) {
 
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool check_range, bool with_views) {
+                                          bool with_views) {
     validate_coords(coords_in);
     validate_active_rows(active_rows);
     validate_positive(kernel_size, "kernel_size");
@@ -129,21 +117,19 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
                                                    stride.data(), padding.data(), dilation.data(), &o,
                                                    ws.data_ptr(), static_cast<size_t>(ws.numel()),
                                                    current_stream(coords)));
-    if (check_range) check_coordinate_range(status);
+    r.status = status;
     return r;
 }
 
 NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
-                                                      Triple kernel_size, Triple dilation, bool check_range,
-                                                      bool with_views) {
-    return make_kernel_relation(coords, active_rows, kernel_size, {1, 1, 1}, {0, 0, 0}, dilation, check_range,
-                                with_views);
+                                                      Triple kernel_size, Triple dilation, bool with_views) {
+    return make_kernel_relation(coords, active_rows, kernel_size, {1, 1, 1}, {0, 0, 0}, dilation, with_views);
 }
 
 NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                                  const at::Tensor& target_in, const at::Tensor& target_active_rows,
                                                  Triple kernel_size, Triple stride, Triple padding,
-                                                 Triple dilation, bool check_range, bool with_views) {
+                                                 Triple dilation, bool with_views) {
     validate_coords(coords_in);
     validate_coords(target_in, "target_coords");
     validate_active_rows(active_rows);
@@ -171,13 +157,13 @@ NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords_in, co
         ci32(coords), rows, ci32(active_rows), ci32(target), target_rows, ci32(target_active_rows),
         kernel_size.data(), stride.data(), padding.data(), dilation.data(), &o, ws.data_ptr(),
         static_cast<size_t>(ws.numel()), current_stream(coords)));
-    if (check_range) check_coordinate_range(status);
+    r.status = status;
     return r;
 }
 
 NativeKernelRelation make_expanded_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                             Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                            bool generative, bool check_range, bool with_views) {
+                                            bool generative, bool with_views) {
     validate_coords(coords_in);
     validate_active_rows(active_rows);
     validate_positive(kernel_size, "kernel_size");
@@ -236,7 +222,7 @@ NativeKernelRelation make_expanded_relation(const at::Tensor& coords_in, const a
             ci32(coords), rows, ci32(active_rows), kernel_size.data(), stride.data(), padding.data(),
             dilation.data(), &o, ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream(coords)));
     }
-    if (check_range) r.status_flags = check_coordinate_range(status);
+    r.status = status;
     return r;
 }
 
@@ -300,7 +286,6 @@ std::tuple<at::Tensor, at::Tensor> make_relation_implicit_gemm_view(
         ci32(source), source_rows, ci32(source_active_rows), ci32(output), output_rows,
         ci32(output_active_rows), ci32(offsets), K, stride.data(), padding.data(), i32(out_in_map),
         i32(row_masks), i32(status), ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream(source)));
-    check_coordinate_range(status);
     return {out_in_map, row_masks};
 }
 

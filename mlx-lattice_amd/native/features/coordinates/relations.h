@@ -27,36 +27,35 @@ struct NativeKernelRelation {
     // Dense implicit-GEMM view computed by the same query pass.
     at::Tensor out_in_map;
     at::Tensor row_masks;
-    // lattice_relation_flags of the build when it was read back (check_range),
-    // else -1.
-    int status_flags = -1;
+    // The build's device status word (lattice_relation_flags), left on the
+    // device: nothing in a build waits for the device.
+    at::Tensor status;
 };
 
 std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation);
 
-// check_range: read the device status word after the build and raise when an
-// active coordinate does not fit the packed key (one host wait).
+// Builds never read device memory back: every int32 coordinate is accepted.
 // with_views: also build the grouped CSR views (otherwise their tensors
 // stay undefined and make_relation_grouped_views builds them on demand).
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool check_range = true, bool with_views = true);
+                                          bool with_views = true);
 
 NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                                       Triple kernel_size, Triple dilation,
-                                                      bool check_range = true, bool with_views = true);
+                                                      bool with_views = true);
 
 NativeKernelRelation make_target_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                                  const at::Tensor& target_coords,
                                                  const at::Tensor& target_active_rows, Triple kernel_size,
                                                  Triple stride, Triple padding, Triple dilation,
-                                                 bool check_range = true, bool with_views = true);
+                                                 bool with_views = true);
 
 // Generative (generative = true; padding and dilation ignored) and
 // transposed relations: output and edge capacities rows * K, no dense view.
 NativeKernelRelation make_expanded_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                             Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                            bool generative, bool check_range = true, bool with_views = true);
+                                            bool generative, bool with_views = true);
 
 // (in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids)
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> make_relation_grouped_views(

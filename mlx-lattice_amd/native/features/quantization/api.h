@@ -16,7 +16,7 @@ namespace lattice_native {
 // a voxel coordinate does not fit the packed key (one host read).
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_quantize(
     const at::Tensor& points, const at::Tensor& batch_indices, const at::Tensor& active_rows,
-    const std::vector<float>& voxel_size, const std::vector<float>& origin, bool check_range = true);
+    const std::vector<float>& voxel_size, const std::vector<float>& origin);
 
 // Stable grouping of keys by value: (offsets [groups + 1], ids [n]); keys
 // outside [0, groups) and positions at or past *count are left out.
@@ -36,7 +36,7 @@ at::Tensor voxelize_features_grad(const at::Tensor& cotangent, const at::Tensor&
 std::tuple<at::Tensor, at::Tensor> build_point_voxel_map(
     const at::Tensor& points, const at::Tensor& batch_indices, const at::Tensor& point_active_rows,
     const at::Tensor& voxel_coords, const at::Tensor& voxel_active_rows, const std::vector<float>& voxel_size,
-    const std::vector<float>& origin, const std::string& interpolation, bool check_range = true);
+    const std::vector<float>& origin, const std::string& interpolation);
 at::Tensor interpolate_point_features(const at::Tensor& voxel_feats, const at::Tensor& rows,
                                       const at::Tensor& weights);
 at::Tensor interpolate_point_features_grad(const at::Tensor& point_grad, const at::Tensor& weights,

@@ -46,19 +46,11 @@ int reduction_code(const std::string& r) {
     throw std::invalid_argument("reduction must be 'sum' or 'mean'.");
 }
 
-void check_range(const at::Tensor& status) {
-    if (status.item<int32_t>() & LATTICE_STATUS_COORD_RANGE) {
-        throw std::invalid_argument(
-            "voxel coordinates exceed the GPU packed-key range: batch must lie in [0, 1022] and x, y, z in "
-            "[-131072, 131071].");
-    }
-}
-
 }  // namespace
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_quantize(
     const at::Tensor& points_in, const at::Tensor& batches_in, const at::Tensor& active_rows,
-    const std::vector<float>& voxel_size, const std::vector<float>& origin, bool check) {
+    const std::vector<float>& voxel_size, const std::vector<float>& origin) {
     validate_points(points_in);
     const int64_t rows = points_in.size(0);
     validate_batches(batches_in, rows);
@@ -84,7 +76,6 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_quantize(
                                              size.data(), org.data(), i32(coords), i32(count), i32(inverse),
                                              i32(counts), i32(status), ws.data_ptr(),
                                              static_cast<size_t>(ws.numel()), current_stream(points)));
-    if (check) check_range(status);
     return {coords, count, inverse, counts};
 }
 
@@ -166,7 +157,7 @@ at::Tensor voxelize_features_grad(const at::Tensor& cot_in, const at::Tensor& in
 std::tuple<at::Tensor, at::Tensor> build_point_voxel_map(
     const at::Tensor& points_in, const at::Tensor& batches_in, const at::Tensor& point_active_rows,
     const at::Tensor& voxel_coords_in, const at::Tensor& voxel_active_rows, const std::vector<float>& voxel_size,
-    const std::vector<float>& origin, const std::string& interpolation, bool check) {
+    const std::vector<float>& origin, const std::string& interpolation) {
     int mode;
     if (interpolation == "nearest") {
         mode = 0;
@@ -203,7 +194,6 @@ std::tuple<at::Tensor, at::Tensor> build_point_voxel_map(
         voxel_rows, ci32(voxel_active_rows), size.data(), org.data(), mode, i32(out_rows),
         weights.data_ptr<float>(), i32(status), ws.data_ptr(), static_cast<size_t>(ws.numel()),
         current_stream(points)));
-    if (check) check_range(status);
     return {out_rows, weights};
 }
 

@@ -199,6 +199,47 @@ def test_sparse_quantize_matches_oracle(size, origin, n, active):
     np.testing.assert_array_equal(to_np(q.counts), ref['counts'])
 
 
+def test_sparse_quantize_full_domain():
+    """Voxels anywhere in int64 and batches anywhere in int32: deduplicated
+    on their int64 value, written as int32 (write_coords); the point map
+    over those voxels matches the oracle too."""
+    ops, _ = _ops()
+    rng = np.random.default_rng(107)
+    scales = np.array([1e3, 6.5e4, 1e6, 2.1e9, -3e9, 1e12, -5e15],
+                      np.float64)
+    n = 7000
+    # one magnitude per point (so about half the points have voxels inside
+    # int32 that the point map can find), a random sign per axis
+    centre = (scales[rng.integers(0, len(scales), (n, 1))]
+              * rng.choice([-1.0, 1.0], (n, 3)))
+    pts = (centre + rng.standard_normal((n, 3)) * 3.0).astype(np.float32)
+    b = rng.choice(np.array([0, 1, 1022, 1023, 5000, -3, 2**31 - 1],
+                            np.int64), n).astype(np.int32)
+    pts[n // 2] = pts[3]
+    b[n // 2] = b[3]
+    print('quantize full domain', flush=True)
+    q = ops.sparse_quantize(_f(pts), 0.5, batch_indices=_i(b))
+    torch.cuda.synchronize()
+    ref = O.sparse_quantize(pts, 0.5, batch_indices=b)
+    assert to_np(q.active_rows).tolist() == ref['active_rows'].tolist()
+    np.testing.assert_array_equal(to_np(q.coords), ref['coords'])
+    np.testing.assert_array_equal(to_np(q.inverse_rows), ref['inverse_rows'])
+    np.testing.assert_array_equal(to_np(q.counts), ref['counts'])
+    n_vox = int(ref['active_rows'][0])
+    for interpolation in ('nearest', 'linear'):
+        pmap = ops.build_point_voxel_map(_f(pts), q.coords, q.active_rows,
+                                         0.5, batch_indices=_i(b),
+                                         interpolation=interpolation)
+        torch.cuda.synchronize()
+        rows, w = O.point_voxel_map(pts, ref['coords'], n_vox, 0.5,
+                                    batch_indices=b,
+                                    interpolation=interpolation)
+        np.testing.assert_array_equal(to_np(pmap.rows), rows)
+        np.testing.assert_array_equal(to_np(pmap.weights), w)
+        # the probes do find voxels (400 nearest, 3062 linear hits)
+        assert (rows >= 0).sum() >= (400 if interpolation == 'nearest' else 3000)
+
+
 @pytest.mark.parametrize('reduction', ['sum', 'mean'])
 def test_voxelize_matches_oracle(reduction):
     ops, _ = _ops()

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_relation_equal, golden, native_relation_dict, to_np
+from helpers import (assert_relation_equal, extreme_cloud, golden,
+                     native_relation_dict, to_np)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -226,13 +227,61 @@ def test_duplicates_negative_and_batches():
         assert_relation_equal(actual, expected, check_coords=False)
 
 
-def test_coordinate_range_is_rejected():
-    coords = np.array([[0, 0, 0, 0], [0, 200000, 0, 0]], np.int32)
-    with pytest.raises(ValueError, match='packed-key range'):
-        gpu_forward(coords)
-    coords = np.array([[1023, 0, 0, 0]], np.int32)
-    with pytest.raises(ValueError, match='packed-key range'):
-        gpu_forward(coords)
+@pytest.mark.parametrize('geom', [
+    dict(kernel_size=3),
+    dict(kernel_size=2, stride=2),
+    dict(kernel_size=3, stride=2, padding=1),
+    dict(kernel_size=3, dilation=2),
+    dict(kernel_size=(3, 1, 2), stride=(1, 3, 2)),
+])
+def test_full_int32_domain_forward(geom):
+    """Coordinates anywhere in int32 (the reference hashes all four words,
+    cpu/common_detail.h:68-107): bit-exact against the oracle."""
+    coords = extreme_cloud(71)
+    check_forward(coords, **geom)
+    check_forward(coords, active=len(coords) - 37, **geom)
+
+
+@pytest.mark.parametrize('geom', [dict(kernel_size=3),
+                                  dict(kernel_size=2, stride=2)])
+def test_full_int32_domain_target(geom):
+    coords = extreme_cloud(72)
+    target = extreme_cloud(73)[:400]
+    print(f'target relation extreme domain {geom}', flush=True)
+    actual = gpu_target(coords, target, **geom)
+    expected = O.target_kernel_relation(coords, target, **geom)
+    assert_relation_equal(actual, expected, check_coords=False)
+
+
+def test_full_int32_domain_through_the_operators():
+    """subm_conv3d and a k2s2 conv3d over an extreme-domain cloud: the
+    relations behind the operators match the oracle's, and so do the
+    features (fp32, rtol 1e-3)."""
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor
+
+    coords = extreme_cloud(74)
+    rng = np.random.default_rng(74)
+    feats = rng.standard_normal((len(coords), 8)).astype(np.float32)
+    w = (rng.standard_normal((16, 3, 3, 3, 8)) * 0.2).astype(np.float32)
+    x = SparseTensor(_t(coords), torch.as_tensor(feats).to(DEV))
+    out = ops.subm_conv3d(x, torch.as_tensor(w).to(DEV), kernel_size=3)
+    rel = O.kernel_relation(coords, kernel_size=3)
+    ref = O.conv_features_fp64(feats, O.mapped_weight(w.astype(np.float64)),
+                               rel)
+    got = out.feats.cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-4)
+    w2 = (rng.standard_normal((8, 2, 2, 2, 8)) * 0.2).astype(np.float32)
+    down = ops.conv3d(x, torch.as_tensor(w2).to(DEV), kernel_size=2, stride=2)
+    rel2 = O.kernel_relation(coords, kernel_size=2, stride=2)
+    n = int(rel2['counts'][1])
+    assert int(down.active_rows.item()) == n
+    np.testing.assert_array_equal(down.coords[:n].cpu().numpy(),
+                                  rel2['out_coords'][:n])
+    ref2 = O.conv_features_fp64(feats, O.mapped_weight(w2.astype(np.float64)),
+                                rel2)
+    np.testing.assert_allclose(down.feats[:n].cpu().numpy(), ref2[:n],
+                               rtol=1e-3, atol=1e-4)
 
 
 def test_range_edges_are_exact():

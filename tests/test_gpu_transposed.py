@@ -16,7 +16,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_relation_equal, golden, native_relation_dict, to_np
+from helpers import (assert_relation_equal, extreme_cloud, golden,
+                     native_relation_dict, to_np)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -169,6 +170,32 @@ def test_transposed_relation_matches_oracle(ks, stride, pad, dil, dup):
     np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
 
 
+@pytest.mark.parametrize('ks,stride,pad,dil', [(2, 2, 0, 1), (3, 2, 0, 1),
+                                                (3, 1, 1, 1), (3, 4, 0, 2)])
+@pytest.mark.parametrize('unique', [False, True])
+def test_transposed_relation_full_int32_domain(ks, stride, pad, dil, unique):
+    """Inputs anywhere in int32; candidates coord * stride + offset leave
+    int32 and are written as int32 (low 32 bits), as the reference's
+    write_coords does with its int64 candidates."""
+    coords = extreme_cloud(81)
+    if unique:
+        coords = np.unique(coords, axis=0)
+        coords = coords[np.random.default_rng(82).permutation(len(coords))]
+    active = len(coords) - 9
+    print(f'transposed extreme k{ks} s{stride} p{pad} d{dil} unique={unique}',
+          flush=True)
+    native = _ext().build_transposed_kernel_relation(
+        _t(coords), _active(active), _triple(ks), _triple(stride),
+        _triple(pad), _triple(dil))
+    torch.cuda.synchronize()
+    got = native_relation_dict(native)
+    ref = O.transposed_kernel_relation(coords, active, kernel_size=ks,
+                                       stride=stride, padding=pad,
+                                       dilation=dil)
+    assert_relation_equal(got, ref)
+    np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
+
+
 @pytest.mark.parametrize('ks,stride', [(2, 2), (3, 2), ((1, 2, 3), 1)])
 def test_generative_relation_matches_oracle(ks, stride):
     rng = np.random.default_rng(60)
@@ -191,10 +218,10 @@ def test_empty_and_repeated_edge_flag():
     coords = np.unique(coords, axis=0)
     rel = build_transposed_kernel_relation(_t(coords), kernel_size=3,
                                            stride=2)
-    assert rel.repeated_edges is False and rel.dense_map_exact
+    assert rel.dense_map_exact and rel.repeated_edges is False
     dup = np.concatenate([coords, coords[:1]])
     rel = build_transposed_kernel_relation(_t(dup), kernel_size=3, stride=2)
-    assert rel.repeated_edges is True and not rel.dense_map_exact
+    assert not rel.dense_map_exact and rel.repeated_edges is True
     rel = build_transposed_kernel_relation(_t(dup), kernel_size=2, stride=2)
     assert not rel.repeated_edges   # direct: one output row per candidate
     empty = build_transposed_kernel_relation(
