@@ -336,6 +336,24 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of the entry above: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops or harnesses that forbid hipMalloc): the
+ * longest-first tile schedule lives in a library-owned device array of
+ * 128 KiB per GPU (kept until the process ends), so the call allocates
+ * nothing and takes no workspace.  out_capacity must not exceed
+ * LATTICE_NOALLOC_CONV_MAX_ROWS (LATTICE_ERROR_INVALID_ARGUMENT otherwise).
+ * The calling thread's current device must be the stream's.  Calls that
+ * overlap on one GPU share the array and race; serialise them (one stream,
+ * or events).  Results are bit-identical to the entry above. */
+#define LATTICE_NOALLOC_CONV_MAX_ROWS 2097088
+int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
+    int dtype, const void* feats, int n_in, int c_in, const void* weights,
+    int weight_layout, int kernel_count, int c_out,
+    const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
+    void* stream);
+
 /* Conv over a direct generative / transposed relation (output row
  * in * K + k holds the single edge (in, k); lattice_hip_build_generative_relation
  * and the direct case of lattice_hip_build_transposed_kernel_relation):

@@ -21,7 +21,9 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
+#include <string>
 #include <type_traits>
 
 #include "lattice_common.h"
@@ -1405,6 +1407,60 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                 tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
                                 static_cast<const __bf16*>(bias), stream);
+}
+
+// ------------------------------------------------- allocation-free entry --
+//
+// The tile schedule of lattice_hip_sparse_conv_features_sorted_implicit_gemm
+// for callers that cannot allocate (code under graph capture, serving loops
+// that forbid hipMalloc): a file-scope device array of kMaxScheduledTiles
+// ints (128 KiB), one copy per GPU, resident until the process ends.  Its
+// address on each device is taken once, with the device current, through
+// hipGetSymbolAddress; in host code the array's own name is only a
+// host-side stand-in and is never passed to a kernel.  schedule_tiles
+// writes every entry a launch reads, so nothing needs clearing.  Calls that
+// overlap on one GPU share the array and race.
+
+namespace lattice {
+namespace {
+
+static __device__ __align__(256) int32_t scratch[kMaxScheduledTiles];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<int32_t*> g_scratch_ptr[kMaxScratchDevices];
+
+int scratch_on_current_device(int32_t** ptr) {
+    int device = 0;
+    LATTICE_HIP_TRY(hipGetDevice(&device));
+    LATTICE_REQUIRE(device >= 0 && device < kMaxScratchDevices, "device index out of range for the conv scratch.");
+    int32_t* p = g_scratch_ptr[device].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        LATTICE_HIP_TRY(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)));
+        g_scratch_ptr[device].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return LATTICE_OK;
+}
+
+}  // namespace
+}  // namespace lattice
+
+extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
+    int dtype, const void* feats, int n_in, int c_in, const void* weights, int weight_layout, int kernel_count,
+    int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
+    int out_capacity, void* out, const void* bias, void* stream_ptr) {
+    LATTICE_REQUIRE(out_capacity <= LATTICE_NOALLOC_CONV_MAX_ROWS,
+                    "out_capacity exceeds the allocation-free conv's limit of " +
+                        std::to_string(LATTICE_NOALLOC_CONV_MAX_ROWS) +
+                        " rows; use lattice_hip_sparse_conv_features_sorted_implicit_gemm with a workspace.");
+    static_assert(static_cast<size_t>(LATTICE_NOALLOC_CONV_MAX_ROWS) / 64 + 1 <= kMaxScheduledTiles,
+                  "the scratch holds the schedule of the largest allowed launch");
+    int32_t* schedule = nullptr;
+    const int rc = scratch_on_current_device(&schedule);
+    if (rc != LATTICE_OK) return rc;
+    return lattice_hip_sparse_conv_features_sorted_implicit_gemm(
+        dtype, feats, n_in, c_in, weights, weight_layout, kernel_count, c_out, sorted_kv_out_in_map, tile_masks,
+        reorder_rows, out_capacity, out, bias, schedule, sizeof(scratch), stream_ptr);
 }
 
 extern "C" int lattice_hip_sparse_quantized_conv_features(
