@@ -154,38 +154,176 @@ insert_rows(CoordTable table, const int32_t* __restrict__ coords, int rows,
 }
 
 // ---------------------------------------------- strided output planning --
+//
+// First-seen placement of the output cells: a flag per input row (the row
+// is its cell's first row), the flag count of every 64-row group (one
+// wave: rows 64g .. 64g + 63), one scan of the group counts
+// (scan_block_totals, which also writes the cell count), and a scatter in
+// which each wave ranks its flags with a ballot.  Grid-stride loops step
+// by whole blocks, so a wave always holds one aligned 64-row group.
+
+// Writes the flag count of the calling wave's 64-row group.
+__device__ inline void write_group_total(bool flag, long long i, int32_t* group_totals) {
+    const uint64_t b = ballot(flag);
+    if (lane_id() == 0) group_totals[i >> 6] = __popcll(b);
+}
+
+// Output row of a flagged input row: its group's offset plus its rank
+// among the group's flags.
+__device__ inline int group_position(bool flag, long long i, const int32_t* group_offsets) {
+    const uint64_t b = ballot(flag);
+    return group_offsets[i >> 6] + lanes_below(b);
+}
 
 // flags[i] = 1 when input row i is the first row of its floor-divided cell.
 __global__ void __launch_bounds__(kThreads)
 flag_cell_representatives(CoordTable cells, const int32_t* __restrict__ coords, int rows,
                           const int32_t* __restrict__ active_rows, Int3 cell,
-                          int32_t* __restrict__ flags) {
+                          int32_t* __restrict__ flags, int32_t* __restrict__ group_totals) {
     const int active = min(max(*active_rows, 0), rows);
     const CellSource src{coords, cell};
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        flags[i] = i < active && cells.find(src.table_key_of(i), src) == i ? 1 : 0;
+        const bool flag = i < active && cells.find(src.table_key_of(i), src) == i;
+        flags[i] = flag ? 1 : 0;
+        write_group_total(flag, i, group_totals);
     }
 }
 
 // Scatters representative cells to their first-seen position; zero tail.
 __global__ void __launch_bounds__(kThreads)
 scatter_cells(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ flags,
-              const int32_t* __restrict__ positions, const int32_t* __restrict__ counts,
+              const int32_t* __restrict__ group_offsets, const int32_t* __restrict__ counts,
               Int3 cell, int32_t* __restrict__ out_coords) {
     const int n_out = counts[1];
     int4* out = reinterpret_cast<int4*>(out_coords);
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
-        if (flags[i]) {
+        const bool flag = flags[i] != 0;
+        const int pos = group_position(flag, i, group_offsets);
+        if (flag) {
             int4 c = load_coord(coords, i);
             int4 q;
             q.x = c.x;
             q.y = static_cast<int>(floor_div_pos(c.y, cell.x));
             q.z = static_cast<int>(floor_div_pos(c.z, cell.y));
             q.w = static_cast<int>(floor_div_pos(c.w, cell.z));
-            out[positions[i]] = q;
+            out[pos] = q;
         }
         if (i >= n_out) out[i] = make_int4(0, 0, 0, 0);
     }
+}
+
+// ------------------------------------------- 2x2x2 stride-2 downsample --
+//
+// kernel_size = stride = 2, no padding, unit dilation: the cell of a voxel
+// is floor(v / 2) per axis, which is exactly the 2x2x2 block the block
+// table buckets by, and offset k = 4 dx + 2 dy + dz of output cell X is the
+// voxel 2X + (dx, dy, dz), i.e. octant k of that block.  So the input rows'
+// block table alone gives the downsample (no cell table): a cell's first
+// row is the minimum of its bucket's eight first rows, and its map row is
+// the bucket's eight rows in order.
+
+// Decoded first row of a bucket entry (-1 when absent).
+__device__ inline int32_t bucket_row(int32_t raw) { return raw == 0 ? -1 : kRowBias - raw; }
+
+// flags[i] = 1 when input row i is its cell's first row; buckets[i] = its
+// cell's bucket.
+__global__ void __launch_bounds__(kThreads)
+flag_block_representatives(BlockTable table, const int32_t* __restrict__ coords, int rows,
+                           const int32_t* __restrict__ active_rows, int32_t* __restrict__ flags,
+                           int32_t* __restrict__ buckets, int32_t* __restrict__ group_totals) {
+    const int active = min(max(*active_rows, 0), rows);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
+        int flag = 0, bucket = -1;
+        if (i < active) {
+            const int4 c = load_coord(coords, i);
+            TableKey key;
+            int octant;
+            block_of(c.x, c.y, c.z, c.w, &key, &octant);
+            bucket = table.find_bucket(key);  // present: row i inserted it
+            const int4* r = reinterpret_cast<const int4*>(table.buckets + bucket);
+            const int4 lo = r[0], mid = r[1];
+            const int2 hi = *reinterpret_cast<const int2*>(r + 2);
+            // stored rows are kRowBias - row (0 = absent): the first row of
+            // the cell is the largest stored value
+            const int32_t top = max(max(max(lo.z, lo.w), max(mid.x, mid.y)), max(max(mid.z, mid.w), max(hi.x, hi.y)));
+            flag = bucket_row(top) == i ? 1 : 0;
+        }
+        flags[i] = flag;
+        buckets[i] = bucket;
+        write_group_total(flag != 0, i, group_totals);
+    }
+}
+
+// Places each cell at its first-seen position: out_coords (zero tail) and
+// the cell's bucket (out_buckets, -1 tail).
+__global__ void __launch_bounds__(kThreads)
+scatter_block_cells(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ flags,
+                    const int32_t* __restrict__ group_offsets, const int32_t* __restrict__ buckets,
+                    const int32_t* __restrict__ counts, int32_t* __restrict__ out_coords,
+                    int32_t* __restrict__ out_buckets) {
+    const int n_out = counts[1];
+    int4* out = reinterpret_cast<int4*>(out_coords);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) {
+        const bool flag = flags[i] != 0;
+        const int pos = group_position(flag, i, group_offsets);
+        if (flag) {
+            const int4 c = load_coord(coords, i);
+            out[pos] = make_int4(c.x, c.y >> 1, c.z >> 1, c.w >> 1);
+            out_buckets[pos] = buckets[i];
+        }
+        if (i >= n_out) {
+            out[i] = make_int4(0, 0, 0, 0);
+            out_buckets[i] = -1;
+        }
+    }
+}
+
+// Map query of the 2x2x2 stride-2 downsample: one lane per output row
+// copies its cell's bucket rows to out_in_map (K = 8) and writes the row
+// mask and degree; per-block degree totals feed the row-offset scan, as in
+// query_map.
+__global__ void __launch_bounds__(kWave)
+query_map_blocks(BlockTable table, const int32_t* __restrict__ out_buckets, int out_capacity,
+                 int32_t* __restrict__ out_in_map, int32_t* __restrict__ row_masks, int32_t* __restrict__ degrees,
+                 int32_t* __restrict__ block_totals) {
+    const int lane = lane_id();
+    const long long row = static_cast<long long>(blockIdx.x) * kWave + lane;  // kQueryRows rows per block
+    int degree = 0;
+    if (row < out_capacity) {
+        const int32_t b = out_buckets[row];
+        int v[8];
+        if (b >= 0) {
+            const int4* r = reinterpret_cast<const int4*>(table.buckets + b);
+            const int4 lo = r[0], mid = r[1];
+            const int2 hi = *reinterpret_cast<const int2*>(r + 2);
+            v[0] = bucket_row(lo.z);
+            v[1] = bucket_row(lo.w);
+            v[2] = bucket_row(mid.x);
+            v[3] = bucket_row(mid.y);
+            v[4] = bucket_row(mid.z);
+            v[5] = bucket_row(mid.w);
+            v[6] = bucket_row(hi.x);
+            v[7] = bucket_row(hi.y);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = -1;
+        }
+        uint32_t mask = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            mask |= v[k] >= 0 ? 1u << k : 0u;
+        }
+        degree = __popc(mask);
+        int4* dst = reinterpret_cast<int4*>(out_in_map + row * 8);
+        dst[0] = make_int4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_int4(v[4], v[5], v[6], v[7]);
+        row_masks[row] = static_cast<int32_t>(mask);
+        degrees[row] = degree;
+    }
+    int sum = degree;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    if (lane == 0) block_totals[blockIdx.x] = sum;
 }
 
 // Identity output support: out_coords = active prefix of coords, zero tail.
@@ -211,6 +349,7 @@ struct QueryArgs {
     int32_t* row_masks;          // [out_capacity, words]
     int32_t* degrees;            // [out_capacity] or null
     int32_t* block_totals;       // [ceil(out_capacity / kQueryRows)] or null
+    const int32_t* out_buckets;  // 2x2x2 stride-2 downsample: bucket of each output cell, else null
 };
 
 template <int kLanes>
@@ -719,7 +858,10 @@ int query_blocks(int out_capacity) { return (out_capacity + kQueryRows - 1) / kQ
 int launch_query(const QueryArgs& a, hipStream_t stream) {
     if (a.out_capacity <= 0) return LATTICE_OK;
     const unsigned blocks = static_cast<unsigned>(query_blocks(a.out_capacity));
-    if (is_unit_k3(a)) {
+    if (a.out_buckets != nullptr) {
+        query_map_blocks<<<blocks, kWave, 0, stream>>>(a.table, a.out_buckets, a.out_capacity, a.out_in_map,
+                                                       a.row_masks, a.degrees, a.block_totals);
+    } else if (is_unit_k3(a)) {
         query_map_k3<<<blocks, kWave, 0, stream>>>(a);
     } else if (a.geom.volume <= 32) {
         query_map<32><<<blocks, kThreads, 0, stream>>>(a);
@@ -742,6 +884,15 @@ int launch_emit(const int32_t* map, int out_capacity, int K, const int32_t* bloc
                                                         out->row_offsets, out->in_rows, out->out_rows,
                                                         out->kernel_ids);
     }
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+// Exclusive scan of the flag counts of the 64-row groups of `rows` rows;
+// *total (device) receives the sum.  rows == 0 writes a zero total.
+int scan_groups(const int32_t* group_totals, int rows, int32_t* group_offsets, int32_t* total, hipStream_t stream) {
+    if (rows <= 0) return fill_i32(total, 1, 0, stream);
+    scan_block_totals<<<1, kBlockScanThreads, 0, stream>>>(group_totals, query_blocks(rows), group_offsets, total);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -888,24 +1039,51 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     if (identity) {
         q.out_coords = coords;
         q.out_active = out->counts + 1;
+    } else if (kernel_size[0] == 2 && kernel_size[1] == 2 && kernel_size[2] == 2 && stride[0] == 2 &&
+               stride[1] == 2 && stride[2] == 2 && padding[0] == 0 && padding[1] == 0 && padding[2] == 0 &&
+               dilation[0] == 1 && dilation[1] == 1 && dilation[2] == 1) {
+        // 2x2x2 stride-2 downsample: the cells are the block table's buckets.
+        int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
+        int32_t* buckets = ws.take<int32_t>(std::max(rows, 1));
+        int32_t* out_buckets = ws.take<int32_t>(std::max(rows, 1));
+        int32_t* group_totals = ws.take<int32_t>(query_blocks(rows) + 1);
+        int32_t* group_offsets = ws.take<int32_t>(query_blocks(rows) + 1);
+        LATTICE_REQUIRE(flags && buckets && out_buckets && group_totals && group_offsets,
+                        "relation workspace too small.");
+        if (rows > 0) {
+            flag_block_representatives<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
+                table, coords, rows, active_rows, flags, buckets, group_totals);
+            LATTICE_LAUNCH_CHECK();
+        }
+        rc = scan_groups(group_totals, rows, group_offsets, out->counts + 1, stream);
+        if (rc != LATTICE_OK) return rc;
+        if (rows > 0) {
+            scatter_block_cells<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
+                coords, rows, flags, group_offsets, buckets, out->counts, out->out_coords, out_buckets);
+            LATTICE_LAUNCH_CHECK();
+        }
+        q.out_coords = out->out_coords;
+        q.out_active = out->counts + 1;
+        q.out_buckets = out_buckets;
     } else {
         const Int3 cell{stride[0], stride[1], stride[2]};
         CoordTable cells;
         rc = build_table(coords, rows, active_rows, cell, ws, stream, &cells);
         if (rc != LATTICE_OK) return rc;
         int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
-        int32_t* positions = ws.take<int32_t>(std::max(rows, 1));
-        LATTICE_REQUIRE(flags != nullptr && positions != nullptr, "relation workspace too small.");
+        int32_t* group_totals = ws.take<int32_t>(query_blocks(rows) + 1);
+        int32_t* group_offsets = ws.take<int32_t>(query_blocks(rows) + 1);
+        LATTICE_REQUIRE(flags && group_totals && group_offsets, "relation workspace too small.");
         if (rows > 0) {
             flag_cell_representatives<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
-                cells, coords, rows, active_rows, cell, flags);
+                cells, coords, rows, active_rows, cell, flags, group_totals);
             LATTICE_LAUNCH_CHECK();
         }
-        rc = exclusive_scan(flags, positions, rows, out->counts + 1, ws, stream);
+        rc = scan_groups(group_totals, rows, group_offsets, out->counts + 1, stream);
         if (rc != LATTICE_OK) return rc;
         if (rows > 0) {
             scatter_cells<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(
-                coords, rows, flags, positions, out->counts, cell, out->out_coords);
+                coords, rows, flags, group_offsets, out->counts, cell, out->out_coords);
             LATTICE_LAUNCH_CHECK();
         }
         q.out_coords = out->out_coords;
