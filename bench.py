@@ -35,8 +35,10 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per conv_igemm launch on this workload, from rocprofv3 FETCH_SIZE
 # and WRITE_SIZE passes scaled by a 1 GiB copy's counter readings
-# (profiles/config3_kernel_traffic.md).  Re-measure when the kernel changes.
-CONV_TRAFFIC_BYTES = 1.1997e9
+# (profiles/config3_kernel_traffic.md), valid for the kernel source whose
+# SHA-256 prefix is given: when csrc/conv.hip changes, the bench reports
+# traffic as null until the counters are measured again.
+CONV_TRAFFIC = {'bytes': 1.2009e9, 'conv_hip_sha256': '92ca61491dedffb4'}
 
 
 def parse_args():
@@ -52,6 +54,10 @@ def parse_args():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-secondary', action='store_true',
                    help='skip the timings of configs 2, 4 and 5')
+    p.add_argument('--phase', choices=('all', 'config3', 'secondary'),
+                   default='all',
+                   help='config3: only the headline step (for profiler '
+                        'runs); secondary: only configs 2, 4 and 5')
     return p.parse_args()
 
 
@@ -71,17 +77,46 @@ def make_workload():
     return coords, feats, weight
 
 
-def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int):
+def host_cpu() -> dict:
+    """The host's CPU model (lscpu's "Model name", read from
+    /proc/cpuinfo), its hardware thread count and the threads this process
+    may run on."""
+    model = 'unknown'
+    try:
+        with open('/proc/cpuinfo') as fh:
+            for line in fh:
+                if line.lower().startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {'model': model, 'hardware_threads': os.cpu_count() or 1,
+            'usable_threads': usable}
+
+
+def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int,
+                 repeats: int = 3):
     """Reference CPU route (oracle restatement, eval_typed with per-FMA fp16
     rounding for 128->128) on the first ``sample_rows`` output rows, plus the
-    single-threaded relation build on the full cloud."""
+    single-threaded relation build on the full cloud; each timed
+    ``repeats`` times, the median reported (BASELINE.md's protocol)."""
+    import statistics
+
     import numpy as np
 
     from oracle import oracle
 
-    t0 = time.perf_counter()
-    rel = oracle.kernel_relation(coords, kernel_size=3)
-    t_map = time.perf_counter() - t0
+    t_maps = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        rel = oracle.kernel_relation(coords, kernel_size=3)
+        t_maps.append(time.perf_counter() - t0)
+    t_map = statistics.median(t_maps)
+    host = host_cpu()
     hw = oracle.hardware_concurrency()
     threads = max(1, min(threads, hw))
     n = min(sample_rows, len(coords))
@@ -91,21 +126,32 @@ def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int):
     sample = dict(rel)
     sample['counts'] = np.array([rel['counts'][0], n], np.int32)
     e_sample = int(rel['row_offsets'][n])
-    t0 = time.perf_counter()
-    oracle.conv_features(feats, weight, sample, out_capacity=n, threads=threads)
-    t_conv = time.perf_counter() - t0
+    t_convs = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        oracle.conv_features(feats, weight, sample, out_capacity=n,
+                             threads=threads)
+        t_convs.append(time.perf_counter() - t0)
+    t_conv = statistics.median(t_convs)
     flops = 2.0 * e_sample * 128 * 128
     return {
         'value': round(flops / t_conv / 1e12, 6),
         'unit': 'TFLOP/s',
         'cores': workers,
         'kind': 'port',
-        'sample': (f'reference CPU route restated (oracle/lattice_oracle.cpp):'
-                   f' relation build on all {len(coords)} rows single-thread '
-                   f'({t_map * 1e3:.1f} ms), conv on the first {n} output '
-                   f'rows ({e_sample} edges, {t_conv:.2f} s, '
-                   f'{n / t_conv / 1e6:.4f} Mvoxels/s), host has {hw} '
-                   f'hardware threads'),
+        'workers': workers,
+        'host_cpu': host['model'],
+        'host_hardware_threads': host['hardware_threads'],
+        'host_usable_threads': host['usable_threads'],
+        'repeats': repeats,
+        'sample': (f'reference CPU route restated (oracle/lattice_oracle.cpp)'
+                   f' on {host["model"]} ({host["hardware_threads"]} hardware'
+                   f' threads, {host["usable_threads"]} usable): relation '
+                   f'build on all {len(coords)} rows, one thread (median of '
+                   f'{repeats}: {t_map * 1e3:.1f} ms); conv on the first {n} '
+                   f'output rows ({e_sample} edges) with {workers} worker '
+                   f'threads (median of {repeats}: {t_conv:.2f} s, '
+                   f'{n / t_conv / 1e6:.4f} Mvoxels/s)'),
         'map_build_ms': round(t_map * 1e3, 3),
         'mvoxels_per_s': round(n / t_conv / 1e6, 6),
     }
@@ -153,7 +199,7 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
     dev = torch.device('cuda:0')
     out = {}
 
-    def layer(coords, feats, run, c_in, c_out, workload):
+    def layer(coords, feats, run, c_in, c_out, k, workload, weight_bytes):
         x = SparseTensor(coords, feats)
         y = run(x)
         torch.cuda.synchronize()
@@ -161,17 +207,38 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
         relation = next(iter(rel.values()))
         edges = int(relation.counts[0].item())
         n_out = int(relation.counts[1].item())
+        cap = int(y.feats.shape[0])
         layer_ms = _timed(lambda: run(SparseTensor(coords, feats)), steps,
                           warmup)
         conv_ms = _timed(lambda: run(x), steps, warmup)
         del y
+        flops = 2.0 * edges * c_in * c_out
+        # algorithmic bytes of the matrix-core conv: input rows once, every
+        # capacity output row written once (fp16), the weight, and the
+        # sorted view it reads (k-major map, reorder rows, tile masks)
+        nbytes = (int(coords.shape[0]) * c_in * 2 + cap * c_out * 2
+                  + weight_bytes + 4 * k * cap + 4 * cap + 16 * (cap // 64 + 1))
+        tflops = flops / conv_ms / 1e9
+        gbs = nbytes / conv_ms / 1e6
+        hbm_bound = flops / nbytes < PEAK_FP16_TFLOPS / PEAK_HBM_GBS * 1e3
         return {
             'workload': workload,
             'voxels_in': int(coords.shape[0]), 'voxels_out': n_out,
             'edges': edges,
             'layer_ms': round(layer_ms, 4), 'conv_ms': round(conv_ms, 4),
-            'tflops': round(2.0 * edges * c_in * c_out / conv_ms / 1e9, 3),
+            'tflops': round(tflops, 3),
             'mvoxels_per_s': round(n_out / conv_ms / 1e3, 3),
+            'roofline': {
+                'bound': 'hbm' if hbm_bound else 'mfma',
+                'achieved': round(gbs if hbm_bound else tflops, 3),
+                'peak': PEAK_HBM_GBS if hbm_bound else PEAK_FP16_TFLOPS,
+                'unit': 'GB/s' if hbm_bound else 'TFLOP/s',
+                'frac': round(gbs / PEAK_HBM_GBS if hbm_bound
+                              else tflops / PEAK_FP16_TFLOPS, 4),
+                'algorithmic_bytes': nbytes,
+                'flops': flops,
+                'interval': 'conv_ms (operator call on a cached relation)',
+            },
         }
 
     rng = config_rng(2)
@@ -182,7 +249,8 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
                           * np.sqrt(2.0 / (8 * 64))).astype(np.float16)).to(dev)
     out['config2'] = layer(
         c2, f2, lambda x: ops.conv3d(x, w2, kernel_size=2, stride=2), 64, 128,
-        'conv3d k=2 s=2 fp16 64->128, 2 x ~100k LiDAR-like voxels')
+        8, 'conv3d k=2 s=2 fp16 64->128, 2 x ~100k LiDAR-like voxels',
+        8 * 64 * 128 * 2)
 
     rng = config_rng(4)
     c4 = torch.as_tensor(sphere_shell_cloud(200000, 256, rng=rng)).to(dev)
@@ -193,8 +261,10 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
     q4 = quantize_weight(w4, group_size=32, bits=4)
     out['config4'] = layer(
         c4, f4, lambda x: ops.subm_conv3d(x, q4, kernel_size=3), 64, 64,
-        'QuantizedConv3d subm k=3 int4 g32 fp16 64->64, 200k sphere-shell '
-        'voxels')
+        27, 'QuantizedConv3d subm k=3 int4 g32 fp16 64->64, 200k sphere-shell '
+        'voxels',
+        # int4 codes + fp16 scales and biases per 32-channel group
+        27 * 64 * 64 // 2 + 2 * 2 * 27 * (64 // 32) * 64)
 
     rng = config_rng(5)
     c5 = torch.as_tensor(lidar_cloud(120000, 4, rng=rng)).to(dev)
@@ -454,30 +524,54 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
     }
 
 
-def map_build_roofline(n: int, edges: int, relation_ms: float) -> dict:
-    """Algorithmic HBM bytes of the submanifold kernel-map build (hash build
-    + map: query, dense map, masks, edges, row offsets, counts) against
-    8 TB/s, with the per-unit figures of the hot-path survey:
+def relation_bytes(n: int, edges: int) -> int:
+    """Algorithmic HBM bytes of the submanifold relation (hash build + map:
+    query, dense map, masks, edges, row offsets, counts), with the per-unit
+    figures of the hot-path survey:
       hash: 16 B coords read + 12 B per insert + 8 B per table slot cleared
         (capacity next_pow2(2N));
       map: 16 B coords + 12 B per probe (K per row) + 4 B per dense-map
-        entry + 12 B per edge + 4 B per row offset + 8 B of counts.
-    The sorted view is not part of this figure (its own kernels are listed
-    in the profile)."""
+        entry + 12 B per edge + 4 B per row offset + 8 B of counts."""
     cap = 1
     while cap < 2 * n:
         cap <<= 1
     k = 27
     b_hash = 16 * n + 12 * n + 8 * cap
     b_map = 16 * n + 12 * k * n + 4 * k * n + 12 * edges + 4 * (n + 1) + 8
-    gbs = (b_hash + b_map) / (relation_ms * 1e-3) / 1e9
+    return b_hash + b_map
+
+
+def sorted_view_bytes(n: int) -> int:
+    """Algorithmic HBM bytes of the mask-sorted view: the stable sort of the
+    row masks (a (key, index) pair, 8 B, read and written per row for each
+    of its ceil(27 / 9) = 3 digit passes) and the gather (4 B order + 4 B
+    mask + 4 K B map row read, 4 K B k-major map written per row, plus the
+    tile quarter masks)."""
+    k = 27
+    return 3 * 16 * n + n * (8 + 8 * k) + 4 * ((n + 63) // 64) * 4
+
+
+def hbm_roofline(nbytes: int, ms: float) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
     return {
-        'bytes': b_hash + b_map,
-        'ms': round(relation_ms, 4),
+        'bytes': nbytes,
+        'ms': round(ms, 4),
         'gbs': round(gbs, 1),
         'peak_gbs': PEAK_HBM_GBS,
         'frac': round(gbs / PEAK_HBM_GBS, 4),
     }
+
+
+def conv_traffic():
+    """CONV_TRAFFIC's bytes while csrc/conv.hip is the source they were
+    measured on, else None."""
+    import hashlib
+
+    src = ROOT / 'mlx-lattice_amd' / 'csrc' / 'conv.hip'
+    sha = hashlib.sha256(src.read_bytes()).hexdigest()[:16]
+    if CONV_TRAFFIC['conv_hip_sha256'] != sha:
+        return None, sha
+    return CONV_TRAFFIC['bytes'], sha
 
 
 def main() -> int:
@@ -492,6 +586,9 @@ def main() -> int:
 
     from mlx_lattice_amd._native import ext
 
+    if args.phase == 'secondary':
+        print(json.dumps({'secondary': secondary_workloads()}), flush=True)
+        return 0
     coords_np, feats_np, weight_np = make_workload()
     dev = torch.device('cuda:0')
     coords = torch.as_tensor(coords_np).to(dev)
@@ -544,6 +641,7 @@ def main() -> int:
     flops = 2.0 * edges * 128 * 128
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
     map_ms = rel_ms + view_ms
+    traffic, conv_sha = conv_traffic()
     del out
 
     record = {
@@ -571,7 +669,12 @@ def main() -> int:
         },
         'mvoxels_per_s': round(n_out / (conv_ms * 1e-3) / 1e6, 3),
         'kernel_map_build_ms': round(map_ms, 4),
-        'kernel_map_hbm': map_build_roofline(n_out, edges, rel_ms),
+        # the whole map build (relation + sorted view), the interval of
+        # kernel_map_build_ms, and its two parts
+        'kernel_map_hbm': hbm_roofline(
+            relation_bytes(n_out, edges) + sorted_view_bytes(n_out), map_ms),
+        'relation_hbm': hbm_roofline(relation_bytes(n_out, edges), rel_ms),
+        'sorted_view_hbm': hbm_roofline(sorted_view_bytes(n_out), view_ms),
         'relation_ms': round(rel_ms, 4),
         'sorted_view_ms': round(view_ms, 4),
         'conv_ms': round(conv_ms, 4),
@@ -581,10 +684,17 @@ def main() -> int:
             'peak': PEAK_FP16_TFLOPS,
             'unit': 'TFLOP/s',
             'frac': round(conv_tflops / PEAK_FP16_TFLOPS, 5),
-            'traffic': CONV_TRAFFIC_BYTES,
+            'traffic': traffic,
+            'traffic_source': ('rocprofv3 FETCH_SIZE + WRITE_SIZE, '
+                               'profiles/config3_kernel_traffic.md'
+                               if traffic is not None else
+                               f'not measured for conv.hip {conv_sha}'),
             'kernel': 'conv_igemm<f16, IgemmShape<128 cols, 32-row waves, 4 waves, 64-channel stages, A via LDS>, FloatB>',
         },
     }
+    if args.phase == 'config3':
+        print(json.dumps(record), flush=True)
+        return 0
     record['backward'] = backward_workload(feats, weight, coords, active,
                                            edges, args.steps, args.warmup)
     record['pooling'] = pooling_workload(coords, args.steps, args.warmup)

@@ -815,6 +815,9 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
                 V b[S::CB];
                 read_b_step<T, S>(b, brow, st, c.lane, lr);
                 mfma_step<T, S>(acc, af, b, st);
+                // Scheduling hint: interleave this step's LDS fragment reads
+                // with its MFMAs (measured 6% faster on the 128-column shape).
+                __builtin_amdgcn_iglp_opt(1);
             }
         }
     }

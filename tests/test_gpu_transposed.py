@@ -170,6 +170,39 @@ def test_transposed_relation_matches_oracle(ks, stride, pad, dil, dup):
     np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
 
 
+@pytest.mark.parametrize('ks,stride,pad,dil', GEOMS)
+@pytest.mark.parametrize('dup', [False, True])
+def test_transposed_relation_dense_cloud_matches_oracle(ks, stride, pad, dil,
+                                                        dup):
+    """The same geometries on a dense cloud (2000 rows in 3 x 14^3 cells):
+    most candidates coincide with another row's, so the cross-row part of
+    the tiled resolve (representative minimum, member counts, ranks) is
+    exercised on nearly every output row."""
+    rng = np.random.default_rng(150 + dup)
+    coords = _cloud(rng, 2000, 7, dup)
+    if not dup:
+        coords = np.unique(coords, axis=0)
+        coords = coords[rng.permutation(len(coords))]
+    active = len(coords) - 40
+    print(f'transposed dense k{ks} s{stride} p{pad} d{dil} dup={dup}',
+          flush=True)
+    native = _ext().build_transposed_kernel_relation(
+        _t(coords), _active(active), _triple(ks), _triple(stride),
+        _triple(pad), _triple(dil))
+    torch.cuda.synchronize()
+    got = native_relation_dict(native)
+    ref = O.transposed_kernel_relation(coords, active, kernel_size=ks,
+                                       stride=stride, padding=pad,
+                                       dilation=dil)
+    assert_relation_equal(got, ref)
+    np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
+    # dense: candidates of different rows share output rows (except in the
+    # direct layout, one output row per candidate)
+    k3, s3, d3 = _triple(ks), _triple(stride), _triple(dil)
+    direct = all(s3[a] > (k3[a] - 1) * d3[a] for a in range(3))
+    assert direct or int(ref['counts'][1]) < int(ref['counts'][0])
+
+
 @pytest.mark.parametrize('ks,stride,pad,dil', [(2, 2, 0, 1), (3, 2, 0, 1),
                                                 (3, 1, 1, 1), (3, 4, 0, 2)])
 @pytest.mark.parametrize('unique', [False, True])
