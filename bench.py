@@ -6,7 +6,9 @@ Kaiming-normal weight, synthetic data (seeded).
 
 One step = one pass of the hot path over the batch, inputs resident in HBM:
   1. kernel-map build: coordinate hash + submanifold relation (edges, CSR
-     views, dense out_in_map / row masks) + mask-sorted implicit-GEMM view;
+     views, dense out_in_map / row masks) + mask-sorted implicit-GEMM view
+     with its longest-first tile order (kept with the view, as the
+     operator path keeps it);
   2. the implicit-GEMM convolution on the matrix cores.
 Each phase is bracketed by HIP events on the stream the kernels run on.
 
@@ -603,14 +605,18 @@ def main() -> int:
         return native
 
     def sorted_view(native):
-        return ext.build_sorted_implicit_gemm_view(native[10], native[11])
+        # The sorted view with its tile order, as the operator path keeps
+        # them (RelationSortedImplicitGemmView.tile_order): computed once per
+        # view, reused by every conv over it.
+        view = ext.build_sorted_implicit_gemm_view(native[10], native[11])
+        return view + (ext.conv_tile_order(view[3], n_out),)
 
     def conv(native, view):
-        reorder, smap, kv, tiles = view
+        reorder, smap, kv, tiles, order = view
         return ext.sparse_conv_features_sorted_implicit_gemm(
             feats, weight, smap, kv, reorder, tiles, native[0], native[1],
             native[2], native[5], native[3], native[6], native[7], native[8],
-            native[9], n_out, 27)
+            native[9], n_out, 27, tile_order=order)
 
     for _ in range(args.warmup):
         native = map_build()
@@ -636,7 +642,19 @@ def main() -> int:
 
     rel_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
     view_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
-    conv_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    conv_in_step_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    # The GEMM phase on its own: the same conv launched back to back over
+    # the last step's resident map and view, so the interval holds the
+    # kernels and not the host's launch gaps between the steps' phases.
+    c0 = torch.cuda.Event(enable_timing=True)
+    c1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    c0.record(stream)
+    for _ in range(args.steps):
+        out = conv(native, view)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    conv_ms = c0.elapsed_time(c1) / args.steps
     edges = int(native[5][0].item())
     flops = 2.0 * edges * 128 * 128
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
@@ -678,6 +696,7 @@ def main() -> int:
         'relation_ms': round(rel_ms, 4),
         'sorted_view_ms': round(view_ms, 4),
         'conv_ms': round(conv_ms, 4),
+        'conv_in_step_ms': round(conv_in_step_ms, 4),
         'roofline': {
             'bound': 'mfma',
             'achieved': round(conv_tflops, 4),

@@ -327,8 +327,21 @@ int lattice_hip_sparse_conv_features(
  * rows the kernel addresses with 32-bit offsets).  weights: (C_out, Kx, Ky,
  * Kz, C_in).  workspace (optional, lattice_hip_conv_workspace_bytes) holds
  * the launch's tile schedule: with it, row tiles run longest-first; with
- * NULL they run in order.  The result does not depend on the schedule. */
+ * NULL they run in order.  The result does not depend on the schedule.
+ * When workspace_bytes carries LATTICE_CONV_ORDER_READY, the workspace
+ * already holds the order lattice_hip_conv_tile_order wrote for the same
+ * tile_masks and out_capacity, and the call only reads it (no schedule
+ * launch): a caller that keeps the sorted view keeps its order with it. */
+#define LATTICE_CONV_ORDER_READY ((size_t)1 << 63)
 size_t lattice_hip_conv_workspace_bytes(int out_capacity);
+/* Longest-first order of the 128-row tiles of a sorted view (the cost of a
+ * tile is the number of offsets its rows use), into `order`
+ * (lattice_hip_conv_workspace_bytes(out_capacity) bytes).  No counterpart
+ * in the reference: it lets a caller compute the matrix-core conv's tile
+ * schedule once per sorted view instead of once per conv call. */
+int lattice_hip_conv_tile_order(const int32_t* tile_masks, int out_capacity,
+                                int32_t* order, size_t order_bytes,
+                                void* stream);
 int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out,

@@ -1164,6 +1164,7 @@ int launch_expand(const T* feats, int n_in, const int32_t* active, int c_in, con
 // order.
 constexpr int kScheduleThreads = 1024;
 constexpr int kMaxScheduledTiles = 32768;
+constexpr int kOrderTileRows = 128;  // rows of the tiles a tile order ranks
 
 template <int QUARTERS>
 __global__ void __launch_bounds__(kScheduleThreads)
@@ -1206,7 +1207,8 @@ schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, in
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
-                       T* out, const T* bias, hipStream_t stream, int out_ld = S::C_OUT, bool scheduled = false) {
+                       T* out, const T* bias, hipStream_t stream, bool scheduled, int out_ld = S::C_OUT) {
+    static_assert(S::BLOCK_ROWS == kOrderTileRows, "every shape uses the tile order's 128-row tiles");
     const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
     if (blocks > kMaxScheduledTiles) schedule = nullptr;
     if (schedule != nullptr && !scheduled) {
@@ -1235,12 +1237,12 @@ template <typename T> PackedB<T> column_half(const PackedB<T>& b, int co_base) {
 
 template <typename T, typename BSource>
 int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
-                 const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, T* out,
-                 const T* bias, hipStream_t stream) {
+                 const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, bool ready,
+                 T* out, const T* bias, hipStream_t stream) {
     if (rows <= 0) return LATTICE_OK;
 #define LATTICE_IGEMM_LAUNCH(...) \
     launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, \
-                                                   schedule, out, bias, stream)
+                                                   schedule, out, bias, stream, ready)
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
@@ -1266,8 +1268,8 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
         for (int h = 0; h < 2; ++h) {
             const int rc = launch_igemm_shape<T, S128>(feats, n_in, c_in, column_half(b, h * 128), kv_map,
                                                       tile_masks, reorder_rows, rows, schedule, out + h * 128,
-                                                      bias != nullptr ? bias + h * 128 : nullptr, stream, 256,
-                                                      h == 1);
+                                                      bias != nullptr ? bias + h * 128 : nullptr, stream,
+                                                      ready || h == 1, 256);
             if (rc != LATTICE_OK) return rc;
         }
         return LATTICE_OK;
@@ -1282,13 +1284,19 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 
 // Workspace of the matrix-core conv: the tile schedule, one int per row
 // tile (tiles are at least 64 rows).  NULL workspace = tiles in order.
+// With LATTICE_CONV_ORDER_READY in workspace_bytes the workspace already
+// holds the order (lattice_hip_conv_tile_order) and is only read.
 size_t conv_schedule_bytes(int rows) { return (static_cast<size_t>(std::max(rows, 0)) / 64 + 1) * sizeof(int32_t); }
 
-int conv_schedule(void* workspace, size_t workspace_bytes, int rows, int32_t** schedule) {
+int conv_schedule(void* workspace, size_t workspace_bytes, int rows, int32_t** schedule, bool* ready) {
     *schedule = nullptr;
+    *ready = false;
     if (workspace == nullptr) return LATTICE_OK;
+    const bool given = (workspace_bytes & LATTICE_CONV_ORDER_READY) != 0;
+    workspace_bytes &= ~static_cast<size_t>(LATTICE_CONV_ORDER_READY);
     LATTICE_REQUIRE(workspace_bytes >= conv_schedule_bytes(rows), "conv workspace too small.");
     *schedule = static_cast<int32_t*>(workspace);
+    *ready = given;
     return LATTICE_OK;
 }
 
@@ -1312,6 +1320,20 @@ int check_dtype(int dtype) {
 using namespace lattice;
 
 extern "C" size_t lattice_hip_conv_workspace_bytes(int out_capacity) { return conv_schedule_bytes(out_capacity); }
+
+extern "C" int lattice_hip_conv_tile_order(const int32_t* tile_masks, int out_capacity, int32_t* order,
+                                           size_t order_bytes, void* stream_ptr) {
+    LATTICE_REQUIRE(out_capacity >= 0, "out_capacity must be nonnegative.");
+    LATTICE_REQUIRE(order != nullptr && (tile_masks != nullptr || out_capacity == 0),
+                    "tile order pointers must be non-null.");
+    LATTICE_REQUIRE(order_bytes >= conv_schedule_bytes(out_capacity), "tile order buffer too small.");
+    const int blocks = (out_capacity + kOrderTileRows - 1) / kOrderTileRows;
+    if (blocks == 0 || blocks > kMaxScheduledTiles) return LATTICE_OK;  // such launches run tiles in order
+    schedule_tiles<kOrderTileRows / 16><<<1, kScheduleThreads, 0, as_stream(stream_ptr)>>>(tile_masks, out_capacity,
+                                                                                         blocks, order);
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
 
 extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, int n_in, int c_in,
                                                 const void* weights, int weight_layout, int kernel_count,
@@ -1395,7 +1417,8 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     LATTICE_REQUIRE(sorted_kv_out_in_map && tile_masks && out && weights && (feats || n_in == 0),
                     "conv pointers must be non-null.");
     int32_t* schedule = nullptr;
-    rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule);
+    bool ready = false;
+    rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule, &ready);
     if (rc != LATTICE_OK) return rc;
     hipStream_t stream = as_stream(stream_ptr);
     const long long s_co = static_cast<long long>(kernel_count) * c_in;
@@ -1403,12 +1426,12 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     if (dtype == LATTICE_F16) {
         FloatB<_Float16> b{static_cast<const _Float16*>(weights), s_co, s_k};
         return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                      tile_masks, reorder_rows, out_capacity, schedule,
+                                      tile_masks, reorder_rows, out_capacity, schedule, ready,
                                       static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
     }
     FloatB<__bf16> b{static_cast<const __bf16*>(weights), s_co, s_k};
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
+                                tile_masks, reorder_rows, out_capacity, schedule, ready, static_cast<__bf16*>(out),
                                 static_cast<const __bf16*>(bias), stream);
 }
 
@@ -1490,19 +1513,20 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const bool sorted = sorted_kv_out_in_map != nullptr && tile_masks != nullptr && reorder_rows != nullptr;
     if (sorted && dtype != LATTICE_F32 && igemm_shape_ok(n_in, c_in, c_out, kernel_count)) {
         int32_t* schedule = nullptr;
-        rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule);
+        bool ready = false;
+        rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule, &ready);
         if (rc != LATTICE_OK) return rc;
         if (dtype == LATTICE_F16) {
             PackedB<_Float16> b{weights, static_cast<const _Float16*>(scales), static_cast<const _Float16*>(biases),
                                 packed_words, groups, group_size, c_out, bits};
             return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                          tile_masks, reorder_rows, out_capacity, schedule,
+                                          tile_masks, reorder_rows, out_capacity, schedule, ready,
                                           static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
         }
         PackedB<__bf16> b{weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases),
                           packed_words, groups, group_size, c_out, bits};
         return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
-                                    tile_masks, reorder_rows, out_capacity, schedule, static_cast<__bf16*>(out),
+                                    tile_masks, reorder_rows, out_capacity, schedule, ready, static_cast<__bf16*>(out),
                                     static_cast<const __bf16*>(bias), stream);
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");

@@ -93,6 +93,8 @@ class RelationSortedImplicitGemmView:
     sorted_kv_out_in_map: torch.Tensor
     reorder_rows: torch.Tensor
     tile_masks: torch.Tensor
+    _tile_order: torch.Tensor | None = field(default=None, compare=False,
+                                             repr=False)
 
     def __post_init__(self) -> None:
         if self.sorted_out_in_map.ndim != 2:
@@ -111,6 +113,17 @@ class RelationSortedImplicitGemmView:
                 self.sorted_out_in_map.shape[0]):
             raise ValueError(
                 'reorder_rows must have one row per sorted_out_in_map row.')
+
+    def tile_order(self) -> torch.Tensor:
+        """Longest-first order of the view's 128-row tiles for the
+        matrix-core conv, computed on first use and kept with the view so
+        repeated convs over it skip their per-call schedule."""
+        if self._tile_order is None:
+            from mlx_lattice_amd._native import ext
+
+            object.__setattr__(self, '_tile_order', ext.conv_tile_order(
+                self.tile_masks, int(self.reorder_rows.shape[0])))
+        return self._tile_order
 
 
 @dataclass(frozen=True, slots=True)

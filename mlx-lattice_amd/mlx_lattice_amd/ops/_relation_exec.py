@@ -160,7 +160,7 @@ def sparse_conv_input_grad_from_relation(cot: torch.Tensor,
             cot, _transposed_weight(weight), view.sorted_out_in_map,
             view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
             None, None, None, None, None, None, None, None, None,
-            in_capacity, relation.n_kernels)
+            in_capacity, relation.n_kernels, tile_order=view.tile_order())
     input_csr = relation.input_csr
     return ext.sparse_conv_input_grad(
         cot, weight, relation.edges.out_rows, relation.edges.kernel_ids,
@@ -228,7 +228,7 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
         relation.edges.kernel_ids, relation.counts,
         relation.output_csr.row_offsets, None, None, None, None,
         relation.n_out_capacity, relation.n_kernels,
-        store_sorted=store_sorted, bias=bias)
+        store_sorted=store_sorted, bias=bias, tile_order=view.tile_order())
 
 
 def sparse_quantized_conv_features_from_relation(
@@ -243,6 +243,7 @@ def sparse_quantized_conv_features_from_relation(
         raise ValueError('quantized weight kernel rows must match the relation.')
     device = feats.device
     kv = reorder = tiles = _empty_i32(device)
+    order = None
     if _matrix_core_eligible(feats.dtype, weight.in_channels,
                              weight.out_channels, relation,
                              int(feats.shape[0])):
@@ -250,6 +251,7 @@ def sparse_quantized_conv_features_from_relation(
         kv = view.sorted_kv_out_in_map
         reorder = view.reorder_rows
         tiles = view.tile_masks
+        order = view.tile_order()
     return ext.sparse_quantized_conv_features(
         feats, weight.weight, weight.scales, weight.biases,
         relation.edges.in_rows, relation.edges.out_rows,
@@ -257,7 +259,7 @@ def sparse_quantized_conv_features_from_relation(
         relation.output_csr.row_offsets, kv, reorder, tiles,
         relation.n_out_capacity, relation.n_kernels, weight.in_channels,
         weight.out_channels, weight.storage_in_channels, weight.group_size,
-        weight.bits, bias=bias)
+        weight.bits, bias=bias, tile_order=order)
 
 
 def sparse_pool_features_from_relation(feats: torch.Tensor,

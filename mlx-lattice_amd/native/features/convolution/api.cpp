@@ -186,12 +186,33 @@ at::Tensor sparse_conv_features_expand(const at::Tensor& feats_in, const at::Ten
     return out;
 }
 
+// The matrix-core conv's tile schedule: the caller's precomputed order
+// (conv_tile_order, flagged LATTICE_CONV_ORDER_READY), or a fresh workspace
+// the conv fills itself.
+at::Tensor schedule_workspace(const std::optional<at::Tensor>& tile_order, int out_capacity, const at::Tensor& like,
+                              size_t* bytes) {
+    const size_t need = lattice_hip_conv_workspace_bytes(out_capacity);
+    if (tile_order.has_value()) {
+        const at::Tensor& t = *tile_order;
+        if (t.dim() != 1 || t.scalar_type() != at::kInt || !t.is_contiguous() ||
+            static_cast<size_t>(t.numel()) * sizeof(int32_t) < need) {
+            throw std::invalid_argument("tile_order must be the contiguous int32 order conv_tile_order returned.");
+        }
+        require_device(t, "tile_order");
+        *bytes = need | LATTICE_CONV_ORDER_READY;
+        return t;
+    }
+    *bytes = need;
+    return workspace(need, like);
+}
+
 at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in, const at::Tensor& weights_in,
                                                      const at::Tensor& sorted_out_in_map,
                                                      const at::Tensor& sorted_kv_out_in_map,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                                      int out_capacity, int n_kernels, bool store_sorted,
-                                                     const std::optional<at::Tensor>& bias) {
+                                                     const std::optional<at::Tensor>& bias,
+                                                     const std::optional<at::Tensor>& tile_order) {
     const char* op = "sparse_conv_features_sorted_implicit_gemm";
     if (sorted_out_in_map.dim() != 2 || sorted_out_in_map.scalar_type() != at::kInt) {
         throw std::invalid_argument("sorted_out_in_map must have shape (N_out, K) and int32 dtype.");
@@ -223,8 +244,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     const at::Tensor kv = sorted_kv_out_in_map.contiguous();
     const at::Tensor tiles = tile_masks.contiguous();
     const at::Tensor order = reorder_rows.contiguous();
-    const size_t ws_bytes = lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity));
-    at::Tensor ws = workspace(ws_bytes, feats);
+    size_t ws_bytes = 0;
+    at::Tensor ws = schedule_workspace(tile_order, out_capacity, feats, &ws_bytes);
     at::Tensor bias_keep;
     const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
@@ -235,6 +256,19 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     return out;
 }
 
+at::Tensor conv_tile_order(const at::Tensor& tile_masks, int out_capacity) {
+    require_i32_vector(tile_masks, "tile_masks must have shape (ceil(N_out / 64) * 4,) and int32 dtype.");
+    if (out_capacity < 0 || tile_masks.size(0) != ((out_capacity + 63) / 64) * 4) {
+        throw std::invalid_argument("tile_masks length must match ceil(out_capacity / 64) * 4.");
+    }
+    require_device(tile_masks, "tile_masks");
+    const at::Tensor tiles = tile_masks.contiguous();
+    const size_t bytes = lattice_hip_conv_workspace_bytes(out_capacity);
+    at::Tensor order = empty_i32({static_cast<int64_t>(bytes / sizeof(int32_t))}, tiles);
+    check_status(lattice_hip_conv_tile_order(ci32(tiles), out_capacity, i32(order), bytes, current_stream(tiles)));
+    return order;
+}
+
 at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::Tensor& weights_in,
                                           const at::Tensor& scales_in, const at::Tensor& biases_in,
                                           const at::Tensor& in_rows, const at::Tensor& out_rows,
@@ -243,7 +277,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
                                           const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits,
-                                          const std::optional<at::Tensor>& bias) {
+                                          const std::optional<at::Tensor>& bias,
+                                          const std::optional<at::Tensor>& tile_order) {
     if (out_capacity < 0 || n_kernels <= 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
     }
@@ -313,8 +348,9 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
         tiles = tile_masks.contiguous();
     }
     at::Tensor out = at::empty({out_capacity, out_channels}, feats.options());
-    const size_t ws_bytes = has_plan ? lattice_hip_conv_workspace_bytes(static_cast<int>(out_capacity)) : 0;
-    at::Tensor ws = workspace(ws_bytes, feats);
+    size_t ws_bytes = 0;
+    at::Tensor ws;
+    if (has_plan) ws = schedule_workspace(tile_order, out_capacity, feats, &ws_bytes);
     at::Tensor bias_keep;
     const void* b = bias_ptr(bias, feats, out_channels, &bias_keep);
     check_status(lattice_hip_sparse_quantized_conv_features(

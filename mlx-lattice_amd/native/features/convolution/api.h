@@ -35,7 +35,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, co
                                                      const at::Tensor& sorted_kv_out_in_map,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                                      int out_capacity, int n_kernels, bool store_sorted,
-                                                     const std::optional<at::Tensor>& bias = std::nullopt);
+                                                     const std::optional<at::Tensor>& bias = std::nullopt,
+                                                     const std::optional<at::Tensor>& tile_order = std::nullopt);
 
 at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Tensor& weights,
                                           const at::Tensor& scales, const at::Tensor& biases,
@@ -45,7 +46,13 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits,
-                                          const std::optional<at::Tensor>& bias = std::nullopt);
+                                          const std::optional<at::Tensor>& bias = std::nullopt,
+                                          const std::optional<at::Tensor>& tile_order = std::nullopt);
+
+// Longest-first order of the 128-row tiles of a sorted view
+// (lattice_hip_conv_tile_order), kept with the view and passed back as
+// `tile_order` so the conv skips its per-call schedule.
+at::Tensor conv_tile_order(const at::Tensor& tile_masks, int out_capacity);
 
 // Gradients (the reference conv primitive's vjp, primitive.cpp:137-176):
 // input gradient over the input-grouped CSR, (in_capacity, C_in) in the

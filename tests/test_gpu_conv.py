@@ -379,6 +379,17 @@ def test_tile_schedule_does_not_change_results():
             qouts.append(out)
         torch.cuda.synchronize()
         assert torch.equal(qouts[0], qouts[1]), c_out
+        # A tile order computed once (lattice_hip_conv_tile_order) and passed
+        # back with LATTICE_CONV_ORDER_READY gives the same bits.
+        order = ext.conv_tile_order(tiles, n)
+        ready = ctypes.c_size_t(wsb | (1 << 63)).value
+        out = torch.empty((n, c_out), dtype=torch.float16, device=DEV)
+        assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27,
+                           c_out, kv.data_ptr(), tiles.data_ptr(),
+                           reorder.data_ptr(), n, out.data_ptr(), None,
+                           order.data_ptr(), ready, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, outs[0]), c_out
     # a workspace that is too small is an argument error, not a fault
     out = torch.empty((n, 128), dtype=torch.float16, device=DEV)
     assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27, 128,
