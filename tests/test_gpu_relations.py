@@ -425,3 +425,28 @@ def test_python_relation_views_on_demand():
                                       expected['kernel_row_offsets'])
         np.testing.assert_array_equal(to_np(rel.kernel_edge_ids)[:e],
                                       expected['kernel_edge_ids'][:e])
+
+
+@pytest.mark.parametrize('n,groups,valid', [(3_000_000, 5000, 2_900_000),
+                                            (4_200_000, 2**26, 4_200_000),
+                                            (5000, 70000, 4000)])
+def test_group_by_key_large_sorts(n, groups, valid):
+    """The device radix sort at edge-list sizes (up to 2,051 tiles of 2048
+    items, one to three digit passes), through the stable grouping: the ids
+    are numpy's stable argsort of the keys, with keys outside [0, groups)
+    and positions at or past the count left out (sorted past the groups)."""
+    rng = np.random.default_rng(n % 97)
+    keys = rng.integers(-3, groups, size=n).astype(np.int32)
+    keys[: n // 3] = keys[n // 3: 2 * (n // 3)]   # long runs of equal keys
+    print(f'group_by_key n={n} groups={groups}', flush=True)
+    offsets, ids = _ext().group_by_key(_t(keys), _active(valid), groups)
+    torch.cuda.synchronize()
+    k = keys.astype(np.int64).copy()
+    k[valid:] = groups
+    k[(k < 0) | (k >= groups)] = groups
+    expect = np.argsort(k, kind='stable')
+    inside = int((k < groups).sum())
+    np.testing.assert_array_equal(to_np(ids)[:inside], expect[:inside])
+    counts = np.bincount(k[k < groups], minlength=groups)
+    np.testing.assert_array_equal(
+        to_np(offsets), np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
