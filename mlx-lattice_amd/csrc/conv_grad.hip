@@ -17,14 +17,16 @@
 //    with the weight transposed to (C_in, K, C_out).
 //  * Weight gradient: dW[k] = sum over the edges of k of
 //    feats[in]^T cot[out] (eval_weight_grad_typed), a contraction over
-//    edges.  The matrix-core kernel splits each k's edges (kernel-grouped
-//    CSR: kernel_row_offsets / kernel_edge_ids) over S blocks per channel
-//    tile (128 x 128 when the channels fill it, so an edge's rows are
-//    gathered once for every channel pair); a block stages 32 edges of both
-//    operands transposed in
-//    LDS (channel-major, so an MFMA fragment is 8 consecutive edges) and
-//    accumulates in fp32.  Each split writes its partial tile; a second
-//    kernel sums the S partials in split order and rounds once, so results
+//    edges.  The matrix-core kernel deals G blocks per channel tile
+//    (128 x 128 when the channels fill it, so an edge's rows are gathered
+//    once for every channel pair) to the offsets in proportion to their
+//    edge counts (kernel-grouped CSR: kernel_row_offsets /
+//    kernel_edge_ids), so every block sums about the same number of edges.
+//    A block stages 64 edges of both operands in LDS as edge rows, reads
+//    the MFMA fragments (8 consecutive edges per lane) with transposing
+//    LDS reads and accumulates in fp32.  Each block writes its partial tile; a second
+//    kernel sums an offset's partials in block order and rounds once, so
+//    results
 //    are deterministic.  Other dtypes and shapes take a one-lane-per-weight
 //    kernel.
 
@@ -164,66 +166,93 @@ template <> struct GradMfma<__bf16> {
     }
 };
 
-constexpr int kXcds = 8;       // XCDs of an MI355X, each with its own L2
 constexpr int kWgEdges = 64;   // edges per staged step (two 32-edge MFMA steps)
-constexpr int kWgRow = 72;     // LDS row stride in elements (64 edges + 8 pad)
 
-// LDS slot of edge column j in channel row r: the 16-byte chunk j/8 is
-// XOR-swizzled by r/8, so a wave's transposing stores (8 edges x 8 channel
-// pieces) and the fragment reads (16 rows, one chunk) spread over the banks.
-__device__ inline int wg_slot(int r, int j) { return r * kWgRow + (((j >> 3) ^ ((r >> 3) & 7)) << 3) + (j & 7); }
-
-// Channel rows r0 .. r0 + 7 at columns (col, col + 1): element c of `lo`
-// and of `hi` (8 x 16 bits each) as one 32-bit word per row.
-template <typename T>
-__device__ inline void store_pairs(T* lds, int r0, int col, uint4 lo, uint4 hi) {
-    const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w};
-    const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        // low halves (element 2d) and high halves (element 2d + 1)
-        *reinterpret_cast<uint32_t*>(lds + wg_slot(r0 + 2 * d, col)) = __builtin_amdgcn_perm(h[d], l[d], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(lds + wg_slot(r0 + 2 * d + 1, col)) =
-            __builtin_amdgcn_perm(h[d], l[d], 0x07060302u);
-    }
+// LDS rows of a weight-gradient step: one row per edge, the operand's
+// channels in 16-byte pieces (TC / 8 of them).  Piece q of row r sits at
+// slot q ^ wg_swizzle(r): the waves' 16-byte stores (two rows of 8 pieces
+// per 16 lanes) and the transposing fragment reads (16 rows x 2 pieces per
+// instruction) then spread over all the banks.
+__device__ inline int wg_swizzle(int r, int pieces) {
+    return (2 * (r & 1) + 4 * ((r >> 1) & 1) + 8 * (((r >> 3) ^ r) & 1)) & (pieces - 1);
 }
 
-// Block (tile_ci * tiles_co + tile_co, k, split): channel tile TCI x TCO,
-// four waves of (TCI/2) x (TCO/2).  Per step of 32 edges the block stages
-// both operands transposed into channel-major LDS rows (64 edges per step).
+template <int TC>
+__device__ inline int wg_piece_slot(int r, int q) { return r * TC + ((q ^ wg_swizzle(r, TC / 8)) << 3); }
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// One MFMA operand fragment (16 channels x 32 edges) from edge-major LDS
+// rows with two transposing reads.  In each 16-lane group, ds_read_b64_tr_b16
+// gives lane i element i % 4 of the 8-byte chunks addressed by lanes
+// i / 4 + 4j (j = 0..3).  Lane s of group g addresses row
+// 32 ks + 8 g + 4 t + s / 4 at channel c0 + 4 (s % 4), so lane i receives
+// channel c0 + i of four consecutive edges; the two reads (t = 0, 1) make
+// the 8 edges 8 g .. 8 g + 7 the MFMA expects of lane i.
+template <typename V, int TC, typename T>
+__device__ inline V wg_fragment(const T* lds, int ks, int c0, int lane) {
+    const int s = lane & 15;
+    const int g = lane >> 4;
+    const int q = (c0 >> 3) + ((s & 3) >> 1);
+    short4_t h[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int r = 32 * ks + 8 * g + 4 * t + (s >> 2);
+        const T* src = lds + wg_piece_slot<TC>(r, q) + 4 * (s & 1);
+        h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) short4_t*)(src));
+    }
+    typedef short short8_t __attribute__((ext_vector_type(8)));
+    const short8_t both = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(V, both);
+}
+
+// Blocks of offset k's edges: the G blocks are dealt to the offsets in
+// proportion to their edge counts, at least one each: offset k owns blocks
+// [wg_first_block(k), wg_first_block(k + 1)), where
+// wg_first_block(k) = k + (G - K) * (edges before k) / (all edges).
+__device__ inline int wg_first_block(const int32_t* koff, int k, int K, int blocks) {
+    const long long total = koff[K] - koff[0];
+    if (total <= 0) return k * (blocks / K);
+    return k + static_cast<int>(static_cast<long long>(blocks - K) * (koff[k] - koff[0]) / total);
+}
+
+// Block (tile, b): channel tile TCI x TCO, four waves of (TCI/2) x
+// (TCO/2), over an equal share of one offset's edges (the offsets get
+// blocks in proportion to their edge counts, so every block sums about the
+// same number of edges and the launch drains evenly).  Per step of 64 edges
+// the block stages both operands into edge-major LDS rows.
 template <typename T, int TCI, int TCO>
 __global__ void __launch_bounds__(256, 3)
 weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ cot, int n_out, int c_out,
                  const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                  const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
-                 const int32_t* __restrict__ kedges, int splits, int tiles_co, float* __restrict__ partial) {
+                 const int32_t* __restrict__ kedges, int K, int tiles_co, float* __restrict__ partial) {
     using V = typename GradMfma<T>::vec;
     constexpr int MB = TCI / 32;  // 16-row blocks per wave
     constexpr int NB = TCO / 32;  // 16-column blocks per wave
-    __shared__ __align__(16) T a_t[TCI * kWgRow];
-    __shared__ __align__(16) T b_t[TCO * kWgRow];
-    // Blocks are dealt to the 8 XCDs round-robin in launch order.  The
-    // logical order (tile, then k, then split) is cut into 8 contiguous
-    // chunks, one per XCD, so the K offsets of a split, which gather the
-    // same neighbourhood of rows, share one XCD's L2.
-    const int K = gridDim.y;
-    const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
-    const int launch = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int per = n_blocks / kXcds;
-    const int extra = n_blocks % kXcds;
-    const int xcd = launch % kXcds;
-    const int slot = launch / kXcds;
-    const int logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + slot;
-    const int tile = logical % gridDim.x;
-    const int k = (logical / gridDim.x) % K;
-    const int s = logical / (gridDim.x * K);
+    __shared__ __align__(16) T a_t[kWgEdges * TCI];
+    __shared__ __align__(16) T b_t[kWgEdges * TCO];
+    const int tile = blockIdx.x;
+    const int b = blockIdx.y;
+    const int blocks = gridDim.y;
+    int k = 0;
+    int first = wg_first_block(koff, 0, K, blocks);
+    int next = wg_first_block(koff, 1, K, blocks);
+    while (k + 1 < K && next <= b) {
+        ++k;
+        first = next;
+        next = wg_first_block(koff, k + 1, K, blocks);
+    }
+    const int share = b - first;
+    const int shares = next - first;
     const int ci0 = (tile / tiles_co) * TCI;
     const int co0 = (tile % tiles_co) * TCO;
     const int E = min(counts[0], edge_capacity);
     const int lo_k = koff[k];
     const int n_k = koff[k + 1] - lo_k;
-    const int lo = lo_k + static_cast<int>(static_cast<long long>(n_k) * s / splits);
-    const int hi = lo_k + static_cast<int>(static_cast<long long>(n_k) * (s + 1) / splits);
+    const int lo = lo_k + static_cast<int>(static_cast<long long>(n_k) * share / shares);
+    const int hi = lo_k + static_cast<int>(static_cast<long long>(n_k) * (share + 1) / shares);
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -235,7 +264,7 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
 #pragma unroll
     for (int a = 0; a < MB; ++a)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NB; ++n) acc[a][n] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     // Thread t stages edges t/8 and t/8 + 32 of the step: 8-channel pieces
     // t%8 + 8i of their feature rows (i < TCI/64) and cotangent rows
@@ -248,7 +277,7 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     // Three-stage pipeline over the steps: the edge ids of step s+3 and the
     // row indices of step s+2 are loaded while the rows of step s+1 are
     // gathered, so no step waits on a dependent index load.  Edges past the
-    // split's end or outside the relation read as zeros (row -1).
+    // share's end or outside the relation read as zeros (row -1).
     auto fetch_edges = [&](int base, int (&ev)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -298,18 +327,16 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     fetch_rows(ev, ri, ro);
     fetch_edges(lo + 2 * kWgEdges, ev);
     for (int base = lo; base < hi; base += kWgEdges) {
-        // The thread's two edges take adjacent columns 2j and 2j + 1 (the
-        // order of edges inside a step is free: the sum over them is in
-        // fp32), so each channel is one 32-bit store of the pair.
+        // The thread's two edges take rows j and j + 32 (the order of edges
+        // inside a step is free: the sum over them is in fp32).
 #pragma unroll
-        for (int i = 0; i < PA; ++i) {
-            store_pairs(a_t, 8 * (p + 8 * i), 2 * j, __builtin_bit_cast(uint4, av[0][i]),
-                        __builtin_bit_cast(uint4, av[1][i]));
-        }
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            store_pairs(b_t, 8 * (p + 8 * i), 2 * j, __builtin_bit_cast(uint4, bv[0][i]),
-                        __builtin_bit_cast(uint4, bv[1][i]));
+            for (int i = 0; i < PA; ++i)
+                *reinterpret_cast<V*>(a_t + wg_piece_slot<TCI>(j + 32 * h, p + 8 * i)) = av[h][i];
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+                *reinterpret_cast<V*>(b_t + wg_piece_slot<TCO>(j + 32 * h, p + 8 * i)) = bv[h][i];
         }
         __syncthreads();
         gather(ri, ro);
@@ -320,10 +347,10 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
             V af[MB], bf[NB];
 #pragma unroll
             for (int m = 0; m < MB; ++m)
-                af[m] = *reinterpret_cast<const V*>(a_t + wg_slot((TCI / 2) * wm + 16 * m + lr, 32 * ks + 8 * g));
+                af[m] = wg_fragment<V, TCI>(a_t, ks, (TCI / 2) * wm + 16 * m, lane);
 #pragma unroll
             for (int n = 0; n < NB; ++n)
-                bf[n] = *reinterpret_cast<const V*>(b_t + wg_slot((TCO / 2) * wn + 16 * n + lr, 32 * ks + 8 * g));
+                bf[n] = wg_fragment<V, TCO>(b_t, ks, (TCO / 2) * wn + 16 * n, lane);
 #pragma unroll
             for (int m = 0; m < MB; ++m)
 #pragma unroll
@@ -332,7 +359,7 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         __syncthreads();
     }
     // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
-    float* out = partial + (static_cast<long long>(s) * K + k) * c_in * c_out;
+    float* out = partial + static_cast<long long>(b) * c_in * c_out;
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
@@ -345,19 +372,24 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
             }
 }
 
-// Sum of the split partials in split order, one rounding, written in the
-// weight's layout.
+// dW[k] = sum of the partials of offset k's blocks in block order, one
+// rounding, written in the weight's layout.
 template <typename T>
 __global__ void __launch_bounds__(256)
-weight_grad_reduce(const float* __restrict__ partial, int splits, GradWeightIndex widx, T* __restrict__ grad) {
-    const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
+weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict__ koff, int blocks,
+                   GradWeightIndex widx, T* __restrict__ grad) {
+    const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
+    const long long per = widx.K * mat;
     for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < per;
          i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int k = static_cast<int>(i / mat);
+        const long long within = i - k * mat;
+        const int end = wg_first_block(koff, k + 1, widx.K, blocks);
         float acc = 0.0f;
-        for (int s = 0; s < splits; ++s) acc += partial[s * per + i];
-        const int co = static_cast<int>(i % widx.c_out);
-        const long long kc = i / widx.c_out;
-        grad[widx(static_cast<int>(kc / widx.c_in), static_cast<int>(kc % widx.c_in), co)] = static_cast<T>(acc);
+        for (int blk = wg_first_block(koff, k, widx.K, blocks); blk < end; ++blk) acc += partial[blk * mat + within];
+        const int co = static_cast<int>(within % widx.c_out);
+        const int ci = static_cast<int>(within / widx.c_out);
+        grad[widx(k, ci, co)] = static_cast<T>(acc);
     }
 }
 
@@ -399,10 +431,22 @@ int check_grad_dtype(int dtype) {
     return LATTICE_OK;
 }
 
-// Splits of each kernel offset's edges for the matrix-core weight gradient.
-int weight_grad_splits(int edge_capacity, int kernel_count) {
-    const long long per_k = std::max(1LL, static_cast<long long>(edge_capacity) / std::max(kernel_count, 1));
-    return static_cast<int>(std::min<long long>(64, std::max<long long>(1, per_k / 4096)));
+// Blocks per channel tile of the matrix-core weight gradient: about 2,048
+// edge slots of the relation's capacity each, at least one per offset, at
+// most 768, one round of three blocks on each of the 256 CUs.  The kernel
+// is bound by its row gathers, so fewer, longer blocks with fewer partial
+// tiles ran faster than two or three rounds (config 3: 768 blocks 436 us,
+// 1,536 blocks 477 us, 1,024 blocks 542 us).
+constexpr int kWgEdgesPerBlock = 2048;
+constexpr int kWgMaxBlocks = 768;
+int weight_grad_blocks(int edge_capacity, int kernel_count) {
+    const long long want = (static_cast<long long>(edge_capacity) + kWgEdgesPerBlock - 1) / kWgEdgesPerBlock;
+    return static_cast<int>(std::max<long long>(kernel_count, std::min<long long>(kWgMaxBlocks, want)));
+}
+
+// One fp32 partial tile per block.
+size_t weight_grad_partial_bytes(int edge_capacity, int kernel_count, int c_in, int c_out) {
+    return static_cast<size_t>(weight_grad_blocks(edge_capacity, kernel_count)) * c_in * c_out * sizeof(float);
 }
 
 bool weight_grad_mfma_ok(int dtype, int c_in, int c_out) {
@@ -430,8 +474,8 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
                        size_t workspace_bytes, hipStream_t stream) {
     if (weight_grad_mfma_ok(dtype, widx.c_in, widx.c_out) && workspace != nullptr) {
         if constexpr (!std::is_same<T, float>::value) {
-            const int splits = weight_grad_splits(edge_capacity, widx.K);
-            const size_t need = static_cast<size_t>(splits) * widx.K * widx.c_in * widx.c_out * sizeof(float);
+            const int blocks = weight_grad_blocks(edge_capacity, widx.K);
+            const size_t need = weight_grad_partial_bytes(edge_capacity, widx.K, widx.c_in, widx.c_out);
             LATTICE_REQUIRE(workspace_bytes >= need, "weight gradient workspace too small.");
             float* partial = static_cast<float*>(workspace);
             // 128-channel tiles where the channels fill them: one gather of
@@ -440,12 +484,11 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
             const int tco = widx.c_out > 64 ? 128 : 64;
             const int tiles_ci = (widx.c_in + tci - 1) / tci;
             const int tiles_co = (widx.c_out + tco - 1) / tco;
-            dim3 grid(static_cast<unsigned>(tiles_ci * tiles_co), static_cast<unsigned>(widx.K),
-                      static_cast<unsigned>(splits));
+            dim3 grid(static_cast<unsigned>(tiles_ci * tiles_co), static_cast<unsigned>(blocks));
 #define LATTICE_WG_LAUNCH(A, B)                                                                                 \
     weight_grad_mfma<T, A, B><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,          \
                                                         static_cast<const T*>(cot), n_out, widx.c_out, in_rows,  \
-                                                        out_rows, counts, edge_capacity, koff, kedges, splits,   \
+                                                        out_rows, counts, edge_capacity, koff, kedges, widx.K,   \
                                                         tiles_co, partial)
             if (tci == 128 && tco == 128) LATTICE_WG_LAUNCH(128, 128);
             else if (tci == 128) LATTICE_WG_LAUNCH(128, 64);
@@ -454,7 +497,7 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
 #undef LATTICE_WG_LAUNCH
             LATTICE_LAUNCH_CHECK();
             const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
-            weight_grad_reduce<T><<<grid_for(per, 256, 4096), 256, 0, stream>>>(partial, splits, widx,
+            weight_grad_reduce<T><<<grid_for(per, 256, 4096), 256, 0, stream>>>(partial, koff, blocks, widx,
                                                                               static_cast<T*>(grad));
             LATTICE_LAUNCH_CHECK();
             return LATTICE_OK;
@@ -537,8 +580,7 @@ extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_
 extern "C" size_t lattice_hip_conv_weight_grad_workspace_bytes(int dtype, int kernel_count, int c_in, int c_out,
                                                                 int edge_capacity) {
     if (!weight_grad_mfma_ok(dtype, c_in, c_out) || kernel_count <= 0) return 0;
-    return static_cast<size_t>(weight_grad_splits(edge_capacity, kernel_count)) * kernel_count * c_in * c_out *
-           sizeof(float);
+    return weight_grad_partial_bytes(edge_capacity, kernel_count, c_in, c_out);
 }
 
 extern "C" int lattice_hip_sparse_conv_weight_grad(int dtype, const void* feats, int n_in, int c_in, const void* cot,

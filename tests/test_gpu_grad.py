@@ -111,6 +111,9 @@ CASES = [
     ('subm', 3, 1, 16, 32, torch.float32, False),      # CSR input grad, simple weight grad
     ('subm', 3, 1, 24, 40, torch.float16, False),      # CSR input grad (C_out % 32), MFMA weight grad
     ('forward', 2, 2, 8, 16, torch.float32, True),
+    ('subm', 3, 1, 128, 128, torch.float16, False),    # 128 x 128 weight-grad tiles
+    ('subm', 3, 1, 96, 136, torch.bfloat16, False),    # ragged 128-channel tiles
+    ('subm', 5, 1, 16, 64, torch.float16, False),      # 125 offsets, fewer edges than block slots
 ]
 
 
@@ -202,6 +205,25 @@ def test_weight_grad_is_deterministic():
     b = sparse_conv_weight_grad_from_relation(feats, cot, weight, rel)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_weight_grad_with_no_edges():
+    """An empty relation gives a zero weight gradient on every route."""
+    from mlx_lattice_amd.ops._relation_exec import (
+        sparse_conv_weight_grad_from_relation,
+    )
+
+    for c_in, c_out, dtype in ((128, 128, torch.float16), (16, 24, torch.float32)):
+        feats = torch.zeros((0, c_in), dtype=dtype, device=DEV)
+        x = _sparse(np.zeros((0, 4), np.int32), feats)
+        rel = _relation(x, 'subm', 3, 1)
+        cot = torch.zeros((0, c_out), dtype=dtype, device=DEV)
+        weight = torch.ones((c_out, 3, 3, 3, c_in), dtype=dtype, device=DEV)
+        print(f'empty weight grad {c_in}->{c_out} {dtype}', flush=True)
+        gw = sparse_conv_weight_grad_from_relation(feats, cot, weight, rel)
+        torch.cuda.synchronize()
+        assert gw.shape == weight.shape
+        assert not gw.any()
 
 
 # ------------------------------------------------------ dense box ----
