@@ -311,7 +311,7 @@ def backward_workload(feats, weight, coords, active, edges: int, steps: int,
                       warmup: int) -> dict:
     """Gradients of the config-3 conv (the reference primitive's vjp):
     the input gradient on the matrix cores over the transposed sorted view,
-    the weight gradient by the split-edge MFMA kernel.  The transposed view
+    the weight gradient by the edge-balanced MFMA kernel.  The transposed view
     is built once per relation and cached, like the forward's sorted view;
     its build time is reported separately."""
     import torch
@@ -340,7 +340,7 @@ def backward_workload(feats, weight, coords, active, edges: int, steps: int,
     flops = 2.0 * edges * 128 * 128
     return {
         'workload': 'config3 gradients: input grad (matrix cores, transposed '
-                    'sorted view) and weight grad (split-edge MFMA)',
+                    'sorted view) and weight grad (edge-balanced MFMA)',
         'input_grad_ms': round(t_in, 4),
         'input_grad_tflops': round(flops / t_in / 1e9, 2),
         'weight_grad_ms': round(t_w, 4),
