@@ -73,6 +73,19 @@ enum lattice_weight_layout {
     LATTICE_WEIGHT_DENSE_5D = 1      /* (C_out, Kx, Ky, Kz, C_in) contiguous */
 };
 
+/* Store-side epilogue flags of the conv entries (the `epilogue` argument
+ * after `bias`).  LATTICE_EPILOGUE_RELU applies the reference's
+ * `maximum(feats, 0)` (ops/feature.py:54-56) to every stored value, after
+ * the rounding and the optional bias: v where v > 0 or v is NaN, +0
+ * otherwise.  The result equals a separate ReLU over the conv's output bit
+ * for bit, on every row.  No counterpart in the reference's conv
+ * primitives: it saves the separate pass over all output rows that a
+ * conv followed by ReLU would make. */
+enum lattice_epilogue_flags {
+    LATTICE_EPILOGUE_NONE = 0,
+    LATTICE_EPILOGUE_RELU = 1
+};
+
 /* Bits of the device status word written by the relation builders.  Every
  * int32 coordinate is accepted (as by the reference's CoordHash over all
  * four words, cpu/common_detail.h:68-77); LATTICE_STATUS_COORD_RANGE is
@@ -307,13 +320,13 @@ int lattice_hip_build_sorted_implicit_gemm_view(
  * rounded to `dtype`, then the bias is added and the sum rounded again, so
  * the output equals the separate add bit for bit, on every row (rows
  * without edges hold the bias).  The same holds for the two entries
- * below. */
+ * below.  epilogue: LATTICE_EPILOGUE_* flags, applied after the bias. */
 int lattice_hip_sparse_conv_features(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,
     int weight_layout, int kernel_count, int c_out, const int32_t* in_rows,
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, int out_capacity, void* out, const void* bias,
-    void* stream);
+    int epilogue, void* stream);
 
 /* Implicit-GEMM conv over the sorted view (the reference's sorted plan):
  * row i of the mask-sorted order gathers feats[sorted_kv_out_in_map[k, i]]
@@ -347,7 +360,7 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int weight_layout, int kernel_count, int c_out,
     const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
     const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
-    void* workspace, size_t workspace_bytes, void* stream);
+    int epilogue, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Allocation-free variant of the entry above: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under
@@ -365,7 +378,7 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     int weight_layout, int kernel_count, int c_out,
     const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
     const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
-    void* stream);
+    int epilogue, void* stream);
 
 /* Conv over a direct generative / transposed relation (output row
  * in * K + k holds the single edge (in, k); lattice_hip_build_generative_relation
@@ -374,11 +387,11 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
  * bias) for the others.  The same sum as the CSR and sorted routes over
  * that relation, as a dense matrix-core GEMM with no gather.  fp16/bf16,
  * c_in, c_out in {32, 64, 128, 256} with c_in * c_out <= 16384; weights (C_out,
- * Kx, Ky, Kz, C_in); out [n_in * K, c_out]; bias optional as above. */
+ * Kx, Ky, Kz, C_in); out [n_in * K, c_out]; bias and epilogue as above. */
 int lattice_hip_sparse_conv_features_expand(
     int dtype, const void* feats, int n_in, const int32_t* active_rows,
     int c_in, const void* weights, int kernel_count, int c_out, void* out,
-    const void* bias, void* stream);
+    const void* bias, int epilogue, void* stream);
 
 /* Quantized conv (cpu/quantized.cpp:64-141): weights uint32
  * [K, storage_c_in*bits/32, c_out] with codes LSB-first along C_in,
@@ -387,7 +400,7 @@ int lattice_hip_sparse_conv_features_expand(
  * tile_masks and reorder_rows are non-NULL the MFMA route with the dequant
  * fused into the
  * B-operand staging is used (fp16/bf16, c_in % 32 == 0); otherwise the CSR
- * route. */
+ * route.  bias and epilogue as for lattice_hip_sparse_conv_features. */
 int lattice_hip_sparse_quantized_conv_features(
     int dtype, const void* feats, int n_in, int c_in, const uint32_t* weights,
     const void* scales, const void* biases, int kernel_count, int c_out,
@@ -395,8 +408,8 @@ int lattice_hip_sparse_quantized_conv_features(
     const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map,
     const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
-    void* out, const void* bias, void* workspace, size_t workspace_bytes,
-    void* stream);
+    void* out, const void* bias, int epilogue, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Input gradient of the float conv (SparseConvFeaturesInputGrad,
  * primitive.cpp:192-260, 597-639; cpu/algorithms.cpp:355-410):

@@ -52,18 +52,41 @@ template <> struct Elem<__bf16> {
     __device__ static void store(__bf16* p, long long i, float v) { p[i] = static_cast<__bf16>(v); }
 };
 
-// Output value with the optional bias added as a separate operation: the
-// conv result is rounded to T first, then bias is added and the sum rounded
-// again, exactly as `feats + bias` over the stored output computes it
-// (ops/conv.py:460-469).
-template <typename T>
-__device__ inline void store_out(T* out, long long i, float acc, const T* bias, int co) {
-    if (bias == nullptr) {
-        Elem<T>::store(out, i, acc);
-        return;
+// Store-side epilogue shared by every conv route.  The conv result is
+// rounded to T; the optional bias is then added and the sum rounded again,
+// exactly as `feats + bias` over the stored output computes it
+// (ops/conv.py:460-469); the optional ReLU then keeps v where v > 0 or v is
+// NaN and stores +0 otherwise, the reference's `maximum(feats, 0)`
+// (ops/feature.py:54-56) applied to the stored value.
+template <typename T> struct Epilogue {
+    const T* bias;  // [c_out] in T, or null
+    bool relu;
+    // Stored value of output channel co for the fp32 sum acc.
+    __device__ inline T apply(float acc, int co) const {
+        return finish(acc, bias != nullptr ? Elem<T>::load(bias, co) : 0.0f);
     }
-    const float rounded = static_cast<float>(static_cast<T>(acc));
-    Elem<T>::store(out, i, rounded + Elem<T>::load(bias, co));
+    // The same with the channel's bias value already loaded (b is unused
+    // when there is no bias).
+    __device__ inline T finish(float acc, float b) const {
+        T v = static_cast<T>(acc);
+        if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + b);
+        if (relu) {
+            const float f = static_cast<float>(v);
+            if (!(f > 0.0f) && f == f) v = static_cast<T>(0.0f);
+        }
+        return v;
+    }
+    // The epilogue of output channels co0 .. (a column slice of the output).
+    Epilogue shifted(int co0) const { return Epilogue{bias != nullptr ? bias + co0 : nullptr, relu}; }
+};
+
+template <typename T> Epilogue<T> epilogue_of(const void* bias, int flags) {
+    return Epilogue<T>{static_cast<const T*>(bias), (flags & LATTICE_EPILOGUE_RELU) != 0};
+}
+
+template <typename T>
+__device__ inline void store_out(T* out, long long i, float acc, const Epilogue<T>& epi, int co) {
+    out[i] = epi.apply(acc, co);
 }
 
 // ------------------------------------------------------------- CSR route --
@@ -89,7 +112,7 @@ __global__ void __launch_bounds__(256)
 conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, WeightIndex widx,
          const int32_t* __restrict__ in_rows, const int32_t* __restrict__ kernel_ids,
          const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ row_offsets,
-         int out_capacity, T* __restrict__ out, const T* __restrict__ bias, bool staged) {
+         int out_capacity, T* __restrict__ out, Epilogue<T> epi, bool staged) {
     extern __shared__ float wlds[];
     const int c_out = widx.c_out;
     if (staged) {
@@ -127,7 +150,7 @@ conv_csr(const T* __restrict__ feats, int c_in, const T* __restrict__ weights, W
                 }
             }
         }
-        store_out(out, t, acc, bias, co);
+        store_out(out, t, acc, epi, co);
     }
 }
 
@@ -152,7 +175,7 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
                const T* __restrict__ biases, QuantIndex q, const int32_t* __restrict__ in_rows,
                const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
                const int32_t* __restrict__ row_offsets, int out_capacity, T* __restrict__ out,
-               const T* __restrict__ bias, bool staged) {
+               Epilogue<T> epi, bool staged) {
     extern __shared__ float wlds[];
     if (staged) {
         const int nw = q.K * q.c_in * q.c_out;
@@ -189,7 +212,7 @@ quant_conv_csr(const T* __restrict__ feats, const uint32_t* __restrict__ weights
                 }
             }
         }
-        store_out(out, t, acc, bias, co);
+        store_out(out, t, acc, epi, co);
     }
 }
 
@@ -207,7 +230,7 @@ conv_csr_rows(const T* __restrict__ feats, int c_in, const T* __restrict__ fweig
               const uint32_t* __restrict__ qweights, const T* __restrict__ scales, const T* __restrict__ qbiases,
               QuantIndex q, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ kernel_ids,
               const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ row_offsets,
-              int out_capacity, T* __restrict__ out, const T* __restrict__ bias) {
+              int out_capacity, T* __restrict__ out, Epilogue<T> epi) {
     // (k, ci, co) with co fastest; each offset's slice is padded by 4 floats
     // so the lanes of a wave, which read different offsets, spread over the
     // LDS banks (16-byte reads).
@@ -256,9 +279,7 @@ conv_csr_rows(const T* __restrict__ feats, int c_in, const T* __restrict__ fweig
         T vals[CO];
 #pragma unroll
         for (int co = 0; co < CO; ++co) {
-            T v = static_cast<T>(acc[co]);
-            if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + Elem<T>::load(bias, co));
-            vals[co] = v;
+            vals[co] = epi.apply(acc[co], co);
         }
         uint4* dst = reinterpret_cast<uint4*>(out + static_cast<long long>(row) * CO);
 #pragma unroll
@@ -830,7 +851,7 @@ template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
-           const int32_t* __restrict__ block_order, T* __restrict__ out, const T* __restrict__ bias, int out_ld) {
+           const int32_t* __restrict__ block_order, T* __restrict__ out, Epilogue<T> epi, int out_ld) {
     using V = typename MfmaOps<T>::vec;
     constexpr int WAVES = S::WAVES;
     constexpr int WAVE_ROWS = S::WAVE_ROWS;
@@ -964,7 +985,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     float bcol[S::CB];
 #pragma unroll
     for (int cb = 0; cb < S::CB; ++cb) {
-        bcol[cb] = bias != nullptr ? static_cast<float>(bias[wc * S::WAVE_COLS + cb * 16 + lr]) : 0.0f;
+        bcol[cb] = epi.bias != nullptr ? static_cast<float>(epi.bias[wc * S::WAVE_COLS + cb * 16 + lr]) : 0.0f;
     }
 #pragma unroll
     for (int rb = 0; rb < S::RB; ++rb) {
@@ -975,8 +996,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
                 const int r = rb * 16 + (lane >> 4) * 4 + q;
                 const int piece = (cb * 16 + lr) / 8;
                 const int slot = piece ^ (r % S::EPIECES);
-                T v = static_cast<T>(acc[rb][cb][q]);
-                if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + bcol[cb]);
+                const T v = epi.finish(acc[rb][cb][q], bcol[cb]);
                 stage[r * S::EROW + slot * 8 + (lr & 7)] = v;
             }
         }
@@ -1014,7 +1034,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
 template <typename T, int KSTEPS, int CB>
 __global__ void __launch_bounds__(256, CB == 16 ? 1 : 2)
 conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ active_rows,
-            const T* __restrict__ weights, int K, T* __restrict__ out, const T* __restrict__ bias) {
+            const T* __restrict__ weights, int K, T* __restrict__ out, Epilogue<T> epi) {
     using V = typename MfmaOps<T>::vec;
     constexpr int C_IN = KSTEPS * 32;
     constexpr int C_OUT = CB * 16;
@@ -1044,7 +1064,7 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
     }
     float bcol[CB];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) bcol[cb] = bias != nullptr ? static_cast<float>(bias[cb * 16 + lr]) : 0.0f;
+    for (int cb = 0; cb < CB; ++cb) bcol[cb] = epi.bias != nullptr ? static_cast<float>(epi.bias[cb * 16 + lr]) : 0.0f;
     // piece p of W[co, k, :] sits at wbuf[co * C_IN + ((p ^ (co % WPIECES)) * 8)]
     V wreg[WPER];
     auto load_w = [&](int k) {
@@ -1100,8 +1120,7 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    T v = static_cast<T>(acc[rb][cb][q]);
-                    if (bias != nullptr) v = static_cast<T>(static_cast<float>(v) + bcol[cb]);
+                    const T v = epi.finish(acc[rb][cb][q], bcol[cb]);
                     st[(rb * 16 + lg * 4 + q) * SROW + cb * 16 + lr] = v;
                 }
         __syncthreads();  // every wave has read W[:, k, :] and staged its tile
@@ -1122,21 +1141,21 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
 // Launches conv_expand for c_in * c_out <= 16384 (the weight slice of one
 // offset fits a 32 KB LDS buffer next to the four 32-row output stages).
 template <typename T, int KSTEPS, int CB>
-int launch_expand_shape(const T* feats, int n_in, const int32_t* active, const T* w, int K, T* out, const T* bias,
+int launch_expand_shape(const T* feats, int n_in, const int32_t* active, const T* w, int K, T* out, Epilogue<T> epi,
                         hipStream_t stream) {
     static_assert(KSTEPS * 32 * CB * 16 <= 16384, "the weight slice must fit its LDS buffer");
     const unsigned blocks = static_cast<unsigned>((n_in + 127) / 128);
-    conv_expand<T, KSTEPS, CB><<<blocks, 256, 0, stream>>>(feats, n_in, active, w, K, out, bias);
+    conv_expand<T, KSTEPS, CB><<<blocks, 256, 0, stream>>>(feats, n_in, active, w, K, out, epi);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
 
 template <typename T>
 int launch_expand(const T* feats, int n_in, const int32_t* active, int c_in, const T* w, int K, int c_out, T* out,
-                  const T* bias, hipStream_t stream) {
+                  Epilogue<T> epi, hipStream_t stream) {
     if (n_in <= 0) return LATTICE_OK;
 #define LATTICE_EXPAND(CI, CO) \
-    if (c_in == CI && c_out == CO) return launch_expand_shape<T, CI / 32, CO / 16>(feats, n_in, active, w, K, out, bias, stream)
+    if (c_in == CI && c_out == CO) return launch_expand_shape<T, CI / 32, CO / 16>(feats, n_in, active, w, K, out, epi, stream)
     LATTICE_EXPAND(32, 32);
     LATTICE_EXPAND(32, 64);
     LATTICE_EXPAND(32, 128);
@@ -1207,7 +1226,7 @@ schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, in
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
-                       T* out, const T* bias, hipStream_t stream, bool scheduled, int out_ld = S::C_OUT) {
+                       T* out, Epilogue<T> epi, hipStream_t stream, bool scheduled, int out_ld = S::C_OUT) {
     static_assert(S::BLOCK_ROWS == kOrderTileRows, "every shape uses the tile order's 128-row tiles");
     const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
     if (blocks > kMaxScheduledTiles) schedule = nullptr;
@@ -1216,7 +1235,7 @@ int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, con
         LATTICE_LAUNCH_CHECK();
     }
     conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks), S::THREADS, 0, stream>>>(
-        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, bias, out_ld);
+        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, epi, out_ld);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
 }
@@ -1238,11 +1257,11 @@ template <typename T> PackedB<T> column_half(const PackedB<T>& b, int co_base) {
 template <typename T, typename BSource>
 int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b, const int32_t* kv_map,
                  const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, bool ready,
-                 T* out, const T* bias, hipStream_t stream) {
+                 T* out, Epilogue<T> epi, hipStream_t stream) {
     if (rows <= 0) return LATTICE_OK;
 #define LATTICE_IGEMM_LAUNCH(...) \
     launch_igemm_shape<T, IgemmShape<__VA_ARGS__>>(feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, \
-                                                   schedule, out, bias, stream, ready)
+                                                   schedule, out, epi, stream, ready)
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
@@ -1268,7 +1287,7 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
         for (int h = 0; h < 2; ++h) {
             const int rc = launch_igemm_shape<T, S128>(feats, n_in, c_in, column_half(b, h * 128), kv_map,
                                                       tile_masks, reorder_rows, rows, schedule, out + h * 128,
-                                                      bias != nullptr ? bias + h * 128 : nullptr, stream,
+                                                      epi.shifted(h * 128), stream,
                                                       ready || h == 1, 256);
             if (rc != LATTICE_OK) return rc;
         }
@@ -1340,7 +1359,8 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
                                                 int c_out, const int32_t* in_rows, const int32_t* kernel_ids,
                                                 const int32_t* counts, int edge_capacity,
                                                 const int32_t* row_offsets, int out_capacity, void* out,
-                                                const void* bias, void* stream_ptr) {
+                                                const void* bias, int epilogue, void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(n_in >= 0 && c_in > 0 && c_out > 0, "feats must have shape (N, C_in).");
@@ -1362,7 +1382,7 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
     conv_csr_rows<T, CO, false><<<rgrid, 256, rlds, stream>>>(                                                    \
         static_cast<const T*>(feats), c_in, static_cast<const T*>(weights), widx, nullptr, nullptr, nullptr, none, \
         in_rows, kernel_ids, counts, edge_capacity, row_offsets, out_capacity, static_cast<T*>(out),             \
-        static_cast<const T*>(bias))
+        epilogue_of<T>(bias, epilogue))
         if (dtype == LATTICE_F32) {
             if (c_out == 16) LATTICE_CSR_ROWS(float, 16); else LATTICE_CSR_ROWS(float, 32);
         } else if (dtype == LATTICE_F16) {
@@ -1381,18 +1401,18 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
         conv_csr<float><<<grid, 256, lds, stream>>>(static_cast<const float*>(feats), c_in,
                                                   static_cast<const float*>(weights), widx, in_rows, kernel_ids,
                                                   counts, edge_capacity, row_offsets, out_capacity,
-                                                  static_cast<float*>(out), static_cast<const float*>(bias), staged);
+                                                  static_cast<float*>(out), epilogue_of<float>(bias, epilogue), staged);
     } else if (dtype == LATTICE_F16) {
         conv_csr<_Float16><<<grid, 256, lds, stream>>>(static_cast<const _Float16*>(feats), c_in,
                                                      static_cast<const _Float16*>(weights), widx, in_rows,
                                                      kernel_ids, counts, edge_capacity, row_offsets, out_capacity,
                                                      static_cast<_Float16*>(out),
-                                                     static_cast<const _Float16*>(bias), staged);
+                                                     epilogue_of<_Float16>(bias, epilogue), staged);
     } else {
         conv_csr<__bf16><<<grid, 256, lds, stream>>>(static_cast<const __bf16*>(feats), c_in,
                                                    static_cast<const __bf16*>(weights), widx, in_rows, kernel_ids,
                                                    counts, edge_capacity, row_offsets, out_capacity,
-                                                   static_cast<__bf16*>(out), static_cast<const __bf16*>(bias),
+                                                   static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue),
                                                    staged);
     }
     LATTICE_LAUNCH_CHECK();
@@ -1402,7 +1422,9 @@ extern "C" int lattice_hip_sparse_conv_features(int dtype, const void* feats, in
 extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     int dtype, const void* feats, int n_in, int c_in, const void* weights, int weight_layout, int kernel_count,
     int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
-    int out_capacity, void* out, const void* bias, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    int out_capacity, void* out, const void* bias, int epilogue, void* workspace, size_t workspace_bytes,
+    void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(dtype != LATTICE_F32, "the implicit GEMM route runs on fp16/bf16 matrix cores.");
@@ -1427,12 +1449,12 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         FloatB<_Float16> b{static_cast<const _Float16*>(weights), s_co, s_k};
         return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                       tile_masks, reorder_rows, out_capacity, schedule, ready,
-                                      static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
+                                      static_cast<_Float16*>(out), epilogue_of<_Float16>(bias, epilogue), stream);
     }
     FloatB<__bf16> b{static_cast<const __bf16*>(weights), s_co, s_k};
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                 tile_masks, reorder_rows, out_capacity, schedule, ready, static_cast<__bf16*>(out),
-                                static_cast<const __bf16*>(bias), stream);
+                                epilogue_of<__bf16>(bias, epilogue), stream);
 }
 
 // ------------------------------------------------- allocation-free entry --
@@ -1474,7 +1496,7 @@ int scratch_on_current_device(int32_t** ptr) {
 extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     int dtype, const void* feats, int n_in, int c_in, const void* weights, int weight_layout, int kernel_count,
     int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
-    int out_capacity, void* out, const void* bias, void* stream_ptr) {
+    int out_capacity, void* out, const void* bias, int epilogue, void* stream_ptr) {
     LATTICE_REQUIRE(out_capacity <= LATTICE_NOALLOC_CONV_MAX_ROWS,
                     "out_capacity exceeds the allocation-free conv's limit of " +
                         std::to_string(LATTICE_NOALLOC_CONV_MAX_ROWS) +
@@ -1486,7 +1508,7 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     if (rc != LATTICE_OK) return rc;
     return lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype, feats, n_in, c_in, weights, weight_layout, kernel_count, c_out, sorted_kv_out_in_map, tile_masks,
-        reorder_rows, out_capacity, out, bias, schedule, sizeof(scratch), stream_ptr);
+        reorder_rows, out_capacity, out, bias, epilogue, schedule, sizeof(scratch), stream_ptr);
 }
 
 extern "C" int lattice_hip_sparse_quantized_conv_features(
@@ -1494,8 +1516,9 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     const void* biases, int kernel_count, int c_out, int storage_c_in, int group_size, int bits,
     const int32_t* in_rows, const int32_t* kernel_ids, const int32_t* counts, int edge_capacity,
     const int32_t* row_offsets, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
-    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias, void* workspace,
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias, int epilogue, void* workspace,
     size_t workspace_bytes, void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized convolution bits must be 4 or 8.");
@@ -1521,13 +1544,13 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
                                 packed_words, groups, group_size, c_out, bits};
             return launch_igemm<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                           tile_masks, reorder_rows, out_capacity, schedule, ready,
-                                          static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
+                                          static_cast<_Float16*>(out), epilogue_of<_Float16>(bias, epilogue), stream);
         }
         PackedB<__bf16> b{weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases),
                           packed_words, groups, group_size, c_out, bits};
         return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                     tile_masks, reorder_rows, out_capacity, schedule, ready, static_cast<__bf16*>(out),
-                                    static_cast<const __bf16*>(bias), stream);
+                                    epilogue_of<__bf16>(bias, epilogue), stream);
     }
     LATTICE_REQUIRE(in_rows && kernel_ids && counts && row_offsets, "relation pointers must be non-null.");
     QuantIndex q{kernel_count, c_in, c_out, packed_words, groups, group_size, bits};
@@ -1540,7 +1563,7 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
     conv_csr_rows<T, CO, true><<<rgrid, 256, rlds, stream>>>(                                                    \
         static_cast<const T*>(feats), c_in, nullptr, none, weights, static_cast<const T*>(scales),              \
         static_cast<const T*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets, out_capacity, \
-        static_cast<T*>(out), static_cast<const T*>(bias))
+        static_cast<T*>(out), epilogue_of<T>(bias, epilogue))
         if (dtype == LATTICE_F32) {
             if (c_out == 16) LATTICE_QCSR_ROWS(float, 16); else LATTICE_QCSR_ROWS(float, 32);
         } else if (dtype == LATTICE_F16) {
@@ -1560,17 +1583,17 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
         quant_conv_csr<float><<<grid, 256, lds, stream>>>(
             static_cast<const float*>(feats), weights, static_cast<const float*>(scales),
             static_cast<const float*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<float*>(out), static_cast<const float*>(bias), staged);
+            out_capacity, static_cast<float*>(out), epilogue_of<float>(bias, epilogue), staged);
     } else if (dtype == LATTICE_F16) {
         quant_conv_csr<_Float16><<<grid, 256, lds, stream>>>(
             static_cast<const _Float16*>(feats), weights, static_cast<const _Float16*>(scales),
             static_cast<const _Float16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), staged);
+            out_capacity, static_cast<_Float16*>(out), epilogue_of<_Float16>(bias, epilogue), staged);
     } else {
         quant_conv_csr<__bf16><<<grid, 256, lds, stream>>>(
             static_cast<const __bf16*>(feats), weights, static_cast<const __bf16*>(scales),
             static_cast<const __bf16*>(biases), q, in_rows, kernel_ids, counts, edge_capacity, row_offsets,
-            out_capacity, static_cast<__bf16*>(out), static_cast<const __bf16*>(bias), staged);
+            out_capacity, static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue), staged);
     }
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
@@ -1578,8 +1601,9 @@ extern "C" int lattice_hip_sparse_quantized_conv_features(
 
 extern "C" int lattice_hip_sparse_conv_features_expand(int dtype, const void* feats, int n_in,
                                                        const int32_t* active_rows, int c_in, const void* weights,
-                                                       int kernel_count, int c_out, void* out, const void* bias,
+                                                       int kernel_count, int c_out, void* out, const void* bias, int epilogue,
                                                        void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
     int rc = check_dtype(dtype);
     if (rc != LATTICE_OK) return rc;
     LATTICE_REQUIRE(dtype != LATTICE_F32, "the expansion conv runs on fp16/bf16 matrix cores.");
@@ -1591,9 +1615,9 @@ extern "C" int lattice_hip_sparse_conv_features_expand(int dtype, const void* fe
     if (dtype == LATTICE_F16) {
         return launch_expand<_Float16>(static_cast<const _Float16*>(feats), n_in, active_rows, c_in,
                                        static_cast<const _Float16*>(weights), kernel_count, c_out,
-                                       static_cast<_Float16*>(out), static_cast<const _Float16*>(bias), stream);
+                                       static_cast<_Float16*>(out), epilogue_of<_Float16>(bias, epilogue), stream);
     }
     return launch_expand<__bf16>(static_cast<const __bf16*>(feats), n_in, active_rows, c_in,
                                  static_cast<const __bf16*>(weights), kernel_count, c_out,
-                                 static_cast<__bf16*>(out), static_cast<const __bf16*>(bias), stream);
+                                 static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue), stream);
 }

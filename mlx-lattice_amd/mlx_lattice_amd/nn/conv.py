@@ -40,10 +40,12 @@ class Conv3d(nn.Module):
 
     def forward(self, x: SparseTensor, *,
                 coordinates: SparseTensor | CoordinateMapKey | torch.Tensor
-                | None = None) -> SparseTensor:
+                | None = None,
+                activation: str | None = None) -> SparseTensor:
         return conv3d(x, self.weight, self.bias, kernel_size=self.spec.size,
                       stride=self.spec.stride, padding=self.spec.padding,
-                      dilation=self.spec.dilation, coordinates=coordinates)
+                      dilation=self.spec.dilation, coordinates=coordinates,
+                      activation=activation)
 
     def to_quantized(self, group_size: int | None = None,
                      bits: int | None = None, *, mode: str = 'affine',
@@ -68,10 +70,12 @@ class SubmConv3d(nn.Module):
         _init_kernel_params(self, in_channels, out_channels, self.spec, bias,
                             device, dtype)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return subm_conv3d(x, self.weight, self.bias,
                            kernel_size=self.spec.size,
-                           dilation=self.spec.dilation)
+                           dilation=self.spec.dilation,
+                           activation=activation)
 
     def to_quantized(self, group_size: int | None = None,
                      bits: int | None = None, *, mode: str = 'affine',
@@ -99,12 +103,14 @@ class ConvTranspose3d(nn.Module):
         _init_kernel_params(self, in_channels, out_channels, self.spec, bias,
                             device, dtype)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return conv_transpose3d(x, self.weight, self.bias,
                                 kernel_size=self.spec.size,
                                 stride=self.spec.stride,
                                 padding=self.spec.padding,
-                                dilation=self.spec.dilation)
+                                dilation=self.spec.dilation,
+                                activation=activation)
 
     def to_quantized(self, group_size: int | None = None,
                      bits: int | None = None, *, mode: str = 'affine',
@@ -129,10 +135,12 @@ class GenerativeConvTranspose3d(nn.Module):
         _init_kernel_params(self, in_channels, out_channels, self.spec, bias,
                             device, dtype)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return generative_conv_transpose3d(x, self.weight, self.bias,
                                            kernel_size=self.spec.size,
-                                           stride=self.spec.stride)
+                                           stride=self.spec.stride,
+                                           activation=activation)
 
     def to_quantized(self, group_size: int | None = None,
                      bits: int | None = None, *, mode: str = 'affine',

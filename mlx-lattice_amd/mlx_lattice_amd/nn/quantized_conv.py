@@ -75,11 +75,12 @@ class QuantizedConv3d(_QuantizedConvBase):
 
     def forward(self, x: SparseTensor, *,
                 coordinates: SparseTensor | CoordinateMapKey | torch.Tensor
-                | None = None) -> SparseTensor:
+                | None = None,
+                activation: str | None = None) -> SparseTensor:
         return conv3d(x, self._quantized_weight(), self.bias,
                       kernel_size=self.spec.size, stride=self.spec.stride,
                       padding=self.spec.padding, dilation=self.spec.dilation,
-                      coordinates=coordinates)
+                      coordinates=coordinates, activation=activation)
 
     @classmethod
     def from_conv(cls, source: Conv3d, group_size: int | None = None,
@@ -104,10 +105,12 @@ class QuantizedSubmConv3d(_QuantizedConvBase):
                                    bias=bias, device=device, dtype=dtype),
                         group_size, bits)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return subm_conv3d(x, self._quantized_weight(), self.bias,
                            kernel_size=self.spec.size,
-                           dilation=self.spec.dilation)
+                           dilation=self.spec.dilation,
+                           activation=activation)
 
     @classmethod
     def from_conv(cls, source: SubmConv3d, group_size: int | None = None,
@@ -136,12 +139,14 @@ class QuantizedConvTranspose3d(_QuantizedConvBase):
                                         device=device, dtype=dtype),
                         group_size, bits)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return conv_transpose3d(x, self._quantized_weight(), self.bias,
                                 kernel_size=self.spec.size,
                                 stride=self.spec.stride,
                                 padding=self.spec.padding,
-                                dilation=self.spec.dilation)
+                                dilation=self.spec.dilation,
+                           activation=activation)
 
     @classmethod
     def from_conv(cls, source: ConvTranspose3d, group_size: int | None = None,
@@ -167,11 +172,13 @@ class QuantizedGenerativeConvTranspose3d(_QuantizedConvBase):
             stride=stride, bias=bias, device=device, dtype=dtype),
             group_size, bits)
 
-    def forward(self, x: SparseTensor) -> SparseTensor:
+    def forward(self, x: SparseTensor, *,
+                activation: str | None = None) -> SparseTensor:
         return generative_conv_transpose3d(x, self._quantized_weight(),
                                            self.bias,
                                            kernel_size=self.spec.size,
-                                           stride=self.spec.stride)
+                                           stride=self.spec.stride,
+                                           activation=activation)
 
     @classmethod
     def from_conv(cls, source: GenerativeConvTranspose3d,

@@ -70,19 +70,25 @@ def sparse_conv_features_from_relation(feats: torch.Tensor,
                                        weight: torch.Tensor,
                                        relation: KernelRelation,
                                        bias: torch.Tensor | None = None,
+                                       relu: bool = False,
                                        ) -> torch.Tensor:
     """Execute sparse convolution over a prebuilt relation
     (_relation_exec.py:84-116).  Differentiable in ``feats`` and ``weight``:
     the backward pass is the reference primitive's vjp
-    (native/features/convolution/primitive.cpp:137-176)."""
+    (native/features/convolution/primitive.cpp:137-176).  ``relu`` fuses a
+    ReLU after the bias into the store (the operators pass it only when
+    autograd does not need the activation)."""
     _require_static(relation)
     if torch.is_grad_enabled() and (feats.requires_grad
                                     or weight.requires_grad
                                     or (bias is not None
                                         and bias.requires_grad)):
+        if relu:
+            raise ValueError('a fused ReLU is not differentiable; apply it '
+                             'separately when gradients are needed.')
         out = _SparseConvFeatures.apply(feats, weight, relation)
         return out if bias is None else _add_bias(out, bias)
-    return _conv_features(feats, weight, relation, bias)
+    return _conv_features(feats, weight, relation, bias, relu)
 
 
 def _add_bias(feats: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
@@ -185,24 +191,27 @@ def sparse_conv_weight_grad_from_relation(feats: torch.Tensor,
 
 def _conv_features(feats: torch.Tensor, weight: torch.Tensor,
                    relation: KernelRelation,
-                   bias: torch.Tensor | None = None) -> torch.Tensor:
+                   bias: torch.Tensor | None = None,
+                   relu: bool = False) -> torch.Tensor:
     """Forward features on the matrix-core or the CSR route; ``bias``
     (optional) is added in the kernels' store, after the conv result is
-    rounded, exactly as a separate ``feats + bias``."""
+    rounded, exactly as a separate ``feats + bias``; ``relu`` then applies
+    ``maximum(v, 0)`` in the same store."""
     c_out = int(weight.shape[2] if weight.ndim == 3 else weight.shape[0])
     if feats.ndim == 2 and _expand_eligible(feats, c_out, relation):
         return ext.sparse_conv_features_expand(
             feats, weight, relation.contract.source_active_rows,
-            relation.n_kernels, bias=bias)
+            relation.n_kernels, bias=bias, relu=relu)
     if feats.ndim == 2 and _matrix_core_eligible(
             feats.dtype, int(feats.shape[1]), c_out, relation,
             int(feats.shape[0])):
         return sparse_conv_features_sorted_from_relation(feats, weight,
-                                                         relation, bias=bias)
+                                                         relation, bias=bias,
+                                                         relu=relu)
     return ext.sparse_conv_features_csr(
         feats, weight, relation.edges.in_rows, relation.edges.kernel_ids,
         relation.counts, relation.output_csr.row_offsets,
-        relation.n_out_capacity, relation.n_kernels, bias=bias)
+        relation.n_out_capacity, relation.n_kernels, bias=bias, relu=relu)
 
 
 def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
@@ -210,6 +219,7 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
                                               relation: KernelRelation, *,
                                               store_sorted: bool = False,
                                               bias: torch.Tensor | None = None,
+                                              relu: bool = False,
                                               ) -> torch.Tensor:
     """Matrix-core implicit GEMM over the sorted view
     (_relation_exec.py:119-156)."""
@@ -228,16 +238,18 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
         relation.edges.kernel_ids, relation.counts,
         relation.output_csr.row_offsets, None, None, None, None,
         relation.n_out_capacity, relation.n_kernels,
-        store_sorted=store_sorted, bias=bias, tile_order=view.tile_order())
+        store_sorted=store_sorted, bias=bias, tile_order=view.tile_order(),
+        relu=relu)
 
 
 def sparse_quantized_conv_features_from_relation(
         feats: torch.Tensor, weight: QuantizedWeight,
         relation: KernelRelation,
-        bias: torch.Tensor | None = None) -> torch.Tensor:
+        bias: torch.Tensor | None = None,
+        relu: bool = False) -> torch.Tensor:
     """Quantized sparse convolution over a prebuilt relation
     (_relation_exec.py:19-61); the sorted plan is passed when the matrix-core
-    route applies."""
+    route applies.  ``bias`` and ``relu`` are fused into the store."""
     _require_static(relation)
     if relation.n_kernels != weight.weight.shape[0]:
         raise ValueError('quantized weight kernel rows must match the relation.')
@@ -259,7 +271,7 @@ def sparse_quantized_conv_features_from_relation(
         relation.output_csr.row_offsets, kv, reorder, tiles,
         relation.n_out_capacity, relation.n_kernels, weight.in_channels,
         weight.out_channels, weight.storage_in_channels, weight.group_size,
-        weight.bits, bias=bias, tile_order=order)
+        weight.bits, bias=bias, tile_order=order, relu=relu)
 
 
 def sparse_pool_features_from_relation(feats: torch.Tensor,

@@ -42,7 +42,8 @@ def conv3d(x: SparseTensor, weight: torch.Tensor | QuantizedWeight,
            padding: int | Sequence[int] = 0,
            dilation: int | Sequence[int] = 1,
            coordinates: SparseTensor | CoordinateMapKey | torch.Tensor | None
-           = None) -> SparseTensor:
+           = None,
+           activation: str | None = None) -> SparseTensor:
     """Sparse 3D convolution (ops/conv.py:34-109).
 
     The pointwise 1x1x1 case without ``coordinates`` is a feature matmul that
@@ -50,12 +51,19 @@ def conv3d(x: SparseTensor, weight: torch.Tensor | QuantizedWeight,
     relation when ``coordinates`` is given) is built or reused and the
     features run through the native kernels.  Output stride is
     ``x.stride * stride``.
+
+    ``activation='relu'`` (not in the reference signature) applies the
+    reference's ``relu`` (``maximum(feats, 0)``, ops/feature.py:54-56) to the
+    result, fused into the conv kernels' store when autograd does not need
+    it; the result equals ``relu(conv3d(...))`` bit for bit.
     """
     spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
                       dilation=dilation)
     output_stride = _mul_stride(x.stride, spec.stride)
+    relu = _relu_requested(activation)
     if coordinates is None and spec.is_pointwise:
-        return x.replace(feats=_with_bias(_pointwise_features(x, weight), bias))
+        return x.replace(feats=_activate(
+            _with_bias(_pointwise_features(x, weight), bias), relu))
     if coordinates is not None:
         target_key = _target_key(x, coordinates, output_stride)
         reuse_input = target_key == x.coord_key
@@ -63,45 +71,55 @@ def conv3d(x: SparseTensor, weight: torch.Tensor | QuantizedWeight,
             x, _target_weight(weight, spec), bias, spec,
             map_kind='forward' if reuse_input else 'target',
             output_stride=target_key.stride, reuse_input_coords=reuse_input,
-            target_key=target_key)
+            target_key=target_key, relu=relu)
     return _relation_conv(x, weight, bias, spec, map_kind='forward',
-                          output_stride=output_stride)
+                          output_stride=output_stride, relu=relu)
 
 
 def subm_conv3d(x: SparseTensor, weight: torch.Tensor | QuantizedWeight,
                 bias: torch.Tensor | None = None, *,
                 kernel_size: int | Sequence[int] = 3,
-                dilation: int | Sequence[int] = 1) -> SparseTensor:
+                dilation: int | Sequence[int] = 1,
+                activation: str | None = None) -> SparseTensor:
     """Submanifold sparse convolution: odd kernel, stride 1, output reuses
-    the input coordinate identity (ops/conv.py:112-150)."""
+    the input coordinate identity (ops/conv.py:112-150).  ``activation`` as
+    for ``conv3d``."""
     spec = KernelSpec(size=kernel_size, stride=1, padding=0,
                       dilation=dilation)
     _require_odd_kernel(spec.size, 'subm_conv3d')
+    relu = _relu_requested(activation)
     if spec.size == (1, 1, 1) and spec.dilation == (1, 1, 1):
-        return x.replace(feats=_with_bias(_pointwise_features(x, weight), bias))
+        return x.replace(feats=_activate(
+            _with_bias(_pointwise_features(x, weight), bias), relu))
     return _relation_conv(x, weight, bias, spec, map_kind='submanifold',
-                          output_stride=x.stride, reuse_input_coords=True)
+                          output_stride=x.stride, reuse_input_coords=True,
+                          relu=relu)
 
 
 def conv_transpose3d(x: SparseTensor, weight, bias=None, *, kernel_size=2,
-                     stride=2, padding=0, dilation=1) -> SparseTensor:
+                     stride=2, padding=0, dilation=1,
+                     activation: str | None = None) -> SparseTensor:
     """Sparse transposed convolution over the transposed relation
     (ops/conv.py:153-186).  The output stride is ``x.stride / stride``; each
-    component of ``stride`` must divide the input stride."""
+    component of ``stride`` must divide the input stride.  ``activation``
+    as for ``conv3d``."""
     spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
                       dilation=dilation)
     return _relation_conv(x, weight, bias, spec, map_kind='transposed',
-                          output_stride=_div_stride(x.stride, spec.stride))
+                          output_stride=_div_stride(x.stride, spec.stride),
+                          relu=_relu_requested(activation))
 
 
 def generative_conv_transpose3d(x: SparseTensor, weight, bias=None, *,
-                                kernel_size=2, stride=2) -> SparseTensor:
+                                kernel_size=2, stride=2,
+                                activation: str | None = None) -> SparseTensor:
     """Transposed convolution whose output support is generated from every
     input row and offset (ops/conv.py:189-214): output row ``in * K + k``
-    at ``coord * stride + offset[k]``."""
+    at ``coord * stride + offset[k]``.  ``activation`` as for ``conv3d``."""
     spec = KernelSpec(size=kernel_size, stride=stride)
     return _relation_conv(x, weight, bias, spec, map_kind='generative',
-                          output_stride=_div_stride(x.stride, spec.stride))
+                          output_stride=_div_stride(x.stride, spec.stride),
+                          relu=_relu_requested(activation))
 
 
 # ------------------------------------------------------ execution policy --
@@ -110,7 +128,8 @@ def generative_conv_transpose3d(x: SparseTensor, weight, bias=None, *,
 def _relation_conv(x: SparseTensor, weight, bias, spec: KernelSpec, *,
                    map_kind: str, output_stride: Triple,
                    reuse_input_coords: bool = False,
-                   target_key: CoordinateMapKey | None = None) -> SparseTensor:
+                   target_key: CoordinateMapKey | None = None,
+                   relu: bool = False) -> SparseTensor:
     _validate_feature_dtype(x.feats, weight)
     _validate_gpu_coord_dtype(x)
     _validate_weight_for_kernel(x, weight, spec.volume)
@@ -122,13 +141,22 @@ def _relation_conv(x: SparseTensor, weight, bias, spec: KernelSpec, *,
     fuse = bias is not None and not (
         torch.is_grad_enabled() and bias.requires_grad)
     fused = bias if fuse else None
-    feats = (sparse_quantized_conv_features_from_relation(x.feats, weight,
-                                                          relation, fused)
+    # The ReLU joins the store when nothing needs its gradient and the bias
+    # (which comes first) is fused or absent.
+    needs_grad = torch.is_grad_enabled() and (
+        x.feats.requires_grad
+        or (isinstance(weight, torch.Tensor) and weight.requires_grad)
+        or (bias is not None and bias.requires_grad))
+    fuse_relu = relu and not needs_grad and (bias is None or fuse)
+    feats = (sparse_quantized_conv_features_from_relation(
+                 x.feats, weight, relation, fused, relu=fuse_relu)
              if isinstance(weight, QuantizedWeight)
-             else sparse_conv_features_from_relation(x.feats, weight, relation,
-                                                     fused))
+             else sparse_conv_features_from_relation(
+                 x.feats, weight, relation, fused, relu=fuse_relu))
     if not fuse:
         feats = _with_bias(feats, bias)
+    if relu and not fuse_relu:
+        feats = _activate(feats, True)
     if reuse_input_coords:
         return x.replace(feats=feats)
     if relation.out_coords is None:
@@ -273,6 +301,24 @@ def _validate_weight_for_kernel(x: SparseTensor, weight,
     if int(weight.shape[1] * weight.shape[2] * weight.shape[3]) != kernel_rows:
         raise ValueError(
             'weight kernel rows must match the convolution kernel.')
+
+
+def _relu_requested(activation: str | None) -> bool:
+    if activation is None:
+        return False
+    if activation != 'relu':
+        raise ValueError("activation must be None or 'relu'.")
+    return True
+
+
+def _activate(feats: torch.Tensor, relu: bool) -> torch.Tensor:
+    """The reference's ``relu`` (``maximum(feats, 0)``, ops/feature.py:54-56):
+    v where v > 0 or v is NaN, +0 otherwise (the fused store's rule)."""
+    if not relu:
+        return feats
+    keep = (feats > 0) | torch.isnan(feats)
+    return torch.where(keep, feats, torch.zeros((), dtype=feats.dtype,
+                                                device=feats.device))
 
 
 def _with_bias(feats: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:

@@ -176,12 +176,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
           py::arg("in_row_offsets"), py::arg("in_edge_ids"), py::arg("kernel_row_offsets"),
           py::arg("kernel_edge_ids"), py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(),
-          py::arg("bias") = py::none());
+          py::arg("bias") = py::none(), py::arg("relu") = false);
     m.def("sparse_conv_features_expand", &ln::sparse_conv_features_expand, py::arg("feats"), py::arg("weights"),
-          py::arg("active_rows"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none());
+          py::arg("active_rows"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none(),
+          py::arg("relu") = false);
     m.def("sparse_conv_features_csr", &ln::sparse_conv_features_csr, py::arg("feats"), py::arg("weights"),
           py::arg("in_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
-          py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none());
+          py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none(),
+          py::arg("relu") = false);
     m.def(
         "sparse_conv_features_sorted_implicit_gemm",
         [](const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& sorted_out_in_map,
@@ -192,24 +194,25 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            const py::object& /*counts*/, const py::object& /*row_offsets*/, const py::object& /*in_row_offsets*/,
            const py::object& /*in_edge_ids*/, const py::object& /*kernel_row_offsets*/,
            const py::object& /*kernel_edge_ids*/, int out_capacity, int n_kernels, bool store_sorted,
-           const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& tile_order) {
+           const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& tile_order, bool relu) {
             return ln::sparse_conv_features_sorted_implicit_gemm(feats, weights, sorted_out_in_map,
                                                                  sorted_kv_out_in_map, reorder_rows, tile_masks,
                                                                  out_capacity, n_kernels, store_sorted, bias,
-                                                                 tile_order);
+                                                                 tile_order, relu);
         },
         py::arg("feats"), py::arg("weights"), py::arg("sorted_out_in_map"), py::arg("sorted_kv_out_in_map"),
         py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("in_rows"), py::arg("out_rows"),
         py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("in_row_offsets"),
         py::arg("in_edge_ids"), py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("out_capacity"),
         py::arg("n_kernels"), py::arg("store_sorted") = false, py::kw_only(), py::arg("bias") = py::none(),
-        py::arg("tile_order") = py::none());
+        py::arg("tile_order") = py::none(), py::arg("relu") = false);
     m.def("sparse_quantized_conv_features", &ln::sparse_quantized_conv_features, py::arg("feats"),
           py::arg("weights"), py::arg("scales"), py::arg("biases"), py::arg("in_rows"), py::arg("out_rows"),
           py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("sorted_kv_out_in_map"),
           py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("out_capacity"), py::arg("n_kernels"),
           py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"), py::arg("group_size"),
-          py::arg("bits"), py::kw_only(), py::arg("bias") = py::none(), py::arg("tile_order") = py::none());
+          py::arg("bits"), py::kw_only(), py::arg("bias") = py::none(), py::arg("tile_order") = py::none(),
+          py::arg("relu") = false);
     m.def("conv_tile_order", &ln::conv_tile_order, py::arg("tile_masks"), py::arg("out_capacity"),
           "Longest-first order of the sorted view's 128-row tiles, for the matrix-core conv's tile_order.");
 

@@ -71,7 +71,7 @@ at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& we
                                 const at::Tensor& row_offsets, const at::Tensor& in_row_offsets,
                                 const at::Tensor& in_edge_ids, const at::Tensor& kernel_row_offsets,
                                 const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels,
-                                const std::optional<at::Tensor>& bias) {
+                                const std::optional<at::Tensor>& bias, bool relu) {
     const char* op = "sparse_conv_features";
     if (out_capacity < 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
@@ -122,14 +122,14 @@ at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& we
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(), b,
-        current_stream(feats)));
+        relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, current_stream(feats)));
     return out;
 }
 
 at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor& weights_in, const at::Tensor& in_rows,
                                     const at::Tensor& kernel_ids, const at::Tensor& counts,
                                     const at::Tensor& row_offsets, int out_capacity, int n_kernels,
-                                    const std::optional<at::Tensor>& bias) {
+                                    const std::optional<at::Tensor>& bias, bool relu) {
     const char* op = "sparse_conv_features";
     if (out_capacity < 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
@@ -158,13 +158,13 @@ at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), out_capacity, out.data_ptr(), b,
-        current_stream(feats)));
+        relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, current_stream(feats)));
     return out;
 }
 
 at::Tensor sparse_conv_features_expand(const at::Tensor& feats_in, const at::Tensor& weights_in,
                                        const at::Tensor& active_rows, int n_kernels,
-                                       const std::optional<at::Tensor>& bias) {
+                                       const std::optional<at::Tensor>& bias, bool relu) {
     const char* op = "sparse_conv_features_expand";
     validate_weights(feats_in, weights_in, n_kernels, op);
     if (active_rows.dim() != 1 || active_rows.size(0) != 1 || active_rows.scalar_type() != at::kInt) {
@@ -182,7 +182,7 @@ at::Tensor sparse_conv_features_expand(const at::Tensor& feats_in, const at::Ten
     check_status(lattice_hip_sparse_conv_features_expand(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(rows), ci32(active_rows),
         static_cast<int>(feats.size(1)), weights.data_ptr(), n_kernels, static_cast<int>(c_out), out.data_ptr(), b,
-        current_stream(feats)));
+        relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, current_stream(feats)));
     return out;
 }
 
@@ -212,7 +212,7 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                                      int out_capacity, int n_kernels, bool store_sorted,
                                                      const std::optional<at::Tensor>& bias,
-                                                     const std::optional<at::Tensor>& tile_order) {
+                                                     const std::optional<at::Tensor>& tile_order, bool relu) {
     const char* op = "sparse_conv_features_sorted_implicit_gemm";
     if (sorted_out_in_map.dim() != 2 || sorted_out_in_map.scalar_type() != at::kInt) {
         throw std::invalid_argument("sorted_out_in_map must have shape (N_out, K) and int32 dtype.");
@@ -251,7 +251,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(kv), ci32(tiles),
-        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), b, ws.data_ptr(), ws_bytes,
+        store_sorted ? nullptr : ci32(order), out_capacity, out.data_ptr(), b,
+        relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, ws.data_ptr(), ws_bytes,
         current_stream(feats)));
     return out;
 }
@@ -278,7 +279,7 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits,
                                           const std::optional<at::Tensor>& bias,
-                                          const std::optional<at::Tensor>& tile_order) {
+                                          const std::optional<at::Tensor>& tile_order, bool relu) {
     if (out_capacity < 0 || n_kernels <= 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
     }
@@ -359,7 +360,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
         n_kernels, out_channels, storage_in_channels, group_size, bits, ci32(in_rows), ci32(kernel_ids),
         ci32(counts), static_cast<int>(in_rows.size(0)), ci32(row_offsets), has_plan ? ci32(kv) : nullptr,
         has_plan ? ci32(tiles) : nullptr, has_plan ? ci32(order) : nullptr, out_capacity, out.data_ptr(), b,
-        has_plan ? ws.data_ptr() : nullptr, ws_bytes, current_stream(feats)));
+        relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, has_plan ? ws.data_ptr() : nullptr, ws_bytes,
+        current_stream(feats)));
     return out;
 }
 

@@ -15,20 +15,20 @@ at::Tensor sparse_conv_features(const at::Tensor& feats, const at::Tensor& weigh
                                 const at::Tensor& row_offsets, const at::Tensor& in_row_offsets,
                                 const at::Tensor& in_edge_ids, const at::Tensor& kernel_row_offsets,
                                 const at::Tensor& kernel_edge_ids, int out_capacity, int n_kernels,
-                                const std::optional<at::Tensor>& bias = std::nullopt);
+                                const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false);
 
 // The CSR conv without the grouped plan views the reference signature
 // carries for its gradient (the forward reads only the output CSR).
 at::Tensor sparse_conv_features_csr(const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& in_rows,
                                     const at::Tensor& kernel_ids, const at::Tensor& counts,
                                     const at::Tensor& row_offsets, int out_capacity, int n_kernels,
-                                    const std::optional<at::Tensor>& bias = std::nullopt);
+                                    const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false);
 
 // Dense expansion conv over a direct generative / transposed relation:
 // (rows * K, C_out), output row in * K + k = feats[in] @ W[k].
 at::Tensor sparse_conv_features_expand(const at::Tensor& feats, const at::Tensor& weights,
                                        const at::Tensor& active_rows, int n_kernels,
-                                       const std::optional<at::Tensor>& bias = std::nullopt);
+                                       const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false);
 
 at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, const at::Tensor& weights,
                                                      const at::Tensor& sorted_out_in_map,
@@ -36,7 +36,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, co
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                                      int out_capacity, int n_kernels, bool store_sorted,
                                                      const std::optional<at::Tensor>& bias = std::nullopt,
-                                                     const std::optional<at::Tensor>& tile_order = std::nullopt);
+                                                     const std::optional<at::Tensor>& tile_order = std::nullopt,
+                                          bool relu = false);
 
 at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Tensor& weights,
                                           const at::Tensor& scales, const at::Tensor& biases,
@@ -47,7 +48,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits,
                                           const std::optional<at::Tensor>& bias = std::nullopt,
-                                          const std::optional<at::Tensor>& tile_order = std::nullopt);
+                                          const std::optional<at::Tensor>& tile_order = std::nullopt,
+                                          bool relu = false);
 
 // Longest-first order of the 128-row tiles of a sorted view
 // (lattice_hip_conv_tile_order), kept with the view and passed back as

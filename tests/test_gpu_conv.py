@@ -332,11 +332,11 @@ def test_tile_schedule_does_not_change_results():
     lib.lattice_hip_conv_workspace_bytes.restype = ctypes.c_size_t
     P, I = ctypes.c_void_p, ctypes.c_int
     sorted_conv = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm
-    sorted_conv.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P, P,
+    sorted_conv.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P, I, P,
                             ctypes.c_size_t, P]
     quant_conv = lib.lattice_hip_sparse_quantized_conv_features
     quant_conv.argtypes = [I, P, I, I, P, P, P, I, I, I, I, I, P, P, P, I, P,
-                           P, P, P, I, P, P, P, ctypes.c_size_t, P]
+                           P, P, P, I, P, P, I, P, ctypes.c_size_t, P]
     coords, rng = _shell(30000, 128, 31)
     n = len(coords)
     c = torch.as_tensor(coords, dtype=torch.int32).to(DEV)
@@ -359,7 +359,7 @@ def test_tile_schedule_does_not_change_results():
             assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1,
                                27, c_out, kv.data_ptr(), tiles.data_ptr(),
                                reorder.data_ptr(), n, out.data_ptr(), None,
-                               workspace, nbytes, stream) == 0
+                               0, workspace, nbytes, stream) == 0
             outs.append(out)
         torch.cuda.synchronize()
         assert torch.equal(outs[0], outs[1]), c_out
@@ -374,7 +374,7 @@ def test_tile_schedule_does_not_change_results():
                               rel[5].data_ptr(), int(rel[0].shape[0]),
                               rel[3].data_ptr(), kv.data_ptr(),
                               tiles.data_ptr(), reorder.data_ptr(), n,
-                              out.data_ptr(), None, workspace, nbytes,
+                              out.data_ptr(), None, 0, workspace, nbytes,
                               stream) == 0
             qouts.append(out)
         torch.cuda.synchronize()
@@ -386,7 +386,7 @@ def test_tile_schedule_does_not_change_results():
         out = torch.empty((n, c_out), dtype=torch.float16, device=DEV)
         assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27,
                            c_out, kv.data_ptr(), tiles.data_ptr(),
-                           reorder.data_ptr(), n, out.data_ptr(), None,
+                           reorder.data_ptr(), n, out.data_ptr(), None, 0,
                            order.data_ptr(), ready, stream) == 0
         torch.cuda.synchronize()
         assert torch.equal(out, outs[0]), c_out
@@ -394,7 +394,7 @@ def test_tile_schedule_does_not_change_results():
     out = torch.empty((n, 128), dtype=torch.float16, device=DEV)
     assert sorted_conv(1, feats.data_ptr(), n, 64, w.data_ptr(), 1, 27, 128,
                        kv.data_ptr(), tiles.data_ptr(), reorder.data_ptr(), n,
-                       out.data_ptr(), None, ws.data_ptr(), 4, stream) == 1
+                       out.data_ptr(), None, 0, ws.data_ptr(), 4, stream) == 1
 
 
 # -------------------------------------------------------- fused bias ----
@@ -437,3 +437,84 @@ def test_fused_bias_equals_separate_add(dtype, c_in, c_out, quant, kind):
         plain = ops.conv3d(x, wt, kernel_size=2, stride=2)
     torch.cuda.synchronize()
     assert torch.equal(fused.feats, plain.feats + b)
+
+
+# -------------------------------------------------------- fused ReLU ----
+
+
+def _bits(t):
+    return t.view(torch.int32 if t.dtype == torch.float32 else torch.int16)
+
+
+@pytest.mark.parametrize('dtype,c_in,c_out,quant,kind', [
+    (torch.float16, 64, 128, None, 'subm'),      # matrix cores
+    (torch.bfloat16, 128, 256, None, 'subm'),    # C_out = 256: two column halves
+    (torch.float16, 32, 16, None, 'subm'),       # C_out = 16 shape
+    (torch.float16, 64, 128, None, 'down'),      # k2s2: rows past the active count hold relu(bias)
+    (torch.float32, 16, 32, None, 'subm'),       # CSR rows (staged weights)
+    (torch.float16, 24, 40, None, 'subm'),       # CSR fp16
+    (torch.float16, 64, 64, 8, 'subm'),          # quantized, matrix cores
+    (torch.float16, 4, 32, 8, 'subm'),           # quantized CSR (staged weights)
+    (torch.float16, 64, 64, None, 'expand'),     # generative transposed: dense expansion
+])
+def test_fused_relu_equals_separate_relu(dtype, c_in, c_out, quant, kind):
+    """activation='relu' in the conv store equals the reference's
+    maximum(feats, 0) over the stored conv + bias, bit for bit on every
+    capacity row: NaN kept, negatives and -0 stored as +0."""
+    from mlx_lattice_amd import quantize_weight
+    from mlx_lattice_amd.ops.conv import _activate
+
+    ops, _ = _imports()
+    coords, rng = _shell(20000, 128, 57 + c_in + c_out)
+    feats = rng.standard_normal((len(coords), c_in)).astype(np.float32)
+    feats[::997, 0] = np.nan
+    ks = 3 if kind == 'subm' else 2
+    w = (rng.standard_normal((c_out, ks, ks, ks, c_in))
+         / np.sqrt(ks ** 3 * c_in)).astype(np.float32)
+    b = torch.as_tensor(rng.standard_normal(c_out).astype(np.float32)).to(
+        DEV, dtype)
+    x = _tensor(coords, feats, stride=2 if kind == 'expand' else 1).astype(
+        dtype)
+    wt = torch.as_tensor(w).to(DEV, dtype)
+    if quant:
+        wt = quantize_weight(wt, group_size=32, bits=quant)
+    print(f'fused relu {dtype} {c_in}->{c_out} quant={quant} {kind}',
+          flush=True)
+    if kind == 'subm':
+        run = lambda **kw: ops.subm_conv3d(x, wt, b, kernel_size=3, **kw)  # noqa: E731
+    elif kind == 'down':
+        run = lambda **kw: ops.conv3d(x, wt, b, kernel_size=2, stride=2, **kw)  # noqa: E731
+    else:
+        run = lambda **kw: ops.generative_conv_transpose3d(  # noqa: E731
+            x, wt, b, kernel_size=2, stride=2, **kw)
+    fused = run(activation='relu').feats
+    plain = run().feats
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(fused), _bits(_activate(plain, True)))
+    assert torch.isnan(plain).any() and torch.equal(torch.isnan(fused),
+                                                    torch.isnan(plain))
+    finite = fused[~torch.isnan(fused)]
+    assert not (finite < 0).any() and not torch.signbit(finite).any()
+
+
+def test_relu_activation_under_autograd():
+    """With gradients needed the ReLU runs separately (autograd sees it) and
+    gives the fused store's values."""
+    ops, _ = _imports()
+    coords, rng = _shell(8000, 96, 61)
+    feats = rng.standard_normal((len(coords), 32)).astype(np.float32)
+    w = torch.as_tensor((rng.standard_normal((32, 3, 3, 3, 32)) * 0.05)
+                        .astype(np.float32)).to(DEV, torch.float16)
+    b = torch.linspace(-1, 1, 32, device=DEV, dtype=torch.float16)
+    x = _tensor(coords, feats).astype(torch.float16)
+    with torch.no_grad():
+        ref = ops.subm_conv3d(x, w, b, kernel_size=3, activation='relu').feats
+    xg = x.replace(feats=x.feats.clone().requires_grad_())
+    wg = w.clone().requires_grad_()
+    out = ops.subm_conv3d(xg, wg, b, kernel_size=3, activation='relu').feats
+    out.float().sum().backward()
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out.detach()), _bits(ref))
+    assert xg.feats.grad is not None and wg.grad is not None
+    with pytest.raises(ValueError, match='activation'):
+        ops.subm_conv3d(x, w, b, kernel_size=3, activation='gelu')

@@ -68,12 +68,12 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == 1 and b'outputs' in lib.lattice_hip_last_error()
     rc = lib.lattice_hip_sparse_quantized_conv_features(
         1, None, 0, 16, None, None, None, 27, 16, 16, 16, 4, None, None, None,
-        0, None, None, None, None, 0, None, None, None, ctypes.c_size_t(0),
+        0, None, None, None, None, 0, None, None, 0, None, ctypes.c_size_t(0),
         None)
     assert rc == 1 and b'group_size' in lib.lattice_hip_last_error()
     rc = lib.lattice_hip_sparse_conv_features(
         7, None, 0, 16, None, 0, 27, 16, None, None, None, 0, None, 0, None,
-        None, None)
+        None, 0, None)
     assert rc == 1 and b'float' in lib.lattice_hip_last_error()
 
 

@@ -29,21 +29,22 @@ def _lib():
     P, I = ctypes.c_void_p, ctypes.c_int
     lib.lattice_hip_conv_workspace_bytes.restype = ctypes.c_size_t
     lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm.argtypes = [
-        I, P, I, I, P, I, I, I, P, P, P, I, P, P, P, ctypes.c_size_t, P]
+        I, P, I, I, P, I, I, I, P, P, P, I, P, P, I, P, ctypes.c_size_t, P]
     lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc.argtypes = [
-        I, P, I, I, P, I, I, I, P, P, P, I, P, P, P]
+        I, P, I, I, P, I, I, I, P, P, P, I, P, P, I, P]
     lib.lattice_hip_last_error.restype = ctypes.c_char_p
     return lib
 
 
-def _case(lib, n, grid, seed, c_in, c_out):
+def _case(lib, n, grid, seed, c_in, c_out, epilogue=0):
     from mlx_lattice_amd._native import ext
     from mlx_lattice_amd.synthetic import sphere_shell_cloud
 
     rng = np.random.default_rng(seed)
     coords = sphere_shell_cloud(n, grid, rng=rng)
     n = len(coords)
-    print(f'no-alloc conv case n={n} c_in={c_in} c_out={c_out}', flush=True)
+    print(f'no-alloc conv case n={n} c_in={c_in} c_out={c_out} '
+          f'epilogue={epilogue}', flush=True)
     c = torch.as_tensor(coords).to(DEV)
     active = torch.full((1,), n, dtype=torch.int32, device=DEV)
     rel = ext.build_submanifold_kernel_relation_with_view(c, active, [3, 3, 3],
@@ -61,10 +62,10 @@ def _case(lib, n, grid, seed, c_in, c_out):
     args = (1, feats.data_ptr(), n, c_in, w.data_ptr(), 1, 27, c_out,
             kv.data_ptr(), tiles.data_ptr(), reorder.data_ptr(), n)
     assert lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm(
-        *args, ref.data_ptr(), bias.data_ptr(), ws.data_ptr(), wsb,
+        *args, ref.data_ptr(), bias.data_ptr(), epilogue, ws.data_ptr(), wsb,
         stream) == 0
     rc = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
-        *args, got.data_ptr(), bias.data_ptr(), stream)
+        *args, got.data_ptr(), bias.data_ptr(), epilogue, stream)
     assert rc == 0, lib.lattice_hip_last_error()
     torch.cuda.synchronize()
     assert not torch.isnan(got).any()
@@ -76,12 +77,13 @@ def test_noalloc_conv_matches_workspace_entry():
     _case(lib, 60000, 160, 5, 64, 128)     # first call
     _case(lib, 9000, 96, 6, 32, 64)        # second call, smaller
     _case(lib, 20000, 128, 7, 64, 256)     # two launches share one schedule
+    _case(lib, 12000, 128, 8, 64, 128, 1)  # with the fused ReLU
 
 
 def test_noalloc_conv_rejects_oversized_launches():
     lib = _lib()
     rc = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
         1, None, 0, 64, None, 1, 27, 64, None, None, None, MAX_ROWS + 1,
-        None, None, None)
+        None, None, 0, None)
     assert rc != 0
     assert b'allocation-free' in lib.lattice_hip_last_error()
