@@ -77,7 +77,7 @@ template <typename T> struct Epilogue {
         return v;
     }
     // The epilogue of output channels co0 .. (a column slice of the output).
-    Epilogue shifted(int co0) const { return Epilogue{bias != nullptr ? bias + co0 : nullptr, relu}; }
+    __host__ __device__ Epilogue shifted(int co0) const { return Epilogue{bias != nullptr ? bias + co0 : nullptr, relu}; }
 };
 
 template <typename T> Epilogue<T> epilogue_of(const void* bias, int flags) {
@@ -847,11 +847,26 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
     __syncthreads();
 }
 
+// A column half of the weight: output channels co_base .. co_base + 127.
+template <typename T> __host__ __device__ FloatB<T> column_half(const FloatB<T>& b, int co_base) {
+    FloatB<T> h = b;
+    h.w += co_base * b.s_co;
+    return h;
+}
+template <typename T> __host__ __device__ PackedB<T> column_half(const PackedB<T>& b, int co_base) {
+    PackedB<T> h = b;  // c_out stays the row stride of the packed arrays
+    h.w += co_base;
+    h.scales += co_base;
+    h.biases += co_base;
+    return h;
+}
+
 template <typename T, typename S, typename BSource>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const int32_t* __restrict__ kv_map,
            const int32_t* __restrict__ tile_masks, const int32_t* __restrict__ reorder_rows, int rows,
-           const int32_t* __restrict__ block_order, T* __restrict__ out, Epilogue<T> epi, int out_ld) {
+           const int32_t* __restrict__ block_order, T* __restrict__ out, Epilogue<T> epi, int out_ld,
+           int halves) {
     using V = typename MfmaOps<T>::vec;
     constexpr int WAVES = S::WAVES;
     constexpr int WAVE_ROWS = S::WAVE_ROWS;
@@ -867,8 +882,16 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     const int wr = wave / S::CG;
     const int wc = wave % S::CG;
     // block_order (optional) lists the row tiles longest-first, so the
-    // costliest tiles start early and the launch drains evenly.
-    const int tile = block_order != nullptr ? block_order[blockIdx.x] : static_cast<int>(blockIdx.x);
+    // costliest tiles start early and the launch drains evenly.  With two
+    // column halves (C_out = 256) consecutive blocks take the two halves of
+    // one tile, so the second gathers rows the first just brought into L2.
+    const int slot = halves > 1 ? static_cast<int>(blockIdx.x) / 2 : static_cast<int>(blockIdx.x);
+    if (halves > 1 && (blockIdx.x & 1u)) {
+        bsrc = column_half(bsrc, C_OUT);
+        out += C_OUT;
+        epi = epi.shifted(C_OUT);
+    }
+    const int tile = block_order != nullptr ? block_order[slot] : slot;
     const int block_row0 = tile * S::BLOCK_ROWS;
     const int row0 = block_row0 + wr * WAVE_ROWS;
     const int quarters = ((rows + 63) / 64) * 4;
@@ -1226,7 +1249,7 @@ schedule_tiles(const int32_t* __restrict__ tile_masks, int rows, int nblocks, in
 template <typename T, typename S, typename BSource>
 int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule,
-                       T* out, Epilogue<T> epi, hipStream_t stream, bool scheduled, int out_ld = S::C_OUT) {
+                       T* out, Epilogue<T> epi, hipStream_t stream, bool scheduled, int halves = 1) {
     static_assert(S::BLOCK_ROWS == kOrderTileRows, "every shape uses the tile order's 128-row tiles");
     const int blocks = (rows + S::BLOCK_ROWS - 1) / S::BLOCK_ROWS;
     if (blocks > kMaxScheduledTiles) schedule = nullptr;
@@ -1234,24 +1257,11 @@ int launch_igemm_shape(const T* feats, int n_in, int c_in, const BSource& b, con
         schedule_tiles<S::BLOCK_ROWS / 16><<<1, kScheduleThreads, 0, stream>>>(tile_masks, rows, blocks, schedule);
         LATTICE_LAUNCH_CHECK();
     }
-    conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks), S::THREADS, 0, stream>>>(
-        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, epi, out_ld);
+    conv_igemm<T, S, BSource><<<static_cast<unsigned>(blocks * halves), S::THREADS, 0, stream>>>(
+        feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, epi, S::C_OUT * halves,
+        halves);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
-}
-
-// A column half of the weight: output channels co_base .. co_base + 127.
-template <typename T> FloatB<T> column_half(const FloatB<T>& b, int co_base) {
-    FloatB<T> h = b;
-    h.w += co_base * b.s_co;
-    return h;
-}
-template <typename T> PackedB<T> column_half(const PackedB<T>& b, int co_base) {
-    PackedB<T> h = b;  // c_out stays the row stride of the packed arrays
-    h.w += co_base;
-    h.scales += co_base;
-    h.biases += co_base;
-    return h;
 }
 
 template <typename T, typename BSource>
@@ -1265,7 +1275,7 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
 // Default shape: 32-row wave tiles, four waves, 64-channel stages (the
 // smaller B tile and register set let three blocks share a CU); c_out = 16
 // keeps 128-channel stages so its B tile still covers every thread.
-// c_out = 256 runs the 128-column shape twice (below).
+// c_out = 256 runs the 128-column shape over both column halves (below).
 // c_out 32..128 gather A in whole lines through LDS (ALDS), three blocks
 // per CU (float and packed weights alike: the packed tile's dequantisation
 // from vector loads of consecutive output channels fits the registers).
@@ -1279,20 +1289,13 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
         LATTICE_IGEMM_CASE(32)
         LATTICE_IGEMM_CASE(64)
         LATTICE_IGEMM_CASE(128)
-    case 256: {
-        // Two launches of the 128-column kernel, each writing its half of
-        // every output row (row stride 256): its occupancy and B tile beat
-        // the 8-wave 256-column shape, at the cost of gathering A twice.
-        using S128 = IgemmShape<128, 32, 4, 64, 1, false, kAldsOcc, 128, false, true>;
-        for (int h = 0; h < 2; ++h) {
-            const int rc = launch_igemm_shape<T, S128>(feats, n_in, c_in, column_half(b, h * 128), kv_map,
-                                                      tile_masks, reorder_rows, rows, schedule, out + h * 128,
-                                                      epi.shifted(h * 128), stream,
-                                                      ready || h == 1, 256);
-            if (rc != LATTICE_OK) return rc;
-        }
-        return LATTICE_OK;
-    }
+    case 256:
+        // One launch of the 128-column kernel over both column halves of
+        // every tile (row stride 256): its occupancy and B tile beat the
+        // 8-wave 256-column shape, at the cost of gathering A twice, and
+        // the two halves of a tile run back to back.
+        return launch_igemm_shape<T, IgemmShape<128, 32, 4, 64, 1, false, kAldsOcc, 128, false, true>>(
+            feats, n_in, c_in, b, kv_map, tile_masks, reorder_rows, rows, schedule, out, epi, stream, ready, 2);
 #undef LATTICE_IGEMM_CASE
 #undef LATTICE_IGEMM_LAUNCH
     default:
