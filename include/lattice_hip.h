@@ -92,7 +92,9 @@ enum lattice_epilogue_flags {
  * kept for ABI stability and is never set. */
 enum lattice_relation_flags {
     LATTICE_STATUS_COORD_RANGE = 1,   /* unused: no coordinate is out of range */
-    LATTICE_STATUS_REPEATED_EDGE = 2  /* transposed relation: two edges share (out_row, kernel_id) */
+    LATTICE_STATUS_REPEATED_EDGE = 2, /* transposed relation: two edges share (out_row, kernel_id) */
+    LATTICE_STATUS_REPEATED_PAIR = 4, /* transposed dense map: two edges share (in_row, kernel_id) */
+    LATTICE_STATUS_REPEATED_COORD = 8 /* submanifold relation: an active row repeats an earlier row's coordinate */
 };
 
 /* Packed-key range: a key with batch in [0, LATTICE_MAX_BATCH] and axes in
@@ -432,13 +434,19 @@ int lattice_hip_sparse_conv_input_grad(
  * [in_capacity, ceil(K/32)] its offset bits, in the layout of
  * build_relation_implicit_gemm_view (relations.cpp:498-538).  The sorted
  * view of this map and the implicit-GEMM conv with the weight transposed to
- * (C_in, Kx, Ky, Kz, C_out) then give the input gradient.  Requires at most
- * one output row per (input row, k), which forward and submanifold
- * relations guarantee. */
+ * (C_in, Kx, Ky, Kz, C_out) then give the input gradient when every
+ * (input row, k) has at most one output row.  A submanifold relation over
+ * repeated coordinates breaks that (each copy of a coordinate is an output
+ * row with the same neighbours): status (int32[1], optional) is cleared
+ * and gets LATTICE_STATUS_REPEATED_PAIR when two edges share (in_row, k),
+ * and in_out_map then holds one of their output rows (the relation build's
+ * LATTICE_STATUS_REPEATED_COORD announces this case in advance; such a
+ * relation's input gradient takes lattice_hip_sparse_conv_input_grad). */
 int lattice_hip_build_transposed_implicit_gemm_map(
     const int32_t* in_rows, const int32_t* out_rows, const int32_t* kernel_ids,
     const int32_t* counts, int edge_capacity, int in_capacity,
-    int kernel_count, int32_t* in_out_map, int32_t* row_masks, void* stream);
+    int kernel_count, int32_t* in_out_map, int32_t* row_masks,
+    int32_t* status, void* stream);
 
 /* Weight gradient of the float conv (SparseConvFeaturesWeightGrad,
  * primitive.cpp:403-440, 641-680; cpu/algorithms.cpp:413-481):

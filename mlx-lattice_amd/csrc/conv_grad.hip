@@ -111,14 +111,15 @@ input_grad_csr(const T* __restrict__ cot, int out_capacity, const T* __restrict_
 __global__ void __launch_bounds__(256)
 transposed_map(const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                const int32_t* __restrict__ kernel_ids, const int32_t* __restrict__ counts, int edge_capacity,
-               int in_capacity, int K, int32_t* __restrict__ in_out_map) {
+               int in_capacity, int K, int32_t* __restrict__ in_out_map, int32_t* __restrict__ status) {
     const int E = min(counts[0], edge_capacity);
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
         const int in = in_rows[e];
         const int o = out_rows[e];
         const int k = kernel_ids[e];
         if (in < 0 || in >= in_capacity || o < 0 || k < 0 || k >= K) continue;
-        in_out_map[static_cast<long long>(in) * K + k] = o;
+        const int prev = atomicCAS(&in_out_map[static_cast<long long>(in) * K + k], -1, o);
+        if (prev != -1 && status != nullptr) atomicOr(status, LATTICE_STATUS_REPEATED_PAIR);
     }
 }
 
@@ -552,9 +553,13 @@ extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_
                                                              const int32_t* kernel_ids, const int32_t* counts,
                                                              int edge_capacity, int in_capacity, int kernel_count,
                                                              int32_t* in_out_map, int32_t* row_masks,
-                                                             void* stream_ptr) {
+                                                             int32_t* status, void* stream_ptr) {
     LATTICE_REQUIRE(edge_capacity >= 0 && in_capacity >= 0 && kernel_count > 0,
                     "transposed map shapes must be nonnegative with a positive kernel count.");
+    if (status != nullptr) {
+        const int rc = fill_i32(status, 1, 0, as_stream(stream_ptr));
+        if (rc != LATTICE_OK) return rc;
+    }
     if (in_capacity == 0) return LATTICE_OK;
     LATTICE_REQUIRE(in_out_map && row_masks && counts && (edge_capacity == 0 || (in_rows && out_rows && kernel_ids)),
                     "transposed map pointers must be non-null.");
@@ -564,7 +569,7 @@ extern "C" int lattice_hip_build_transposed_implicit_gemm_map(const int32_t* in_
     if (rc != LATTICE_OK) return rc;
     if (edge_capacity > 0) {
         transposed_map<<<grid_for(edge_capacity, 256, 1u << 16), 256, 0, stream>>>(
-            in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, in_out_map);
+            in_rows, out_rows, kernel_ids, counts, edge_capacity, in_capacity, kernel_count, in_out_map, status);
         LATTICE_LAUNCH_CHECK();
     }
     // At most 64 KB of map rows per block, and at most one row per lane.

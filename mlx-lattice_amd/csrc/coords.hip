@@ -350,7 +350,20 @@ struct QueryArgs {
     int32_t* degrees;            // [out_capacity] or null
     int32_t* block_totals;       // [ceil(out_capacity / kQueryRows)] or null
     const int32_t* out_buckets;  // 2x2x2 stride-2 downsample: bucket of each output cell, else null
+    // Submanifold relations: status word that gets LATTICE_STATUS_REPEATED_COORD
+    // when an active row's self lookup (offset index `center`, the zero
+    // offset) finds an earlier row with the same coordinate; else null.
+    int32_t* repeat_status;
+    int center;
 };
+
+// Flags a repeated coordinate seen by any lane of the wave (one atomic).
+__device__ inline void flag_repeats(int32_t* status, bool repeated) {
+    const uint64_t any = ballot(repeated);
+    if (any != 0 && lane_id() == __ffsll(static_cast<long long>(any)) - 1) {
+        atomicOr(status, LATTICE_STATUS_REPEATED_COORD);
+    }
+}
 
 template <int kLanes>
 __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
@@ -390,6 +403,7 @@ __global__ void __launch_bounds__(kThreads) query_map(QueryArgs a) {
                 if (block_of(oc.x, x, y, z, &block_key, &octant)) found = a.table.find(block_key, octant);
             }
             if (row_ok && k < K) a.out_in_map[row * K + k] = found;
+            if (a.repeat_status != nullptr) flag_repeats(a.repeat_status, row_active && k == a.center && found != row);
             const uint64_t hits = ballot(found >= 0);
             const uint64_t mine = kLanes == 64 ? hits : ((hits >> (sub * kLanes)) & 0xffffffffull);
             degree += __popcll(mine);
@@ -552,6 +566,11 @@ __global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
     const int degree = query_rows_k3(a, row0, lane, stage);
     if (a.degrees != nullptr && row0 + lane < a.out_capacity) a.degrees[row0 + lane] = degree;
     __syncthreads();
+    if (a.repeat_status != nullptr) {
+        const long long r = row0 + lane;
+        const int n_active = min(max(*a.out_active, 0), a.out_capacity);
+        flag_repeats(a.repeat_status, r < n_active && stage[lane * kK3 + kK3 / 2] != r);
+    }
     store_map_rows_k3(a, row0, lane, stage);
     if (a.block_totals != nullptr) {
         int sum = degree;
@@ -1039,6 +1058,13 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     if (identity) {
         q.out_coords = coords;
         q.out_active = out->counts + 1;
+        // The self lookup: the zero offset sits at index size/2 of each odd
+        // axis and at index 0 of an even one.
+        const int cx = kernel_size[0] % 2 ? kernel_size[0] / 2 : 0;
+        const int cy = kernel_size[1] % 2 ? kernel_size[1] / 2 : 0;
+        const int cz = kernel_size[2] % 2 ? kernel_size[2] / 2 : 0;
+        q.repeat_status = out->status;
+        q.center = (cx * kernel_size[1] + cy) * kernel_size[2] + cz;
     } else if (kernel_size[0] == 2 && kernel_size[1] == 2 && kernel_size[2] == 2 && stride[0] == 2 &&
                stride[1] == 2 && stride[2] == 2 && padding[0] == 0 && padding[1] == 0 && padding[2] == 0 &&
                dilation[0] == 1 && dilation[1] == 1 && dilation[2] == 1) {

@@ -229,7 +229,9 @@ def _kernel_relation_from_native(
     relation_out_coords = (native_out_coords if out_coords is None
                            else out_coords)
     implicit = (RelationImplicitGemmView(view[0], row_masks=view[1])
-                if len(view) == 2 else None)
+                if len(view) >= 2 else None)
+    # The status word of a submanifold relation flags repeated coordinates.
+    repeated_coords = view[2] if len(view) == 3 and kind == 'submanifold' else None
     grouped_views = None
     if in_row_offsets is None:
         n_kernels = len(offsets)
@@ -249,7 +251,7 @@ def _kernel_relation_from_native(
         target_active_rows=target_active_rows, stride=stride,
         padding=padding, kind=kind, implicit_gemm=implicit,
         grouped_views=grouped_views, repeated_edges=repeated_edges,
-        direct_expansion=direct_expansion)
+        direct_expansion=direct_expansion, repeated_coords=repeated_coords)
 
 
 def _require_positive(values: Triple, name: str) -> None:

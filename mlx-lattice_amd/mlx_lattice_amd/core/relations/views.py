@@ -126,6 +126,28 @@ class RelationSortedImplicitGemmView:
         return self._tile_order
 
 
+class _StatusWord:
+    """A device status word copied to pinned host memory when the relation
+    is built: the copy is queued on the current stream and never waited
+    for there; read() waits only for the copy's event (usually long
+    complete by the time a backward pass asks)."""
+
+    def __init__(self, word: torch.Tensor) -> None:
+        if word.is_cuda:
+            self._host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            self._host.copy_(word, non_blocking=True)
+            self._event = torch.cuda.Event()
+            self._event.record()
+        else:
+            self._host = word.clone()
+            self._event = None
+
+    def read(self) -> int:
+        if self._event is not None:
+            self._event.synchronize()
+        return int(self._host[0])
+
+
 @dataclass(frozen=True, slots=True)
 class SparseRelationContract:
     """Counts, capacities, coordinate context and geometry of a relation."""
@@ -219,6 +241,12 @@ class KernelRelation:
     # Generative, and transposed relations whose stride exceeds the offsets'
     # extent: output row in * K + k holds the single edge (in, k).
     direct_expansion: bool = False
+    # Submanifold relations: whether an active row repeats an earlier row's
+    # coordinate (each copy is an output row with the same neighbours, so
+    # an input row can have several output rows at one offset).  Held as a
+    # _StatusWord copied to pinned memory at build time and read on the
+    # first question (transposed_map_exact).  None: no repeats possible.
+    repeated_coords: bool | _StatusWord | None = None
 
     def __init__(
         self,
@@ -249,6 +277,7 @@ class KernelRelation:
         grouped_views: Callable[[], tuple] | None = None,
         repeated_edges: bool | torch.Tensor | None = None,
         direct_expansion: bool = False,
+        repeated_coords: torch.Tensor | None = None,
     ) -> None:
         """``grouped_views``, when given and the input/kernel CSR arrays are
         not, is called on first access of ``input_csr`` / ``kernel_csr`` and
@@ -315,6 +344,10 @@ class KernelRelation:
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
         object.__setattr__(self, 'transposed_sorted_implicit_gemm', None)
         object.__setattr__(self, 'repeated_edges', repeated_edges)
+        object.__setattr__(
+            self, 'repeated_coords',
+            _StatusWord(repeated_coords) if repeated_coords is not None
+            else None)
         object.__setattr__(self, 'direct_expansion', bool(direct_expansion))
 
     @property
@@ -444,6 +477,23 @@ class KernelRelation:
             return False
         return not self.repeated_edges
 
+    @property
+    def transposed_map_exact(self) -> bool:
+        """Whether the dense transposed (in_row, offset) -> out_row map holds
+        every edge: at most one edge per (in_row, kernel_id).  Forward,
+        generative and transposed relations hold it by construction (their
+        output coordinates are distinct, or each output row has one edge); a
+        submanifold relation does unless a coordinate repeats.  The first
+        question reads the build's status word from pinned memory (copied
+        when the relation was built), so it waits for that copy only."""
+        if self.contract.kind == 'target':
+            return False
+        if isinstance(self.repeated_coords, _StatusWord):
+            # lattice_relation_flags: bit 8 = repeated coordinate
+            flags = self.repeated_coords.read()
+            object.__setattr__(self, 'repeated_coords', bool(flags & 8))
+        return not self.repeated_coords
+
     def _expanded_implicit_gemm(self) -> RelationImplicitGemmView:
         """Dense map of a generative or transposed relation, scattered from
         its edges: out_in_map[out][k] = in (the expanded relations carry no
@@ -454,7 +504,7 @@ class KernelRelation:
                              'edges.')
         from mlx_lattice_amd._native import ext
 
-        out_in_map, row_masks = ext.build_transposed_implicit_gemm_map(
+        out_in_map, row_masks, _ = ext.build_transposed_implicit_gemm_map(
             self.edges.out_rows, self.edges.in_rows, self.edges.kernel_ids,
             self.counts, int(self.n_out_capacity), int(self.n_kernels))
         return RelationImplicitGemmView(out_in_map, row_masks=row_masks)
@@ -485,10 +535,12 @@ class KernelRelation:
         """Mask-sorted view of the transposed relation (input row -> output
         row per offset), built on first use and cached: the matrix-core
         route of the input gradient runs the forward's implicit GEMM over
-        it.  Forward and submanifold relations have at most one output row
-        per (input row, offset), and generative and transposed relations
-        exactly one, so the transposed map is dense; target relations (whose
-        target may repeat a coordinate) are refused."""
+        it.  Forward relations have at most one output row per (input row,
+        offset), generative and transposed relations exactly one, and
+        submanifold relations too unless a coordinate repeats
+        (``transposed_map_exact``, which the input gradient checks first);
+        target relations (whose target may repeat a coordinate) are
+        refused."""
         if self.transposed_sorted_implicit_gemm is not None:
             return self.transposed_sorted_implicit_gemm
         if self.contract.kind not in ('forward', 'submanifold', 'transposed',
@@ -503,7 +555,7 @@ class KernelRelation:
                 'sorted implicit GEMM view currently supports K <= 32.')
         from mlx_lattice_amd._native import ext
 
-        in_out_map, row_masks = ext.build_transposed_implicit_gemm_map(
+        in_out_map, row_masks, _ = ext.build_transposed_implicit_gemm_map(
             self.edges.in_rows, self.edges.out_rows, self.edges.kernel_ids,
             self.counts, int(self.n_in_capacity), int(self.n_kernels))
         reorder, sorted_map, kv_map, tiles = ext.build_sorted_implicit_gemm_view(

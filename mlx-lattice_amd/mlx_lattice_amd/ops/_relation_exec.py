@@ -139,7 +139,10 @@ def _input_grad_matrix_core_eligible(cot: torch.Tensor, weight: torch.Tensor,
             and c_out % 32 == 0 and c_out <= 512
             and c_in in _MATRIX_CORE_C_OUT
             and relation.n_kernels is not None and relation.n_kernels <= 32
-            and int(cot.shape[0]) * c_out * 2 < 2 ** 31)
+            and int(cot.shape[0]) * c_out * 2 < 2 ** 31
+            # a repeated coordinate gives an input row several output rows
+            # at one offset, which the dense transposed map cannot hold
+            and relation.transposed_map_exact)
 
 
 def _transposed_weight(weight: torch.Tensor) -> torch.Tensor:

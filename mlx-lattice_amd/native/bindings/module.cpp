@@ -33,10 +33,11 @@ py::tuple relation_tuple(const ln::NativeKernelRelation& r) {
 }
 
 // Grouped views are not built here (None); build_relation_grouped_views
-// makes them on demand.
+// makes them on demand.  The device status word (lattice_relation_flags)
+// follows the implicit-GEMM view.
 py::tuple relation_tuple_with_view(const ln::NativeKernelRelation& r) {
     return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
-                          py::none(), py::none(), py::none(), py::none(), r.out_in_map, r.row_masks);
+                          py::none(), py::none(), py::none(), py::none(), r.out_in_map, r.row_masks, r.status);
 }
 
 }  // namespace
@@ -226,10 +227,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            const at::Tensor& counts, int in_capacity, int n_kernels) {
             auto r = ln::build_transposed_implicit_gemm_map(in_rows, out_rows, kernel_ids, counts, in_capacity,
                                                             n_kernels);
-            return py::make_tuple(std::get<0>(r), std::get<1>(r));
+            return py::make_tuple(std::get<0>(r), std::get<1>(r), std::get<2>(r));
         },
         py::arg("in_rows"), py::arg("out_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("in_capacity"),
-        py::arg("n_kernels"), "Return (in_out_map, row_masks) of a forward or submanifold relation.");
+        py::arg("n_kernels"),
+        "Return (in_out_map, row_masks, status) of a forward or submanifold relation; status flags an incomplete "
+        "map (repeated coordinates).");
     m.def("sparse_conv_weight_grad", &ln::sparse_conv_weight_grad, py::arg("feats"), py::arg("cotangent"),
           py::arg("weights"), py::arg("in_rows"), py::arg("out_rows"), py::arg("counts"),
           py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("n_kernels"),

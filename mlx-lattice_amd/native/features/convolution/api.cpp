@@ -409,7 +409,7 @@ at::Tensor sparse_conv_input_grad(const at::Tensor& cot_in, const at::Tensor& we
     return grad;
 }
 
-std::tuple<at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
+std::tuple<at::Tensor, at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
                                                                       const at::Tensor& out_rows,
                                                                       const at::Tensor& kernel_ids,
                                                                       const at::Tensor& counts, int in_capacity,
@@ -429,10 +429,11 @@ std::tuple<at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::
     require_device(in_rows, "in_rows");
     at::Tensor map = empty_i32({in_capacity, n_kernels}, in_rows);
     at::Tensor masks = empty_i32({in_capacity, (n_kernels + 31) / 32}, in_rows);
+    at::Tensor status = empty_i32({1}, in_rows);
     check_status(lattice_hip_build_transposed_implicit_gemm_map(
         ci32(in_rows), ci32(out_rows), ci32(kernel_ids), ci32(counts), static_cast<int>(in_rows.size(0)),
-        in_capacity, n_kernels, i32(map), i32(masks), current_stream(in_rows)));
-    return {map, masks};
+        in_capacity, n_kernels, i32(map), i32(masks), i32(status), current_stream(in_rows)));
+    return {map, masks, status};
 }
 
 at::Tensor sparse_conv_weight_grad(const at::Tensor& feats_in, const at::Tensor& cot_in, const at::Tensor& weights,

@@ -64,9 +64,10 @@ at::Tensor sparse_conv_input_grad(const at::Tensor& cot, const at::Tensor& weigh
                                   const at::Tensor& in_row_offsets, const at::Tensor& in_edge_ids, int in_capacity,
                                   int n_kernels);
 
-// Transposed dense map (in_out_map (in_capacity, K), row_masks) of a
-// forward or submanifold relation, for the matrix-core input gradient.
-std::tuple<at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
+// Transposed dense map (in_out_map (in_capacity, K), row_masks, status) of
+// a forward or submanifold relation, for the matrix-core input gradient;
+// status (1,) gets LATTICE_STATUS_REPEATED_PAIR when the map is incomplete.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> build_transposed_implicit_gemm_map(const at::Tensor& in_rows,
                                                                       const at::Tensor& out_rows,
                                                                       const at::Tensor& kernel_ids,
                                                                       const at::Tensor& counts, int in_capacity,

@@ -207,6 +207,56 @@ def test_weight_grad_is_deterministic():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize('ks', [3, 5])
+def test_gradients_with_repeated_coordinates(ks):
+    """A submanifold relation over repeated coordinates: every copy of a
+    coordinate is an output row with the same neighbours (first-row
+    lookups), so an input row has several output rows at one offset.  The
+    relation build flags it, the input gradient leaves the dense transposed
+    map for the input-grouped CSR, and both gradients match the oracle."""
+    from mlx_lattice_amd._native import ext
+    from mlx_lattice_amd.ops._relation_exec import (
+        sparse_conv_input_grad_from_relation,
+        sparse_conv_weight_grad_from_relation,
+    )
+
+    rng = np.random.default_rng(17 + ks)
+    base = _cloud(4000, 128, 23 + ks)
+    repeats = base[rng.choice(len(base), 300, replace=False)]
+    coords = np.concatenate([base, repeats, repeats[:50]])
+    coords = coords[rng.permutation(len(coords))]
+    n = len(coords)
+    k3 = ks ** 3
+    feats = torch.as_tensor(rng.standard_normal((n, 64)).astype(np.float32)
+                            ).to(DEV, torch.float16)
+    weight = torch.as_tensor((rng.standard_normal((64, ks, ks, ks, 64))
+                              / np.sqrt(k3 * 64)).astype(np.float32)
+                             ).to(DEV, torch.float16)
+    cot = torch.as_tensor(rng.standard_normal((n, 64)).astype(np.float32)
+                          ).to(DEV, torch.float16)
+    x = _sparse(coords, feats)
+    rel = _relation(x, 'subm', ks, 1)
+    print(f'repeated coordinates k={ks} N={n}', flush=True)
+    assert not rel.transposed_map_exact
+    _, _, status = ext.build_transposed_implicit_gemm_map(
+        rel.edges.in_rows, rel.edges.out_rows, rel.edges.kernel_ids,
+        rel.counts, n, k3)
+    gin = sparse_conv_input_grad_from_relation(cot, weight, rel, n)
+    gw = sparse_conv_weight_grad_from_relation(feats, cot, weight, rel)
+    torch.cuda.synchronize()
+    assert int(status.item()) & 4  # LATTICE_STATUS_REPEATED_PAIR
+    orel = _oracle_relation(rel)
+    f32 = lambda t: to_np(t.float())  # noqa: E731
+    _close(to_np(gin.float()),
+           O.conv_input_grad(f32(cot), f32(weight), orel, n), 2e-2, 1e-2)
+    _close(to_np(gw.float()),
+           O.conv_weight_grad(f32(feats), f32(cot), tuple(weight.shape), orel),
+           2e-2, 1e-2)
+    # the same cloud without the copies keeps the matrix-core route
+    y = _sparse(base, feats[:len(base)])
+    assert _relation(y, 'subm', ks, 1).transposed_map_exact
+
+
 def test_weight_grad_with_no_edges():
     """An empty relation gives a zero weight gradient on every route."""
     from mlx_lattice_amd.ops._relation_exec import (
