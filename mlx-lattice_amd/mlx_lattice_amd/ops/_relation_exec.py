@@ -154,16 +154,49 @@ def _transposed_weight(weight: torch.Tensor) -> torch.Tensor:
     return weight.permute(1, 0, 2).contiguous().reshape(c_in, k, 1, 1, c_out)
 
 
+def _mirrored_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The transposed weight with its offsets reversed, W'[j] = W[K-1-j]^T,
+    as a 5D (C_in, Kx, Ky, Kz, C_out) weight."""
+    if weight.ndim == 5:
+        return weight.permute(4, 1, 2, 3, 0).flip(1, 2, 3).contiguous()
+    k, c_in, c_out = weight.shape
+    return weight.flip(0).permute(1, 0, 2).contiguous().reshape(
+        c_in, k, 1, 1, c_out)
+
+
+def _mirror_symmetric(relation: KernelRelation) -> bool:
+    """A submanifold relation whose offsets come in opposite pairs,
+    offset[K-1-k] = -offset[k] (odd kernels), and whose coordinates do not
+    repeat: input row i then meets output row o at offset k exactly when
+    o = out_in_map[i][K-1-k], so the transposed map is the forward map with
+    its offsets reversed."""
+    if relation.contract.kind != 'submanifold':
+        return False
+    offs = relation.contract.kernel_offsets
+    k = len(offs)
+    return k > 0 and all(
+        tuple(-v for v in offs[k - 1 - j]) == tuple(offs[j]) for j in range(k))
+
+
 def sparse_conv_input_grad_from_relation(cot: torch.Tensor,
                                          weight: torch.Tensor,
                                          relation: KernelRelation,
                                          in_capacity: int) -> torch.Tensor:
     """Input gradient ``(in_capacity, C_in)`` (make_sparse_conv_features_
-    input_grad, primitive.cpp:597-639): on the matrix cores over the
-    transposed sorted view when the shapes allow, otherwise over the
-    input-grouped CSR."""
+    input_grad, primitive.cpp:597-639): on the matrix cores when the shapes
+    allow, otherwise over the input-grouped CSR.  A submanifold relation
+    over distinct coordinates runs the forward's own sorted view with the
+    mirrored transposed weight (grad[i] = sum_j cot[out_in_map[i][j]] @
+    W[K-1-j]^T); other relations run their transposed sorted view."""
     _require_static(relation)
     if _input_grad_matrix_core_eligible(cot, weight, relation):
+        if _mirror_symmetric(relation):
+            view = relation.require_sorted_implicit_gemm()
+            return ext.sparse_conv_features_sorted_implicit_gemm(
+                cot, _mirrored_weight(weight), view.sorted_out_in_map,
+                view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
+                None, None, None, None, None, None, None, None, None,
+                in_capacity, relation.n_kernels, tile_order=view.tile_order())
         view = relation.require_transposed_sorted_implicit_gemm()
         return ext.sparse_conv_features_sorted_implicit_gemm(
             cot, _transposed_weight(weight), view.sorted_out_in_map,

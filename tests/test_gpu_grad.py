@@ -164,10 +164,13 @@ def test_gradients_match_oracle(kind, ks, stride, c_in, c_out, dtype, mapped):
 
 
 def test_input_grad_routes_agree():
-    """The matrix-core route (transposed sorted view) and the CSR route of
-    the input gradient give the same numbers to fp16 rounding."""
+    """The matrix-core routes (the forward sorted view with the mirrored
+    weight, which a submanifold relation takes, and the transposed sorted
+    view) and the CSR route of the input gradient give the same numbers to
+    fp16 rounding."""
     from mlx_lattice_amd._native import ext
     from mlx_lattice_amd.ops._relation_exec import (
+        _transposed_weight,
         sparse_conv_input_grad_from_relation,
     )
 
@@ -184,8 +187,15 @@ def test_input_grad_routes_agree():
     csr = ext.sparse_conv_input_grad(
         cot, weight, rel.edges.out_rows, rel.edges.kernel_ids, rel.counts,
         rel.input_csr.row_offsets, rel.input_csr.edge_ids, n, 27)
+    # the transposed sorted view, which the submanifold route skips
+    tview = rel.require_transposed_sorted_implicit_gemm()
+    transposed = ext.sparse_conv_features_sorted_implicit_gemm(
+        cot, _transposed_weight(weight), tview.sorted_out_in_map,
+        tview.sorted_kv_out_in_map, tview.reorder_rows, tview.tile_masks,
+        None, None, None, None, None, None, None, None, None, n, 27)
     torch.cuda.synchronize()
     _close(to_np(fast.float()), to_np(csr.float()), 2e-2, 1e-2)
+    _close(to_np(transposed.float()), to_np(csr.float()), 2e-2, 1e-2)
 
 
 def test_weight_grad_is_deterministic():
