@@ -21,8 +21,9 @@ from mlx_lattice_amd.core.quantized import QuantizedWeight
 from mlx_lattice_amd.core.relations import KernelRelation
 
 _MATRIX_CORE_C_OUT = (16, 32, 64, 128, 256)
-_WEIGHT_CACHE: dict[int, tuple[weakref.ReferenceType, tuple, torch.dtype,
-                               torch.Tensor]] = {}
+# (id(weight), kind) -> (weak reference, shape, dtype, version, value)
+_WEIGHT_CACHE: dict[tuple[int, str], tuple[weakref.ReferenceType, tuple,
+                                           torch.dtype, int, torch.Tensor]] = {}
 
 
 def _empty_i32(device) -> torch.Tensor:
@@ -147,21 +148,27 @@ def _input_grad_matrix_core_eligible(cot: torch.Tensor, weight: torch.Tensor,
 
 def _transposed_weight(weight: torch.Tensor) -> torch.Tensor:
     """(C_out, Kx, Ky, Kz, C_in) or (K, C_in, C_out) -> the 5D weight of the
-    transposed conv, (C_in, Kx, Ky, Kz, C_out)."""
-    if weight.ndim == 5:
-        return weight.permute(4, 1, 2, 3, 0).contiguous()
-    k, c_in, c_out = weight.shape
-    return weight.permute(1, 0, 2).contiguous().reshape(c_in, k, 1, 1, c_out)
+    transposed conv, (C_in, Kx, Ky, Kz, C_out) (cached)."""
+    def make(w):
+        if w.ndim == 5:
+            return w.permute(4, 1, 2, 3, 0).contiguous()
+        k, c_in, c_out = w.shape
+        return w.permute(1, 0, 2).contiguous().reshape(c_in, k, 1, 1, c_out)
+
+    return _cached_weight(weight, 'transposed', make)
 
 
 def _mirrored_weight(weight: torch.Tensor) -> torch.Tensor:
     """The transposed weight with its offsets reversed, W'[j] = W[K-1-j]^T,
-    as a 5D (C_in, Kx, Ky, Kz, C_out) weight."""
-    if weight.ndim == 5:
-        return weight.permute(4, 1, 2, 3, 0).flip(1, 2, 3).contiguous()
-    k, c_in, c_out = weight.shape
-    return weight.flip(0).permute(1, 0, 2).contiguous().reshape(
-        c_in, k, 1, 1, c_out)
+    as a 5D (C_in, Kx, Ky, Kz, C_out) weight (cached)."""
+    def make(w):
+        if w.ndim == 5:
+            return w.flip(1, 2, 3).permute(4, 1, 2, 3, 0).contiguous()
+        k, c_in, c_out = w.shape
+        return w.flip(0).permute(1, 0, 2).contiguous().reshape(
+            c_in, k, 1, 1, c_out)
+
+    return _cached_weight(weight, 'mirrored', make)
 
 
 def _mirror_symmetric(relation: KernelRelation) -> bool:
@@ -357,25 +364,21 @@ class _SparsePoolFeatures(torch.autograd.Function):
         return grad, None, None, None
 
 
-def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:
-    """5D weights go to the kernels as they are (C_in contiguous per
-    (C_out, k)); a mapped ``(K, C_in, C_out)`` weight is transposed once to
-    ``(C_out, K, 1, 1, C_in)`` and cached by identity like the reference's
-    ``_mapped_weight`` (_relation_exec.py:217-250)."""
-    if weight.ndim == 5:
-        return weight
-    key = id(weight)
+def _cached_weight(weight: torch.Tensor, kind: str, make) -> torch.Tensor:
+    """``make(weight)``, cached by the weight's identity, shape, dtype and
+    version counter (so an in-place update, as an optimizer step makes,
+    rebuilds it), like the reference's ``_mapped_weight``
+    (_relation_exec.py:217-250)."""
+    key = (id(weight), kind)
     shape = tuple(weight.shape)
     cached = _WEIGHT_CACHE.get(key)
     if cached is not None:
-        ref, cached_shape, cached_dtype, value = cached
+        ref, cached_shape, cached_dtype, version, value = cached
         if (ref() is weight and cached_shape == shape
                 and cached_dtype == weight.dtype
-                and value._version_of_source == weight._version):
+                and version == weight._version):
             return value
-    k, c_in, c_out = shape
-    packed = weight.permute(2, 0, 1).contiguous().reshape(c_out, k, 1, 1, c_in)
-    packed._version_of_source = weight._version
+    value = make(weight)
 
     def _drop(ref, key=key):
         entry = _WEIGHT_CACHE.get(key)
@@ -383,5 +386,19 @@ def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:
             _WEIGHT_CACHE.pop(key, None)
 
     _WEIGHT_CACHE[key] = (weakref.ref(weight, _drop), shape, weight.dtype,
-                          packed)
-    return packed
+                          weight._version, value)
+    return value
+
+
+def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:
+    """5D weights go to the kernels as they are (C_in contiguous per
+    (C_out, k)); a mapped ``(K, C_in, C_out)`` weight is transposed once to
+    ``(C_out, K, 1, 1, C_in)`` and cached."""
+    if weight.ndim == 5:
+        return weight
+
+    def make(w):
+        k, c_in, c_out = w.shape
+        return w.permute(2, 0, 1).contiguous().reshape(c_out, k, 1, 1, c_in)
+
+    return _cached_weight(weight, 'mapped', make)
