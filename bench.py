@@ -179,7 +179,8 @@ def _timed(fn, steps: int, warmup: int) -> float:
 
 
 def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
-    """Configs 2, 4 and 5 through the operator API.
+    """Configs 2, 4 and 5, and config 3 read literally (a uniform subsample
+    of the complete shells), through the operator API.
 
     ``layer_ms`` builds a fresh coordinate manager every call, so it covers
     the kernel-map build, the sorted view, the conv and the bias;
@@ -196,7 +197,8 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
                                                    QuantizedSubmConv3d)
     from mlx_lattice_amd.synthetic import (config_rng, encoder_layers,
                                            kaiming_weight, lidar_cloud,
-                                           sphere_shell_cloud)
+                                           sphere_shell_cloud,
+                                           sphere_shell_subsample_cloud)
 
     dev = torch.device('cuda:0')
     out = {}
@@ -267,6 +269,20 @@ def secondary_workloads(steps: int = 10, warmup: int = 3) -> dict:
         'voxels',
         # int4 codes + fp16 scales and biases per 32-channel group
         27 * 64 * 64 // 2 + 2 * 2 * 27 * (64 // 32) * 64)
+
+    # Config 3 read literally: a uniform 400k subsample of the 200 complete
+    # shells (about 2 active offsets per row, gather-bound).
+    rng = config_rng(3)
+    c3l = torch.as_tensor(sphere_shell_subsample_cloud(400000, 512,
+                                                       rng=rng)).to(dev)
+    f3l = torch.as_tensor(rng.standard_normal((c3l.shape[0], 128)).astype(
+        np.float16)).to(dev)
+    w3l = torch.as_tensor(kaiming_weight((128, 3, 3, 3, 128), rng=rng)).to(
+        dev, torch.float16)
+    out['config3_spec_literal'] = layer(
+        c3l, f3l, lambda x: ops.subm_conv3d(x, w3l, kernel_size=3), 128, 128,
+        27, 'subm_conv3d k=3 fp16 128->128, a uniform 400k subsample of the '
+        'complete shells of 200 spheres in 512^3', 27 * 128 * 128 * 2)
 
     rng = config_rng(5)
     c5 = torch.as_tensor(lidar_cloud(120000, 4, rng=rng)).to(dev)

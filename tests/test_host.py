@@ -186,3 +186,29 @@ def test_quantized_words_follow_the_unpack_rule():
         deq = dequantize_weight(q).numpy()
         mapped = deq.transpose(1, 2, 3, 4, 0).reshape(27, 64, 8)
         np.testing.assert_array_equal(mapped, deq_oracle)
+
+
+def test_spec_literal_shell_subsample():
+    """The literal config-3 cloud: distinct voxels, all on complete shells,
+    drawn uniformly, so neighbours are sparse (about 2 active offsets per
+    row at the full 400k / 200-sphere scale; checked here on 12 spheres)."""
+    import numpy as np
+
+    from mlx_lattice_amd.synthetic import (_shell_voxels,
+                                           sphere_shell_subsample_cloud)
+
+    rng = np.random.default_rng(5)
+    cloud = sphere_shell_subsample_cloud(20000, 256, spheres=12, rng=rng)
+    assert cloud.shape == (20000, 4) and cloud.dtype == np.int32
+    assert len(np.unique(cloud, axis=0)) == 20000
+    assert (cloud[:, 0] == 0).all()
+    # every voxel lies on one of the 12 shells drawn by the same seed
+    rng = np.random.default_rng(5)
+    shells = set()
+    for _ in range(12):
+        r = rng.uniform(8.0, 60.0)
+        margin = int(np.ceil(r)) + 1
+        c = rng.uniform(margin, 256 - margin, size=3)
+        shells.update(map(tuple, _shell_voxels(c, r).tolist()))
+    assert all(tuple(v) in shells for v in cloud[:, 1:].tolist())
+    assert len(shells) > 20000
