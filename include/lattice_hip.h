@@ -145,6 +145,14 @@ typedef struct lattice_relation_outputs {
 } lattice_relation_outputs;
 
 size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kernel_count);
+/* Set in workspace_bytes of lattice_hip_build_kernel_relation: the
+ * workspace is the one an earlier lattice_hip_build_kernel_relation call
+ * used over the same coords and active_rows (any kernel geometry), and its
+ * block table of those coordinates, which no later step of a build
+ * modifies, is reused instead of cleared and rebuilt.  No counterpart in
+ * the reference: a submanifold relation and the downsample relation of the
+ * same level hash the same coordinates. */
+#define LATTICE_RELATION_TABLE_READY ((size_t)1 << 62)
 size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows,
                                                    int kernel_count);
 

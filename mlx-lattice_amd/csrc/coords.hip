@@ -798,8 +798,12 @@ size_t block_table_bytes(int rows) {
     return aligned_bytes(static_cast<size_t>(block_capacity(rows)) * sizeof(BlockBucket));
 }
 
+// The block table sits at the start of the workspace.  With `ready` the
+// workspace already holds the table of these coordinates and active rows
+// (an earlier relation build over them): only the prologue runs.
 int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows,
-                      const Prologue& prologue, Workspace& ws, hipStream_t stream, BlockTable* table) {
+                      const Prologue& prologue, Workspace& ws, hipStream_t stream, BlockTable* table,
+                      bool ready = false) {
     const int cap = block_capacity(rows);
     table->buckets = ws.take<BlockBucket>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
@@ -808,11 +812,11 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
         set_error("relation workspace too small for the coordinate table");
         return LATTICE_ERROR_INVALID_ARGUMENT;
     }
-    const long long quarters = 4ll * cap;
-    clear_blocks<<<grid_for(std::max<long long>(quarters, prologue.copy_rows), kThreads, 8192), kThreads, 0, stream>>>(
-        table->buckets, quarters, prologue);
+    const long long quarters = ready ? 0 : 4ll * cap;
+    clear_blocks<<<grid_for(std::max<long long>({quarters, prologue.copy_rows, 1}), kThreads, 8192), kThreads, 0,
+                   stream>>>(table->buckets, quarters, prologue);
     LATTICE_LAUNCH_CHECK();
-    if (rows > 0) {
+    if (rows > 0 && !ready) {
         insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows);
         LATTICE_LAUNCH_CHECK();
     }
@@ -1026,6 +1030,8 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     const KernelGeometry geom = make_geometry(kernel_size, stride, padding, dilation);
     const int K = geom.volume;
     LATTICE_REQUIRE(static_cast<long long>(rows) * K < INT_MAX, "relation edge capacity exceeds int32.");
+    const bool table_ready = (workspace_bytes & LATTICE_RELATION_TABLE_READY) != 0;
+    workspace_bytes &= ~static_cast<size_t>(LATTICE_RELATION_TABLE_READY);
     LATTICE_REQUIRE(workspace_bytes >= forward_relation_bytes(rows, K), "relation workspace too small.");
     hipStream_t stream = as_stream(stream_ptr);
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
@@ -1044,7 +1050,7 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
         prologue.copy_dst = out->out_coords;
     }
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table);
+    rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table, table_ready);
     if (rc != LATTICE_OK) return rc;
 
     QueryArgs q{};

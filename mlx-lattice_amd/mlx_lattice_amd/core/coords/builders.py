@@ -81,8 +81,11 @@ def build_kernel_relation(coords: torch.Tensor,
                           kernel_size: int | Sequence[int] = 3,
                           stride: int | Sequence[int] = 1,
                           padding: int | Sequence[int] = 0,
-                          dilation: int | Sequence[int] = 1) -> KernelRelation:
-    """Forward sparse convolution relation (builders.py:156-191)."""
+                          dilation: int | Sequence[int] = 1, *,
+                          table: torch.Tensor | None = None) -> KernelRelation:
+    """Forward sparse convolution relation (builders.py:156-191).  ``table``
+    (optional): the ``block_table`` workspace of an earlier relation over
+    the same coordinates, whose block table the build then reuses."""
     validate_coords(coords)
     spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
                       dilation=dilation)
@@ -90,7 +93,7 @@ def build_kernel_relation(coords: torch.Tensor,
     source_active = _active_rows(active_rows, coords)
     native = _ext().build_kernel_relation_with_view(
         coords, source_active, list(spec.size), list(spec.stride),
-        list(spec.padding), list(spec.dilation))
+        list(spec.padding), list(spec.dilation), table=table)
     return _kernel_relation_from_native(
         native, offsets=offsets, in_capacity=int(coords.shape[0]),
         source_coords=coords, source_active_rows=source_active,
@@ -100,9 +103,13 @@ def build_kernel_relation(coords: torch.Tensor,
 def build_submanifold_kernel_relation(
         coords: torch.Tensor, active_rows: torch.Tensor | None = None,
         kernel_size: int | Sequence[int] = 3,
-        dilation: int | Sequence[int] = 1) -> KernelRelation:
+        dilation: int | Sequence[int] = 1, *,
+        keep_table: bool = False) -> KernelRelation:
     """Submanifold relation whose output support is ``coords``
-    (builders.py:194-233)."""
+    (builders.py:194-233).  ``keep_table``: keep the build's workspace as
+    ``block_table`` (its start holds the block table of ``coords``) for a
+    later ``build_kernel_relation(..., table=...)`` over the same
+    coordinates."""
     validate_coords(coords)
     spec = KernelSpec(size=kernel_size, stride=1, padding=0,
                       dilation=dilation)
@@ -119,7 +126,7 @@ def build_submanifold_kernel_relation(
         out_coords=coords, source_coords=coords,
         source_active_rows=source_active, target_coords=coords,
         target_active_rows=source_active, stride=spec.stride,
-        padding=spec.padding, kind='submanifold')
+        padding=spec.padding, kind='submanifold', keep_table=keep_table)
 
 
 def build_target_kernel_relation(
@@ -222,7 +229,8 @@ def _kernel_relation_from_native(
         stride: Triple = (1, 1, 1), padding: Triple = (0, 0, 0),
         kind: RelationKind = 'forward',
         repeated_edges: bool | torch.Tensor | None = None,
-        direct_expansion: bool = False) -> KernelRelation:
+        direct_expansion: bool = False,
+        keep_table: bool = False) -> KernelRelation:
     (in_rows, out_rows, kernel_ids, row_offsets, native_out_coords, counts,
      in_row_offsets, in_edge_ids, kernel_row_offsets, kernel_edge_ids,
      *view) = native
@@ -230,8 +238,11 @@ def _kernel_relation_from_native(
                            else out_coords)
     implicit = (RelationImplicitGemmView(view[0], row_masks=view[1])
                 if len(view) >= 2 else None)
-    # The status word of a submanifold relation flags repeated coordinates.
-    repeated_coords = view[2] if len(view) == 3 and kind == 'submanifold' else None
+    # The status word of a submanifold relation flags repeated coordinates;
+    # its workspace holds the block table of its coordinates.
+    repeated_coords = (view[2] if len(view) >= 3 and kind == 'submanifold'
+                       else None)
+    block_table = view[3] if len(view) >= 4 and keep_table else None
     grouped_views = None
     if in_row_offsets is None:
         n_kernels = len(offsets)
@@ -251,7 +262,8 @@ def _kernel_relation_from_native(
         target_active_rows=target_active_rows, stride=stride,
         padding=padding, kind=kind, implicit_gemm=implicit,
         grouped_views=grouped_views, repeated_edges=repeated_edges,
-        direct_expansion=direct_expansion, repeated_coords=repeated_coords)
+        direct_expansion=direct_expansion, repeated_coords=repeated_coords,
+        block_table=block_table)
 
 
 def _require_positive(values: Triple, name: str) -> None:

@@ -54,6 +54,11 @@ class CoordinateManager:
     _kernel_relations: dict[
         tuple[CoordinateMapKey, CoordinateMapKey | None, KernelSpec, str],
         KernelRelation] = field(default_factory=dict)
+    # The workspace of the last submanifold relation built over a key: its
+    # start holds the block table of the key's coordinates, which the next
+    # forward relation over the same key reuses (and releases).
+    _block_tables: dict[CoordinateMapKey, torch.Tensor] = field(
+        default_factory=dict)
 
     def insert_coords(self, coords: torch.Tensor,
                       stride: int | Sequence[int] = 1,
@@ -110,7 +115,8 @@ class CoordinateManager:
             self._kernel_relations[cache_key] = build_kernel_relation(
                 self.coords(key), active_rows=self.active_rows(key),
                 kernel_size=spec.size, stride=spec.stride,
-                padding=spec.padding, dilation=spec.dilation)
+                padding=spec.padding, dilation=spec.dilation,
+                table=self._block_tables.pop(key, None))
         return self._kernel_relations[cache_key]
 
     def generative_relation(self, key: CoordinateMapKey, *,
@@ -154,10 +160,15 @@ class CoordinateManager:
                           dilation=dilation)
         cache_key = (key, key, spec, 'submanifold')
         if cache_key not in self._kernel_relations:
-            self._kernel_relations[cache_key] = (
-                build_submanifold_kernel_relation(
-                    self.coords(key), active_rows=self.active_rows(key),
-                    kernel_size=spec.size, dilation=spec.dilation))
+            relation = build_submanifold_kernel_relation(
+                self.coords(key), active_rows=self.active_rows(key),
+                kernel_size=spec.size, dilation=spec.dilation,
+                keep_table=True)
+            table = relation.block_table
+            if table is not None:
+                self._block_tables[key] = table
+                object.__setattr__(relation, 'block_table', None)
+            self._kernel_relations[cache_key] = relation
         return self._kernel_relations[cache_key]
 
     def target_kernel_relation(

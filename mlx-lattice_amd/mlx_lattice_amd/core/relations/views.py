@@ -247,6 +247,10 @@ class KernelRelation:
     # _StatusWord copied to pinned memory at build time and read on the
     # first question (transposed_map_exact).  None: no repeats possible.
     repeated_coords: bool | _StatusWord | None = None
+    # Submanifold relations built with their workspace: it starts with the
+    # block table of the coordinates (the coordinate manager hands it to
+    # the next forward relation over the same key).
+    block_table: torch.Tensor | None = None
 
     def __init__(
         self,
@@ -278,6 +282,7 @@ class KernelRelation:
         repeated_edges: bool | torch.Tensor | None = None,
         direct_expansion: bool = False,
         repeated_coords: torch.Tensor | None = None,
+        block_table: torch.Tensor | None = None,
     ) -> None:
         """``grouped_views``, when given and the input/kernel CSR arrays are
         not, is called on first access of ``input_csr`` / ``kernel_csr`` and
@@ -348,6 +353,7 @@ class KernelRelation:
             self, 'repeated_coords',
             _StatusWord(repeated_coords) if repeated_coords is not None
             else None)
+        object.__setattr__(self, 'block_table', block_table)
         object.__setattr__(self, 'direct_expansion', bool(direct_expansion))
 
     @property

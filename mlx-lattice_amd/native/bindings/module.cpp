@@ -34,10 +34,12 @@ py::tuple relation_tuple(const ln::NativeKernelRelation& r) {
 
 // Grouped views are not built here (None); build_relation_grouped_views
 // makes them on demand.  The device status word (lattice_relation_flags)
-// follows the implicit-GEMM view.
+// and the build's workspace (whose block table a later build over the same
+// coordinates may reuse: `table=`) follow the implicit-GEMM view.
 py::tuple relation_tuple_with_view(const ln::NativeKernelRelation& r) {
     return py::make_tuple(r.in_rows, r.out_rows, r.kernel_ids, r.output_row_offsets, r.out_coords, r.counts,
-                          py::none(), py::none(), py::none(), py::none(), r.out_in_map, r.row_masks, r.status);
+                          py::none(), py::none(), py::none(), py::none(), r.out_in_map, r.row_masks, r.status,
+                          r.table);
 }
 
 }  // namespace
@@ -57,19 +59,21 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     auto forward = [](bool with_view) {
         return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,
                            const std::vector<int>& kernel_size, const std::vector<int>& stride,
-                           const std::vector<int>& padding, const std::vector<int>& dilation) {
+                           const std::vector<int>& padding, const std::vector<int>& dilation,
+                           const std::optional<at::Tensor>& table) {
             auto r = ln::make_kernel_relation(coords, active_rows, triple_from_values(kernel_size, "kernel_size"),
                                               triple_from_values(stride, "stride"),
                                               triple_from_values(padding, "padding"),
-                                              triple_from_values(dilation, "dilation"), !with_view);
+                                              triple_from_values(dilation, "dilation"), !with_view, table);
             return with_view ? relation_tuple_with_view(r) : relation_tuple(r);
         };
     };
     m.def("build_kernel_relation", forward(false), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"),
-          "Build a forward sparse kernel relation.");
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
+          py::arg("table") = py::none(), "Build a forward sparse kernel relation.");
     m.def("build_kernel_relation_with_view", forward(true), py::arg("coords"), py::arg("active_rows"),
-          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"));
+          py::arg("kernel_size"), py::arg("stride"), py::arg("padding"), py::arg("dilation"), py::kw_only(),
+          py::arg("table") = py::none());
 
     auto subm = [](bool with_view) {
         return [with_view](const at::Tensor& coords, const at::Tensor& active_rows,

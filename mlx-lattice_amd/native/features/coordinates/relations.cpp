@@ -98,7 +98,7 @@ std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation) {
 
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool with_views) {
+                                          bool with_views, const std::optional<at::Tensor>& table) {
     validate_coords(coords_in);
     validate_active_rows(active_rows);
     validate_positive(kernel_size, "kernel_size");
@@ -112,12 +112,20 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
     NativeKernelRelation r = allocate(coords, rows, rows, K, true, with_views);
     at::Tensor status = empty_i32({1}, coords);
     lattice_relation_outputs o = outputs_of(r, status);
-    at::Tensor ws = workspace(lattice_hip_kernel_relation_workspace_bytes(rows, K), coords);
+    const size_t need = lattice_hip_kernel_relation_workspace_bytes(rows, K);
+    // An earlier build's workspace over the same coordinates keeps its block
+    // table at its start; reuse it when it is large enough for this build.
+    const bool reuse = table.has_value() && table->defined() && table->scalar_type() == at::kByte &&
+                       table->is_contiguous() && table->device() == coords.device() &&
+                       static_cast<size_t>(table->numel()) >= need;
+    at::Tensor ws = reuse ? *table : workspace(need, coords);
+    size_t ws_bytes = static_cast<size_t>(ws.numel());
+    if (reuse) ws_bytes |= LATTICE_RELATION_TABLE_READY;
     check_status(lattice_hip_build_kernel_relation(ci32(coords), rows, ci32(active_rows), kernel_size.data(),
                                                    stride.data(), padding.data(), dilation.data(), &o,
-                                                   ws.data_ptr(), static_cast<size_t>(ws.numel()),
-                                                   current_stream(coords)));
+                                                   ws.data_ptr(), ws_bytes, current_stream(coords)));
     r.status = status;
+    r.table = ws;
     return r;
 }
 

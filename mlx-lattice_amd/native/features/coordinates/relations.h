@@ -30,6 +30,10 @@ struct NativeKernelRelation {
     // The build's device status word (lattice_relation_flags), left on the
     // device: nothing in a build waits for the device.
     at::Tensor status;
+    // The build's workspace, whose start holds the block table of the input
+    // coordinates: a later build over the same coordinates may reuse it
+    // (LATTICE_RELATION_TABLE_READY).
+    at::Tensor table;
 };
 
 std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation);
@@ -37,9 +41,12 @@ std::vector<Triple> kernel_offsets(Triple kernel_size, Triple dilation);
 // Builds never read device memory back: every int32 coordinate is accepted.
 // with_views: also build the grouped CSR views (otherwise their tensors
 // stay undefined and make_relation_grouped_views builds them on demand).
+// table (optional): the `table` of an earlier build over the same coords
+// and active_rows; its block table is reused instead of rebuilt.
 NativeKernelRelation make_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                           Triple kernel_size, Triple stride, Triple padding, Triple dilation,
-                                          bool with_views = true);
+                                          bool with_views = true,
+                                          const std::optional<at::Tensor>& table = std::nullopt);
 
 NativeKernelRelation make_submanifold_kernel_relation(const at::Tensor& coords, const at::Tensor& active_rows,
                                                       Triple kernel_size, Triple dilation,

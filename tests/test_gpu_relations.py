@@ -450,3 +450,49 @@ def test_group_by_key_large_sorts(n, groups, valid):
     counts = np.bincount(k[k < groups], minlength=groups)
     np.testing.assert_array_equal(
         to_np(offsets), np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
+
+
+@pytest.mark.parametrize('ks,stride', [(2, 2), (3, 2), (3, 1)])
+def test_forward_relation_reuses_the_submanifold_block_table(ks, stride):
+    """A forward relation built over the block table a submanifold relation
+    of the same coordinates left in its workspace
+    (LATTICE_RELATION_TABLE_READY) equals one built from scratch, bit for
+    bit; the manager hands the table over once."""
+    from mlx_lattice_amd import SparseTensor
+    from mlx_lattice_amd.core.coords.builders import build_kernel_relation
+
+    if ks == 3 and stride == 1:
+        coords = extreme_cloud(40 + ks)
+    else:
+        from mlx_lattice_amd.synthetic import lidar_cloud
+        coords = lidar_cloud(3000, 2, rng=np.random.default_rng(40 + ks))
+    n = len(coords)
+    c = _t(coords)
+    x = SparseTensor(c, torch.zeros((n, 4), device=DEV))
+    mgr = x.coord_manager
+    mgr.submanifold_kernel_relation(x.coord_key, kernel_size=3)
+    assert x.coord_key in mgr._block_tables
+    print(f'table reuse k={ks} s={stride} N={n}', flush=True)
+    reused = mgr.kernel_relation(x.coord_key, kernel_size=ks, stride=stride)
+    assert x.coord_key not in mgr._block_tables
+    fresh = build_kernel_relation(c, _active(n), kernel_size=ks,
+                                  stride=stride)
+    torch.cuda.synchronize()
+
+    def arrays(rel):
+        return {'in_rows': to_np(rel.edges.in_rows),
+                'out_rows': to_np(rel.edges.out_rows),
+                'kernel_ids': to_np(rel.edges.kernel_ids),
+                'counts': to_np(rel.counts),
+                'row_offsets': to_np(rel.output_csr.row_offsets),
+                'in_row_offsets': to_np(rel.input_csr.row_offsets),
+                'in_edge_ids': to_np(rel.input_csr.edge_ids),
+                'kernel_row_offsets': to_np(rel.kernel_csr.row_offsets),
+                'kernel_edge_ids': to_np(rel.kernel_csr.edge_ids),
+                'out_coords': to_np(rel.out_coords)}
+
+    assert_relation_equal(arrays(reused), arrays(fresh))
+    n_out = int(fresh.counts[1].item())
+    np.testing.assert_array_equal(
+        to_np(reused.require_implicit_gemm().out_in_map)[:n_out],
+        to_np(fresh.require_implicit_gemm().out_in_map)[:n_out])
