@@ -228,7 +228,10 @@ struct CoordTable {
             const bool hit = prev == kEmptyKey || (k.wide ? same_tag(prev, k) && src.key_of(claim_row(prev)) == k.full
                                                           : prev == k.word);
             if (hit) {
-                atomicMin(&slots[slot].row, row);
+                // The stored row only decreases, so a row at or below ours,
+                // even a stale read of it, makes the atomic a no-op: skip it
+                // (a key inserted by several rows mostly needs one).
+                if (prev == kEmptyKey || slots[slot].row > row) atomicMin(&slots[slot].row, row);
                 return slot;
             }
             slot = (slot + 1) & mask;
