@@ -56,10 +56,13 @@ def parse_args():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-secondary', action='store_true',
                    help='skip the timings of configs 2, 4 and 5')
-    p.add_argument('--phase', choices=('all', 'config3', 'secondary'),
+    p.add_argument('--phase', choices=('all', 'config3', 'secondary',
+                                       'backward'),
                    default='all',
                    help='config3: only the headline step (for profiler '
-                        'runs); secondary: only configs 2, 4 and 5')
+                        'runs); secondary: only configs 2, 4 and 5 and '
+                        'config 3 read literally; backward: only the config-3 '
+                        'gradients')
     return p.parse_args()
 
 
@@ -331,7 +334,7 @@ def backward_workload(feats, weight, coords, active, edges: int, steps: int,
     the input gradient on the matrix cores over the forward's own sorted
     view with the mirrored transposed weight (a submanifold relation over
     distinct coordinates needs no transposed view), the weight gradient by
-    the edge-balanced MFMA kernel."""
+    the edge-balanced lock-step MFMA kernel."""
     import torch
 
     from mlx_lattice_amd import SparseTensor
@@ -356,7 +359,7 @@ def backward_workload(feats, weight, coords, active, edges: int, steps: int,
     return {
         'workload': 'config3 gradients: input grad (matrix cores over the '
                     'forward sorted view, mirrored weight) and weight grad '
-                    '(edge-balanced MFMA)',
+                    '(edge-balanced lock-step MFMA)',
         'input_grad_ms': round(t_in, 4),
         'input_grad_tflops': round(flops / t_in / 1e9, 2),
         'weight_grad_ms': round(t_w, 4),
@@ -613,6 +616,14 @@ def main() -> int:
     weight = torch.as_tensor(weight_np).to(dev)
     active = torch.tensor([coords.shape[0]], dtype=torch.int32, device=dev)
     n_out = int(coords.shape[0])
+    if args.phase == 'backward':
+        native = ext.build_submanifold_kernel_relation_with_view(
+            coords, active, [3, 3, 3], [1, 1, 1])
+        edges = int(native[5][0].item())
+        print(json.dumps({'backward': backward_workload(
+            feats, weight, coords, active, edges, args.steps, args.warmup)}),
+            flush=True)
+        return 0
 
     def map_build():
         native = ext.build_submanifold_kernel_relation_with_view(

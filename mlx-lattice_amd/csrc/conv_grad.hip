@@ -17,18 +17,20 @@
 //    with the weight transposed to (C_in, K, C_out).
 //  * Weight gradient: dW[k] = sum over the edges of k of
 //    feats[in]^T cot[out] (eval_weight_grad_typed), a contraction over
-//    edges.  The matrix-core kernel deals G blocks per channel tile
-//    (128 x 128 when the channels fill it, so an edge's rows are gathered
-//    once for every channel pair) to the offsets in proportion to their
-//    edge counts (kernel-grouped CSR: kernel_row_offsets /
-//    kernel_edge_ids), so every block sums about the same number of edges.
-//    A block stages 64 edges of both operands in LDS as edge rows, reads
-//    the MFMA fragments (8 consecutive edges per lane) with transposing
-//    LDS reads and accumulates in fp32.  Each block writes its partial tile; a second
-//    kernel sums an offset's partials in block order and rounds once, so
-//    results
-//    are deterministic.  Other dtypes and shapes take a one-lane-per-weight
-//    kernel.
+//    edges.  The matrix-core kernel splits each offset's kernel-grouped
+//    edges (kernel_row_offsets / kernel_edge_ids, in output-row order) into
+//    eight parts, one per XCD, and deals an XCD's blocks to the offsets in
+//    proportion to their edge counts; an offset's blocks take its part's
+//    64-edge chunks in turn, so the XCD's blocks sweep the same output rows
+//    together and a cotangent row stays in L2 between the offsets that read
+//    it.  Channel tiles are 128 x 128 when the channels fill them (an
+//    edge's rows are gathered once for every channel pair).  A block stages
+//    64 edges of both operands in LDS as edge rows, reads the MFMA
+//    fragments (8 consecutive edges per lane) with transposing LDS reads
+//    and accumulates in fp32.  Each block writes its partial tile; a second
+//    kernel sums an offset's partials in a fixed order and rounds once, so
+//    results are deterministic.  Other dtypes and shapes take a
+//    one-lane-per-weight kernel.
 
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
@@ -208,52 +210,88 @@ __device__ inline V wg_fragment(const T* lds, int ks, int c0, int lane) {
     return __builtin_bit_cast(V, both);
 }
 
-// Blocks of offset k's edges: the G blocks are dealt to the offsets in
-// proportion to their edge counts, at least one each: offset k owns blocks
-// [wg_first_block(k), wg_first_block(k + 1)), where
-// wg_first_block(k) = k + (G - K) * (edges before k) / (all edges).
-__device__ inline int wg_first_block(const int32_t* koff, int k, int K, int blocks) {
+// Lock-step plan of the weight gradient.  The kernel-grouped edges of each
+// offset are in output-row order, so part x (of kXcds equal parts) of every
+// offset's edges covers about the same output rows.  The blocks of XCD x
+// (launch index = x mod kXcds) all work on part x: S slots per XCD dealt
+// to the offsets in proportion to their edge counts (at least one each),
+// and the m_k blocks of offset k take its part's 64-edge chunks in turn
+// (block j: chunks j, j + m_k, ...).  Every block then sums about the same
+// number of edges, and all blocks of an XCD move through their part's
+// output rows together, so the cotangent row of an output row, read once
+// per offset, stays in that XCD's L2 between the offsets that read it.
+constexpr int kXcds = 8;
+
+// Blocks offset k gets on each XCD; first = blocks of the offsets before k.
+__device__ inline void wg_share(const int32_t* koff, int K, int slots, int k, int* first, int* count) {
     const long long total = koff[K] - koff[0];
-    if (total <= 0) return k * (blocks / K);
-    return k + static_cast<int>(static_cast<long long>(blocks - K) * (koff[k] - koff[0]) / total);
+    int nz = 0;
+    for (int i = 0; i < K; ++i) nz += koff[i + 1] > koff[i] ? 1 : 0;
+    const long long spare = slots - nz;
+    int acc = 0;
+    *first = 0;
+    *count = 0;
+    for (int i = 0; i <= k; ++i) {
+        const long long n = koff[i + 1] - koff[i];
+        const int m = n > 0 ? 1 + static_cast<int>(spare * n / total) : 0;
+        if (i == k) {
+            *first = acc;
+            *count = m;
+        }
+        acc += m;
+    }
 }
 
-// Block (tile, b): channel tile TCI x TCO, four waves of (TCI/2) x
-// (TCO/2), over an equal share of one offset's edges (the offsets get
-// blocks in proportion to their edge counts, so every block sums about the
-// same number of edges and the launch drains evenly).  Per step of 64 edges
-// the block stages both operands into edge-major LDS rows.
+// Block (launch index): XCD x = index mod 8, then (tile, slot) from
+// index / 8; channel tile TCI x TCO, four waves of (TCI/2) x (TCO/2).  Per
+// step of 64 edges the block stages both operands into edge-major LDS rows.
 template <typename T, int TCI, int TCO>
 __global__ void __launch_bounds__(256, 3)
 weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ cot, int n_out, int c_out,
                  const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
                  const int32_t* __restrict__ counts, int edge_capacity, const int32_t* __restrict__ koff,
-                 const int32_t* __restrict__ kedges, int K, int tiles_co, float* __restrict__ partial) {
+                 const int32_t* __restrict__ kedges, int K, int tiles, int tiles_co, int slots,
+                 float* __restrict__ partial) {
     using V = typename GradMfma<T>::vec;
     constexpr int MB = TCI / 32;  // 16-row blocks per wave
     constexpr int NB = TCO / 32;  // 16-column blocks per wave
     __shared__ __align__(16) T a_t[kWgEdges * TCI];
     __shared__ __align__(16) T b_t[kWgEdges * TCO];
-    const int tile = blockIdx.x;
-    const int b = blockIdx.y;
-    const int blocks = gridDim.y;
-    int k = 0;
-    int first = wg_first_block(koff, 0, K, blocks);
-    int next = wg_first_block(koff, 1, K, blocks);
-    while (k + 1 < K && next <= b) {
-        ++k;
-        first = next;
-        next = wg_first_block(koff, k + 1, K, blocks);
+    const int x = static_cast<int>(blockIdx.x) % kXcds;
+    const int q = static_cast<int>(blockIdx.x) / kXcds;
+    const int tile = q % tiles;
+    const int slot = q / tiles;
+    // The offset and the turn of this slot.
+    int k = -1, turn = 0, turns = 0;
+    {
+        const long long total = koff[K] - koff[0];
+        if (total <= 0) return;
+        int nz = 0;
+        for (int i = 0; i < K; ++i) nz += koff[i + 1] > koff[i] ? 1 : 0;
+        const long long spare = slots - nz;
+        int acc = 0;
+        for (int i = 0; i < K; ++i) {
+            const long long n = koff[i + 1] - koff[i];
+            const int m = n > 0 ? 1 + static_cast<int>(spare * n / total) : 0;
+            if (slot < acc + m) {
+                k = i;
+                turn = slot - acc;
+                turns = m;
+                break;
+            }
+            acc += m;
+        }
     }
-    const int share = b - first;
-    const int shares = next - first;
+    if (k < 0) return;  // a spare slot: no partial tile is read for it
     const int ci0 = (tile / tiles_co) * TCI;
     const int co0 = (tile % tiles_co) * TCO;
     const int E = min(counts[0], edge_capacity);
     const int lo_k = koff[k];
-    const int n_k = koff[k + 1] - lo_k;
-    const int lo = lo_k + static_cast<int>(static_cast<long long>(n_k) * share / shares);
-    const int hi = lo_k + static_cast<int>(static_cast<long long>(n_k) * (share + 1) / shares);
+    const long long n_k = koff[k + 1] - lo_k;
+    const int lo = lo_k + static_cast<int>(n_k * x / kXcds);
+    const int hi = lo_k + static_cast<int>(n_k * (x + 1) / kXcds);
+    const int stride = turns * kWgEdges;  // the block's chunks: lo + 64 (turn + t turns)
+    const int start = lo + turn * kWgEdges;
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -321,13 +359,13 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         }
     };
     int ev[2], ri[2], ro[2];
-    fetch_edges(lo, ev);
+    fetch_edges(start, ev);
     fetch_rows(ev, ri, ro);
     gather(ri, ro);
-    fetch_edges(lo + kWgEdges, ev);
+    fetch_edges(start + stride, ev);
     fetch_rows(ev, ri, ro);
-    fetch_edges(lo + 2 * kWgEdges, ev);
-    for (int base = lo; base < hi; base += kWgEdges) {
+    fetch_edges(start + 2 * stride, ev);
+    for (int base = start; base < hi; base += stride) {
         // The thread's two edges take rows j and j + 32 (the order of edges
         // inside a step is free: the sum over them is in fp32).
 #pragma unroll
@@ -342,7 +380,7 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         __syncthreads();
         gather(ri, ro);
         fetch_rows(ev, ri, ro);
-        fetch_edges(base + 3 * kWgEdges, ev);
+        fetch_edges(base + 3 * stride, ev);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             V af[MB], bf[NB];
@@ -360,7 +398,7 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         __syncthreads();
     }
     // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
-    float* out = partial + static_cast<long long>(b) * c_in * c_out;
+    float* out = partial + static_cast<long long>(x * slots + slot) * c_in * c_out;
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
@@ -373,21 +411,23 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
             }
 }
 
-// dW[k] = sum of the partials of offset k's blocks in block order, one
-// rounding, written in the weight's layout.
+// dW[k] = sum of the partial tiles of offset k's blocks (XCD by XCD, then
+// turn by turn), one rounding, written in the weight's layout.  Blocks
+// (x, k): offset k's share is worked out once per thread, then the block
+// strides over the offset's C_in x C_out entries.
 template <typename T>
 __global__ void __launch_bounds__(256)
-weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict__ koff, int blocks,
+weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict__ koff, int slots,
                    GradWeightIndex widx, T* __restrict__ grad) {
     const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
-    const long long per = widx.K * mat;
-    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < per;
-         i += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const int k = static_cast<int>(i / mat);
-        const long long within = i - k * mat;
-        const int end = wg_first_block(koff, k + 1, widx.K, blocks);
+    const int k = blockIdx.y;
+    int first = 0, count = 0;
+    if (koff[widx.K] > koff[0]) wg_share(koff, widx.K, slots, k, &first, &count);
+    for (long long within = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; within < mat;
+         within += static_cast<long long>(gridDim.x) * blockDim.x) {
         float acc = 0.0f;
-        for (int blk = wg_first_block(koff, k, widx.K, blocks); blk < end; ++blk) acc += partial[blk * mat + within];
+        for (int x = 0; x < kXcds; ++x)
+            for (int j = 0; j < count; ++j) acc += partial[(x * slots + first + j) * mat + within];
         const int co = static_cast<int>(within % widx.c_out);
         const int ci = static_cast<int>(within / widx.c_out);
         grad[widx(k, ci, co)] = static_cast<T>(acc);
@@ -432,22 +472,22 @@ int check_grad_dtype(int dtype) {
     return LATTICE_OK;
 }
 
-// Blocks per channel tile of the matrix-core weight gradient: about 2,048
-// edge slots of the relation's capacity each, at least one per offset, at
-// most 768, one round of three blocks on each of the 256 CUs.  The kernel
-// is bound by its row gathers, so fewer, longer blocks with fewer partial
-// tiles ran faster than two or three rounds (config 3: 768 blocks 436 us,
-// 1,536 blocks 477 us, 1,024 blocks 542 us).
+// Slots per XCD (blocks per channel tile = 8 x slots) of the matrix-core
+// weight gradient: about 2,048 edge slots of the relation's capacity per
+// block, at least one per offset, at most 96 (three blocks on each of an
+// XCD's 32 CUs: one round, so the blocks of an XCD move together).
 constexpr int kWgEdgesPerBlock = 2048;
-constexpr int kWgMaxBlocks = 768;
-int weight_grad_blocks(int edge_capacity, int kernel_count) {
-    const long long want = (static_cast<long long>(edge_capacity) + kWgEdgesPerBlock - 1) / kWgEdgesPerBlock;
-    return static_cast<int>(std::max<long long>(kernel_count, std::min<long long>(kWgMaxBlocks, want)));
+constexpr int kWgMaxSlots = 96;
+int weight_grad_slots(int edge_capacity, int kernel_count) {
+    const long long want =
+        (static_cast<long long>(edge_capacity) + kXcds * kWgEdgesPerBlock - 1) / (kXcds * kWgEdgesPerBlock);
+    return static_cast<int>(std::max<long long>(kernel_count, std::min<long long>(kWgMaxSlots, want)));
 }
 
 // One fp32 partial tile per block.
 size_t weight_grad_partial_bytes(int edge_capacity, int kernel_count, int c_in, int c_out) {
-    return static_cast<size_t>(weight_grad_blocks(edge_capacity, kernel_count)) * c_in * c_out * sizeof(float);
+    return static_cast<size_t>(kXcds) * weight_grad_slots(edge_capacity, kernel_count) * c_in * c_out *
+           sizeof(float);
 }
 
 bool weight_grad_mfma_ok(int dtype, int c_in, int c_out) {
@@ -475,7 +515,7 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
                        size_t workspace_bytes, hipStream_t stream) {
     if (weight_grad_mfma_ok(dtype, widx.c_in, widx.c_out) && workspace != nullptr) {
         if constexpr (!std::is_same<T, float>::value) {
-            const int blocks = weight_grad_blocks(edge_capacity, widx.K);
+            const int slots = weight_grad_slots(edge_capacity, widx.K);
             const size_t need = weight_grad_partial_bytes(edge_capacity, widx.K, widx.c_in, widx.c_out);
             LATTICE_REQUIRE(workspace_bytes >= need, "weight gradient workspace too small.");
             float* partial = static_cast<float*>(workspace);
@@ -485,21 +525,22 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
             const int tco = widx.c_out > 64 ? 128 : 64;
             const int tiles_ci = (widx.c_in + tci - 1) / tci;
             const int tiles_co = (widx.c_out + tco - 1) / tco;
-            dim3 grid(static_cast<unsigned>(tiles_ci * tiles_co), static_cast<unsigned>(blocks));
+            const int tiles = tiles_ci * tiles_co;
+            const unsigned grid = static_cast<unsigned>(kXcds) * slots * tiles;
 #define LATTICE_WG_LAUNCH(A, B)                                                                                 \
     weight_grad_mfma<T, A, B><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,          \
                                                         static_cast<const T*>(cot), n_out, widx.c_out, in_rows,  \
                                                         out_rows, counts, edge_capacity, koff, kedges, widx.K,   \
-                                                        tiles_co, partial)
+                                                        tiles, tiles_co, slots, partial)
             if (tci == 128 && tco == 128) LATTICE_WG_LAUNCH(128, 128);
             else if (tci == 128) LATTICE_WG_LAUNCH(128, 64);
             else if (tco == 128) LATTICE_WG_LAUNCH(64, 128);
             else LATTICE_WG_LAUNCH(64, 64);
 #undef LATTICE_WG_LAUNCH
             LATTICE_LAUNCH_CHECK();
-            const long long per = static_cast<long long>(widx.K) * widx.c_in * widx.c_out;
-            weight_grad_reduce<T><<<grid_for(per, 256, 4096), 256, 0, stream>>>(partial, koff, blocks, widx,
-                                                                              static_cast<T*>(grad));
+            const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
+            const dim3 rgrid(grid_for(mat, 256, 256), static_cast<unsigned>(widx.K));
+            weight_grad_reduce<T><<<rgrid, 256, 0, stream>>>(partial, koff, slots, widx, static_cast<T*>(grad));
             LATTICE_LAUNCH_CHECK();
             return LATTICE_OK;
         }
