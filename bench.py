@@ -57,12 +57,13 @@ def parse_args():
     p.add_argument('--no-secondary', action='store_true',
                    help='skip the timings of configs 2, 4 and 5')
     p.add_argument('--phase', choices=('all', 'config3', 'secondary',
-                                       'backward'),
+                                       'backward', 'widened'),
                    default='all',
                    help='config3: only the headline step (for profiler '
                         'runs); secondary: only configs 2, 4 and 5 and '
                         'config 3 read literally; backward: only the config-3 '
-                        'gradients')
+                        'gradients; widened: only the gradient, pooling, '
+                        'decoder and quantization lines')
     return p.parse_args()
 
 
@@ -623,6 +624,18 @@ def main() -> int:
         print(json.dumps({'backward': backward_workload(
             feats, weight, coords, active, edges, args.steps, args.warmup)}),
             flush=True)
+        return 0
+    if args.phase == 'widened':
+        native = ext.build_submanifold_kernel_relation_with_view(
+            coords, active, [3, 3, 3], [1, 1, 1])
+        edges = int(native[5][0].item())
+        print(json.dumps({
+            'backward': backward_workload(feats, weight, coords, active,
+                                          edges, args.steps, args.warmup),
+            'pooling': pooling_workload(coords, args.steps, args.warmup),
+            'decoder': decoder_workload(coords, args.steps, args.warmup),
+            'quantization': quantization_workload(coords, args.steps,
+                                                  args.warmup)}), flush=True)
         return 0
 
     def map_build():

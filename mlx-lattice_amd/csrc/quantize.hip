@@ -315,18 +315,57 @@ map_points(BlockTable table, const float* __restrict__ points, const int32_t* __
                     ok = floor_int(pos[a], &lo[a]) && ok;
                     frac[a] = (pos[a] - static_cast<float>(lo[a]));
                 }
-                if (ok) {
+                const auto weight = [&](int dx, int dy, int dz) {
+                    const float wx = dx == 0 ? (1.0f - frac[0]) : frac[0];
+                    const float wy = dy == 0 ? (1.0f - frac[1]) : frac[1];
+                    const float wz = dz == 0 ? (1.0f - frac[2]) : frac[2];
+                    return ((wx * wy) * wz);
+                };
+                // When the cell's blocks have packed keys (batch in [0, 1022],
+                // lo in [-2^18, 2^18 - 2] per axis) every corner's home bucket
+                // (key word and the corner's row word) is read before any is
+                // resolved, so the eight lookups overlap; a corner whose home
+                // bucket holds another key continues by linear probing.
+                const auto packs = [](int64_t v) { return v >= -(1 << 18) && v <= (1 << 18) - 2; };
+                if (ok && b >= 0 && b <= LATTICE_MAX_BATCH && packs(lo[0]) && packs(lo[1]) && packs(lo[2])) {
+                    const int x0 = static_cast<int>(lo[0]), y0 = static_cast<int>(lo[1]), z0 = static_cast<int>(lo[2]);
+                    uint64_t want[8];
+                    uint32_t slot[8];
+                    unsigned long long seen[8];
+                    int32_t raw[8];
+#pragma unroll
+                    for (int corner = 0; corner < 8; ++corner) {
+                        const int x = x0 + (corner & 1), y = y0 + ((corner >> 1) & 1), z = z0 + ((corner >> 2) & 1);
+                        pack_key(b, x >> 1, y >> 1, z >> 1, &want[corner]);
+                        slot[corner] = static_cast<uint32_t>(mix64(want[corner])) & table.mask;
+                        seen[corner] = table.buckets[slot[corner]].key;
+                        raw[corner] = table.buckets[slot[corner]].rows[((x & 1) << 2) | ((y & 1) << 1) | (z & 1)];
+                    }
 #pragma unroll
                     for (int corner = 0; corner < 8; ++corner) {
                         const int dx = corner & 1, dy = (corner >> 1) & 1, dz = (corner >> 2) & 1;
-                        const int row = probe(table, b, lo[0] + dx, lo[1] + dy, lo[2] + dz);
-                        if (row < 0) continue;
-                        const float wx = dx == 0 ? (1.0f - frac[0]) : frac[0];
-                        const float wy = dy == 0 ? (1.0f - frac[1]) : frac[1];
-                        const float wz = dz == 0 ? (1.0f - frac[2]) : frac[2];
-                        r[corner] = row;
-                        w[corner] = ((wx * wy) * wz);
+                        const int oct = (((x0 + dx) & 1) << 2) | (((y0 + dy) & 1) << 1) | ((z0 + dz) & 1);
+                        while (seen[corner] != want[corner] && seen[corner] != kEmptyKey) {
+                            slot[corner] = (slot[corner] + 1) & table.mask;
+                            seen[corner] = table.buckets[slot[corner]].key;
+                            raw[corner] = table.buckets[slot[corner]].rows[oct];
+                        }
+                        if (seen[corner] == want[corner] && raw[corner] != 0) {
+                            r[corner] = kRowBias - raw[corner];
+                            w[corner] = weight(dx, dy, dz);
+                        }
                     }
+                } else if (ok) {
+                    // Wide block keys: the table's full lookup per corner,
+                    // written straight out.
+#pragma unroll 1
+                    for (int corner = 0; corner < 8; ++corner) {
+                        const int dx = corner & 1, dy = (corner >> 1) & 1, dz = (corner >> 2) & 1;
+                        const int row = probe(table, b, lo[0] + dx, lo[1] + dy, lo[2] + dz);
+                        rows_out[8ll * p + corner] = row < 0 ? -1 : row;
+                        weights_out[8ll * p + corner] = row < 0 ? 0.0f : weight(dx, dy, dz);
+                    }
+                    continue;
                 }
             }
         }

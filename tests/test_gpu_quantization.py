@@ -240,6 +240,49 @@ def test_sparse_quantize_full_domain():
         assert (rows >= 0).sum() >= (400 if interpolation == 'nearest' else 3000)
 
 
+def test_point_map_at_the_packed_block_range_edges():
+    """Cells whose lower corner sits on either side of the edge of the
+    packed block-key range (lower corner in [-2^18, 2^18 - 2] per axis and
+    batch in [0, 1022] take the overlapped home-bucket reads, the others
+    the full lookup); every corner voxel present, bit-exact against the
+    oracle."""
+    ops, _ = _ops()
+    edges = np.array([-(1 << 18) - 2, -(1 << 18) - 1, -(1 << 18),
+                      -(1 << 18) + 1, (1 << 18) - 3, (1 << 18) - 2,
+                      (1 << 18) - 1, (1 << 18)], np.int64)
+    cells = []
+    for bt in (0, 1022, 1023):
+        for v in edges:
+            for axis in range(3):
+                c = np.array([5, -7, 11], np.int64)
+                c[axis] = v
+                cells.append((bt, c))
+    vox, pts, bs = [], [], []
+    rng = np.random.default_rng(113)
+    for bt, c in cells:
+        for corner in range(8):
+            d = np.array([corner & 1, (corner >> 1) & 1, (corner >> 2) & 1])
+            vox.append(np.concatenate([[bt], c + d]))
+        # a point at c + frac (unit voxels, origin 0) has the cell lower
+        # corner c; float32 keeps 1/32 at 2^18
+        pts.append(c + rng.uniform(0.1, 0.9, 3))
+        bs.append(bt)
+    vox = np.unique(np.array(vox, np.int64), axis=0).astype(np.int32)
+    pts = np.array(pts, np.float64).astype(np.float32)
+    bs = np.array(bs, np.int32)
+    n_vox = len(vox)
+    print(f'point map range edges voxels={n_vox}', flush=True)
+    pmap = ops.build_point_voxel_map(
+        _f(pts), _i(vox), _i([n_vox]), 1.0, batch_indices=_i(bs),
+        interpolation='linear')
+    torch.cuda.synchronize()
+    rows, w = O.point_voxel_map(pts, vox, n_vox, 1.0, batch_indices=bs,
+                                interpolation='linear')
+    np.testing.assert_array_equal(to_np(pmap.rows), rows)
+    np.testing.assert_array_equal(to_np(pmap.weights), w)
+    assert (rows >= 0).all()
+
+
 @pytest.mark.parametrize('reduction', ['sum', 'mean'])
 def test_voxelize_matches_oracle(reduction):
     ops, _ = _ops()
