@@ -35,6 +35,7 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------ element IO --
 
@@ -1069,7 +1070,7 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
     __shared__ __align__(16) T wbuf[C_OUT * C_IN];
     __shared__ __align__(16) T stage[4][32 * SROW];
     const int lane = lane_id();
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
     const int lr = lane & 15;
     const int lg = lane >> 4;
     const int active = min(max(*active_rows, 0), n_in);
@@ -1085,16 +1086,18 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
                             : V{};
         }
     }
-    float bcol[CB];
+    // bias of the four output channels cb*16 + lg*4 .. +3 this lane stores
+    uint2 bias4[CB];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) bcol[cb] = epi.bias != nullptr ? static_cast<float>(epi.bias[cb * 16 + lr]) : 0.0f;
+    for (int cb = 0; cb < CB; ++cb)
+        bias4[cb] = epi.bias != nullptr ? *reinterpret_cast<const uint2*>(epi.bias + cb * 16 + lg * 4) : uint2{0u, 0u};
     // piece p of W[co, k, :] sits at wbuf[co * C_IN + ((p ^ (co % WPIECES)) * 8)]
     V wreg[WPER];
     auto load_w = [&](int k) {
 #pragma unroll
         for (int j = 0; j < WPER; ++j) {
             const int i = j * 256 + threadIdx.x;
-            if (i < WTOTAL) {
+            if (WTOTAL % 256 == 0 || i < WTOTAL) {
                 const int co = i / WPIECES;
                 const int p = i - co * WPIECES;
                 wreg[j] = *reinterpret_cast<const V*>(weights + (static_cast<long long>(co) * K + k) * C_IN + p * 8);
@@ -1105,7 +1108,7 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
 #pragma unroll
         for (int j = 0; j < WPER; ++j) {
             const int i = j * 256 + threadIdx.x;
-            if (i < WTOTAL) {
+            if (WTOTAL % 256 == 0 || i < WTOTAL) {
                 const int co = i / WPIECES;
                 const int p = i - co * WPIECES;
                 *reinterpret_cast<V*>(wbuf + co * C_IN + ((p ^ (co % WPIECES)) * 8)) = wreg[j];
@@ -1116,8 +1119,17 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
     store_w();
     __syncthreads();
     T* st = stage[wave];
+    // The wave's output rows in0 .. in0 + 31 as a raw buffer: rows past
+    // n_in lie beyond its range, so their stores are dropped with no branch.
+    const long long out_bytes = (in0 < n_in ? static_cast<long long>(n_in - in0) : 0ll) * K * C_OUT * sizeof(T);
+    const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out + static_cast<long long>(min(in0, n_in)) * K * C_OUT, 0,
+        static_cast<int>(min(out_bytes, static_cast<long long>(INT_MAX))), 0x00020000);
     for (int k = 0; k < K; ++k) {
-        if (k + 1 < K) load_w(k + 1);  // in flight during this offset's MFMAs
+        // W[:, k+1, :] (the last offset reloads its own slice, so the loop
+        // body has no branch around its loads and stores) is in flight
+        // during this offset's MFMAs.
+        load_w(min(k + 1, K - 1));
         float4_t acc[2][CB];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -1132,31 +1144,50 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
                 const int p = ks * 4 + lg;
                 b[cb] = *reinterpret_cast<const V*>(wbuf + co * C_IN + ((p ^ (co % WPIECES)) * 8));
             }
+            // The transposed product W[k]^T-fragment x feats^T-fragment:
+            // lane (lr, lg) then holds output channels cb*16 + lg*4 .. +3 of
+            // row rb*16 + lr, four consecutive halves for one 8-byte store.
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = MfmaOps<T>::mfma(a[rb][ks], b[cb], acc[rb][cb]);
+                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = MfmaOps<T>::mfma(b[cb], a[rb][ks], acc[rb][cb]);
         }
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int cb = 0; cb < CB; ++cb) {
+            const T* bq = reinterpret_cast<const T*>(&bias4[cb]);
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
+            for (int rb = 0; rb < 2; ++rb) {
+                T v[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const T v = epi.finish(acc[rb][cb][q], bcol[cb]);
-                    st[(rb * 16 + lg * 4 + q) * SROW + cb * 16 + lr] = v;
-                }
-        __syncthreads();  // every wave has read W[:, k, :] and staged its tile
-        for (int p = lane; p < 32 * PIECES; p += kWave) {
-            const int r = p / PIECES;
-            const int piece = p - r * PIECES;
-            const int in = in0 + r;
-            if (in < n_in) {
-                *reinterpret_cast<V*>(out + (static_cast<long long>(in) * K + k) * C_OUT + piece * 8) =
-                    *reinterpret_cast<const V*>(st + r * SROW + piece * 8);
+                for (int q = 0; q < 4; ++q) v[q] = epi.finish(acc[rb][cb][q], static_cast<float>(bq[q]));
+                *reinterpret_cast<uint2*>(st + (rb * 16 + lr) * SROW + cb * 16 + lg * 4) =
+                    *reinterpret_cast<const uint2*>(v);
             }
         }
-        if (k + 1 < K) store_w();
+        __syncthreads();  // every wave has read W[:, k, :] and staged its tile
+        // W[:, k+1, :] goes to LDS before this offset's rows are stored: the
+        // wait for its loads then covers only stores issued an offset ago,
+        // and this offset's stores drain during the next offset's MFMAs.
+        store_w();
+        {
+            // All of the wave's row pieces are read from the stage first,
+            // then stored: 32 rows x PIECES pieces over the 64 lanes.
+            constexpr int PER = 32 * PIECES / kWave;
+            static_assert(32 * PIECES % kWave == 0, "whole pieces per lane");
+            V piece_v[PER];
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int p = lane + j * kWave;
+                piece_v[j] = *reinterpret_cast<const V*>(st + (p / PIECES) * SROW + (p % PIECES) * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int p = lane + j * kWave;
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4_t, piece_v[j]), out_rsrc,
+                    static_cast<int>((((p / PIECES) * K + k) * C_OUT + (p % PIECES) * 8) * sizeof(T)), 0, 0);
+            }
+        }
         __syncthreads();  // W[:, k+1, :] in LDS; the stage is free again
     }
 }
