@@ -1,5 +1,6 @@
-// Stable LSD radix sort of (key, index) pairs with 9-bit digits
-// (reduce-then-scan).  Per digit pass:
+// Stable LSD radix sort of (key, index) pairs with digits of up to 11 bits
+// (reduce-then-scan): a key of b bits takes ceil(b / 11) passes of equal
+// digit width (27 bits: 3 x 9, 20 bits: 2 x 10).  Per digit pass:
 //   1. sort_count: each tile of 2048 items counts its digits in LDS, writes
 //      them digit-major, count[d * tiles + tile], and adds them to the
 //      per-digit totals;
@@ -23,13 +24,14 @@ namespace {
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 8;                         // per thread
 constexpr int kSortTile = kSortThreads * kSortItems;  // items per tile
-constexpr int kRadixBits = 9;
-constexpr int kDigits = 1 << kRadixBits;
+constexpr int kMaxRadixBits = 11;
+constexpr int kDigits = 1 << kMaxRadixBits;  // digit slots of the widest pass
 constexpr int kSortWaves = kSortThreads / kWave;
 
 struct PassPlan {
     int shift;
     int bits;
+    int rows;  // digit rows of the count matrix: 2^bits, at least kScanRows
 };
 
 // Items of one pass: pass 0 reads the source keys (index = position),
@@ -71,7 +73,7 @@ sort_count(PassInput in, int n, PassPlan plan, int tiles, uint32_t* __restrict__
            uint32_t* __restrict__ digit_totals) {
     if (in.src.run_if != nullptr && *in.src.run_if == 0) return;
     __shared__ uint32_t hist[kDigits];
-    for (int d = threadIdx.x; d < kDigits; d += kSortThreads) hist[d] = 0;
+    for (int d = threadIdx.x; d < plan.rows; d += kSortThreads) hist[d] = 0;
     __syncthreads();
     const int valid_src = valid_items(in, n);
     const uint32_t digit_mask = (1u << plan.bits) - 1u;
@@ -87,7 +89,7 @@ sort_count(PassInput in, int n, PassPlan plan, int tiles, uint32_t* __restrict__
     }
     __syncthreads();
     const int stride = padded_tiles(tiles);
-    for (int d = threadIdx.x; d < kDigits; d += kSortThreads) {
+    for (int d = threadIdx.x; d < plan.rows; d += kSortThreads) {
         counts[static_cast<long long>(d) * stride + blockIdx.x] = hist[d];
         if (hist[d] != 0) atomicAdd(&digit_totals[d], hist[d]);
         if (static_cast<int>(blockIdx.x) == tiles - 1) {
@@ -126,7 +128,8 @@ sort_scan(uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_tota
     __shared__ uint32_t wave_sum[kScanWaves];
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
-    // base(d) for the block's rows: exclusive scan of the 512 digit totals,
+    // base(d) for the block's rows: exclusive scan of the digit totals
+    // (zero past the pass's digits),
     // kDigits / kScanBlockThreads per thread.
     {
         constexpr int kPer = kDigits / kScanBlockThreads;
@@ -203,7 +206,7 @@ sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __re
     const int wave = t / kWave;
     const int lane = lane_id();
     const int tile = blockIdx.x;
-    for (int d = t; d < kDigits; d += kSortThreads) {
+    for (int d = t; d < plan.rows; d += kSortThreads) {
         offset[d] = offsets[static_cast<long long>(d) * padded_tiles(tiles) + tile];
 #pragma unroll
         for (int w = 0; w < kSortWaves; ++w) wave_run[w][d] = 0;
@@ -241,7 +244,7 @@ sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __re
         if (has && below == 0) run[digit[r]] += static_cast<uint32_t>(__popcll(peers));
     }
     __syncthreads();
-    for (int d = t; d < kDigits; d += kSortThreads) {
+    for (int d = t; d < plan.rows; d += kSortThreads) {
         uint32_t sum = 0;
 #pragma unroll
         for (int w = 0; w < kSortWaves; ++w) {
@@ -264,7 +267,16 @@ sort_scatter(PassInput in, int n, PassPlan plan, int tiles, const uint32_t* __re
     }
 }
 
-int pass_count(int end_bit) { return (end_bit + kRadixBits - 1) / kRadixBits; }
+int pass_count(int end_bit) { return (end_bit + kMaxRadixBits - 1) / kMaxRadixBits; }
+
+// Pass p of `passes` over end_bit bits: equal widths, the remainder spread
+// over the first passes.
+PassPlan pass_plan(int p, int passes, int end_bit) {
+    const int base = end_bit / passes, extra = end_bit % passes;
+    const int shift = p * base + std::min(p, extra);
+    const int bits = base + (p < extra ? 1 : 0);
+    return PassPlan{shift, bits, std::max(1 << bits, kScanRows)};
+}
 
 }  // namespace
 
@@ -294,7 +306,7 @@ int radix_sort_indices(const SortKeys& keys, int n, int end_bit, int32_t* sorted
     int rc = fill_i32(reinterpret_cast<int*>(totals), static_cast<long long>(passes) * kDigits, 0, stream);
     if (rc != LATTICE_OK) return rc;
     for (int p = 0; p < passes; ++p) {
-        const PassPlan plan{p * kRadixBits, std::min(kRadixBits, end_bit - p * kRadixBits)};
+        const PassPlan plan = pass_plan(p, passes, end_bit);
         const bool final = p == passes - 1;
         const int in = (p + 1) % 2;  // buffers written by pass p - 1
         const int out = p % 2;
@@ -302,7 +314,7 @@ int radix_sort_indices(const SortKeys& keys, int n, int end_bit, int32_t* sorted
         uint32_t* pass_totals = totals + static_cast<size_t>(p) * kDigits;
         sort_count<<<tiles, kSortThreads, 0, stream>>>(input, n, plan, tiles, counts, pass_totals);
         LATTICE_LAUNCH_CHECK();
-        sort_scan<<<kDigits / kScanRows, kScanBlockThreads, 0, stream>>>(counts, pass_totals, tiles, keys.run_if);
+        sort_scan<<<plan.rows / kScanRows, kScanBlockThreads, 0, stream>>>(counts, pass_totals, tiles, keys.run_if);
         LATTICE_LAUNCH_CHECK();
         sort_scatter<<<tiles, kSortThreads, 0, stream>>>(input, n, plan, tiles, counts, final,
                                                           final ? nullptr : key_buf[out],
