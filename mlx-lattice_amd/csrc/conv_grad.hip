@@ -313,58 +313,76 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
     const int j = threadIdx.x >> 3;
     const int p = threadIdx.x & 7;
     V av[2][PA], bv[2][PB];
+    bool aok[2][PA], bok[2][PB];
     // Three-stage pipeline over the steps: the edge ids of step s+3 and the
     // row indices of step s+2 are loaded while the rows of step s+1 are
     // gathered, so no step waits on a dependent index load.  Edges past the
-    // share's end or outside the relation read as zeros (row -1).
-    auto fetch_edges = [&](int base, int (&ev)[2]) {
+    // share's end or outside the relation count as zeros.  Every load is
+    // issued unconditionally (clamped address, validity kept aside) and the
+    // index loads go out before the gathers: gfx950's vector-memory counter
+    // retires in issue order, so a wait for an index issued after the
+    // gathers would also wait for the gathers.
+    const int last_edge = max(hi - 1, 0);
+    auto issue_edges = [&](int base, int (&evr)[2], bool (&evv)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int cur = base + j + 32 * h;
-            ev[h] = cur < hi ? kedges[cur] : -1;
+            evv[h] = cur < hi;
+            evr[h] = kedges[min(cur, last_edge)];
         }
     };
-    auto fetch_rows = [&](const int (&ev)[2], int (&ri)[2], int (&ro)[2]) {
+    auto edges_of = [&](const int (&evr)[2], const bool (&evv)[2], int (&ev)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ev[h] = evv[h] ? evr[h] : -1;
+    };
+    auto issue_rows = [&](const int (&ev)[2], int (&rin)[2], int (&rout)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            ri[h] = -1;
-            ro[h] = -1;
-            const int e = ev[h];
-            if (e < 0 || e >= E) continue;
-            const int in = in_rows[e];
-            const int o = out_rows[e];
-            if (in < 0 || in >= n_in || o < 0 || o >= n_out) continue;
-            ri[h] = in;
-            ro[h] = o;
+            const int e = ev[h] >= 0 && ev[h] < E ? ev[h] : 0;
+            rin[h] = in_rows[e];
+            rout[h] = out_rows[e];
+        }
+    };
+    auto rows_of = [&](const int (&ev)[2], const int (&rin)[2], const int (&rout)[2], int (&ri)[2], int (&ro)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool ok = ev[h] >= 0 && ev[h] < E && rin[h] >= 0 && rin[h] < n_in && rout[h] >= 0 &&
+                            rout[h] < n_out;
+            ri[h] = ok ? rin[h] : -1;
+            ro[h] = ok ? rout[h] : -1;
         }
     };
     auto gather = [&](const int (&ri)[2], const int (&ro)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int i = 0; i < PA; ++i) av[h][i] = V{};
-#pragma unroll
-            for (int i = 0; i < PB; ++i) bv[h][i] = V{};
-            if (ri[h] < 0) continue;
+            const long long rin = ri[h] >= 0 ? ri[h] : 0, rout = ro[h] >= 0 ? ro[h] : 0;
 #pragma unroll
             for (int i = 0; i < PA; ++i) {
                 const int c = ci0 + 8 * (p + 8 * i);
-                if (c < c_in) av[h][i] = *reinterpret_cast<const V*>(feats + static_cast<long long>(ri[h]) * c_in + c);
+                aok[h][i] = ri[h] >= 0 && c < c_in;
+                av[h][i] = *reinterpret_cast<const V*>(feats + rin * c_in + (c < c_in ? c : 0));
             }
 #pragma unroll
             for (int i = 0; i < PB; ++i) {
                 const int c = co0 + 8 * (p + 8 * i);
-                if (c < c_out) bv[h][i] = *reinterpret_cast<const V*>(cot + static_cast<long long>(ro[h]) * c_out + c);
+                bok[h][i] = ro[h] >= 0 && c < c_out;
+                bv[h][i] = *reinterpret_cast<const V*>(cot + rout * c_out + (c < c_out ? c : 0));
             }
         }
     };
-    int ev[2], ri[2], ro[2];
-    fetch_edges(start, ev);
-    fetch_rows(ev, ri, ro);
+    int ev[2], evr[2], ri[2], ro[2], rin[2], rout[2];
+    bool evv[2];
+    issue_edges(start, evr, evv);
+    edges_of(evr, evv, ev);
+    issue_rows(ev, rin, rout);
+    rows_of(ev, rin, rout, ri, ro);
     gather(ri, ro);
-    fetch_edges(start + stride, ev);
-    fetch_rows(ev, ri, ro);
-    fetch_edges(start + 2 * stride, ev);
+    issue_edges(start + stride, evr, evv);
+    edges_of(evr, evv, ev);
+    issue_rows(ev, rin, rout);
+    rows_of(ev, rin, rout, ri, ro);
+    issue_edges(start + 2 * stride, evr, evv);
+    edges_of(evr, evv, ev);
     for (int base = start; base < hi; base += stride) {
         // The thread's two edges take rows j and j + 32 (the order of edges
         // inside a step is free: the sum over them is in fp32).
@@ -372,29 +390,41 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int i = 0; i < PA; ++i)
-                *reinterpret_cast<V*>(a_t + wg_piece_slot<TCI>(j + 32 * h, p + 8 * i)) = av[h][i];
+                *reinterpret_cast<V*>(a_t + wg_piece_slot<TCI>(j + 32 * h, p + 8 * i)) = aok[h][i] ? av[h][i] : V{};
 #pragma unroll
             for (int i = 0; i < PB; ++i)
-                *reinterpret_cast<V*>(b_t + wg_piece_slot<TCO>(j + 32 * h, p + 8 * i)) = bv[h][i];
+                *reinterpret_cast<V*>(b_t + wg_piece_slot<TCO>(j + 32 * h, p + 8 * i)) = bok[h][i] ? bv[h][i] : V{};
         }
         __syncthreads();
-        gather(ri, ro);
-        fetch_rows(ev, ri, ro);
-        fetch_edges(base + 3 * stride, ev);
+        issue_rows(ev, rin, rout);                   // row indices of step s+2
+        int ev_next[2];
+        {
+            int evr_n[2];
+            bool evv_n[2];
+            issue_edges(base + 3 * stride, evr_n, evv_n);  // edge ids of step s+3
+            // Keep the index loads ahead of the gathers in issue order.
+            __builtin_amdgcn_sched_barrier(0);
+            gather(ri, ro);  // rows of step s+1
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            V af[MB], bf[NB];
+            for (int ks = 0; ks < 2; ++ks) {
+                V af[MB], bf[NB];
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
-                af[m] = wg_fragment<V, TCI>(a_t, ks, (TCI / 2) * wm + 16 * m, lane);
+                for (int m = 0; m < MB; ++m)
+                    af[m] = wg_fragment<V, TCI>(a_t, ks, (TCI / 2) * wm + 16 * m, lane);
 #pragma unroll
-            for (int n = 0; n < NB; ++n)
-                bf[n] = wg_fragment<V, TCO>(b_t, ks, (TCO / 2) * wn + 16 * n, lane);
+                for (int n = 0; n < NB; ++n)
+                    bf[n] = wg_fragment<V, TCO>(b_t, ks, (TCO / 2) * wn + 16 * n, lane);
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
+                for (int m = 0; m < MB; ++m)
 #pragma unroll
-                for (int n = 0; n < NB; ++n) acc[m][n] = GradMfma<T>::mfma(af[m], bf[n], acc[m][n]);
+                    for (int n = 0; n < NB; ++n) acc[m][n] = GradMfma<T>::mfma(af[m], bf[n], acc[m][n]);
+            }
+            edges_of(evr_n, evv_n, ev_next);
         }
+        rows_of(ev, rin, rout, ri, ro);
+        ev[0] = ev_next[0];
+        ev[1] = ev_next[1];
         __syncthreads();
     }
     // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
