@@ -1438,6 +1438,7 @@ resolve_candidates(BlockTable table, const int32_t* __restrict__ coords, int row
 
 constexpr int kResolveRows = 64;
 constexpr int kResolveCells = 64;
+constexpr int kMaxRowMembers = 8;  // candidate list slots per representative
 
 // Exclusive scan of an (x, y) pair over the block's threads; the block
 // total comes back through `total`.  Every thread of the block calls it.
@@ -1535,7 +1536,7 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
                          Int3 step, int32_t* status,
                          int32_t* __restrict__ reps, int32_t* __restrict__ flags, int32_t* __restrict__ sizes,
                          int32_t* __restrict__ ranks, int32_t* __restrict__ tile_firsts,
-                         int32_t* __restrict__ tile_edges) {
+                         int32_t* __restrict__ tile_edges, int32_t* __restrict__ member_ids, int max_members) {
     __shared__ int32_t found[kResolveRows * kResolveCells];
     const int K = g.volume;
     const int active = min(max(*active_rows, 0), rows);
@@ -1601,12 +1602,28 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
                             }
                         }
                     }
+                    // The representative lists its output row's candidates
+                    // (in * K + k) in kernel-id order, the row's edge order.
+                    if (member_ids != nullptr && rep == j) {
+                        int32_t* dst = member_ids + static_cast<long long>(j) * max_members;
+                        int m = 0;
+                        for (int ax = ax0, tx = tx0; ax < g.size.x; ax += period.x, --tx) {
+                            const int cx = tx * step.x + reach.x;
+                            for (int ay = ay0, ty = ty0; ay < g.size.y; ay += period.y, --ty) {
+                                const int cy = ty * step.y + reach.y;
+                                for (int az = az0, tz = tz0; az < g.size.z; az += period.z, --tz) {
+                                    const int r = f[(cx * dy_n + cy) * dz_n + tz * step.z + reach.z];
+                                    if (r >= 0) dst[m++] = r * K + ax * yz + ay * g.size.z + az;
+                                }
+                            }
+                        }
+                    }
                 }
             }
             reps[j] = rep;
             flags[j] = rep == j ? 1 : 0;
             sizes[j] = rep == j ? members : 0;
-            ranks[j] = before;
+            if (member_ids == nullptr) ranks[j] = before;  // the listed path places edges without ranks
             if (rep == j) {
                 mine.x += 1;
                 mine.y += members;
@@ -1633,7 +1650,9 @@ __global__ void __launch_bounds__(kThreads)
 place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
                  KernelGeometry g, const int32_t* __restrict__ reps, const int32_t* __restrict__ flags,
                  const int32_t* __restrict__ positions, const int32_t* __restrict__ edge_offsets,
-                 const int32_t* __restrict__ ranks, lattice_relation_outputs out, int32_t* __restrict__ keys) {
+                 const int32_t* __restrict__ ranks, const int32_t* __restrict__ sizes,
+                 const int32_t* __restrict__ member_ids, int max_members, lattice_relation_outputs out,
+                 int32_t* __restrict__ keys) {
     const int K = g.volume;
     const int cap = rows * K;
     const int total = min(max(*active_rows, 0), rows) * K;
@@ -1657,7 +1676,25 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
         if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
         if (!emit) keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
         if (emit) {
-            if (j < total) {
+            if (j < total && member_ids != nullptr) {
+                // The representative writes its output row's edges, one
+                // contiguous run; consecutive representatives' runs are
+                // adjacent, so a wave's stores cover whole lines.
+                if (first) {
+                    const int e0 = edge_offsets[j];
+                    const int pos = positions[j];
+                    const int n = sizes[j];
+                    const int32_t* ids = member_ids + static_cast<long long>(j) * max_members;
+                    for (int m = 0; m < n; ++m) {
+                        const int id = ids[m];
+                        const int src = id / K;
+                        out.in_rows[e0 + m] = src;
+                        out.out_rows[e0 + m] = pos;
+                        out.kernel_ids[e0 + m] = id - src * K;
+                    }
+                    out.row_offsets[pos] = e0;
+                }
+            } else if (j < total) {
                 const int e = edge_offsets[rep] + ranks[j];
                 out.in_rows[e] = in;
                 out.out_rows[e] = positions[rep];
@@ -1713,6 +1750,7 @@ size_t expanded_relation_bytes(int rows, int K, bool direct) {
     if (direct) return bytes;
     const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
     const size_t tiles = static_cast<size_t>(std::max(rows, 0)) / kResolveRows + 1;
+    bytes += aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * kMaxRowMembers * sizeof(int32_t));
     bytes += block_table_bytes(std::max(rows, 0)) + 9 * n + 2 * aligned_bytes(tiles * sizeof(int32_t)) +
              aligned_bytes(2 * sizeof(int32_t)) + scan_workspace_bytes(cap);
     bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
@@ -1772,6 +1810,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         int32_t* ranks = ws.take<int32_t>(cap);
         int32_t* edge_offsets = ws.take<int32_t>(cap);
         const int resolve_tiles = (rows + kResolveRows - 1) / kResolveRows;
+        int32_t* member_ids = ws.take<int32_t>(static_cast<size_t>(cap) * kMaxRowMembers);
         int32_t* tile_firsts = ws.take<int32_t>(resolve_tiles);
         int32_t* tile_edges = ws.take<int32_t>(resolve_tiles);
         LATTICE_REQUIRE(reps && flags && positions && keys && sorted_keys && sorted_index && sizes && ranks &&
@@ -1797,11 +1836,16 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
                           g.stride.z / gcd(g.stride.z, g.dilation.z)};
         const Int3 step{g.dilation.x / gcd(g.stride.x, g.dilation.x), g.dilation.y / gcd(g.stride.y, g.dilation.y),
                         g.dilation.z / gcd(g.stride.z, g.dilation.z)};
+        // Candidates of one output row: the offsets of each axis that meet
+        // an offset i step by the period, at most ceil(size / period) of them.
+        const int row_members = ((g.size.x + period.x - 1) / period.x) * ((g.size.y + period.y - 1) / period.y) *
+                                ((g.size.z + period.z - 1) / period.z);
+        const bool listed = tiled && member_ids != nullptr && row_members <= kMaxRowMembers;
         if (tiled) {
             const int tiles = (rows + kResolveRows - 1) / kResolveRows;
             resolve_candidates_tiled<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
                 table, coords, rows, active_rows, g, reach, period, step, out->status, reps, flags, sizes, ranks,
-                tile_firsts, tile_edges);
+                tile_firsts, tile_edges, listed ? member_ids : nullptr, kMaxRowMembers);
         } else {
             resolve_candidates<<<grid, kThreads, 0, stream>>>(table, coords, rows, active_rows, g, reps,
                                                               flags);
@@ -1819,7 +1863,8 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
             if (rc != LATTICE_OK) return rc;
         }
         place_candidates<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
-            coords, rows, active_rows, g, reps, flags, positions, tiled ? edge_offsets : nullptr, ranks, *out, keys);
+            coords, rows, active_rows, g, reps, flags, positions, tiled ? edge_offsets : nullptr, ranks, sizes,
+            listed ? member_ids : nullptr, kMaxRowMembers, *out, keys);
         LATTICE_LAUNCH_CHECK();
         const int32_t* run_if = tiled ? out->status : nullptr;
         SortKeys sk{keys, 1, nullptr, cap, false};
