@@ -1744,16 +1744,24 @@ bool direct_expansion(const KernelGeometry& g) {
            g.stride.z > (g.size.z - 1) * g.dilation.z;
 }
 
+// The deduplicating build's shared region: the candidate lists, or the
+// ranks, keys, sorted keys and index plus the radix sort's workspace.
+size_t expanded_shared_bytes(long long cap) {
+    const size_t c = static_cast<size_t>(std::max<long long>(cap, 1));
+    const size_t n = aligned_bytes(c * sizeof(int32_t));
+    return std::max(aligned_bytes(c * kMaxRowMembers * sizeof(int32_t)),
+                    4 * n + radix_sort_workspace_bytes(static_cast<int>(c), 32));
+}
+
 size_t expanded_relation_bytes(int rows, int K, bool direct) {
     const long long cap = static_cast<long long>(std::max(rows, 0)) * K;
     size_t bytes = group_view_bytes(static_cast<int>(cap)) + 4096;
     if (direct) return bytes;
     const size_t n = aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * sizeof(int32_t));
     const size_t tiles = static_cast<size_t>(std::max(rows, 0)) / kResolveRows + 1;
-    bytes += aligned_bytes(static_cast<size_t>(std::max<long long>(cap, 1)) * kMaxRowMembers * sizeof(int32_t));
-    bytes += block_table_bytes(std::max(rows, 0)) + 9 * n + 2 * aligned_bytes(tiles * sizeof(int32_t)) +
-             aligned_bytes(2 * sizeof(int32_t)) + scan_workspace_bytes(cap);
-    bytes += radix_sort_workspace_bytes(static_cast<int>(cap), 32);
+    bytes += block_table_bytes(std::max(rows, 0)) + 5 * n + expanded_shared_bytes(cap) +
+             2 * aligned_bytes(tiles * sizeof(int32_t)) + aligned_bytes(2 * sizeof(int32_t)) +
+             scan_workspace_bytes(cap);
     return bytes;
 }
 
@@ -1784,8 +1792,11 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
     LATTICE_REQUIRE(workspace_bytes >= expanded_relation_bytes(rows, K, direct), "relation workspace too small.");
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
     const int cap = rows * K;
-    clear_status<<<1, 1, 0, stream>>>(out->status);
-    LATTICE_LAUNCH_CHECK();
+    if (direct || cap == 0) {
+        // (the deduplicating path clears the status word in its table clear)
+        clear_status<<<1, 1, 0, stream>>>(out->status);
+        LATTICE_LAUNCH_CHECK();
+    }
     if (direct) {
         expand_direct<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 16), kThreads, 0, stream>>>(
             coords, rows, active_rows, g, *out);
@@ -1803,14 +1814,21 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         int32_t* reps = ws.take<int32_t>(cap);
         int32_t* flags = ws.take<int32_t>(cap);
         int32_t* positions = ws.take<int32_t>(cap);
-        int32_t* keys = ws.take<int32_t>(cap);
-        int32_t* sorted_keys = ws.take<int32_t>(cap);
-        int32_t* sorted_index = ws.take<int32_t>(cap);
         int32_t* sizes = ws.take<int32_t>(cap);
-        int32_t* ranks = ws.take<int32_t>(cap);
         int32_t* edge_offsets = ws.take<int32_t>(cap);
+        // One region holds either the representatives' candidate lists
+        // (read by place_candidates only while the status word is clear) or
+        // the fallback's ranks, keys and sort buffers (used only when it is
+        // set, or when the lists are not built), so they share it.
+        const size_t region_bytes = expanded_shared_bytes(cap);
+        char* region = ws.take<char>(region_bytes);
+        Workspace shared{region, region ? region_bytes : 0};
+        int32_t* member_ids = reinterpret_cast<int32_t*>(region);
+        int32_t* ranks = shared.take<int32_t>(cap);
+        int32_t* keys = shared.take<int32_t>(cap);
+        int32_t* sorted_keys = shared.take<int32_t>(cap);
+        int32_t* sorted_index = shared.take<int32_t>(cap);
         const int resolve_tiles = (rows + kResolveRows - 1) / kResolveRows;
-        int32_t* member_ids = ws.take<int32_t>(static_cast<size_t>(cap) * kMaxRowMembers);
         int32_t* tile_firsts = ws.take<int32_t>(resolve_tiles);
         int32_t* tile_edges = ws.take<int32_t>(resolve_tiles);
         LATTICE_REQUIRE(reps && flags && positions && keys && sorted_keys && sorted_index && sizes && ranks &&
@@ -1869,7 +1887,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         const int32_t* run_if = tiled ? out->status : nullptr;
         SortKeys sk{keys, 1, nullptr, cap, false};
         sk.run_if = run_if;
-        rc = radix_sort_indices(sk, cap, bit_width(cap), sorted_keys, sorted_index, ws, stream);
+        rc = radix_sort_indices(sk, cap, bit_width(cap), sorted_keys, sorted_index, shared, stream);
         if (rc != LATTICE_OK) return rc;
         emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out,
                                                          run_if);
