@@ -148,6 +148,7 @@ GEOMS = [
     (3, 4, 0, 2),          # dilated, offset period 2 (tiled neighbourhood)
     ((5, 3, 2), (3, 2, 1), (1, 0, 0), 1),  # anisotropic 3x3x3 neighbourhood
     (4, 2, 0, 1),          # even kernel, two preimages per axis
+    ((3, 2, 2), 1, 0, 1),  # 45-cell neighbourhood, 12 candidates per output row (ranked, not listed)
 ]
 
 
