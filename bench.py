@@ -547,8 +547,7 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
 
 def relation_bytes(n: int, edges: int) -> int:
     """Algorithmic HBM bytes of the submanifold relation (hash build + map:
-    query, dense map, masks, edges, row offsets, counts), with the per-unit
-    figures of the hot-path survey:
+    query, dense map, masks, edges, row offsets, counts), per unit:
       hash: 16 B coords read + 12 B per insert + 8 B per table slot cleared
         (capacity next_pow2(2N));
       map: 16 B coords + 12 B per probe (K per row) + 4 B per dense-map
@@ -600,7 +599,7 @@ def main() -> int:
     if args.gpus != 1:
         print(f'bench.py: --gpus {args.gpus} is not supported: this build '
               'measures one MI355X; the path shards by batch index with no '
-              'exchange (see DESIGN.md), so run one process per GPU.',
+              'exchange, so run one process per GPU.',
               file=sys.stderr)
         return 2
     import torch
