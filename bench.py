@@ -165,11 +165,22 @@ def cpu_baseline(coords, feats, weight, threads: int, sample_rows: int,
 
 def _timed(fn, steps: int, warmup: int) -> float:
     """Mean milliseconds of ``fn`` over ``steps`` calls, HIP events on the
-    current stream (the one the bindings launch on)."""
+    current stream (the one the bindings launch on).  The warm-up repeats
+    batches of ``warmup`` calls until 20 ms have passed: after the host
+    work between two lines the GPU's clocks ramp up again over a few
+    milliseconds of load, and the timed calls should see the clocks a busy
+    GPU holds, as the headline's conv launches do."""
+    import time
+
     import torch
 
-    for _ in range(warmup):
-        fn()
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(max(warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= 0.02:
+            break
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
