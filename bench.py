@@ -689,9 +689,10 @@ def main() -> int:
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall
 
-    rel_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    view_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    rel_in_step_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    view_in_step_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
     conv_in_step_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+
     # The GEMM phase on its own: the same conv launched back to back over
     # the last step's resident map and view, so the interval holds the
     # kernels and not the host's launch gaps between the steps' phases.
@@ -704,10 +705,28 @@ def main() -> int:
     c1.record(stream)
     torch.cuda.synchronize()
     conv_ms = c0.elapsed_time(c1) / args.steps
+
+    # The map-build phase on its own, like the GEMM phase above: the build
+    # launched back to back, bracketed by one pair of events (each timing
+    # event inside a step drains the queue before its timestamp, about
+    # 5 us per event), then each of its two parts the same way.
+    def back_to_back(fn):
+        b0 = torch.cuda.Event(enable_timing=True)
+        b1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        b0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        b1.record(stream)
+        torch.cuda.synchronize()
+        return b0.elapsed_time(b1) / args.steps
+
+    map_ms = back_to_back(lambda: sorted_view(map_build()))
+    rel_ms = back_to_back(map_build)
+    view_ms = back_to_back(lambda: sorted_view(native))
     edges = int(native[5][0].item())
     flops = 2.0 * edges * 128 * 128
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
-    map_ms = rel_ms + view_ms
     traffic, conv_sha = conv_traffic()
     del out
 
@@ -736,6 +755,8 @@ def main() -> int:
         },
         'mvoxels_per_s': round(n_out / (conv_ms * 1e-3) / 1e6, 3),
         'kernel_map_build_ms': round(map_ms, 4),
+        'kernel_map_build_in_step_ms': round(rel_in_step_ms + view_in_step_ms,
+                                             4),
         # the whole map build (relation + sorted view), the interval of
         # kernel_map_build_ms, and its two parts
         'kernel_map_hbm': hbm_roofline(
