@@ -1641,11 +1641,12 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
 // Output coordinates of the representatives at their first-seen position,
 // zero tail; keys[t] (t = k * rows + in) = output row of candidate in*K+k,
 // -1 for inactive rows (sorted last).  With edge_offsets (the exclusive scan
-// of the representatives' group sizes) and ranks, and while the status word
-// is clear (no repeated input coordinate), the
-// edges are written in their final (out_row, kernel_id, in_row) order here:
-// candidate j is edge edge_offsets[rep] + ranks[j] and out row positions[j]
-// of a representative starts at edge_offsets[j].
+// of the representatives' group sizes), and while the status word is clear
+// (no repeated input coordinate), the edges are written in their final
+// (out_row, kernel_id, in_row) order here: out row positions[j] of a
+// representative starts at edge_offsets[j]; with member_ids the
+// representative writes its row's edges from its candidate list, otherwise
+// candidate j is edge edge_offsets[rep] + ranks[j].
 __global__ void __launch_bounds__(kThreads)
 place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
                  KernelGeometry g, const int32_t* __restrict__ reps, const int32_t* __restrict__ flags,
