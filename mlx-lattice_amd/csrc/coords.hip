@@ -602,6 +602,9 @@ scan_block_totals(const int32_t* __restrict__ totals, int blocks, int32_t* __res
     const int per = (blocks + kBlockScanThreads - 1) / kBlockScanThreads;
     const int begin = threadIdx.x * per;
     const int end = min(begin + per, blocks);
+    // Up to kScanBatch totals per thread (blocks <= 16384) stay in registers
+    // between the two passes; larger inputs reload them.
+    int first[kScanBatch];
     int sum = 0;
     for (int i0 = begin; i0 < end; i0 += kScanBatch) {
         int v[kScanBatch];
@@ -609,6 +612,10 @@ scan_block_totals(const int32_t* __restrict__ totals, int blocks, int32_t* __res
         for (int j = 0; j < kScanBatch; ++j) v[j] = i0 + j < end ? totals[i0 + j] : 0;
 #pragma unroll
         for (int j = 0; j < kScanBatch; ++j) sum += v[j];
+        if (i0 == begin) {
+#pragma unroll
+            for (int j = 0; j < kScanBatch; ++j) first[j] = v[j];
+        }
     }
     int incl = sum;
 #pragma unroll
@@ -624,7 +631,8 @@ scan_block_totals(const int32_t* __restrict__ totals, int blocks, int32_t* __res
     for (int i0 = begin; i0 < end; i0 += kScanBatch) {
         int v[kScanBatch];
 #pragma unroll
-        for (int j = 0; j < kScanBatch; ++j) v[j] = i0 + j < end ? totals[i0 + j] : 0;
+        for (int j = 0; j < kScanBatch; ++j)
+            v[j] = i0 == begin ? first[j] : (i0 + j < end ? totals[i0 + j] : 0);
 #pragma unroll
         for (int j = 0; j < kScanBatch; ++j) {
             if (i0 + j < end) offsets[i0 + j] = run;
