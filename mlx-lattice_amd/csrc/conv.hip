@@ -485,23 +485,41 @@ template <typename T> struct PackedB {
         }
     }
 
-    // Pieces of output channels co .. co + N - 1 (co a multiple of N) for
-    // input channels ci0 .. ci0 + 7: one N-word load per word row and N-half
-    // loads of the scales and biases.
-    template <int N>
-    __device__ inline void load_n(int k, int co, int ci0, typename MfmaOps<T>::vec (&out)[N]) const {
-        static_assert(N == 2 || N == 4, "two or four output channels per thread");
+    // The raw words, scales and biases of output channels co .. co + N - 1
+    // (co a multiple of N) for input channels ci0 .. ci0 + 7: one N-word
+    // load per word row and N-half loads of the scales and biases.  They are
+    // loaded when a stage starts and dequantised when it stores its B tile,
+    // so no wait for them sits before the stage's gathers and MFMAs.
+    template <int N> struct Raw {
         using W = typename std::conditional<N == 4, uint4, uint2>::type;
         using H = typename std::conditional<N == 4, uint2, uint32_t>::type;
+        W w0, w1;  // w1: the second word row of 8-bit codes
+        H s, b;
+    };
+    template <int N>
+    __device__ inline void load_raw_n(int k, int co, int ci0, Raw<N>& r) const {
+        static_assert(N == 2 || N == 4, "two or four output channels per thread");
+        using W = typename Raw<N>::W;
+        using H = typename Raw<N>::H;
         const long long s = (static_cast<long long>(k) * groups + ci0 / group_size) * c_out + co;
         const long long wbase = static_cast<long long>(k) * packed_words * c_out + co;
-        const H sraw = *reinterpret_cast<const H*>(scales + s);
-        const H braw = *reinterpret_cast<const H*>(biases + s);
-        const T* sv = reinterpret_cast<const T*>(&sraw);
-        const T* bv = reinterpret_cast<const T*>(&braw);
+        r.s = *reinterpret_cast<const H*>(scales + s);
+        r.b = *reinterpret_cast<const H*>(biases + s);
+        // Both word rows are loaded unconditionally (4-bit codes reread the
+        // first and ignore the second): a branch here would leave a load
+        // of one path pending into the other's registers, and the wait for
+        // it would drain every load in flight.
+        const int row0 = bits == 4 ? (ci0 >> 3) : (ci0 >> 2);
+        const int row1 = bits == 4 ? row0 : row0 + 1;
+        r.w0 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(row0) * c_out);
+        r.w1 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(row1) * c_out);
+    }
+    template <int N>
+    __device__ inline void dequant_n(const Raw<N>& r, typename MfmaOps<T>::vec (&out)[N]) const {
+        const T* sv = reinterpret_cast<const T*>(&r.s);
+        const T* bv = reinterpret_cast<const T*>(&r.b);
         if (bits == 4) {
-            const W wv = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(ci0 >> 3) * c_out);
-            const uint32_t* words = reinterpret_cast<const uint32_t*>(&wv);
+            const uint32_t* words = reinterpret_cast<const uint32_t*>(&r.w0);
 #pragma unroll
             for (int c = 0; c < N; ++c) {
                 if constexpr (std::is_same<T, _Float16>::value) {
@@ -509,9 +527,9 @@ template <typename T> struct PackedB {
                     const half2_t bi = {bv[c], bv[c]};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const half2_t r = affine_pair(code_pair((words[c] >> (4 * j)) & 0x000F000Fu), sc, bi);
-                        out[c][j] = r[0];
-                        out[c][j + 4] = r[1];
+                        const half2_t h = affine_pair(code_pair((words[c] >> (4 * j)) & 0x000F000Fu), sc, bi);
+                        out[c][j] = h[0];
+                        out[c][j + 4] = h[1];
                     }
                 } else {
                     const float sc = static_cast<float>(sv[c]);
@@ -523,10 +541,8 @@ template <typename T> struct PackedB {
                 }
             }
         } else {
-            const W w0 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>(ci0 >> 2) * c_out);
-            const W w1 = *reinterpret_cast<const W*>(w + wbase + static_cast<long long>((ci0 >> 2) + 1) * c_out);
-            const uint32_t* lo = reinterpret_cast<const uint32_t*>(&w0);
-            const uint32_t* hi = reinterpret_cast<const uint32_t*>(&w1);
+            const uint32_t* lo = reinterpret_cast<const uint32_t*>(&r.w0);
+            const uint32_t* hi = reinterpret_cast<const uint32_t*>(&r.w1);
 #pragma unroll
             for (int c = 0; c < N; ++c) {
                 if constexpr (std::is_same<T, _Float16>::value) {
@@ -628,10 +644,16 @@ struct MultiB {
 template <typename T, typename S, typename BSource, typename V>
 __device__ inline void stage_b_load(const BSource& bsrc, int k, int ci0, int cw, V (&breg)[S::B_PIECES]) {
     if constexpr (MultiB<S, BSource>::value) {
+        // raw codes, scales and biases, kept in breg's registers until the
+        // stage stores its B tile
         constexpr int N = MultiB<S, BSource>::N;
+        using Raw = typename BSource::template Raw<N>;
+        static_assert(sizeof(Raw) <= sizeof(breg), "the raw words fit the staged pieces");
         const int co = N * (threadIdx.x % (S::C_OUT / N));
         const int piece = threadIdx.x / (S::C_OUT / N);
-        bsrc.template load_n<N>(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0), breg);
+        Raw raw;
+        bsrc.template load_raw_n<N>(k, co, ci0 + (piece * 8 < cw ? piece * 8 : 0), raw);
+        __builtin_memcpy(&breg[0], &raw, sizeof(Raw));
     } else {
 #pragma unroll
         for (int i = 0; i < S::B_PIECES; ++i) {
@@ -643,15 +665,20 @@ __device__ inline void stage_b_load(const BSource& bsrc, int k, int ci0, int cw,
 }
 
 template <typename T, typename S, typename BSource, typename V>
-__device__ inline void stage_b_store(T* dst, const V (&breg)[S::B_PIECES]) {
+__device__ inline void stage_b_store(T* dst, const V (&breg)[S::B_PIECES], const BSource& bsrc) {
     if constexpr (MultiB<S, BSource>::value) {
         constexpr int N = MultiB<S, BSource>::N;
+        using Raw = typename BSource::template Raw<N>;
+        Raw raw;
+        __builtin_memcpy(&raw, &breg[0], sizeof(Raw));
+        V vals[N];
+        bsrc.template dequant_n<N>(raw, vals);
         const int co0 = N * (threadIdx.x % (S::C_OUT / N));
         const int piece = threadIdx.x / (S::C_OUT / N);
 #pragma unroll
         for (int c = 0; c < N; ++c) {
             const int co = co0 + c;
-            *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = breg[c];
+            *reinterpret_cast<V*>(dst + co * S::BROW + swizzle_piece<S::PIECES>(piece, co) * 8) = vals[c];
         }
     } else {
 #pragma unroll
@@ -739,7 +766,7 @@ __device__ inline void igemm_stage(int s, const StageCtx& c, const T* bcur, T* b
             }
         }
     }
-    stage_b_store<T, S, BSource>(bnext, breg);
+    stage_b_store<T, S, BSource>(bnext, breg, bsrc);
     __syncthreads();
 }
 
@@ -843,7 +870,7 @@ __device__ inline void igemm_stage_alds(int s, const StageCtx& c, const T* bcur,
             }
         }
     }
-    stage_b_store<T, S, BSource>(bnext, breg);
+    stage_b_store<T, S, BSource>(bnext, breg, bsrc);
     if (need_a) store_a_coal<T, V, S::RB>(abuf, areg, c.lane);
     __syncthreads();
 }
@@ -946,7 +973,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
                 stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
                 V areg[S::RB][2];
                 load_a_coal<T, V, S::RB>(areg, idx[0], rows_rsrc, c_in, 0, min(S::CHUNK, c_in), lane);
-                stage_b_store<T, S, BSource>(bbuf0, breg);
+                stage_b_store<T, S, BSource>(bbuf0, breg, bsrc);
                 store_a_coal<T, V, S::RB>(abuf, areg, lane);
             }
             __syncthreads();
@@ -975,7 +1002,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         {
             V breg[S::B_PIECES];
             stage_b_load<T, S>(bsrc, stage_k[0], 0, min(S::CHUNK, c_in), breg);
-            stage_b_store<T, S, BSource>(bbuf0, breg);
+            stage_b_store<T, S, BSource>(bbuf0, breg, bsrc);
         }
 #pragma unroll
         for (int j = 0; j < S::DEPTH; ++j) {
