@@ -1660,8 +1660,9 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
                  KernelGeometry g, const int32_t* __restrict__ reps, const int32_t* __restrict__ flags,
                  const int32_t* __restrict__ positions, const int32_t* __restrict__ edge_offsets,
                  const int32_t* __restrict__ ranks, const int32_t* __restrict__ sizes,
-                 const int32_t* __restrict__ member_ids, int max_members, lattice_relation_outputs out,
+                 const int32_t* __restrict__ member_ids, lattice_relation_outputs out,
                  int32_t* __restrict__ keys) {
+    static_assert(kMaxRowMembers == 8, "a candidate list is two 16-byte words");
     const int K = g.volume;
     const int cap = rows * K;
     const int total = min(max(*active_rows, 0), rows) * K;
@@ -1693,13 +1694,20 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
                     const int e0 = edge_offsets[j];
                     const int pos = positions[j];
                     const int n = sizes[j];
-                    const int32_t* ids = member_ids + static_cast<long long>(j) * max_members;
-                    for (int m = 0; m < n; ++m) {
-                        const int id = ids[m];
-                        const int src = id / K;
-                        out.in_rows[e0 + m] = src;
-                        out.out_rows[e0 + m] = pos;
-                        out.kernel_ids[e0 + m] = id - src * K;
+                    // The whole list in two 16-byte loads, so the stores
+                    // below wait for one memory round trip, not one per edge.
+                    const int4* ids = reinterpret_cast<const int4*>(member_ids + static_cast<long long>(j) * kMaxRowMembers);
+                    const int4 lo = ids[0];
+                    const int4 hi = ids[1];
+                    const int id8[kMaxRowMembers] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                    for (int m = 0; m < kMaxRowMembers; ++m) {
+                        if (m < n) {
+                            const int src = id8[m] / K;
+                            out.in_rows[e0 + m] = src;
+                            out.out_rows[e0 + m] = pos;
+                            out.kernel_ids[e0 + m] = id8[m] - src * K;
+                        }
                     }
                     out.row_offsets[pos] = e0;
                 }
@@ -1867,7 +1875,10 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         // an offset i step by the period, at most ceil(size / period) of them.
         const int row_members = ((g.size.x + period.x - 1) / period.x) * ((g.size.y + period.y - 1) / period.y) *
                                 ((g.size.z + period.z - 1) / period.z);
-        const bool listed = tiled && member_ids != nullptr && row_members <= kMaxRowMembers;
+        // (place_candidates reads a list as two 16-byte words: a workspace that
+        // is not 16-byte aligned takes the ranked placement instead)
+        const bool listed = tiled && member_ids != nullptr && row_members <= kMaxRowMembers &&
+                            (reinterpret_cast<uintptr_t>(member_ids) & 15) == 0;
         if (tiled) {
             const int tiles = (rows + kResolveRows - 1) / kResolveRows;
             resolve_candidates_tiled<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
@@ -1891,7 +1902,7 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         }
         place_candidates<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
             coords, rows, active_rows, g, reps, flags, positions, tiled ? edge_offsets : nullptr, ranks, sizes,
-            listed ? member_ids : nullptr, kMaxRowMembers, *out, keys);
+            listed ? member_ids : nullptr, *out, keys);
         LATTICE_LAUNCH_CHECK();
         const int32_t* run_if = tiled ? out->status : nullptr;
         SortKeys sk{keys, 1, nullptr, cap, false};
