@@ -1668,61 +1668,100 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
     const int total = min(max(*active_rows, 0), rows) * K;
     const int n_out = out.counts[1];
     const bool emit = edge_offsets != nullptr && *out.status == 0;
+    const bool listed = emit && member_ids != nullptr;
     int4* oc = reinterpret_cast<int4*>(out.out_coords);
+    // Listed placement: the representatives of one wave own one contiguous
+    // run of edges (their group sizes are scanned in candidate order), so
+    // each representative spreads its list into the wave's LDS run and the
+    // wave then writes the run with whole-line stores.
+    __shared__ int32_t run_ids[kThreads / kWave][kWave * kMaxRowMembers];
+    __shared__ int32_t run_pos[kThreads / kWave][kWave * kMaxRowMembers];
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
     if (emit && blockIdx.x == 0 && threadIdx.x == 0) out.counts[0] = total;
-    for (int j = blockIdx.x * kThreads + threadIdx.x; j <= cap; j += gridDim.x * kThreads) {
+    // every lane of a block runs the same number of iterations (the wave
+    // steps below need all 64 lanes)
+    for (int base = blockIdx.x * kThreads; base <= cap; base += gridDim.x * kThreads) {
+        const int j = base + threadIdx.x;
+        bool rep_here = false;
+        int e0 = 0, n_here = 0, pos_here = 0;
+        int4 lo = make_int4(0, 0, 0, 0), hi = make_int4(0, 0, 0, 0);
         if (j == cap) {
             if (emit) out.row_offsets[cap] = total;
-            continue;
+        } else if (j < cap) {
+            const int in = j / K;
+            const int k = j - in * K;
+            const int rep = reps[j];
+            const bool first = flags[j] != 0;
+            if (first) {
+                int64_t x, y, z;
+                oc[positions[j]] = candidate_of(coords, in, k, g, &x, &y, &z);
+            }
+            if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
+            if (!emit) keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
+            if (emit) {
+                if (j < total && listed) {
+                    if (first) {
+                        // the list in two 16-byte loads: one memory round trip
+                        const int4* ids = reinterpret_cast<const int4*>(
+                            member_ids + static_cast<long long>(j) * kMaxRowMembers);
+                        lo = ids[0];
+                        hi = ids[1];
+                        e0 = edge_offsets[j];
+                        pos_here = positions[j];
+                        n_here = sizes[j];
+                        rep_here = true;
+                        out.row_offsets[pos_here] = e0;
+                    }
+                } else if (j < total) {
+                    const int e = edge_offsets[rep] + ranks[j];
+                    out.in_rows[e] = in;
+                    out.out_rows[e] = positions[rep];
+                    out.kernel_ids[e] = k;
+                    if (first) out.row_offsets[positions[j]] = edge_offsets[j];
+                } else {
+                    out.in_rows[j] = 0;
+                    out.out_rows[j] = 0;
+                    out.kernel_ids[j] = 0;
+                }
+                if (j >= n_out) out.row_offsets[j] = total;
+            }
         }
-        const int in = j / K;
-        const int k = j - in * K;
-        const int rep = reps[j];
-        const bool first = flags[j] != 0;
-        if (first) {
-            int64_t x, y, z;
-            oc[positions[j]] = candidate_of(coords, in, k, g, &x, &y, &z);
-        }
-        if (j >= n_out) oc[j] = make_int4(0, 0, 0, 0);
-        if (!emit) keys[static_cast<long long>(k) * rows + in] = rep >= 0 ? positions[rep] : -1;
-        if (emit) {
-            if (j < total && member_ids != nullptr) {
-                // The representative writes its output row's edges, one
-                // contiguous run; consecutive representatives' runs are
-                // adjacent, so a wave's stores cover whole lines.
-                if (first) {
-                    const int e0 = edge_offsets[j];
-                    const int pos = positions[j];
-                    const int n = sizes[j];
-                    // The whole list in two 16-byte loads, so the stores
-                    // below wait for one memory round trip, not one per edge.
-                    const int4* ids = reinterpret_cast<const int4*>(member_ids + static_cast<long long>(j) * kMaxRowMembers);
-                    const int4 lo = ids[0];
-                    const int4 hi = ids[1];
+        if (listed) {
+            const uint64_t mask = ballot(rep_here);
+            if (mask != 0) {
+                // the wave's run: from its first representative's offset to
+                // its last one's end
+                const int first_lane = __builtin_ctzll(mask);
+                const int last_lane = 63 - __builtin_clzll(mask);
+                const int run0 = __builtin_amdgcn_readlane(e0, first_lane);
+                const int run_n = __builtin_amdgcn_readlane(e0 + n_here, last_lane) - run0;
+                if (rep_here) {
                     const int id8[kMaxRowMembers] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    const int r = e0 - run0;
 #pragma unroll
                     for (int m = 0; m < kMaxRowMembers; ++m) {
-                        if (m < n) {
-                            const int src = id8[m] / K;
-                            out.in_rows[e0 + m] = src;
-                            out.out_rows[e0 + m] = pos;
-                            out.kernel_ids[e0 + m] = id8[m] - src * K;
+                        if (m < n_here) {
+                            run_ids[wave][r + m] = id8[m];
+                            run_pos[wave][r + m] = pos_here;
                         }
                     }
-                    out.row_offsets[pos] = e0;
                 }
-            } else if (j < total) {
-                const int e = edge_offsets[rep] + ranks[j];
-                out.in_rows[e] = in;
-                out.out_rows[e] = positions[rep];
-                out.kernel_ids[e] = k;
-                if (first) out.row_offsets[positions[j]] = edge_offsets[j];
-            } else {
-                out.in_rows[j] = 0;
-                out.out_rows[j] = 0;
-                out.kernel_ids[j] = 0;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                for (int t = lane; t < run_n; t += kWave) {
+                    const int id = run_ids[wave][t];
+                    const int src = id / K;
+                    out.in_rows[run0 + t] = src;
+                    out.out_rows[run0 + t] = run_pos[wave][t];
+                    out.kernel_ids[run0 + t] = id - src * K;
+                }
+                // the next iteration's stores into the run wait for these reads
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
-            if (j >= n_out) out.row_offsets[j] = total;
         }
     }
 }
