@@ -740,14 +740,20 @@ fill_group_tail(const int32_t* __restrict__ tail, int groups, int32_t* __restric
     }
 }
 
+constexpr unsigned kConditionalGrid = 1024;
+
 // Row offsets of sorted group keys (sentinel `groups` for inactive slots);
 // skipped on the device when run_if is non-null and *run_if == 0.
 int launch_group_offsets(const int32_t* sorted_keys, int capacity, int groups, int32_t* offsets,
                          int32_t* tail, hipStream_t stream, const int32_t* run_if = nullptr) {
-    group_offsets<<<grid_for(static_cast<long long>(capacity) + 1, kThreads, 8192), kThreads, 0, stream>>>(
+    // A conditional launch mostly returns at once, and the dispatch of its
+    // workgroups is then its whole cost: it gets four blocks per CU, which
+    // the grid-stride loops cover any size with.
+    const unsigned max_grid = run_if != nullptr ? kConditionalGrid : 8192;
+    group_offsets<<<grid_for(static_cast<long long>(capacity) + 1, kThreads, max_grid), kThreads, 0, stream>>>(
         sorted_keys, capacity, groups, offsets, tail, run_if);
     LATTICE_LAUNCH_CHECK();
-    fill_group_tail<<<grid_for(static_cast<long long>(groups) + 1, kThreads, 8192), kThreads, 0, stream>>>(
+    fill_group_tail<<<grid_for(static_cast<long long>(groups) + 1, kThreads, max_grid), kThreads, 0, stream>>>(
         tail, groups, offsets, run_if);
     LATTICE_LAUNCH_CHECK();
     return LATTICE_OK;
@@ -1948,8 +1954,8 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
         sk.run_if = run_if;
         rc = radix_sort_indices(sk, cap, bit_width(cap), sorted_keys, sorted_index, shared, stream);
         if (rc != LATTICE_OK) return rc;
-        emit_sorted_edges<<<grid, kThreads, 0, stream>>>(sorted_keys, sorted_index, rows, K, active_rows, *out,
-                                                         run_if);
+        emit_sorted_edges<<<run_if != nullptr ? std::min(grid, kConditionalGrid) : grid, kThreads, 0, stream>>>(
+            sorted_keys, sorted_index, rows, K, active_rows, *out, run_if);
         LATTICE_LAUNCH_CHECK();
         int32_t* tail = ws.take<int32_t>(2);
         LATTICE_REQUIRE(tail, "relation workspace too small.");
