@@ -1556,12 +1556,63 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
     const int active = min(max(*active_rows, 0), rows);
     const int dx_n = 2 * reach.x + 1, dy_n = 2 * reach.y + 1, dz_n = 2 * reach.z + 1;
     const int cells = dx_n * dy_n * dz_n;
+    const bool windowed = reach.x == 1 && reach.y == 1 && reach.z == 1;
     const int yz = g.size.y * g.size.z;
     const int tiles = (rows + kResolveRows - 1) / kResolveRows;
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int r0 = tile * kResolveRows;
         const int tile_rows = min(kResolveRows, rows - r0);
-        for (int i = threadIdx.x; i < tile_rows * cells; i += kThreads) {
+        if (windowed) {
+            // Unit reach (3x3x3 cells): the cells of a row lie in the 2x2x2
+            // blocks floor((v - 1) / 2) .. +1 per axis, so one lane per
+            // (row, block) reads that block's bucket once and places its
+            // octants' rows: octant o of block j is window index 2j + o,
+            // cell 2j + o - 1 + (v & 1) per axis when that lies in 0..2.
+            for (int i = threadIdx.x; i < tile_rows * 8; i += kThreads) {
+                const int lr = i >> 3;
+                const int jb = i & 7;
+                const int row = r0 + lr;
+                if (row >= active) continue;
+                const int4 c = load_coord(coords, row);
+                const int jx = jb >> 2, jy = (jb >> 1) & 1, jz = jb & 1;
+                const TableKey key = table_key(c.x, ((static_cast<int64_t>(c.y) - 1) >> 1) + jx,
+                                               ((static_cast<int64_t>(c.z) - 1) >> 1) + jy,
+                                               ((static_cast<int64_t>(c.w) - 1) >> 1) + jz);
+                // key and rows of a slot are read together
+                uint32_t slot = static_cast<uint32_t>(key.hash) & table.mask;
+                int32_t raw[8];
+                while (true) {
+                    const unsigned long long k = table.buckets[slot].key;
+#pragma unroll
+                    for (int o = 0; o < 8; ++o) raw[o] = table.buckets[slot].rows[o];
+                    if (table.holds(k, key)) break;
+                    if (k == kEmptyKey) {
+#pragma unroll
+                        for (int o = 0; o < 8; ++o) raw[o] = 0;
+                        break;
+                    }
+                    slot = (slot + 1) & table.mask;
+                }
+                const int sx = (c.y & 1) - 1, sy = (c.z & 1) - 1, sz = (c.w & 1) - 1;
+                int32_t* f = found + lr * cells;
+#pragma unroll
+                for (int o = 0; o < 8; ++o) {
+                    const int cx = 2 * jx + (o >> 2) + sx;
+                    const int cy = 2 * jy + ((o >> 1) & 1) + sy;
+                    const int cz = 2 * jz + (o & 1) + sz;
+                    if (cx >= 0 && cx <= 2 && cy >= 0 && cy <= 2 && cz >= 0 && cz <= 2) {
+                        const int r = bucket_row(raw[o]);
+                        f[(cx * 3 + cy) * 3 + cz] = r;
+                        // A later row with the coordinate of an earlier one
+                        // gives a second edge for some (out_row, kernel_id).
+                        if (cx == 1 && cy == 1 && cz == 1 && r >= 0 && r != row) {
+                            atomicOr(status, LATTICE_STATUS_REPEATED_EDGE);
+                        }
+                    }
+                }
+            }
+        }
+        for (int i = threadIdx.x; !windowed && i < tile_rows * cells; i += kThreads) {
             const int row = r0 + i / cells;
             const int d = i - (i / cells) * cells;
             int r = -1;

@@ -171,6 +171,31 @@ def test_transposed_relation_matches_oracle(ks, stride, pad, dil, dup):
     np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
 
 
+@pytest.mark.parametrize('ks,stride,pad,dil', [(3, 2, 0, 1), (4, 2, 0, 1),
+                                               (2, 1, 0, 1)])
+def test_transposed_relation_wide_coordinates_match_oracle(ks, stride, pad,
+                                                           dil):
+    """A dense cloud moved to coordinates beyond the packed key range
+    (|v| around 2^29, odd and even): the unit-reach resolve looks its blocks
+    up by full keys."""
+    rng = np.random.default_rng(250)
+    coords = _cloud(rng, 2000, 7, True)
+    coords[:, 1:] += np.array([(1 << 29) + 1, -(1 << 29), 3 << 20],
+                              dtype=np.int32)
+    active = len(coords) - 40
+    print(f'transposed wide k{ks} s{stride}', flush=True)
+    native = _ext().build_transposed_kernel_relation(
+        _t(coords), _active(active), _triple(ks), _triple(stride),
+        _triple(pad), _triple(dil))
+    torch.cuda.synchronize()
+    got = native_relation_dict(native)
+    ref = O.transposed_kernel_relation(coords, active, kernel_size=ks,
+                                       stride=stride, padding=pad,
+                                       dilation=dil)
+    assert_relation_equal(got, ref)
+    np.testing.assert_array_equal(got['out_coords'], ref['out_coords'])
+
+
 @pytest.mark.parametrize('ks,stride,pad,dil', GEOMS)
 @pytest.mark.parametrize('dup', [False, True])
 def test_transposed_relation_dense_cloud_matches_oracle(ks, stride, pad, dil,
