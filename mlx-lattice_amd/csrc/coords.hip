@@ -1543,7 +1543,11 @@ finalize_tiles(const int32_t* __restrict__ flags, const int32_t* __restrict__ si
 // extent / stride)), into LDS, one lane per (row, d), so a wave's lanes probe
 // neighbouring lines; then each (row, k) lane takes the minimum over its
 // preimages from LDS.  Used when the neighbourhood has at most
-// kResolveCells cells.
+// kResolveCells cells.  kK3S2 is the instance for kernel 3, stride 2,
+// dilation 1 on every axis (the decoder's upsampling): its sizes, period,
+// step and reach are compile-time constants, so the member walks unroll and
+// the divisions by K and the period become shifts and multiplies.
+template <bool kK3S2>
 __global__ void __launch_bounds__(kThreads)
 resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, int rows,
                          const int32_t* __restrict__ active_rows, KernelGeometry g, Int3 reach, Int3 period,
@@ -1551,6 +1555,14 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
                          int32_t* __restrict__ reps, int32_t* __restrict__ flags, int32_t* __restrict__ sizes,
                          int32_t* __restrict__ ranks, int32_t* __restrict__ tile_firsts,
                          int32_t* __restrict__ tile_edges, int32_t* __restrict__ member_ids, int max_members) {
+    if constexpr (kK3S2) {
+        g.size = Int3{3, 3, 3};
+        g.volume = 27;
+        reach = Int3{1, 1, 1};
+        period = Int3{2, 2, 2};
+        step = Int3{1, 1, 1};
+        max_members = kMaxRowMembers;
+    }
     __shared__ int32_t found[kResolveRows * kResolveCells];
     const int K = g.volume;
     const int active = min(max(*active_rows, 0), rows);
@@ -1977,7 +1989,11 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
                             (reinterpret_cast<uintptr_t>(member_ids) & 15) == 0;
         if (tiled) {
             const int tiles = (rows + kResolveRows - 1) / kResolveRows;
-            resolve_candidates_tiled<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
+            const bool k3s2 = g.size.x == 3 && g.size.y == 3 && g.size.z == 3 && g.stride.x == 2 &&
+                              g.stride.y == 2 && g.stride.z == 2 && g.dilation.x == 1 && g.dilation.y == 1 &&
+                              g.dilation.z == 1;
+            const auto kernel = k3s2 ? resolve_candidates_tiled<true> : resolve_candidates_tiled<false>;
+            kernel<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
                 table, coords, rows, active_rows, g, reach, period, step, out->status, reps, flags, sizes, ranks,
                 tile_firsts, tile_edges, listed ? member_ids : nullptr, kMaxRowMembers);
         } else {
