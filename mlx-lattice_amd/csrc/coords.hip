@@ -1724,6 +1724,7 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
 // representative starts at edge_offsets[j]; with member_ids the
 // representative writes its row's edges from its candidate list, otherwise
 // candidate j is edge edge_offsets[rep] + ranks[j].
+template <bool kK3S2>
 __global__ void __launch_bounds__(kThreads)
 place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __restrict__ active_rows,
                  KernelGeometry g, const int32_t* __restrict__ reps, const int32_t* __restrict__ flags,
@@ -1732,6 +1733,12 @@ place_candidates(const int32_t* __restrict__ coords, int rows, const int32_t* __
                  const int32_t* __restrict__ member_ids, lattice_relation_outputs out,
                  int32_t* __restrict__ keys) {
     static_assert(kMaxRowMembers == 8, "a candidate list is two 16-byte words");
+    if constexpr (kK3S2) {  // kernel 3, stride 2, dilation 1: constant divisors
+        g.size = Int3{3, 3, 3};
+        g.stride = Int3{2, 2, 2};
+        g.dilation = Int3{1, 1, 1};
+        g.volume = 27;
+    }
     const int K = g.volume;
     const int cap = rows * K;
     const int total = min(max(*active_rows, 0), rows) * K;
@@ -1985,13 +1992,12 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
                                 ((g.size.z + period.z - 1) / period.z);
         // (place_candidates reads a list as two 16-byte words: a workspace that
         // is not 16-byte aligned takes the ranked placement instead)
+        const bool k3s2 = g.size.x == 3 && g.size.y == 3 && g.size.z == 3 && g.stride.x == 2 && g.stride.y == 2 &&
+                          g.stride.z == 2 && g.dilation.x == 1 && g.dilation.y == 1 && g.dilation.z == 1;
         const bool listed = tiled && member_ids != nullptr && row_members <= kMaxRowMembers &&
                             (reinterpret_cast<uintptr_t>(member_ids) & 15) == 0;
         if (tiled) {
             const int tiles = (rows + kResolveRows - 1) / kResolveRows;
-            const bool k3s2 = g.size.x == 3 && g.size.y == 3 && g.size.z == 3 && g.stride.x == 2 &&
-                              g.stride.y == 2 && g.stride.z == 2 && g.dilation.x == 1 && g.dilation.y == 1 &&
-                              g.dilation.z == 1;
             const auto kernel = k3s2 ? resolve_candidates_tiled<true> : resolve_candidates_tiled<false>;
             kernel<<<static_cast<unsigned>(std::min(tiles, 1 << 16)), kThreads, 0, stream>>>(
                 table, coords, rows, active_rows, g, reach, period, step, out->status, reps, flags, sizes, ranks,
@@ -2012,7 +2018,8 @@ int build_expanded_relation(const int32_t* coords, int rows, const int32_t* acti
             rc = exclusive_scan(flags, positions, cap, out->counts + 1, ws, stream);
             if (rc != LATTICE_OK) return rc;
         }
-        place_candidates<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
+        const auto place = k3s2 ? place_candidates<true> : place_candidates<false>;
+        place<<<grid_for(static_cast<long long>(cap) + 1, kThreads, 1u << 14), kThreads, 0, stream>>>(
             coords, rows, active_rows, g, reps, flags, positions, tiled ? edge_offsets : nullptr, ranks, sizes,
             listed ? member_ids : nullptr, *out, keys);
         LATTICE_LAUNCH_CHECK();
