@@ -660,12 +660,18 @@ def main() -> int:
         view = ext.build_sorted_implicit_gemm_view(native[10], native[11])
         return view + (ext.conv_tile_order(view[3], n_out),)
 
+    # The weight in the streamed kernel's fragment order, made once per
+    # weight as the operator path caches it (ops/_relation_exec.py
+    # _weight_fragments), like the tile order per view.
+    fragments = ext.conv_weight_fragments(weight)
+
     def conv(native, view):
         reorder, smap, kv, tiles, order = view
         return ext.sparse_conv_features_sorted_implicit_gemm(
             feats, weight, smap, kv, reorder, tiles, native[0], native[1],
             native[2], native[5], native[3], native[6], native[7], native[8],
-            native[9], n_out, 27, tile_order=order)
+            native[9], n_out, 27, tile_order=order,
+            weight_fragments=fragments)
 
     for _ in range(args.warmup):
         native = map_build()
@@ -778,7 +784,7 @@ def main() -> int:
                                'profiles/config3_kernel_traffic.md'
                                if traffic is not None else
                                f'not measured for conv.hip {conv_sha}'),
-            'kernel': 'conv_igemm<f16, IgemmShape<128 cols, 32-row waves, 4 waves, 64-channel stages, A via LDS>, FloatB>',
+            'kernel': 'conv_igemm_stream<f16, StreamShape<128, 1>, 2>',
         },
     }
     if args.phase == 'config3':

@@ -372,6 +372,29 @@ int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
     int epilogue, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Streamed matrix-core route of the entry above (no counterpart in the
+ * reference, which has one conv entry per layout; this one takes the weight
+ * already in the kernel's fragment order).  fp16/bf16 features, c_in a
+ * multiple of 32 up to 256, c_out in {64, 128, 256}, kernel_count <= 32 and
+ * (n_in + 1) * c_in * 2 <= 2^32 bytes of features.  Same sum, output rows,
+ * bias, epilogue, workspace and tile order as the entry above; the result is
+ * bit-identical to it.  weight_fragments holds
+ * lattice_hip_conv_weight_fragments_bytes(...) bytes written by
+ * lattice_hip_conv_weight_fragments from the (C_out, Kx, Ky, Kz, C_in)
+ * weight; a caller keeps them as long as the weight is unchanged. */
+size_t lattice_hip_conv_weight_fragments_bytes(int dtype, int kernel_count,
+                                               int c_in, int c_out);
+int lattice_hip_conv_weight_fragments(int dtype, const void* weights,
+                                      int kernel_count, int c_in, int c_out,
+                                      void* fragments, size_t fragments_bytes,
+                                      void* stream);
+int lattice_hip_sparse_conv_features_sorted_fragments(
+    int dtype, const void* feats, int n_in, int c_in,
+    const void* weight_fragments, int kernel_count, int c_out,
+    const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
+    int epilogue, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free variant of the entry above: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops or harnesses that forbid hipMalloc): the

@@ -1065,6 +1065,412 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
     }
 }
 
+// --------------------------------------------- streamed implicit GEMM ----
+//
+// The matrix-core conv for fp16/bf16 features and weights with C_out in
+// {64, 128, 256} and C_in <= 256 (a multiple of 32).  A block owns a tile
+// of 128 mask-sorted rows and 128 (or 64) output channels; its 4 waves
+// split the tile by columns (C_out = 128: every wave owns all 128 rows and
+// 32 columns; C_out = 64: 64 rows x 32 columns).  A stage is one
+// (offset k, 64-channel chunk) pair that some row of the tile uses.
+//
+//  * A (the gathered input rows) goes global -> LDS with no register
+//    staging: `buffer_load_dwordx4 ... lds` copies whole 128-byte row lines
+//    (8 rows x 64 channels per instruction, 32 rows per wave) two stages
+//    ahead into a ring of three 16 KB buffers.  Lane l of a copy writes slot
+//    l % 8 of its row; the slot holds piece slot ^ (row % 8), so the 16-row
+//    MFMA fragment reads hit distinct banks.  A missing row (map entry -1)
+//    wraps past the buffer's range and reads as zeros.
+//  * B never passes through LDS: each wave loads its own fragments (its 32
+//    columns x 64 channels, four 1 KB runs) from a fragment-ordered copy of
+//    the weight (lattice_hip_conv_weight_fragments), two stages ahead.
+//  * LDS therefore carries only A: per 16x16x32 MFMA, the 1 KB A fragment
+//    is read once for two column blocks (512 B) plus a 128 B share of the
+//    copy, 640 B in all, against 896 B when four waves each read a shared
+//    B tile (the register-staged kernel above).
+//  * v_mfma_f32_16x16x32 runs the transposed product (B fragment as the
+//    first operand), so each lane accumulates 4 consecutive output channels
+//    of one row and the results leave as 8-byte stores straight from
+//    registers to out[reorder_rows[row]].  16-row blocks whose rows do not
+//    use k skip their MFMAs.
+//
+// The main loop's memory instructions are inline assembly issued in a
+// fixed order per stage (row indices of stage s + 3, B(s + 2), the copy of
+// A(s + 2)), spread over the stage's 16-row blocks, and the loop waits on
+// the vector-memory counter itself: loads complete in issue order, so "at
+// most N younger loads outstanding" names exactly the group a stage needs.
+// The registers such a load writes are tied to the wait that covers them
+// (an asm operand), so the compiler places no read of them earlier; no
+// value written by these loads is copied or spilled before its wait (checked
+// in the generated code: the loads only ever feed the tied waits).
+// The stages of one offset form a trip of NCH = ceil(C_in / 64) stages; the
+// offsets are popped from the tile's mask once per trip into a small ring of
+// scalars, so every stage's offset, chunk and lead resolve at compile time
+// in the unrolled loop.
+
+typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource of `bytes` bytes at `base` (raw, no stride): loads past
+// the range return zeros.
+__device__ inline u32x4v_t raw_rsrc(const void* base, unsigned bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    return u32x4v_t{static_cast<unsigned>(a), static_cast<unsigned>(a >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+__device__ inline int asm_load_i32(u32x4v_t r, unsigned voff) {
+    int v;
+    asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+    return v;
+}
+
+template <typename V>
+__device__ inline V asm_load_b128(u32x4v_t r, unsigned voff) {
+    V v;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+    return v;
+}
+
+// 16 bytes per lane from byte offset voff into LDS at lds_base + 16 * lane.
+__device__ inline void asm_copy_b128(u32x4v_t r, unsigned voff, unsigned lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
+// Wait until at most N vector-memory loads are outstanding; the registers
+// passed are those the awaited loads write.
+template <int N, int G>
+__device__ inline void wait_vm_idx(int (&d)[G]) {
+    static_assert(G == 4, "four row indices");
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]) : "n"(N));
+}
+
+template <int N, typename V, int CB, int ST>
+__device__ inline void wait_vm_b(V (&b)[CB][ST]) {
+    static_assert(CB * ST == 4, "four B fragments");
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[1][0]), "+v"(b[1][1]) : "n"(N));
+}
+
+// f(integral_constant<J>) for J = B .. E - 1.
+template <int B, int E, typename F>
+__device__ inline void static_for(F& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+// The same for J in [lo, hi) (lo and hi fold to constants once the
+// caller's loop is unrolled).
+template <int B = 0, int MAXN = 64, typename F>
+__device__ inline void static_for_range(F& f, int lo, int hi) {
+    if constexpr (B < MAXN) {
+        if (B >= lo && B < hi) f(std::integral_constant<int, B>{});
+        static_for_range<B + 1, MAXN>(f, lo, hi);
+    }
+}
+
+constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+constexpr int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
+
+// Tile of the streamed kernel: C_OUT output channels per block (a column
+// half when C_out = 256), its 4 waves in WR row groups x 4 / WR column
+// groups of 32 columns.
+template <int C_OUT_, int WR_>
+struct StreamShape {
+    static constexpr int C_OUT = C_OUT_;
+    static constexpr int WAVES = 4;
+    static constexpr int THREADS = WAVES * 64;
+    static constexpr int WR = WR_;
+    static constexpr int WC = WAVES / WR_;
+    static constexpr int ROWS = 128;          // tile rows (the tile order's 128-row tiles)
+    static constexpr int WROWS = ROWS / WR;   // rows per wave
+    static constexpr int WCOLS = C_OUT / WC;  // columns per wave
+    static constexpr int RB = WROWS / 16;     // 16-row MFMA blocks per wave
+    static constexpr int CB = WCOLS / 16;     // 16-column MFMA blocks per wave
+    static constexpr int CHUNK = 64;          // input channels per stage
+    static constexpr int ST = CHUNK / 32;     // 32-channel MFMA steps per stage
+    static constexpr int GATHER = ROWS * (CHUNK / 8) / THREADS;  // row-line copies per thread and stage
+    static constexpr int ABUF = ROWS * CHUNK;  // halves of one A buffer
+    static constexpr int OCC = 3;              // blocks per CU (3 x 48 KB of LDS)
+    static constexpr int LB = 2;               // B loads lead by LB stages
+    static constexpr int LI = 3;               // row-index loads lead by LI stages
+    static constexpr int READ_AHEAD = 2;       // 16-row fragment reads in flight
+    static_assert(WCOLS == 32 && WROWS % 16 == 0 && GATHER == 4, "stream tile shape");
+};
+
+// Fragment (k, ks, cg, cb) of a weight: the 16 x 32 block of output
+// channels cg*32 + cb*16 .. + 15 and input channels ks*32 .. + 31 of offset
+// k, as 64 lanes x 8 values: lane (lr, lg) holds W[co = cg*32 + cb*16 + lr]
+// [k][ci = ks*32 + lg*8 .. + 7].  Fragments are stored in (k, ks, cg, cb)
+// order, 1 KB each.
+__host__ __device__ inline long long fragment_piece(int k, int ks, int cg, int cb, int lane, int ksteps, int ncg) {
+    return ((((static_cast<long long>(k) * ksteps + ks) * ncg + cg) * 2 + cb) * 64 + lane);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+weight_fragments(const T* __restrict__ w, int K, int c_in, int c_out, T* __restrict__ frag) {
+    const int ksteps = c_in / 32;
+    const int ncg = c_out / 32;
+    const long long pieces = static_cast<long long>(K) * c_in * c_out / 8;
+    for (long long p = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; p < pieces;
+         p += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int lane = static_cast<int>(p % 64);
+        long long f = p / 64;
+        const int cb = static_cast<int>(f % 2);
+        f /= 2;
+        const int cg = static_cast<int>(f % ncg);
+        f /= ncg;
+        const int ks = static_cast<int>(f % ksteps);
+        const int k = static_cast<int>(f / ksteps);
+        const int co = cg * 32 + cb * 16 + (lane & 15);
+        const int ci = ks * 32 + (lane >> 4) * 8;
+        *reinterpret_cast<uint4*>(frag + p * 8) =
+            *reinterpret_cast<const uint4*>(w + (static_cast<long long>(co) * K + k) * c_in + ci);
+    }
+}
+
+template <typename T, typename S, int NCH>
+__global__ void __launch_bounds__(S::THREADS, S::OCC)
+conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ wfrag, int kernel_count,
+                  int c_out_total, const int32_t* __restrict__ kv_map, const int32_t* __restrict__ tile_masks,
+                  const int32_t* __restrict__ reorder_rows, int rows, const int32_t* __restrict__ block_order,
+                  T* __restrict__ out, Epilogue<T> epi, int halves) {
+    using V = typename MfmaOps<T>::vec;
+    constexpr int RB = S::RB;
+    constexpr int CB = S::CB;
+    constexpr int ST = S::ST;
+    constexpr int G = S::GATHER;
+    constexpr int NB = CB * ST;  // B loads per stage
+    constexpr int NI = G;        // row-index loads per stage
+    constexpr int ND = G;        // LDS copies per stage
+    constexpr int NT = NI + NB + ND;
+    constexpr int ABYTES = S::ABUF * static_cast<int>(sizeof(T));
+    __shared__ __align__(16) T lds[3 * S::ABUF];
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int wr = wave / S::WC;
+    const int wc = wave % S::WC;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int col0 = wc * S::WCOLS;
+    // Longest-first tile order; with C_out = 256 consecutive blocks take the
+    // two column halves of one tile (the second finds its rows in L2).
+    const int slot = halves > 1 ? static_cast<int>(blockIdx.x) / 2 : static_cast<int>(blockIdx.x);
+    const int half = halves > 1 ? static_cast<int>(blockIdx.x & 1u) : 0;
+    const int cg = half * (S::C_OUT / S::WCOLS) + wc;  // 32-column group of the weight
+    const int out_ld = S::C_OUT * halves;
+    const int tile = block_order != nullptr ? block_order[slot] : slot;
+    const int row0 = tile * S::ROWS;
+    const int quarters = ((rows + 63) / 64) * 4;
+    // Offset masks of the wave's 16-row blocks and of the whole tile.
+    uint32_t qm[RB];
+    uint32_t bmask = 0;
+#pragma unroll
+    for (int q = 0; q < S::ROWS / 16; ++q) {
+        const int qi = row0 / 16 + q;
+        const uint32_t m = qi < quarters ? static_cast<uint32_t>(tile_masks[qi]) : 0u;
+        bmask |= m;
+        if (q / RB == wr) qm[q % RB] = m;
+    }
+    const int ntrips = __popc(bmask);
+
+    float4_t acc[RB][CB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (ntrips > 0) {
+        const int grow = wave * (8 * G) + (lane >> 3);  // first tile row this lane copies
+        const int gp = (lane & 7) ^ ((lane >> 3) & 7);  // piece it copies (its slot ^ row % 8)
+        const int ksteps = c_in / 32;
+        const int ncg = c_out_total / S::WCOLS;
+        const bool partial = (c_in % S::CHUNK) != 0;  // the last chunk holds 32 channels
+        const u32x4v_t frs = raw_rsrc(feats, static_cast<unsigned>(static_cast<long long>(n_in) * c_in * sizeof(T)));
+        const u32x4v_t krs =
+            raw_rsrc(kv_map, static_cast<unsigned>(static_cast<long long>(kernel_count) * rows * sizeof(int32_t)));
+        const u32x4v_t wrs = raw_rsrc(
+            wfrag, static_cast<unsigned>(static_cast<long long>(kernel_count) * c_in * c_out_total * sizeof(T)));
+        const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<unsigned long long>(lds));
+
+        constexpr int LA = 2, LB = S::LB, LI = S::LI;
+        constexpr int NIS = LI - LA + 1;  // row-index register sets
+        constexpr int NBS = LB + 1;       // B register sets
+        // stages per unrolled block: whole trips that cycle every register set
+        constexpr int U = lcm_int(lcm_int(NIS, NBS), NCH);
+        constexpr int TPU = U / NCH;                 // trips per unrolled block
+        constexpr int R = TPU + (U - 1 + LI) / NCH;  // ring entries a block reaches
+        // Offset ring: kr[i] is the offset of trip t + i (t = the block's
+        // first trip); past the last trip it repeats the last offset, whose
+        // prefetched operands are never used.
+        uint32_t rem = bmask;
+        int klast = 0;
+        auto pop = [&]() {
+            if (rem) {
+                klast = __builtin_ctz(rem);
+                rem &= rem - 1;
+            }
+            return klast;
+        };
+        int kr[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) kr[i] = pop();
+
+        auto idx_load = [&](int (&d)[G], int k, int i) {
+            const int r = min(row0 + grow + 8 * i, rows - 1);
+            d[i] = asm_load_i32(krs, static_cast<unsigned>((k * rows + r) * 4));
+        };
+        auto b_load = [&](V (&b)[CB][ST], int k, int ch, int cb, int st) {
+            b[cb][st] = asm_load_b128<V>(
+                wrs, static_cast<unsigned>(fragment_piece(k, ch * ST + st, cg, cb, lane, ksteps, ncg) * 16));
+        };
+        auto a_copy = [&](const int (&d)[G], int ch, int buf, int i) {
+            const int ci = ch * S::CHUNK;
+            // a partial last chunk copies its four pieces twice
+            const int off = (partial && ch == NCH - 1 && gp >= 4) ? (gp - 4) * 8 : gp * 8;
+            const unsigned dst = lds0 + buf * ABYTES + (wave * (8 * G) + 8 * i) * S::CHUNK * sizeof(T);
+            const unsigned row = static_cast<unsigned>(d[i]) * static_cast<unsigned>(c_in * sizeof(T));
+            asm_copy_b128(frs, row + (ci + off) * sizeof(T), __builtin_amdgcn_readfirstlane(dst));
+        };
+
+        constexpr int W_IDX = NB + ND + (LI - LA - 1) * NT;  // row indices of s + LA, at stage s
+        constexpr int W_B = ND + (LB - 1) * NT;              // B(s), before stage s issues
+        constexpr int W_A = (LA - 1) * NT;                   // A(s + 1), at the end of stage s
+        static_assert(W_IDX < 64 && W_B < 64, "waits fit the counter");
+        int idx[NIS][G];
+        V b[NBS][CB][ST];
+        // Prologue: indices of stages 0 .. LI - 1, A(0) .. A(LA - 1), B(0) ..
+        // B(LB - 1), all complete before stage 0.
+#pragma unroll
+        for (int u = 0; u < LI; ++u) {
+#pragma unroll
+            for (int i = 0; i < G; ++i) idx_load(idx[u % NIS], kr[u / NCH], i);
+            if (u < LA) {
+                wait_vm_idx<0>(idx[u % NIS]);
+#pragma unroll
+                for (int i = 0; i < G; ++i) a_copy(idx[u % NIS], u % NCH, u, i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < LB; ++u)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int st = 0; st < ST; ++st) b_load(b[u % NBS], kr[u / NCH], u % NCH, cb, st);
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+        int buf = 0;  // LDS buffer of A(s)
+        // The stage at position P of the unrolled block.
+        auto step = [&](auto P) {
+            constexpr int p = decltype(P)::value;
+            constexpr int ch = p % NCH;
+            int (&ia)[G] = idx[(p + LA) % NIS];
+            int (&ifill)[G] = idx[(p + LI) % NIS];
+            V (&bcur)[CB][ST] = b[p % NBS];
+            V (&bfill)[CB][ST] = b[(p + LB) % NBS];
+            const int k = kr[p / NCH];
+            const int k_i = kr[(p + LI) / NCH];
+            const int k_b = kr[(p + LB) / NCH];
+            const int abuf_fill = buf == 0 ? 2 : buf - 1;  // (s + 2) % 3
+            wait_vm_idx<W_IDX>(ia);
+            wait_vm_b<W_B>(bcur);
+            // Memory op q of this stage, in the fixed order.
+            auto issue_op = [&](auto Q) {
+                constexpr int q = decltype(Q)::value;
+                if constexpr (q < NI) {
+                    idx_load(ifill, k_i, q);
+                } else if constexpr (q < NI + NB) {
+                    b_load(bfill, k_b, (p + LB) % NCH, (q - NI) / ST, (q - NI) % ST);
+                } else {
+                    a_copy(ia, (p + LA) % NCH, abuf_fill, q - NI - NB);
+                }
+            };
+            const int nst = (partial && ch == NCH - 1) ? 1 : ST;
+            const T* arow = lds + buf * S::ABUF + (wr * S::WROWS + lr) * S::CHUNK;
+            auto read_a = [&](V (&a)[ST], int rb) {
+#pragma unroll
+                for (int st = 0; st < ST; ++st) {
+                    a[st] = *reinterpret_cast<const V*>(arow + rb * 16 * S::CHUNK + (((st * 4 + lg) ^ (lr & 7)) * 8));
+                }
+            };
+            constexpr int RA = S::READ_AHEAD;
+            V af[RA + 1][ST];
+#pragma unroll
+            for (int r = 0; r < RA && r < RB; ++r) read_a(af[r], r);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                if (rb + RA < RB) read_a(af[(rb + RA) % (RA + 1)], rb + RA);
+                // this 16-row block's share of the stage's memory ops
+                static_for_range(issue_op, rb * NT / RB, (rb + 1) * NT / RB);
+                if ((qm[rb] >> k) & 1u) {
+#pragma unroll
+                    for (int st = 0; st < ST; ++st) {
+                        if (st < nst) {
+#pragma unroll
+                            for (int cb = 0; cb < CB; ++cb) {
+                                // transposed product: lane (lr, lg) accumulates
+                                // row rb*16 + lr, columns cb*16 + lg*4 .. + 3
+                                acc[rb][cb] = MfmaOps<T>::mfma(bcur[cb][st], af[rb % (RA + 1)][st], acc[rb][cb]);
+                            }
+                        }
+                    }
+                }
+            }
+            // A(s + 1) has landed for this wave; the barrier makes it so for
+            // every wave and frees buffer `buf` for the copy of A(s + 3).
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(W_A) : "memory");
+            buf = buf == 2 ? 0 : buf + 1;
+        };
+        auto block = [&](int t0) {
+            auto guarded = [&](auto P) {
+                constexpr int p = decltype(P)::value;
+                if (t0 + p / NCH < ntrips) step(P);
+            };
+            static_for<0, U>(guarded);
+#pragma unroll
+            for (int i = 0; i < R; ++i) kr[i] = i + TPU < R ? kr[i + TPU] : pop();
+        };
+        for (int t = 0; t < ntrips; t += TPU) block(t);
+        // No copy may land in this block's LDS after it ends.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+
+    // Each lane holds 4 consecutive output channels of one row per (rb,
+    // cb): 8-byte stores straight from registers to out[reorder_rows[row]].
+    // Rows with no edges store zeros (plus bias).
+    T* const obase = out + half * S::C_OUT + col0 + lg * 4;
+    uint2 bias4[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+        bias4[cb] = epi.bias != nullptr
+                        ? *reinterpret_cast<const uint2*>(epi.bias + half * S::C_OUT + col0 + cb * 16 + lg * 4)
+                        : uint2{0u, 0u};
+    int orow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int sr = min(row0 + wr * S::WROWS + rb * 16 + lr, rows - 1);
+        orow[rb] = reorder_rows != nullptr ? reorder_rows[sr] : sr;
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int sr = row0 + wr * S::WROWS + rb * 16 + lr;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const T* bq = reinterpret_cast<const T*>(&bias4[cb]);
+            T v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = epi.finish(acc[rb][cb][q], static_cast<float>(bq[q]));
+            if (sr < rows) {
+                *reinterpret_cast<uint2*>(obase + static_cast<long long>(orow[rb]) * out_ld + cb * 16) =
+                    *reinterpret_cast<const uint2*>(v);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------- direct expansion ----
 //
 // Conv over a direct generative / transposed relation (output row
@@ -1362,6 +1768,75 @@ int launch_igemm(const T* feats, int n_in, int c_in, int c_out, const BSource& b
     }
 }
 
+// Shapes the streamed kernel takes: fp16/bf16, C_in a multiple of 32 up to
+// 256, C_out in {64, 128, 256}, K <= 32, and a feature table whose byte
+// offsets (with the wrapped -1 rows above them) fit 32 bits.
+bool stream_shape_ok(long long n_in, int c_in, int c_out, int K) {
+    const long long row_bytes = static_cast<long long>(c_in) * 2;
+    return c_in > 0 && c_in % 32 == 0 && c_in <= 256 && K > 0 && K <= 32 &&
+           (c_out == 64 || c_out == 128 || c_out == 256) && n_in >= 0 && (n_in + 1) * row_bytes <= (1ll << 32);
+}
+
+size_t fragments_bytes(int K, int c_in, int c_out) {
+    return static_cast<size_t>(K) * static_cast<size_t>(c_in) * static_cast<size_t>(c_out) * 2;
+}
+
+template <typename T, typename S, int NCH>
+void launch_stream_nch(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
+                       const int32_t* tile_masks, const int32_t* reorder_rows, int rows, const int32_t* order, T* out,
+                       Epilogue<T> epi, int halves, hipStream_t stream) {
+    const int tiles = (rows + S::ROWS - 1) / S::ROWS;
+    conv_igemm_stream<T, S, NCH><<<static_cast<unsigned>(tiles * halves), S::THREADS, 0, stream>>>(
+        feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order, out, epi, halves);
+}
+
+template <typename T, typename S>
+void launch_stream_shape(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
+                         const int32_t* tile_masks, const int32_t* reorder_rows, int rows, const int32_t* order,
+                         T* out, Epilogue<T> epi, int halves, hipStream_t stream) {
+    switch ((c_in + S::CHUNK - 1) / S::CHUNK) {
+    case 1:
+        launch_stream_nch<T, S, 1>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+                                   out, epi, halves, stream);
+        break;
+    case 2:
+        launch_stream_nch<T, S, 2>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+                                   out, epi, halves, stream);
+        break;
+    case 3:
+        launch_stream_nch<T, S, 3>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+                                   out, epi, halves, stream);
+        break;
+    default:
+        launch_stream_nch<T, S, 4>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+                                   out, epi, halves, stream);
+        break;
+    }
+}
+
+template <typename T>
+int launch_stream(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
+                  const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, bool ready,
+                  T* out, Epilogue<T> epi, hipStream_t stream) {
+    if (rows <= 0) return LATTICE_OK;
+    const int tiles = (rows + kOrderTileRows - 1) / kOrderTileRows;
+    if (tiles > kMaxScheduledTiles) schedule = nullptr;
+    if (schedule != nullptr && !ready) {
+        schedule_tiles<kOrderTileRows / 16><<<1, kScheduleThreads, 0, stream>>>(tile_masks, rows, tiles, schedule);
+        LATTICE_LAUNCH_CHECK();
+    }
+    if (c_out == 64) {
+        launch_stream_shape<T, StreamShape<64, 2>>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
+                                                   reorder_rows, rows, schedule, out, epi, 1, stream);
+    } else {
+        launch_stream_shape<T, StreamShape<128, 1>>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
+                                                    reorder_rows, rows, schedule, out, epi, c_out == 256 ? 2 : 1,
+                                                    stream);
+    }
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
 // Workspace of the matrix-core conv: the tile schedule, one int per row
 // tile (tiles are at least 64 rows).  NULL workspace = tiles in order.
 // With LATTICE_CONV_ORDER_READY in workspace_bytes the workspace already
@@ -1516,6 +1991,68 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm(
     return launch_igemm<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in, c_out, b, sorted_kv_out_in_map,
                                 tile_masks, reorder_rows, out_capacity, schedule, ready, static_cast<__bf16*>(out),
                                 epilogue_of<__bf16>(bias, epilogue), stream);
+}
+
+extern "C" size_t lattice_hip_conv_weight_fragments_bytes(int dtype, int kernel_count, int c_in, int c_out) {
+    if (dtype != LATTICE_F16 && dtype != LATTICE_BF16) return 0;
+    if (!stream_shape_ok(0, c_in, c_out, kernel_count)) return 0;
+    return fragments_bytes(kernel_count, c_in, c_out);
+}
+
+extern "C" int lattice_hip_conv_weight_fragments(int dtype, const void* weights, int kernel_count, int c_in, int c_out,
+                                                 void* fragments, size_t fragments_bytes_given, void* stream_ptr) {
+    const size_t need = lattice_hip_conv_weight_fragments_bytes(dtype, kernel_count, c_in, c_out);
+    if (need == 0) {
+        set_error("weight fragments need fp16/bf16 weights with c_in % 32 == 0 (<= 256), c_out in {64, 128, 256} "
+                  "and K <= 32.");
+        return LATTICE_ERROR_UNSUPPORTED;
+    }
+    LATTICE_REQUIRE(weights != nullptr && fragments != nullptr, "weight fragment pointers must be non-null.");
+    LATTICE_REQUIRE(fragments_bytes_given >= need, "weight fragment buffer too small.");
+    hipStream_t stream = as_stream(stream_ptr);
+    const long long pieces = static_cast<long long>(need / 16);
+    const unsigned grid = grid_for(pieces, 256, 1u << 14);
+    if (dtype == LATTICE_F16) {
+        weight_fragments<_Float16><<<grid, 256, 0, stream>>>(static_cast<const _Float16*>(weights), kernel_count,
+                                                             c_in, c_out, static_cast<_Float16*>(fragments));
+    } else {
+        weight_fragments<__bf16><<<grid, 256, 0, stream>>>(static_cast<const __bf16*>(weights), kernel_count, c_in,
+                                                           c_out, static_cast<__bf16*>(fragments));
+    }
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_sparse_conv_features_sorted_fragments(
+    int dtype, const void* feats, int n_in, int c_in, const void* weight_fragments, int kernel_count, int c_out,
+    const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows, int out_capacity,
+    void* out, const void* bias, int epilogue, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
+    LATTICE_REQUIRE(dtype == LATTICE_F16 || dtype == LATTICE_BF16,
+                    "the streamed matrix-core conv takes float16 or bfloat16 features.");
+    LATTICE_REQUIRE(n_in >= 0 && out_capacity >= 0, "feats must have shape (N, C_in).");
+    if (!stream_shape_ok(n_in, c_in, c_out, kernel_count)) {
+        set_error("the streamed conv needs c_in % 32 == 0 (<= 256), c_out in {64, 128, 256}, K <= 32 and feats "
+                  "under 4 GiB.");
+        return LATTICE_ERROR_UNSUPPORTED;
+    }
+    LATTICE_REQUIRE(sorted_kv_out_in_map && tile_masks && out && weight_fragments && (feats || n_in == 0),
+                    "conv pointers must be non-null.");
+    int32_t* schedule = nullptr;
+    bool ready = false;
+    int rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule, &ready);
+    if (rc != LATTICE_OK) return rc;
+    hipStream_t stream = as_stream(stream_ptr);
+    if (dtype == LATTICE_F16) {
+        return launch_stream<_Float16>(static_cast<const _Float16*>(feats), n_in, c_in,
+                                       static_cast<const _Float16*>(weight_fragments), kernel_count, c_out,
+                                       sorted_kv_out_in_map, tile_masks, reorder_rows, out_capacity, schedule, ready,
+                                       static_cast<_Float16*>(out), epilogue_of<_Float16>(bias, epilogue), stream);
+    }
+    return launch_stream<__bf16>(static_cast<const __bf16*>(feats), n_in, c_in,
+                                 static_cast<const __bf16*>(weight_fragments), kernel_count, c_out,
+                                 sorted_kv_out_in_map, tile_masks, reorder_rows, out_capacity, schedule, ready,
+                                 static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue), stream);
 }
 
 // ------------------------------------------------- allocation-free entry --

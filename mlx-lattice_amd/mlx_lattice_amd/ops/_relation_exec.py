@@ -199,17 +199,21 @@ def sparse_conv_input_grad_from_relation(cot: torch.Tensor,
     if _input_grad_matrix_core_eligible(cot, weight, relation):
         if _mirror_symmetric(relation):
             view = relation.require_sorted_implicit_gemm()
+            mirrored = _mirrored_weight(weight)
             return ext.sparse_conv_features_sorted_implicit_gemm(
-                cot, _mirrored_weight(weight), view.sorted_out_in_map,
+                cot, mirrored, view.sorted_out_in_map,
                 view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
                 None, None, None, None, None, None, None, None, None,
-                in_capacity, relation.n_kernels, tile_order=view.tile_order())
+                in_capacity, relation.n_kernels, tile_order=view.tile_order(),
+                weight_fragments=_weight_fragments(mirrored))
         view = relation.require_transposed_sorted_implicit_gemm()
+        transposed = _transposed_weight(weight)
         return ext.sparse_conv_features_sorted_implicit_gemm(
-            cot, _transposed_weight(weight), view.sorted_out_in_map,
+            cot, transposed, view.sorted_out_in_map,
             view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
             None, None, None, None, None, None, None, None, None,
-            in_capacity, relation.n_kernels, tile_order=view.tile_order())
+            in_capacity, relation.n_kernels, tile_order=view.tile_order(),
+            weight_fragments=_weight_fragments(transposed))
     input_csr = relation.input_csr
     return ext.sparse_conv_input_grad(
         cot, weight, relation.edges.out_rows, relation.edges.kernel_ids,
@@ -274,15 +278,16 @@ def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
             'sorted implicit GEMM is not supported for this relation, '
             'feature tensor, or weight tensor.')
     view = relation.require_sorted_implicit_gemm()
+    w5 = _matrix_core_weight(weight)
     return ext.sparse_conv_features_sorted_implicit_gemm(
-        feats, _matrix_core_weight(weight), view.sorted_out_in_map,
+        feats, w5, view.sorted_out_in_map,
         view.sorted_kv_out_in_map, view.reorder_rows, view.tile_masks,
         relation.edges.in_rows, relation.edges.out_rows,
         relation.edges.kernel_ids, relation.counts,
         relation.output_csr.row_offsets, None, None, None, None,
         relation.n_out_capacity, relation.n_kernels,
         store_sorted=store_sorted, bias=bias, tile_order=view.tile_order(),
-        relu=relu)
+        relu=relu, weight_fragments=_weight_fragments(w5))
 
 
 def sparse_quantized_conv_features_from_relation(
@@ -388,6 +393,13 @@ def _cached_weight(weight: torch.Tensor, kind: str, make) -> torch.Tensor:
     _WEIGHT_CACHE[key] = (weakref.ref(weight, _drop), shape, weight.dtype,
                           weight._version, value)
     return value
+
+
+def _weight_fragments(weight5d: torch.Tensor) -> torch.Tensor:
+    """The streamed matrix-core conv's fragment-ordered copy of a 5D
+    fp16/bf16 weight (``ext.conv_weight_fragments``; empty when the shape
+    takes the other matrix-core kernel), cached with the weight."""
+    return _cached_weight(weight5d, 'fragments', ext.conv_weight_fragments)
 
 
 def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:

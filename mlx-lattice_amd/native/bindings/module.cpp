@@ -199,18 +199,22 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            const py::object& /*counts*/, const py::object& /*row_offsets*/, const py::object& /*in_row_offsets*/,
            const py::object& /*in_edge_ids*/, const py::object& /*kernel_row_offsets*/,
            const py::object& /*kernel_edge_ids*/, int out_capacity, int n_kernels, bool store_sorted,
-           const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& tile_order, bool relu) {
+           const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& tile_order, bool relu,
+           const std::optional<at::Tensor>& weight_fragments) {
             return ln::sparse_conv_features_sorted_implicit_gemm(feats, weights, sorted_out_in_map,
                                                                  sorted_kv_out_in_map, reorder_rows, tile_masks,
                                                                  out_capacity, n_kernels, store_sorted, bias,
-                                                                 tile_order, relu);
+                                                                 tile_order, relu, weight_fragments);
         },
         py::arg("feats"), py::arg("weights"), py::arg("sorted_out_in_map"), py::arg("sorted_kv_out_in_map"),
         py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("in_rows"), py::arg("out_rows"),
         py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("in_row_offsets"),
         py::arg("in_edge_ids"), py::arg("kernel_row_offsets"), py::arg("kernel_edge_ids"), py::arg("out_capacity"),
         py::arg("n_kernels"), py::arg("store_sorted") = false, py::kw_only(), py::arg("bias") = py::none(),
-        py::arg("tile_order") = py::none(), py::arg("relu") = false);
+        py::arg("tile_order") = py::none(), py::arg("relu") = false, py::arg("weight_fragments") = py::none());
+    m.def("conv_weight_fragments", &ln::conv_weight_fragments, py::arg("weights"),
+          "Fragment-ordered copy of a 5D fp16/bf16 weight for the streamed matrix-core conv (empty when the shape "
+          "does not take it).");
     m.def("sparse_quantized_conv_features", &ln::sparse_quantized_conv_features, py::arg("feats"),
           py::arg("weights"), py::arg("scales"), py::arg("biases"), py::arg("in_rows"), py::arg("out_rows"),
           py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"), py::arg("sorted_kv_out_in_map"),

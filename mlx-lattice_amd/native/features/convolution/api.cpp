@@ -212,7 +212,8 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
                                                      const at::Tensor& reorder_rows, const at::Tensor& tile_masks,
                                                      int out_capacity, int n_kernels, bool store_sorted,
                                                      const std::optional<at::Tensor>& bias,
-                                                     const std::optional<at::Tensor>& tile_order, bool relu) {
+                                                     const std::optional<at::Tensor>& tile_order, bool relu,
+                                                     const std::optional<at::Tensor>& weight_fragments) {
     const char* op = "sparse_conv_features_sorted_implicit_gemm";
     if (sorted_out_in_map.dim() != 2 || sorted_out_in_map.scalar_type() != at::kInt) {
         throw std::invalid_argument("sorted_out_in_map must have shape (N_out, K) and int32 dtype.");
@@ -248,6 +249,32 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
     at::Tensor ws = schedule_workspace(tile_order, out_capacity, feats, &ws_bytes);
     at::Tensor bias_keep;
     const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
+    const int dtype = dtype_code(feats, op);
+    const int c_in = static_cast<int>(feats.size(1));
+    const size_t frag_bytes =
+        lattice_hip_conv_weight_fragments_bytes(dtype, n_kernels, c_in, static_cast<int>(c_out));
+    const bool small_table = (feats.size(0) + 1) * static_cast<int64_t>(c_in) * 2 <= (int64_t{1} << 32);
+    if (frag_bytes > 0 && small_table) {
+        // Streamed route: the weight in fragment order (the caller's cached
+        // copy, or made now).
+        at::Tensor frag;
+        if (weight_fragments.has_value() && weight_fragments->numel() > 0) {
+            frag = *weight_fragments;
+            if (!frag.is_contiguous() || static_cast<size_t>(frag.numel()) * frag.element_size() < frag_bytes ||
+                frag.scalar_type() != feats.scalar_type()) {
+                throw std::invalid_argument("weight_fragments must be the conv_weight_fragments of this weight.");
+            }
+            require_device(frag, "weight_fragments");
+        } else {
+            frag = conv_weight_fragments(weights);
+        }
+        check_status(lattice_hip_sparse_conv_features_sorted_fragments(
+            dtype, feats.data_ptr(), static_cast<int>(feats.size(0)), c_in, frag.data_ptr(), n_kernels,
+            static_cast<int>(c_out), ci32(kv), ci32(tiles), store_sorted ? nullptr : ci32(order), out_capacity,
+            out.data_ptr(), b, relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, ws.data_ptr(), ws_bytes,
+            current_stream(feats)));
+        return out;
+    }
     check_status(lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), LATTICE_WEIGHT_DENSE_5D, n_kernels, static_cast<int>(c_out), ci32(kv), ci32(tiles),
@@ -255,6 +282,27 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats_in,
         relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, ws.data_ptr(), ws_bytes,
         current_stream(feats)));
     return out;
+}
+
+at::Tensor conv_weight_fragments(const at::Tensor& weights_in) {
+    if (weights_in.dim() != 5 && weights_in.dim() != 3) {
+        throw std::invalid_argument("weights must have shape (K, C_in, C_out) or (C_out, Kx, Ky, Kz, C_in).");
+    }
+    require_device(weights_in, "weights");
+    const at::Tensor weights =
+        weights_in.dim() == 5 ? weights_in.contiguous() : weights_in.permute({2, 0, 1}).contiguous();
+    const int c_out = static_cast<int>(weights.size(0));
+    const int c_in = static_cast<int>(weights.size(-1));
+    const int k = static_cast<int>(weights.numel() / (static_cast<int64_t>(c_out) * c_in));
+    int dtype = -1;
+    if (weights.scalar_type() == at::kHalf) dtype = LATTICE_F16;
+    if (weights.scalar_type() == at::kBFloat16) dtype = LATTICE_BF16;
+    const size_t bytes = dtype < 0 ? 0 : lattice_hip_conv_weight_fragments_bytes(dtype, k, c_in, c_out);
+    at::Tensor frag = at::empty({static_cast<int64_t>(bytes / weights.element_size())}, weights.options());
+    if (bytes == 0) return frag;
+    check_status(lattice_hip_conv_weight_fragments(dtype, weights.data_ptr(), k, c_in, c_out, frag.data_ptr(), bytes,
+                                                   current_stream(weights)));
+    return frag;
 }
 
 at::Tensor conv_tile_order(const at::Tensor& tile_masks, int out_capacity) {

@@ -37,7 +37,14 @@ at::Tensor sparse_conv_features_sorted_implicit_gemm(const at::Tensor& feats, co
                                                      int out_capacity, int n_kernels, bool store_sorted,
                                                      const std::optional<at::Tensor>& bias = std::nullopt,
                                                      const std::optional<at::Tensor>& tile_order = std::nullopt,
-                                          bool relu = false);
+                                                     bool relu = false,
+                                                     const std::optional<at::Tensor>& weight_fragments = std::nullopt);
+
+// The fragment-ordered copy of a 5D fp16/bf16 weight that the streamed
+// matrix-core conv reads (lattice_hip_conv_weight_fragments), kept with the
+// weight and passed back as `weight_fragments`; an empty tensor when the
+// weight's shape does not take that route.
+at::Tensor conv_weight_fragments(const at::Tensor& weights);
 
 at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Tensor& weights,
                                           const at::Tensor& scales, const at::Tensor& biases,
