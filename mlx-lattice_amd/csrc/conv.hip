@@ -1140,10 +1140,9 @@ __device__ inline void asm_copy_b128(u32x4v_t r, unsigned voff, unsigned lds_bas
 
 // Wait until at most N vector-memory loads are outstanding; the registers
 // passed are those the awaited loads write.
-template <int N, int G>
-__device__ inline void wait_vm_idx(int (&d)[G]) {
-    static_assert(G == 4, "four row indices");
-    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]) : "n"(N));
+template <int N>
+__device__ inline void wait_vm_1(int& d) {
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(d) : "n"(N));
 }
 
 template <int N, typename V, int CB, int ST>
@@ -1243,9 +1242,7 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
     constexpr int ST = S::ST;
     constexpr int G = S::GATHER;
     constexpr int NB = CB * ST;  // B loads per stage
-    constexpr int NI = G;        // row-index loads per stage
     constexpr int ND = G;        // LDS copies per stage
-    constexpr int NT = NI + NB + ND;
     constexpr int ABYTES = S::ABUF * static_cast<int>(sizeof(T));
     __shared__ __align__(16) T lds[3 * S::ABUF];
 
@@ -1284,7 +1281,6 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
         for (int j = 0; j < CB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     if (ntrips > 0) {
-        const int grow = wave * (8 * G) + (lane >> 3);  // first tile row this lane copies
         const int gp = (lane & 7) ^ ((lane >> 3) & 7);  // piece it copies (its slot ^ row % 8)
         const int ksteps = c_in / 32;
         const int ncg = c_out_total / S::WCOLS;
@@ -1297,10 +1293,16 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
         const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<unsigned long long>(lds));
 
         constexpr int LA = 2, LB = S::LB, LI = S::LI;
-        constexpr int NIS = LI - LA + 1;  // row-index register sets
-        constexpr int NBS = LB + 1;       // B register sets
+        static_assert(LI - LA == 1, "row indices arrive one stage before their copies");
+        // Row indices are loaded once per trip (an offset's NCH stages share
+        // them): one dword per lane, lane j < 32 holding copy row j of the
+        // wave, at the stage LI stages before the trip's first stage.  At
+        // most two trips' indices are in flight when a trip is one stage.
+        constexpr int NRS = NCH == 1 ? 2 : 1;  // row-index register sets
+        constexpr int NBS = LB + 1;            // B register sets
         // stages per unrolled block: whole trips that cycle every register set
-        constexpr int U = lcm_int(lcm_int(NIS, NBS), NCH);
+        constexpr int U = lcm_int(NRS * NCH, NBS);
+        static_assert(U % NCH == 0, "whole trips per unrolled block");
         constexpr int TPU = U / NCH;                 // trips per unrolled block
         constexpr int R = TPU + (U - 1 + LI) / NCH;  // ring entries a block reaches
         // Offset ring: kr[i] is the offset of trip t + i (t = the block's
@@ -1319,9 +1321,15 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
 #pragma unroll
         for (int i = 0; i < R; ++i) kr[i] = pop();
 
-        auto idx_load = [&](int (&d)[G], int k, int i) {
-            const int r = min(row0 + grow + 8 * i, rows - 1);
-            d[i] = asm_load_i32(krs, static_cast<unsigned>((k * rows + r) * 4));
+        // Lanes j and j + 32 load the index of copy row j of the wave.
+        auto idx_load = [&](int& raw, int k) {
+            const int r = min(row0 + wave * (8 * G) + (lane & 31), rows - 1);
+            raw = asm_load_i32(krs, static_cast<unsigned>((k * rows + r) * 4));
+        };
+        // Copy i of this lane reads row 8 i + lane / 8 of the wave's 32.
+        auto idx_expand = [&](int (&d)[G], int raw) {
+#pragma unroll
+            for (int i = 0; i < G; ++i) d[i] = __builtin_amdgcn_ds_bpermute((8 * i + (lane >> 3)) << 2, raw);
         };
         auto b_load = [&](V (&b)[CB][ST], int k, int ch, int cb, int st) {
             b[cb][st] = asm_load_b128<V>(
@@ -1336,22 +1344,27 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
             asm_copy_b128(frs, row + (ci + off) * sizeof(T), __builtin_amdgcn_readfirstlane(dst));
         };
 
-        constexpr int W_IDX = NB + ND + (LI - LA - 1) * NT;  // row indices of s + LA, at stage s
-        constexpr int W_B = ND + (LB - 1) * NT;              // B(s), before stage s issues
-        constexpr int W_A = (LA - 1) * NT;                   // A(s + 1), at the end of stage s
-        static_assert(W_IDX < 64 && W_B < 64, "waits fit the counter");
-        int idx[NIS][G];
+        // Memory ops of stage j: the trip's row indices when stage j + LI
+        // starts a trip, then NB B loads, then ND copies.
+        constexpr auto has_idx = [](int j) { return ((j + LI) % NCH + NCH) % NCH == 0; };
+        constexpr auto ops = [](int j) { return (((j + LI) % NCH + NCH) % NCH == 0 ? 1 : 0) + NB + ND; };
+        constexpr int W_IDX = NB + ND;  // indices of stage s + LA's trip, at stage s (issued first in s - 1)
+        static_assert(W_IDX < 64 && ND + ops(0) < 64, "waits fit the counter");
+        int raw[NRS];
+        int d[G];
         V b[NBS][CB][ST];
         // Prologue: indices of stages 0 .. LI - 1, A(0) .. A(LA - 1), B(0) ..
         // B(LB - 1), all complete before stage 0.
 #pragma unroll
         for (int u = 0; u < LI; ++u) {
-#pragma unroll
-            for (int i = 0; i < G; ++i) idx_load(idx[u % NIS], kr[u / NCH], i);
+            if (u % NCH == 0) idx_load(raw[(u / NCH) % NRS], kr[u / NCH]);
             if (u < LA) {
-                wait_vm_idx<0>(idx[u % NIS]);
+                if (u % NCH == 0) {
+                    wait_vm_1<0>(raw[(u / NCH) % NRS]);
+                    idx_expand(d, raw[(u / NCH) % NRS]);
+                }
 #pragma unroll
-                for (int i = 0; i < G; ++i) a_copy(idx[u % NIS], u % NCH, u, i);
+                for (int i = 0; i < G; ++i) a_copy(d, u % NCH, u, i);
             }
         }
 #pragma unroll
@@ -1367,25 +1380,32 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
         auto step = [&](auto P) {
             constexpr int p = decltype(P)::value;
             constexpr int ch = p % NCH;
-            int (&ia)[G] = idx[(p + LA) % NIS];
-            int (&ifill)[G] = idx[(p + LI) % NIS];
+            constexpr int NI = has_idx(p) ? 1 : 0;
+            constexpr int NT = NI + NB + ND;
+            constexpr int W_B = ND + ops(p - 1);  // B(s), before stage s issues (LB = 2)
+            constexpr int W_A = NT;                // A(s + 1), at the end of stage s (LA = 2)
+            static_assert(LB == 2, "W_B counts one stage between a B load and its use");
             V (&bcur)[CB][ST] = b[p % NBS];
             V (&bfill)[CB][ST] = b[(p + LB) % NBS];
             const int k = kr[p / NCH];
             const int k_i = kr[(p + LI) / NCH];
             const int k_b = kr[(p + LB) / NCH];
             const int abuf_fill = buf == 0 ? 2 : buf - 1;  // (s + 2) % 3
-            wait_vm_idx<W_IDX>(ia);
+            if constexpr ((p + LA) % NCH == 0) {
+                int& ra = raw[((p + LA) / NCH) % NRS];
+                wait_vm_1<W_IDX>(ra);
+                idx_expand(d, ra);
+            }
             wait_vm_b<W_B>(bcur);
             // Memory op q of this stage, in the fixed order.
             auto issue_op = [&](auto Q) {
                 constexpr int q = decltype(Q)::value;
                 if constexpr (q < NI) {
-                    idx_load(ifill, k_i, q);
+                    idx_load(raw[((p + LI) / NCH) % NRS], k_i);
                 } else if constexpr (q < NI + NB) {
                     b_load(bfill, k_b, (p + LB) % NCH, (q - NI) / ST, (q - NI) % ST);
                 } else {
-                    a_copy(ia, (p + LA) % NCH, abuf_fill, q - NI - NB);
+                    a_copy(d, (p + LA) % NCH, abuf_fill, q - NI - NB);
                 }
             };
             const int nst = (partial && ch == NCH - 1) ? 1 : ST;
