@@ -497,8 +497,10 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
         twice, inverse 4 B, counts 4 B per point; coords 16 B per voxel;
       voxelize: feats read, output written, the grouping read (4 B per
         point, 4 B per voxel);
-      interpolate: 8 rows + 8 weights per point read, the feature row of
-        every corner found read once per (point, corner), output written."""
+      interpolate: 8 rows + 8 weights per point read, each distinct voxel
+        row a corner names read once, output written (the minimum; the
+        bytes of one read per (point, corner) are reported beside it as
+        a diagnostic of the gather)."""
     import torch
 
     import mlx_lattice_amd.ops as ops
@@ -537,8 +539,11 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
     hbm = PEAK_HBM_GBS * 1e6
     b_q = n * (12 + 4 + 8 * 3 + 4 + 4) + v * 16
     b_vox = n * c * 4 + v * c * 4 + 4 * n + 4 * v
-    corners = int((pmap.rows >= 0).sum().item())
-    b_int = n * (32 + 32) + n * c * 4 + corners * c * 4
+    found = pmap.rows[pmap.rows >= 0]
+    corners = int(found.numel())
+    distinct = int(torch.unique(found).numel())
+    b_int = n * (32 + 32) + n * c * 4 + distinct * c * 4
+    b_int_gather = n * (32 + 32) + n * c * 4 + corners * c * 4
     return {
         'workload': '1M points in the config-3 voxels (unit voxel): '
                     'sparse_quantize, voxelize mean 64 ch, trilinear '
@@ -550,9 +555,11 @@ def quantization_workload(coords, steps: int, warmup: int) -> dict:
         'voxelize_ms': round(t_vox, 4),
         'voxelize_hbm_frac': round(b_vox / t_vox / hbm, 4),
         'corners_found': corners,
+        'distinct_corner_rows': distinct,
         'point_map_ms': round(t_map, 4),
         'interpolate_ms': round(t_int, 4),
         'interpolate_hbm_frac': round(b_int / t_int / hbm, 4),
+        'interpolate_per_corner_gbs': round(b_int_gather / t_int / 1e6, 1),
     }
 
 

@@ -94,7 +94,8 @@ enum lattice_relation_flags {
     LATTICE_STATUS_COORD_RANGE = 1,   /* unused: no coordinate is out of range */
     LATTICE_STATUS_REPEATED_EDGE = 2, /* transposed relation: two edges share (out_row, kernel_id) */
     LATTICE_STATUS_REPEATED_PAIR = 4, /* transposed dense map: two edges share (in_row, kernel_id) */
-    LATTICE_STATUS_REPEATED_COORD = 8 /* submanifold relation: an active row repeats an earlier row's coordinate */
+    LATTICE_STATUS_REPEATED_COORD = 8, /* submanifold relation: an active row repeats an earlier row's coordinate */
+    LATTICE_STATUS_TABLE_OVERFLOW = 16 /* a coordinate table filled up (a sizing error; the relation is void) */
 };
 
 /* Packed-key range: a key with batch in [0, LATTICE_MAX_BATCH] and axes in
@@ -111,6 +112,11 @@ const char* lattice_hip_version(void);
 
 /* next_pow2(max(2*rows, 1)): relations.cpp:95-105. */
 int lattice_hip_coord_hash_capacity(int rows);
+/* Bucket count of the 2x2x2 block table the relation builders query: a
+ * power of two above 1.5 * rows, so at least a third of the buckets stay
+ * empty whatever the coordinates (no reference counterpart: the reference
+ * hashes single voxels). */
+int lattice_hip_block_table_capacity(int rows);
 
 /* Kernel offsets in the reference order (offsets.cpp:11-45): odd sizes
  * -r..r, even sizes 0..k-1, x outer, z inner, times dilation.  Writes K*3
@@ -153,6 +159,9 @@ size_t lattice_hip_kernel_relation_workspace_bytes(int rows, int kernel_count);
  * the reference: a submanifold relation and the downsample relation of the
  * same level hash the same coordinates. */
 #define LATTICE_RELATION_TABLE_READY ((size_t)1 << 62)
+/* Bytes of the 2x2x2 block table of `rows` input rows (the first part of
+ * the lattice_hip_build_kernel_relation workspace). */
+size_t lattice_hip_block_table_bytes(int rows);
 size_t lattice_hip_target_relation_workspace_bytes(int rows, int target_rows,
                                                    int kernel_count);
 
@@ -165,6 +174,19 @@ int lattice_hip_build_kernel_relation(
     const int kernel_size[3], const int stride[3], const int padding[3],
     const int dilation[3], const lattice_relation_outputs* out,
     void* workspace, size_t workspace_bytes, void* stream);
+/* lattice_hip_build_kernel_relation with the block table in memory of its
+ * own: `table` holds at least lattice_hip_block_table_bytes(rows) bytes
+ * (LATTICE_RELATION_TABLE_READY may be set in table_bytes when it already
+ * holds the table of these coords and active_rows), `workspace` at least
+ * lattice_hip_kernel_relation_workspace_bytes(rows, K) -
+ * lattice_hip_block_table_bytes(rows).  A caller that keeps the table for
+ * the next relation over the same coordinates keeps only the table.  No
+ * reference counterpart (the reference hashes each build anew). */
+int lattice_hip_build_kernel_relation_with_table(
+    const int32_t* coords, int rows, const int32_t* active_rows,
+    const int kernel_size[3], const int stride[3], const int padding[3],
+    const int dilation[3], const lattice_relation_outputs* out, void* table,
+    size_t table_bytes, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Target relation: write_target_kernel_relation (relation_build_detail.h:43-80). */
 int lattice_hip_build_target_kernel_relation(

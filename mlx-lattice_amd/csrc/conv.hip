@@ -2095,9 +2095,17 @@ static __device__ __align__(256) int32_t scratch[kMaxScheduledTiles];
 constexpr int kMaxScratchDevices = 64;
 std::atomic<int32_t*> g_scratch_ptr[kMaxScratchDevices];
 
-int scratch_on_current_device(int32_t** ptr) {
+// The scratch of the current device, which must be the stream's device
+// (hipGetSymbolAddress answers for the current device).
+int scratch_on_current_device(hipStream_t stream, int32_t** ptr) {
     int device = 0;
     LATTICE_HIP_TRY(hipGetDevice(&device));
+    if (stream != nullptr) {
+        int stream_device = 0;
+        LATTICE_HIP_TRY(hipStreamGetDevice(stream, &stream_device));
+        LATTICE_REQUIRE(stream_device == device,
+                        "the allocation-free conv's stream belongs to another device than the current one.");
+    }
     LATTICE_REQUIRE(device >= 0 && device < kMaxScratchDevices, "device index out of range for the conv scratch.");
     int32_t* p = g_scratch_ptr[device].load(std::memory_order_acquire);
     if (p == nullptr) {
@@ -2122,7 +2130,7 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     static_assert(static_cast<size_t>(LATTICE_NOALLOC_CONV_MAX_ROWS) / 64 + 1 <= kMaxScheduledTiles,
                   "the scratch holds the schedule of the largest allowed launch");
     int32_t* schedule = nullptr;
-    const int rc = scratch_on_current_device(&schedule);
+    const int rc = scratch_on_current_device(as_stream(stream_ptr), &schedule);
     if (rc != LATTICE_OK) return rc;
     return lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype, feats, n_in, c_in, weights, weight_layout, kernel_count, c_out, sorted_kv_out_in_map, tile_masks,

@@ -761,9 +761,11 @@ int launch_group_offsets(const int32_t* sorted_keys, int capacity, int groups, i
 
 // ------------------------------------------------------------- helpers ----
 
+// Slot count of the coordinate table: a power of two at least twice the
+// row count (so at least half the slots stay empty).
 int table_capacity(int rows) {
     int cap = 1;
-    int want = std::max(rows * 2, 1);
+    const long long want = std::max(2ll * rows, 1ll);
     while (cap < want) cap <<= 1;
     return cap;
 }
@@ -785,9 +787,10 @@ int make_table(int rows, Workspace& ws, CoordTable* table) {
 }
 
 int build_table(const int32_t* coords, int rows, const int32_t* active_rows, Int3 cell,
-                Workspace& ws, hipStream_t stream, CoordTable* table) {
+                Workspace& ws, hipStream_t stream, CoordTable* table, int32_t* status = nullptr) {
     int rc = make_table(rows, ws, table);
     if (rc != LATTICE_OK) return rc;
+    table->status = status;
     const int cap = static_cast<int>(table->mask) + 1;
     clear_table<<<grid_for(cap, kThreads, 4096), kThreads, 0, stream>>>(table->slots, cap);
     LATTICE_LAUNCH_CHECK();
@@ -822,6 +825,7 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
     table->buckets = ws.take<BlockBucket>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
     table->src = BlockSource{coords};
+    table->status = prologue.status;
     if (table->buckets == nullptr) {
         set_error("relation workspace too small for the coordinate table");
         return LATTICE_ERROR_INVALID_ARGUMENT;
@@ -998,6 +1002,8 @@ using namespace lattice;
 
 extern "C" int lattice_hip_coord_hash_capacity(int rows) { return table_capacity(rows); }
 
+extern "C" int lattice_hip_block_table_capacity(int rows) { return block_capacity(rows); }
+
 extern "C" int lattice_hip_kernel_offsets(const int kernel_size[3], const int dilation[3], int32_t* out) {
     for (int a = 0; a < 3; ++a) {
         if (kernel_size[a] <= 0 || dilation[a] <= 0) return -1;
@@ -1029,11 +1035,28 @@ extern "C" size_t lattice_hip_target_relation_workspace_bytes(int rows, int targ
     return bytes + 4096;
 }
 
+extern "C" size_t lattice_hip_block_table_bytes(int rows) { return block_table_bytes(std::max(rows, 0)); }
+
 extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows, const int32_t* active_rows,
                                                  const int kernel_size[3], const int stride[3],
                                                  const int padding[3], const int dilation[3],
                                                  const lattice_relation_outputs* out, void* workspace,
                                                  size_t workspace_bytes, void* stream_ptr) {
+    // The block table sits at the start of the workspace, the rest after it.
+    const size_t flags = workspace_bytes & LATTICE_RELATION_TABLE_READY;
+    const size_t bytes = workspace_bytes & ~static_cast<size_t>(LATTICE_RELATION_TABLE_READY);
+    const size_t tbytes = block_table_bytes(std::max(rows, 0));
+    const bool split = workspace != nullptr && bytes >= tbytes;  // else the callee reports what is wrong
+    return lattice_hip_build_kernel_relation_with_table(
+        coords, rows, active_rows, kernel_size, stride, padding, dilation, out, workspace,
+        (split ? tbytes : bytes) | flags, split ? static_cast<char*>(workspace) + tbytes : nullptr,
+        split ? bytes - tbytes : 0, stream_ptr);
+}
+
+extern "C" int lattice_hip_build_kernel_relation_with_table(
+    const int32_t* coords, int rows, const int32_t* active_rows, const int kernel_size[3], const int stride[3],
+    const int padding[3], const int dilation[3], const lattice_relation_outputs* out, void* table_mem,
+    size_t table_bytes, void* workspace, size_t workspace_bytes, void* stream_ptr) {
     int rc = validate_geometry(kernel_size, stride, padding, dilation);
     if (rc != LATTICE_OK) return rc;
     rc = check_outputs(out, true, rows, kernel_size[0] * kernel_size[1] * kernel_size[2]);
@@ -1044,10 +1067,13 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     const KernelGeometry geom = make_geometry(kernel_size, stride, padding, dilation);
     const int K = geom.volume;
     LATTICE_REQUIRE(static_cast<long long>(rows) * K < INT_MAX, "relation edge capacity exceeds int32.");
-    const bool table_ready = (workspace_bytes & LATTICE_RELATION_TABLE_READY) != 0;
-    workspace_bytes &= ~static_cast<size_t>(LATTICE_RELATION_TABLE_READY);
-    LATTICE_REQUIRE(workspace_bytes >= forward_relation_bytes(rows, K), "relation workspace too small.");
+    const bool table_ready = (table_bytes & LATTICE_RELATION_TABLE_READY) != 0;
+    table_bytes &= ~static_cast<size_t>(LATTICE_RELATION_TABLE_READY);
+    LATTICE_REQUIRE(table_mem != nullptr && table_bytes >= block_table_bytes(rows), "block table too small.");
+    LATTICE_REQUIRE(workspace_bytes >= forward_relation_bytes(rows, K) - block_table_bytes(rows),
+                    "relation workspace too small.");
     hipStream_t stream = as_stream(stream_ptr);
+    Workspace tws{static_cast<char*>(table_mem), table_bytes};
     Workspace ws{static_cast<char*>(workspace), workspace_bytes};
 
     const bool identity = stride[0] == 1 && stride[1] == 1 && stride[2] == 1 && padding[0] == 0 &&
@@ -1064,7 +1090,7 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
         prologue.copy_dst = out->out_coords;
     }
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, prologue, ws, stream, &table, table_ready);
+    rc = build_block_table(coords, rows, active_rows, prologue, tws, stream, &table, table_ready);
     if (rc != LATTICE_OK) return rc;
 
     QueryArgs q{};
@@ -1114,7 +1140,7 @@ extern "C" int lattice_hip_build_kernel_relation(const int32_t* coords, int rows
     } else {
         const Int3 cell{stride[0], stride[1], stride[2]};
         CoordTable cells;
-        rc = build_table(coords, rows, active_rows, cell, ws, stream, &cells);
+        rc = build_table(coords, rows, active_rows, cell, ws, stream, &cells, out->status);
         if (rc != LATTICE_OK) return rc;
         int32_t* flags = ws.take<int32_t>(std::max(rows, 1));
         int32_t* group_totals = ws.take<int32_t>(query_blocks(rows) + 1);
@@ -1593,17 +1619,21 @@ resolve_candidates_tiled(BlockTable table, const int32_t* __restrict__ coords, i
                 // key and rows of a slot are read together
                 uint32_t slot = static_cast<uint32_t>(key.hash) & table.mask;
                 int32_t raw[8];
-                while (true) {
+                bool hit = false;
+                for (uint32_t probe = 0; probe <= table.mask; ++probe) {
                     const unsigned long long k = table.buckets[slot].key;
 #pragma unroll
                     for (int o = 0; o < 8; ++o) raw[o] = table.buckets[slot].rows[o];
-                    if (table.holds(k, key)) break;
-                    if (k == kEmptyKey) {
-#pragma unroll
-                        for (int o = 0; o < 8; ++o) raw[o] = 0;
+                    if (table.holds(k, key)) {
+                        hit = true;
                         break;
                     }
+                    if (k == kEmptyKey) break;
                     slot = (slot + 1) & table.mask;
+                }
+                if (!hit) {
+#pragma unroll
+                    for (int o = 0; o < 8; ++o) raw[o] = 0;
                 }
                 const int sx = (c.y & 1) - 1, sy = (c.z & 1) - 1, sz = (c.w & 1) - 1;
                 int32_t* f = found + lr * cells;

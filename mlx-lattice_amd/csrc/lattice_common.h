@@ -212,9 +212,20 @@ static_assert(sizeof(CoordSlot) == 16, "one 16-byte slot per key");
 // Cleared slot: empty key, row INT_MAX (as one 16-byte store).
 __host__ __device__ inline int4 empty_coord_slot() { return int4{-1, -1, 0x7fffffff, 0}; }
 
+// Every probe loop stops after `capacity` probes.  The tables are sized
+// above their key count (at least one empty slot always remains), so a
+// probe meets its key or an empty slot first; the bound only keeps a sizing
+// mistake from spinning forever.  A lookup that exhausts the table answers
+// "absent" (it visited every slot); an insert that does sets
+// LATTICE_STATUS_TABLE_OVERFLOW in `status` (when given) and gives up.
+__device__ inline void flag_table_overflow(int32_t* status) {
+    if (status != nullptr) atomicOr(status, LATTICE_STATUS_TABLE_OVERFLOW);
+}
+
 struct CoordTable {
     CoordSlot* slots;
     uint32_t mask;  // capacity - 1
+    int32_t* status = nullptr;  // overflow flag word, or null
 
     // Inserts `row` under key `k` (keeping the minimum row) and returns the
     // key's slot.  `src` recomputes the key of a claiming row.
@@ -222,7 +233,7 @@ struct CoordTable {
     __device__ inline uint32_t insert(const TableKey& k, int32_t row, const Source& src) const {
         uint32_t slot = static_cast<uint32_t>(k.hash) & mask;
         const unsigned long long mine = k.wide ? (k.word | static_cast<uint32_t>(row)) : k.word;
-        while (true) {
+        for (uint32_t probe = 0; probe <= mask; ++probe) {
             const unsigned long long prev = atomicCAS(&slots[slot].key, static_cast<unsigned long long>(kEmptyKey),
                                                       mine);
             const bool hit = prev == kEmptyKey || (k.wide ? same_tag(prev, k) && src.key_of(claim_row(prev)) == k.full
@@ -236,13 +247,16 @@ struct CoordTable {
             }
             slot = (slot + 1) & mask;
         }
+        // Full table: flag it and hand back a valid slot (its results are void).
+        flag_table_overflow(status);
+        return static_cast<uint32_t>(k.hash) & mask;
     }
 
     // Slot of key `k`, or -1.
     template <typename Source>
     __device__ inline int32_t find_slot(const TableKey& k, const Source& src) const {
         uint32_t slot = static_cast<uint32_t>(k.hash) & mask;
-        while (true) {
+        for (uint32_t probe = 0; probe <= mask; ++probe) {
             const uint64_t w = slots[slot].key;
             if (k.wide ? same_tag(w, k) && src.key_of(claim_row(w)) == k.full : w == k.word) {
                 return static_cast<int32_t>(slot);
@@ -250,6 +264,7 @@ struct CoordTable {
             if (w == kEmptyKey) return -1;
             slot = (slot + 1) & mask;
         }
+        return -1;
     }
 
     // First row of key `k`, or -1.  Packed keys read the key and the row
@@ -258,7 +273,7 @@ struct CoordTable {
     __device__ inline int32_t find(const TableKey& k, const Source& src) const {
         if (!k.wide) {
             uint32_t slot = static_cast<uint32_t>(k.hash) & mask;
-            while (true) {
+            for (uint32_t probe = 0; probe <= mask; ++probe) {
                 const int4 v = *reinterpret_cast<const int4*>(slots + slot);
                 const uint64_t w = static_cast<uint64_t>(static_cast<uint32_t>(v.x)) |
                                    (static_cast<uint64_t>(static_cast<uint32_t>(v.y)) << 32);
@@ -266,6 +281,7 @@ struct CoordTable {
                 if (w == kEmptyKey) return -1;
                 slot = (slot + 1) & mask;
             }
+            return -1;
         }
         const int32_t slot = find_slot(k, src);
         return slot < 0 ? -1 : slots[slot].row;
@@ -306,12 +322,13 @@ struct BlockTable {
     BlockBucket* buckets;
     uint32_t mask;  // bucket count - 1; the count exceeds the block count
     BlockSource src;  // the input coordinates the table was built from
+    int32_t* status = nullptr;  // overflow flag word, or null
 
     __device__ inline void insert(const TableKey& block_key, int octant, int32_t row) const {
         uint32_t slot = static_cast<uint32_t>(block_key.hash) & mask;
         const unsigned long long mine =
             block_key.wide ? (block_key.word | static_cast<uint32_t>(row)) : block_key.word;
-        while (true) {
+        for (uint32_t probe = 0; probe <= mask; ++probe) {
             // One compare-and-swap claims an empty slot or reports its key.
             const unsigned long long k = atomicCAS(&buckets[slot].key, static_cast<unsigned long long>(kEmptyKey),
                                                    mine);
@@ -324,6 +341,7 @@ struct BlockTable {
             }
             slot = (slot + 1) & mask;
         }
+        flag_table_overflow(status);
     }
 
     // Whether slot word `w` holds block key `k`.
@@ -334,24 +352,26 @@ struct BlockTable {
     // Bucket of the block, or -1.
     __device__ inline int32_t find_bucket(const TableKey& block_key) const {
         uint32_t slot = static_cast<uint32_t>(block_key.hash) & mask;
-        while (true) {
+        for (uint32_t probe = 0; probe <= mask; ++probe) {
             const unsigned long long k = buckets[slot].key;
             if (holds(k, block_key)) return static_cast<int32_t>(slot);
             if (k == kEmptyKey) return -1;
             slot = (slot + 1) & mask;
         }
+        return -1;
     }
 
     // First row of the voxel, or -1.
     __device__ inline int32_t find(const TableKey& block_key, int octant) const {
         uint32_t slot = static_cast<uint32_t>(block_key.hash) & mask;
-        while (true) {
+        for (uint32_t probe = 0; probe <= mask; ++probe) {
             const unsigned long long k = buckets[slot].key;
             const int32_t r = buckets[slot].rows[octant];
             if (holds(k, block_key)) return r == 0 ? -1 : kRowBias - r;
             if (k == kEmptyKey) return -1;
             slot = (slot + 1) & mask;
         }
+        return -1;
     }
 };
 

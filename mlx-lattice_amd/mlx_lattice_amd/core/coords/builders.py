@@ -84,8 +84,9 @@ def build_kernel_relation(coords: torch.Tensor,
                           dilation: int | Sequence[int] = 1, *,
                           table: torch.Tensor | None = None) -> KernelRelation:
     """Forward sparse convolution relation (builders.py:156-191).  ``table``
-    (optional): the ``block_table`` workspace of an earlier relation over
-    the same coordinates, whose block table the build then reuses."""
+    (optional): the ``block_table`` of an earlier relation over the same
+    coordinates (built on the current stream), which the build then reuses
+    instead of hashing the coordinates again."""
     validate_coords(coords)
     spec = KernelSpec(size=kernel_size, stride=stride, padding=padding,
                       dilation=dilation)
@@ -106,10 +107,10 @@ def build_submanifold_kernel_relation(
         dilation: int | Sequence[int] = 1, *,
         keep_table: bool = False) -> KernelRelation:
     """Submanifold relation whose output support is ``coords``
-    (builders.py:194-233).  ``keep_table``: keep the build's workspace as
-    ``block_table`` (its start holds the block table of ``coords``) for a
-    later ``build_kernel_relation(..., table=...)`` over the same
-    coordinates."""
+    (builders.py:194-233).  ``keep_table``: keep the build's block table of
+    ``coords`` (a buffer of its own, about 96-192 B per row) as
+    ``block_table`` for a later ``build_kernel_relation(..., table=...)``
+    over the same coordinates."""
     validate_coords(coords)
     spec = KernelSpec(size=kernel_size, stride=1, padding=0,
                       dilation=dilation)

@@ -54,10 +54,12 @@ class CoordinateManager:
     _kernel_relations: dict[
         tuple[CoordinateMapKey, CoordinateMapKey | None, KernelSpec, str],
         KernelRelation] = field(default_factory=dict)
-    # The workspace of the last submanifold relation built over a key: its
-    # start holds the block table of the key's coordinates, which the next
-    # forward relation over the same key reuses (and releases).
-    _block_tables: dict[CoordinateMapKey, torch.Tensor] = field(
+    # The block table of the last submanifold relation built over a key
+    # (its buffer only, not the rest of the build's workspace) and the
+    # stream it was written on (64 B per bucket, 1.5-3 buckets per row): the
+    # next forward relation over the same key takes the entry, and reuses
+    # the table when it runs on that stream.
+    _block_tables: dict[CoordinateMapKey, tuple[torch.Tensor, object]] = field(
         default_factory=dict)
 
     def insert_coords(self, coords: torch.Tensor,
@@ -116,8 +118,20 @@ class CoordinateManager:
                 self.coords(key), active_rows=self.active_rows(key),
                 kernel_size=spec.size, stride=spec.stride,
                 padding=spec.padding, dilation=spec.dilation,
-                table=self._block_tables.pop(key, None))
+                table=self._take_block_table(key))
         return self._kernel_relations[cache_key]
+
+    def _take_block_table(self, key: CoordinateMapKey) -> torch.Tensor | None:
+        """Pop the key's kept block table; hand it out only when the
+        current stream is the one that wrote it (stream order then makes
+        the table complete before the new build reads it)."""
+        entry = self._block_tables.pop(key, None)
+        if entry is None:
+            return None
+        table, stream = entry
+        if table.is_cuda and torch.cuda.current_stream(table.device) != stream:
+            return None
+        return table
 
     def generative_relation(self, key: CoordinateMapKey, *,
                             kernel_size: int | Sequence[int] = 2,
@@ -166,7 +180,9 @@ class CoordinateManager:
                 keep_table=True)
             table = relation.block_table
             if table is not None:
-                self._block_tables[key] = table
+                stream = (torch.cuda.current_stream(table.device)
+                          if table.is_cuda else None)
+                self._block_tables[key] = (table, stream)
                 object.__setattr__(relation, 'block_table', None)
             self._kernel_relations[cache_key] = relation
         return self._kernel_relations[cache_key]

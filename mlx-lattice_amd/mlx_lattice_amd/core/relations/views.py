@@ -143,9 +143,18 @@ class _StatusWord:
             self._event = None
 
     def read(self) -> int:
+        """The word's value.  Raises RuntimeError when the builder's
+        coordinate table overflowed (lattice_relation_flags bit 16): the
+        table is sized above its key count, so this marks a sizing error
+        and the relation's contents are void."""
         if self._event is not None:
             self._event.synchronize()
-        return int(self._host[0])
+        value = int(self._host[0])
+        if value & 16:
+            raise RuntimeError('relation build: the coordinate table '
+                               'overflowed (status word bit 16); the '
+                               'relation is invalid.')
+        return value
 
 
 @dataclass(frozen=True, slots=True)
@@ -235,9 +244,10 @@ class KernelRelation:
     transposed_sorted_implicit_gemm: RelationSortedImplicitGemmView | None = None
     # Transposed relations only: whether two edges share (out_row, kernel_id)
     # (a repeated input coordinate).  The builder hands over its device
-    # status word; it is read on the first question (dense_map_exact), so
-    # building the relation never waits for the device.  None: unknown.
-    repeated_edges: bool | torch.Tensor | None = None
+    # status word, copied to pinned memory at build time (a _StatusWord) and
+    # read on the first question (dense_map_exact), so building the relation
+    # never waits for the device.  None: unknown.
+    repeated_edges: bool | _StatusWord | None = None
     # Generative, and transposed relations whose stride exceeds the offsets'
     # extent: output row in * K + k holds the single edge (in, k).
     direct_expansion: bool = False
@@ -348,7 +358,10 @@ class KernelRelation:
         object.__setattr__(self, 'implicit_gemm', implicit_gemm)
         object.__setattr__(self, 'sorted_implicit_gemm', sorted_implicit_gemm)
         object.__setattr__(self, 'transposed_sorted_implicit_gemm', None)
-        object.__setattr__(self, 'repeated_edges', repeated_edges)
+        object.__setattr__(
+            self, 'repeated_edges',
+            _StatusWord(repeated_edges)
+            if isinstance(repeated_edges, torch.Tensor) else repeated_edges)
         object.__setattr__(
             self, 'repeated_coords',
             _StatusWord(repeated_coords) if repeated_coords is not None
@@ -475,9 +488,9 @@ class KernelRelation:
         row); a transposed relation does unless an input coordinate repeats."""
         if self.contract.kind != 'transposed':
             return True
-        if isinstance(self.repeated_edges, torch.Tensor):
+        if isinstance(self.repeated_edges, _StatusWord):
             # lattice_relation_flags: bit 2 = repeated (out_row, kernel_id)
-            flags = int(self.repeated_edges.item())
+            flags = self.repeated_edges.read()
             object.__setattr__(self, 'repeated_edges', bool(flags & 2))
         if self.repeated_edges is None:
             return False

@@ -112,20 +112,23 @@ NativeKernelRelation make_kernel_relation(const at::Tensor& coords_in, const at:
     NativeKernelRelation r = allocate(coords, rows, rows, K, true, with_views);
     at::Tensor status = empty_i32({1}, coords);
     lattice_relation_outputs o = outputs_of(r, status);
-    const size_t need = lattice_hip_kernel_relation_workspace_bytes(rows, K);
-    // An earlier build's workspace over the same coordinates keeps its block
-    // table at its start; reuse it when it is large enough for this build.
+    // The block table lives in a buffer of its own, so a caller keeping it
+    // for the next relation over the same coordinates keeps only the table;
+    // an earlier build's table over these coordinates is reused as it is.
+    const size_t tneed = lattice_hip_block_table_bytes(rows);
+    const size_t need = lattice_hip_kernel_relation_workspace_bytes(rows, K) - tneed;
     const bool reuse = table.has_value() && table->defined() && table->scalar_type() == at::kByte &&
                        table->is_contiguous() && table->device() == coords.device() &&
-                       static_cast<size_t>(table->numel()) >= need;
-    at::Tensor ws = reuse ? *table : workspace(need, coords);
-    size_t ws_bytes = static_cast<size_t>(ws.numel());
-    if (reuse) ws_bytes |= LATTICE_RELATION_TABLE_READY;
-    check_status(lattice_hip_build_kernel_relation(ci32(coords), rows, ci32(active_rows), kernel_size.data(),
-                                                   stride.data(), padding.data(), dilation.data(), &o,
-                                                   ws.data_ptr(), ws_bytes, current_stream(coords)));
+                       static_cast<size_t>(table->numel()) >= tneed;
+    at::Tensor tb = reuse ? *table : workspace(tneed, coords);
+    at::Tensor ws = workspace(need, coords);
+    size_t tb_bytes = static_cast<size_t>(tb.numel());
+    if (reuse) tb_bytes |= LATTICE_RELATION_TABLE_READY;
+    check_status(lattice_hip_build_kernel_relation_with_table(
+        ci32(coords), rows, ci32(active_rows), kernel_size.data(), stride.data(), padding.data(), dilation.data(),
+        &o, tb.data_ptr(), tb_bytes, ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream(coords)));
     r.status = status;
-    r.table = ws;
+    r.table = tb;
     return r;
 }
 

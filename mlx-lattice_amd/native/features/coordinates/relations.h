@@ -30,8 +30,8 @@ struct NativeKernelRelation {
     // The build's device status word (lattice_relation_flags), left on the
     // device: nothing in a build waits for the device.
     at::Tensor status;
-    // The build's workspace, whose start holds the block table of the input
-    // coordinates: a later build over the same coordinates may reuse it
+    // The block table of the input coordinates (a buffer of its own): a
+    // later build over the same coordinates may reuse it
     // (LATTICE_RELATION_TABLE_READY).
     at::Tensor table;
 };

@@ -118,3 +118,35 @@ def test_quantized_layers_run_without_host_waits():
             group_size=mod.group_size, bits=mod.bits)[:n]
         ref = ref.astype(np.float32) + to_np(mod.bias).astype(np.float32)
         _close(to_np(out.feats[:n].float()), ref, f'quantized {geom}')
+
+
+@pytest.mark.parametrize('ks', [2, 3])
+def test_conv_transpose_runs_without_host_waits(ks):
+    """Decoder step: conv_transpose3d from a stride-2 level back to stride
+    1.  k=2 takes the direct expansion; k=3 the deduplicating transposed
+    relation, whose repeated-edge flag is copied to pinned memory at build
+    time instead of read back with ``.item()``."""
+    import mlx_lattice_amd.ops as ops
+    from mlx_lattice_amd import SparseTensor
+    from mlx_lattice_amd.synthetic import sphere_shell_cloud
+
+    rng = np.random.default_rng(92 + ks)
+    fine = sphere_shell_cloud(20000, 128, rng=rng)
+    down = O.kernel_relation(fine, kernel_size=2, stride=2)
+    coarse = down['out_coords'][:int(down['counts'][1])]
+    feats = rng.standard_normal((len(coarse), 64)).astype(np.float16)
+    w = (rng.standard_normal((32, ks, ks, ks, 64)) * 0.03).astype(np.float16)
+    c = torch.as_tensor(coarse).to(DEV)
+    f = torch.as_tensor(feats).to(DEV)
+    wt = torch.as_tensor(w).to(DEV)
+    print(f'async conv_transpose3d k={ks} N={len(coarse)}', flush=True)
+    with no_host_waits():
+        x = SparseTensor(c, f, stride=2)
+        y = ops.conv_transpose3d(x, wt, kernel_size=ks, stride=2)
+    torch.cuda.synchronize()
+    rel = O.transposed_kernel_relation(coarse, kernel_size=ks, stride=2)
+    n = int(rel['counts'][1])
+    assert int(y.active_rows.item()) == n
+    np.testing.assert_array_equal(to_np(y.coords[:n]), rel['out_coords'][:n])
+    ref = O.conv_features_fp64(feats, O.mapped_weight(w.astype(np.float64)), rel)
+    _close(to_np(y.feats[:n].float()), ref[:n], f'conv_transpose3d k={ks}')

@@ -472,6 +472,10 @@ def test_forward_relation_reuses_the_submanifold_block_table(ks, stride):
     mgr = x.coord_manager
     mgr.submanifold_kernel_relation(x.coord_key, kernel_size=3)
     assert x.coord_key in mgr._block_tables
+    # only the table is kept: one 64-byte bucket per block-table slot
+    # (a power of two above 1.5 n), not the rest of the build's workspace
+    kept = mgr._block_tables[x.coord_key][0]
+    assert kept.numel() <= 64 * 2 * (n + n // 2 + 1) + 4096
     print(f'table reuse k={ks} s={stride} N={n}', flush=True)
     reused = mgr.kernel_relation(x.coord_key, kernel_size=ks, stride=stride)
     assert x.coord_key not in mgr._block_tables
@@ -496,3 +500,38 @@ def test_forward_relation_reuses_the_submanifold_block_table(ks, stride):
     np.testing.assert_array_equal(
         to_np(reused.require_implicit_gemm().out_in_map)[:n_out],
         to_np(fresh.require_implicit_gemm().out_in_map)[:n_out])
+
+
+def test_block_table_is_not_reused_on_another_stream():
+    """The kept block table was written on the stream of its submanifold
+    build; a forward relation over the same key built on another stream
+    hashes the coordinates again (no cross-stream read) and still matches
+    a fresh build."""
+    from mlx_lattice_amd import SparseTensor
+    from mlx_lattice_amd.core.coords.builders import build_kernel_relation
+    from mlx_lattice_amd.synthetic import lidar_cloud
+
+    coords = lidar_cloud(3000, 2, rng=np.random.default_rng(47))
+    n = len(coords)
+    c = _t(coords)
+    x = SparseTensor(c, torch.zeros((n, 4), device=DEV))
+    mgr = x.coord_manager
+    mgr.submanifold_kernel_relation(x.coord_key, kernel_size=3)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    kept = mgr._block_tables[x.coord_key]
+    print(f'table reuse across streams N={n}', flush=True)
+    with torch.cuda.stream(side):
+        assert mgr._take_block_table(x.coord_key) is None
+        mgr._block_tables[x.coord_key] = kept
+        other = mgr.kernel_relation(x.coord_key, kernel_size=2, stride=2)
+    assert x.coord_key not in mgr._block_tables
+    torch.cuda.current_stream().wait_stream(side)
+    fresh = build_kernel_relation(c, _active(n), kernel_size=2, stride=2)
+    torch.cuda.synchronize()
+    e = int(fresh.counts[0].item())
+    np.testing.assert_array_equal(to_np(other.counts), to_np(fresh.counts))
+    np.testing.assert_array_equal(to_np(other.edges.in_rows)[:e],
+                                  to_np(fresh.edges.in_rows)[:e])
+    np.testing.assert_array_equal(to_np(other.edges.out_rows)[:e],
+                                  to_np(fresh.edges.out_rows)[:e])

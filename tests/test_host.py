@@ -47,6 +47,8 @@ def test_c_abi_host_queries():
     assert lib.lattice_hip_kernel_offsets(bad, dil, None) == -1
     lib.lattice_hip_kernel_relation_workspace_bytes.restype = ctypes.c_size_t
     assert lib.lattice_hip_kernel_relation_workspace_bytes(400000, 27) > 0
+    lib.lattice_hip_block_table_bytes.restype = ctypes.c_size_t
+    assert lib.lattice_hip_block_table_bytes(400000) == 64 << 20
     lib.lattice_hip_version.restype = ctypes.c_char_p
     assert b'gfx950' in lib.lattice_hip_version()
 
@@ -212,3 +214,39 @@ def test_spec_literal_shell_subsample():
         shells.update(map(tuple, _shell_voxels(c, r).tolist()))
     assert all(tuple(v) in shells for v in cloud[:, 1:].tolist())
     assert len(shells) > 20000
+
+
+@pytest.mark.parametrize('rows', [0, 1, 2, 3, 7, 8, 63, 64, 65, 1000, 65535,
+                                  65536, 400000, 699050, 699051, 10 ** 7,
+                                  (1 << 28) - 1])
+def test_table_capacities_always_leave_empty_slots(rows):
+    """Every probe loop of the coordinate tables stops at the first empty
+    slot (or after `capacity` probes, flagging an overflow).  Both tables
+    are sized so that empty slots always remain: the voxel table holds at
+    most `rows` keys in at least 2 * rows slots, the 2x2x2 block table at
+    most `rows` blocks in more than 1.5 * rows buckets."""
+    lib = ctypes.CDLL(str(LIB))
+    lib.lattice_hip_coord_hash_capacity.restype = ctypes.c_int
+    lib.lattice_hip_block_table_capacity.restype = ctypes.c_int
+    lib.lattice_hip_block_table_bytes.restype = ctypes.c_size_t
+    cap = lib.lattice_hip_coord_hash_capacity(rows)
+    assert cap >= max(2 * rows, 1) and cap & (cap - 1) == 0
+    buckets = lib.lattice_hip_block_table_capacity(rows)
+    assert buckets > rows + rows // 2 and buckets & (buckets - 1) == 0
+    assert buckets < 2 * (rows + rows // 2 + 1)      # the next power of two
+    assert lib.lattice_hip_block_table_bytes(rows) >= 64 * buckets
+
+
+def test_header_declares_the_table_overflow_flag():
+    """The overflow bit the bounded probe loops set is part of the ABI and
+    is the bit the host-side status reader raises on."""
+    text = HEADER.read_text()
+    assert re.search(r'LATTICE_STATUS_TABLE_OVERFLOW\s*=\s*16', text)
+
+
+def test_status_word_reader_raises_on_table_overflow():
+    from mlx_lattice_amd.core.relations.views import _StatusWord
+
+    assert _StatusWord(torch.tensor([8], dtype=torch.int32)).read() == 8
+    with pytest.raises(RuntimeError, match='overflowed'):
+        _StatusWord(torch.tensor([16 | 2], dtype=torch.int32)).read()
