@@ -278,14 +278,20 @@ PassPlan pass_plan(int p, int passes, int end_bit) {
     return PassPlan{shift, bits, std::max(1 << bits, kScanRows)};
 }
 
+// Digit rows of the count matrix for an end_bit sort: those of its widest
+// pass (the first; pass_plan spreads the remainder bits first).
+int count_rows(int end_bit) {
+    end_bit = std::min(std::max(end_bit, 1), 32);
+    return pass_plan(0, pass_count(end_bit), end_bit).rows;
+}
+
 }  // namespace
 
 size_t radix_sort_workspace_bytes(int n, int end_bit) {
-    (void)end_bit;
     const size_t items = static_cast<size_t>(std::max(n, 1));
     const size_t tiles = (items + kSortTile - 1) / kSortTile;
     size_t bytes = 4 * aligned_bytes(items * sizeof(uint32_t));  // two (key, index) buffers
-    bytes += aligned_bytes(static_cast<size_t>(padded_tiles(static_cast<int>(tiles))) * kDigits *
+    bytes += aligned_bytes(static_cast<size_t>(padded_tiles(static_cast<int>(tiles))) * count_rows(end_bit) *
                            sizeof(uint32_t));  // digit x tile counts
     bytes += aligned_bytes(4 * kDigits * sizeof(uint32_t));  // digit totals of up to 4 passes
     return bytes + 256;
@@ -299,7 +305,7 @@ int radix_sort_indices(const SortKeys& keys, int n, int end_bit, int32_t* sorted
     const int tiles = (n + kSortTile - 1) / kSortTile;
     uint32_t* key_buf[2] = {ws.take<uint32_t>(n), ws.take<uint32_t>(n)};
     int32_t* idx_buf[2] = {ws.take<int32_t>(n), ws.take<int32_t>(n)};
-    uint32_t* counts = ws.take<uint32_t>(static_cast<size_t>(padded_tiles(tiles)) * kDigits);
+    uint32_t* counts = ws.take<uint32_t>(static_cast<size_t>(padded_tiles(tiles)) * count_rows(end_bit));
     uint32_t* totals = ws.take<uint32_t>(static_cast<size_t>(passes) * kDigits);
     LATTICE_REQUIRE(key_buf[0] && key_buf[1] && idx_buf[0] && idx_buf[1] && counts && totals,
                     "radix sort workspace too small.");

@@ -250,6 +250,70 @@ def test_config3_headline_fp16_400k():
     _close(to_np(out.feats.float()), ref, RTOL_F16, ATOL_F16, 'config3')
 
 
+def _route_bound(feats, w, rel, n):
+    """Bound on |GPU - reference fp16 route| over output rows [0, n): the
+    reference route (eval_typed, cpu/algorithms.cpp:180-239) rounds its
+    running sum to fp16 after each of the L = edges(row) * c_in steps,
+    error <= ((1 + u)^L - 1) * S with u = 2^-11 and S the sum of |f * w|
+    over the row's terms; the GPU accumulates in fp32 (the same with
+    u = 2^-24) and rounds once to fp16 (<= 2^-11 |exact| <= 2^-11 S)."""
+    e = int(rel['row_offsets'][n])
+    absw = np.abs(O.mapped_weight(w.astype(np.float64)))
+    absf = np.abs(feats.astype(np.float64))
+    s = np.zeros((n, absw.shape[2]))
+    ins, outs, ks = (rel[k][:e] for k in ('in_rows', 'out_rows', 'kernel_ids'))
+    for k in range(absw.shape[0]):
+        sel = ks == k
+        if sel.any():
+            np.add.at(s, outs[sel], absf[ins[sel]] @ absw[k])
+    steps = np.diff(rel['row_offsets'][:n + 1]).astype(np.float64)[:, None] * feats.shape[1]
+    # (1 + u)^L - 1 bounds the relative growth of L roundings whatever L
+    # (gamma_L = L u / (1 - L u) needs L u < 1); fp16 subnormals add up to
+    # 2^-25 absolute per rounding.
+    grow16 = np.expm1(steps * np.log1p(2.0 ** -11))
+    grow32 = np.expm1(steps * np.log1p(2.0 ** -24))
+    return grow16 * s + grow32 * s + 2.0 ** -11 * s + (steps + 1) * 2.0 ** -25
+
+
+@pytest.mark.parametrize('config', [2, 3])
+def test_fp16_distance_to_the_reference_route(config):
+    """The GPU output against the reference's own fp16 CPU route (per-FMA
+    fp16 rounding, the route the reference takes for 64->128 and 128->128)
+    on the first output rows of configs 2 and 3: every element within the
+    derived rounding bound, the distance reported, and at least 99.9% of
+    elements within rtol 2e-2 (atol 1e-2) of the reference route."""
+    from mlx_lattice_amd.synthetic import (config_rng, kaiming_weight,
+                                           lidar_cloud, sphere_shell_cloud)
+
+    rng = config_rng(config)
+    if config == 2:
+        coords = lidar_cloud(100000, 2, rng=rng)
+        feats = rng.standard_normal((len(coords), 64)).astype(np.float16)
+        w = kaiming_weight((128, 2, 2, 2, 64), rng=rng).astype(np.float16)
+        geom = dict(kernel_size=2, stride=2)
+    else:
+        coords = sphere_shell_cloud(400000, 512, rng=rng)
+        feats = rng.standard_normal((len(coords), 128)).astype(np.float16)
+        w = kaiming_weight((128, 3, 3, 3, 128), rng=rng).astype(np.float16)
+        geom = dict(kernel_size=3)
+    print(f'fp16 distance to the reference route, config {config}', flush=True)
+    out = _run_conv(coords, feats, w, torch.float16, subm=config == 3, **geom)
+    rel = O.kernel_relation(coords, **geom)
+    n = min(16384, int(rel['counts'][1]))
+    sample = dict(rel)
+    sample['counts'] = np.array([rel['counts'][0], n], np.int32)
+    route = O.conv_features(feats, w, sample, out_capacity=n).astype(np.float64)
+    got = to_np(out.feats[:n].float()).astype(np.float64)
+    diff = np.abs(got - route)
+    assert (diff <= _route_bound(feats, w, rel, n)).all()
+    rel_err = diff / np.maximum(np.abs(route), 1e-2)
+    within = float((diff <= ATOL_F16 + RTOL_F16 * np.abs(route)).mean())
+    print(f'config {config}: {n} rows x {got.shape[1]} channels, max |gpu - '
+          f'route| {diff.max():.3e}, max relative {rel_err.max():.3e}, '
+          f'within rtol 2e-2: {within:.6f}', flush=True)
+    assert within >= 0.999
+
+
 # ------------------------------------------------------- quantized ----
 
 

@@ -278,6 +278,29 @@ def test_k2s2_matches_strided_dense_conv():
                                rtol=1e-5, atol=1e-5)
 
 
+def per_fma_fp16_bound(feats, weight5d, rel) -> np.ndarray:
+    """Elementwise error bound of the reference's per-FMA fp16 route
+    (cpu/algorithms.cpp:180-239) against the exact sum: recursive summation
+    over L = edges(row) * c_in steps, each rounded to fp16 (u = 2^-11):
+    ((1 + u)^L - 1) * sum over the row's terms of |f * w|, plus 2^-25
+    absolute per rounding (fp16 subnormal spacing)."""
+    u = 2.0 ** -11
+    e = int(rel['counts'][0])
+    n_out = rel['row_offsets'].shape[0] - 1
+    c_in = feats.shape[1]
+    absw = np.abs(O.mapped_weight(weight5d.astype(np.float64)))
+    absf = np.abs(feats.astype(np.float64))
+    s = np.zeros((n_out, absw.shape[2]))
+    ins, outs, ks = (rel[k][:e] for k in ('in_rows', 'out_rows', 'kernel_ids'))
+    for k in range(absw.shape[0]):
+        sel = ks == k
+        if sel.any():
+            np.add.at(s, outs[sel], absf[ins[sel]] @ absw[k])
+    steps = np.diff(rel['row_offsets']).astype(np.float64)[:, None] * c_in
+    grow = np.expm1(steps * np.log1p(u))  # (1 + u)^L - 1, valid for any L
+    return grow * s + (steps + 1) * 2.0 ** -25
+
+
 def test_fp16_routes_rounding_semantics():
     rng = np.random.default_rng(9)
     coords = np.unique(rng.integers(0, 10, size=(400, 4)), axis=0)
@@ -296,9 +319,14 @@ def test_fp16_routes_rounding_semantics():
             # fp32 accumulator, single rounding (eval_dense_channels_typed).
             assert err <= np.abs(ref).max() * 2 ** -10
         else:
-            # per-FMA fp16 rounding (eval_typed) is measurably worse.
+            # per-FMA fp16 rounding (eval_typed) is measurably worse, and
+            # bounded by recursive summation with a rounding to fp16 after
+            # each of the L = edges(row) * c_in steps:
+            # |err| <= ((1 + u)^L - 1) * sum |f * w|, u = 2^-11, plus
+            # 2^-25 absolute per rounding in the fp16 subnormal range.
             assert err > 0
-            assert err < 0.1
+            bound = per_fma_fp16_bound(f, w, rel)
+            assert (np.abs(got - ref) <= bound).all()
 
 
 # ---------------------------------------------------------- quantized ----
