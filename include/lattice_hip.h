@@ -466,6 +466,30 @@ int lattice_hip_sparse_quantized_conv_features(
     void* out, const void* bias, int epilogue, void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* Streamed matrix-core route of the quantized conv above (no counterpart in
+ * the reference; the dequant stays fused: the packed codes, scale and bias
+ * of each B fragment are loaded in one 16-byte load per lane and turned
+ * into w = q*scale + bias in registers right before the fragment's MFMAs).
+ * Shapes as for lattice_hip_sparse_conv_features_sorted_fragments.
+ * weight_fragments holds lattice_hip_quantized_weight_fragments_bytes(...)
+ * bytes written by lattice_hip_quantized_weight_fragments from the packed
+ * weights, scales and biases (layout of the entry above); a caller keeps
+ * them as long as the weight is unchanged.  bits is the weight's (4 or 8). */
+size_t lattice_hip_quantized_weight_fragments_bytes(int dtype,
+                                                    int kernel_count,
+                                                    int c_in, int c_out);
+int lattice_hip_quantized_weight_fragments(
+    int dtype, const uint32_t* weights, const void* scales,
+    const void* biases, int kernel_count, int c_in, int c_out,
+    int storage_c_in, int group_size, int bits, void* fragments,
+    size_t fragments_bytes, void* stream);
+int lattice_hip_sparse_quantized_conv_features_sorted_fragments(
+    int dtype, const void* feats, int n_in, int c_in,
+    const void* weight_fragments, int bits, int kernel_count, int c_out,
+    const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks,
+    const int32_t* reorder_rows, int out_capacity, void* out, const void* bias,
+    int epilogue, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Input gradient of the float conv (SparseConvFeaturesInputGrad,
  * primitive.cpp:192-260, 597-639; cpu/algorithms.cpp:355-410):
  * grad[in, ci] = sum over the edges of input row `in` in the input-grouped

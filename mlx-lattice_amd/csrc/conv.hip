@@ -1230,7 +1230,95 @@ weight_fragments(const T* __restrict__ w, int K, int c_in, int c_out, T* __restr
     }
 }
 
-template <typename T, typename S, int NCH>
+// Packed fragment of a quantized weight (lattice_hip_quantized_weight_
+// fragments): the 16 bytes of lane (lr, lg) of fragment (k, ks, cg, cb)
+// hold the codes of W[co][k][ci .. ci + 7] (co = cg*32 + cb*16 + lr,
+// ci = ks*32 + lg*8) and the affine scale and bias of their group:
+// x = 4-bit codes (nibble j = ci + j) or the first four 8-bit codes (byte
+// j), y = the last four 8-bit codes, z = scale | bias << 16, w unused.
+// Dequantised in registers once the load has landed: w = q * scale + bias,
+// one rounding to T (packed fp16 math as in PackedB::load).
+// Packed fragments of a quantized weight (layout above dequant_fragment):
+// w (K, packed_words, c_out) uint32 codes, scales / biases (K, groups,
+// c_out) of type T.
+template <typename T>
+__global__ void __launch_bounds__(256)
+packed_weight_fragments(const uint32_t* __restrict__ w, const T* __restrict__ scales, const T* __restrict__ biases,
+                        int K, int c_in, int c_out, int packed_words, int groups, int group_size, int bits,
+                        uint4* __restrict__ frag) {
+    const int ksteps = c_in / 32;
+    const int ncg = c_out / 32;
+    const long long pieces = static_cast<long long>(K) * c_in * c_out / 8;
+    for (long long p = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; p < pieces;
+         p += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int lane = static_cast<int>(p % 64);
+        long long f = p / 64;
+        const int cb = static_cast<int>(f % 2);
+        f /= 2;
+        const int cg = static_cast<int>(f % ncg);
+        f /= ncg;
+        const int ks = static_cast<int>(f % ksteps);
+        const int k = static_cast<int>(f / ksteps);
+        const int co = cg * 32 + cb * 16 + (lane & 15);
+        const int ci = ks * 32 + (lane >> 4) * 8;
+        const long long wbase = static_cast<long long>(k) * packed_words * c_out + co;
+        const long long sidx = (static_cast<long long>(k) * groups + ci / group_size) * c_out + co;
+        uint4 r;
+        if (bits == 4) {
+            r.x = w[wbase + static_cast<long long>(ci >> 3) * c_out];
+            r.y = 0u;
+        } else {
+            r.x = w[wbase + static_cast<long long>(ci >> 2) * c_out];
+            r.y = w[wbase + static_cast<long long>((ci >> 2) + 1) * c_out];
+        }
+        r.z = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, scales[sidx])) |
+              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, biases[sidx])) << 16);
+        r.w = 0u;
+        frag[p] = r;
+    }
+}
+
+template <typename T, int QB>
+__device__ inline typename MfmaOps<T>::vec dequant_fragment(typename MfmaOps<T>::vec raw) {
+    using V = typename MfmaOps<T>::vec;
+    const uint4 r = __builtin_bit_cast(uint4, raw);
+    V out;
+    if constexpr (std::is_same<T, _Float16>::value) {
+        const half2_t sb = __builtin_bit_cast(half2_t, r.z);
+        const half2_t sc = {sb[0], sb[0]};
+        const half2_t bi = {sb[1], sb[1]};
+        if constexpr (QB == 4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half2_t v = affine_pair(code_pair((r.x >> (4 * j)) & 0x000F000Fu), sc, bi);
+                out[j] = v[0];
+                out[j + 4] = v[1];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t word = i == 0 ? r.x : r.y;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const half2_t v = affine_pair(code_pair((word >> (8 * j)) & 0x00FF00FFu), sc, bi);
+                    out[4 * i + j] = v[0];
+                    out[4 * i + j + 2] = v[1];
+                }
+            }
+        }
+    } else {
+        const float sc = static_cast<float>(__builtin_bit_cast(T, static_cast<uint16_t>(r.z & 0xFFFFu)));
+        const float bi = static_cast<float>(__builtin_bit_cast(T, static_cast<uint16_t>(r.z >> 16)));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t q = QB == 4 ? (r.x >> (4 * j)) & 15u : ((j < 4 ? r.x : r.y) >> (8 * (j & 3))) & 255u;
+            out[j] = static_cast<T>(static_cast<float>(q) * sc + bi);
+        }
+    }
+    return out;
+}
+
+template <typename T, typename S, int NCH, int QB>
 __global__ void __launch_bounds__(S::THREADS, S::OCC)
 conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __restrict__ wfrag, int kernel_count,
                   int c_out_total, const int32_t* __restrict__ kv_map, const int32_t* __restrict__ tile_masks,
@@ -1397,6 +1485,12 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
                 idx_expand(d, ra);
             }
             wait_vm_b<W_B>(bcur);
+            if constexpr (QB != 0) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                    for (int st = 0; st < ST; ++st) bcur[cb][st] = dequant_fragment<T, QB>(bcur[cb][st]);
+            }
             // Memory op q of this stage, in the fixed order.
             auto issue_op = [&](auto Q) {
                 constexpr int q = decltype(Q)::value;
@@ -1801,40 +1895,40 @@ size_t fragments_bytes(int K, int c_in, int c_out) {
     return static_cast<size_t>(K) * static_cast<size_t>(c_in) * static_cast<size_t>(c_out) * 2;
 }
 
-template <typename T, typename S, int NCH>
+template <typename T, typename S, int NCH, int QB>
 void launch_stream_nch(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
                        const int32_t* tile_masks, const int32_t* reorder_rows, int rows, const int32_t* order, T* out,
                        Epilogue<T> epi, int halves, hipStream_t stream) {
     const int tiles = (rows + S::ROWS - 1) / S::ROWS;
-    conv_igemm_stream<T, S, NCH><<<static_cast<unsigned>(tiles * halves), S::THREADS, 0, stream>>>(
+    conv_igemm_stream<T, S, NCH, QB><<<static_cast<unsigned>(tiles * halves), S::THREADS, 0, stream>>>(
         feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order, out, epi, halves);
 }
 
-template <typename T, typename S>
+template <typename T, typename S, int QB>
 void launch_stream_shape(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
                          const int32_t* tile_masks, const int32_t* reorder_rows, int rows, const int32_t* order,
                          T* out, Epilogue<T> epi, int halves, hipStream_t stream) {
     switch ((c_in + S::CHUNK - 1) / S::CHUNK) {
     case 1:
-        launch_stream_nch<T, S, 1>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+        launch_stream_nch<T, S, 1, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
                                    out, epi, halves, stream);
         break;
     case 2:
-        launch_stream_nch<T, S, 2>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+        launch_stream_nch<T, S, 2, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
                                    out, epi, halves, stream);
         break;
     case 3:
-        launch_stream_nch<T, S, 3>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+        launch_stream_nch<T, S, 3, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
                                    out, epi, halves, stream);
         break;
     default:
-        launch_stream_nch<T, S, 4>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
+        launch_stream_nch<T, S, 4, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks, reorder_rows, rows, order,
                                    out, epi, halves, stream);
         break;
     }
 }
 
-template <typename T>
+template <typename T, int QB = 0>
 int launch_stream(const T* feats, int n_in, int c_in, const T* frag, int K, int c_out, const int32_t* kv_map,
                   const int32_t* tile_masks, const int32_t* reorder_rows, int rows, int32_t* schedule, bool ready,
                   T* out, Epilogue<T> epi, hipStream_t stream) {
@@ -1846,10 +1940,10 @@ int launch_stream(const T* feats, int n_in, int c_in, const T* frag, int K, int 
         LATTICE_LAUNCH_CHECK();
     }
     if (c_out == 64) {
-        launch_stream_shape<T, StreamShape<64, 2>>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
+        launch_stream_shape<T, StreamShape<64, 2>, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
                                                    reorder_rows, rows, schedule, out, epi, 1, stream);
     } else {
-        launch_stream_shape<T, StreamShape<128, 1>>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
+        launch_stream_shape<T, StreamShape<128, 1>, QB>(feats, n_in, c_in, frag, K, c_out, kv_map, tile_masks,
                                                     reorder_rows, rows, schedule, out, epi, c_out == 256 ? 2 : 1,
                                                     stream);
     }
@@ -2073,6 +2167,91 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_fragments(
                                  static_cast<const __bf16*>(weight_fragments), kernel_count, c_out,
                                  sorted_kv_out_in_map, tile_masks, reorder_rows, out_capacity, schedule, ready,
                                  static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue), stream);
+}
+
+extern "C" size_t lattice_hip_quantized_weight_fragments_bytes(int dtype, int kernel_count, int c_in, int c_out) {
+    return lattice_hip_conv_weight_fragments_bytes(dtype, kernel_count, c_in, c_out);
+}
+
+extern "C" int lattice_hip_quantized_weight_fragments(int dtype, const uint32_t* weights, const void* scales,
+                                                      const void* biases, int kernel_count, int c_in, int c_out,
+                                                      int storage_c_in, int group_size, int bits, void* fragments,
+                                                      size_t fragments_bytes_given, void* stream_ptr) {
+    const size_t need = lattice_hip_quantized_weight_fragments_bytes(dtype, kernel_count, c_in, c_out);
+    if (need == 0) {
+        set_error("quantized weight fragments need fp16/bf16 scales with c_in % 32 == 0 (<= 256), c_out in "
+                  "{64, 128, 256} and K <= 32.");
+        return LATTICE_ERROR_UNSUPPORTED;
+    }
+    LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized weight bits must be 4 or 8.");
+    LATTICE_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+                    "quantized weight group_size must be 32, 64, or 128.");
+    LATTICE_REQUIRE(storage_c_in >= c_in && storage_c_in % group_size == 0, "quantized weight channel metadata is invalid.");
+    LATTICE_REQUIRE(weights != nullptr && scales != nullptr && biases != nullptr && fragments != nullptr,
+                    "quantized weight fragment pointers must be non-null.");
+    LATTICE_REQUIRE(fragments_bytes_given >= need, "quantized weight fragment buffer too small.");
+    hipStream_t stream = as_stream(stream_ptr);
+    const long long pieces = static_cast<long long>(need / 16);
+    const unsigned grid = grid_for(pieces, 256, 1u << 14);
+    const int packed_words = storage_c_in * bits / 32;
+    const int groups = storage_c_in / group_size;
+    if (dtype == LATTICE_F16) {
+        packed_weight_fragments<_Float16><<<grid, 256, 0, stream>>>(
+            weights, static_cast<const _Float16*>(scales), static_cast<const _Float16*>(biases), kernel_count, c_in,
+            c_out, packed_words, groups, group_size, bits, static_cast<uint4*>(fragments));
+    } else {
+        packed_weight_fragments<__bf16><<<grid, 256, 0, stream>>>(
+            weights, static_cast<const __bf16*>(scales), static_cast<const __bf16*>(biases), kernel_count, c_in,
+            c_out, packed_words, groups, group_size, bits, static_cast<uint4*>(fragments));
+    }
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+extern "C" int lattice_hip_sparse_quantized_conv_features_sorted_fragments(
+    int dtype, const void* feats, int n_in, int c_in, const void* weight_fragments, int bits, int kernel_count,
+    int c_out, const int32_t* sorted_kv_out_in_map, const int32_t* tile_masks, const int32_t* reorder_rows,
+    int out_capacity, void* out, const void* bias, int epilogue, void* workspace, size_t workspace_bytes,
+    void* stream_ptr) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
+    LATTICE_REQUIRE(dtype == LATTICE_F16 || dtype == LATTICE_BF16,
+                    "the streamed matrix-core conv takes float16 or bfloat16 features.");
+    LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized convolution bits must be 4 or 8.");
+    LATTICE_REQUIRE(n_in >= 0 && out_capacity >= 0, "feats must have shape (N, C_in).");
+    if (!stream_shape_ok(n_in, c_in, c_out, kernel_count)) {
+        set_error("the streamed conv needs c_in % 32 == 0 (<= 256), c_out in {64, 128, 256}, K <= 32 and feats "
+                  "under 4 GiB.");
+        return LATTICE_ERROR_UNSUPPORTED;
+    }
+    LATTICE_REQUIRE(sorted_kv_out_in_map && tile_masks && out && weight_fragments && (feats || n_in == 0),
+                    "conv pointers must be non-null.");
+    int32_t* schedule = nullptr;
+    bool ready = false;
+    int rc = conv_schedule(workspace, workspace_bytes, out_capacity, &schedule, &ready);
+    if (rc != LATTICE_OK) return rc;
+    hipStream_t stream = as_stream(stream_ptr);
+    if (dtype == LATTICE_F16) {
+        auto* f = static_cast<const _Float16*>(feats);
+        auto* w = static_cast<const _Float16*>(weight_fragments);
+        auto* o = static_cast<_Float16*>(out);
+        const Epilogue<_Float16> epi = epilogue_of<_Float16>(bias, epilogue);
+        return bits == 4 ? launch_stream<_Float16, 4>(f, n_in, c_in, w, kernel_count, c_out, sorted_kv_out_in_map,
+                                                       tile_masks, reorder_rows, out_capacity, schedule, ready, o,
+                                                       epi, stream)
+                         : launch_stream<_Float16, 8>(f, n_in, c_in, w, kernel_count, c_out, sorted_kv_out_in_map,
+                                                       tile_masks, reorder_rows, out_capacity, schedule, ready, o,
+                                                       epi, stream);
+    }
+    auto* f = static_cast<const __bf16*>(feats);
+    auto* w = static_cast<const __bf16*>(weight_fragments);
+    auto* o = static_cast<__bf16*>(out);
+    const Epilogue<__bf16> epi = epilogue_of<__bf16>(bias, epilogue);
+    return bits == 4 ? launch_stream<__bf16, 4>(f, n_in, c_in, w, kernel_count, c_out, sorted_kv_out_in_map,
+                                                 tile_masks, reorder_rows, out_capacity, schedule, ready, o, epi,
+                                                 stream)
+                     : launch_stream<__bf16, 8>(f, n_in, c_in, w, kernel_count, c_out, sorted_kv_out_in_map,
+                                                 tile_masks, reorder_rows, out_capacity, schedule, ready, o, epi,
+                                                 stream);
 }
 
 // ------------------------------------------------- allocation-free entry --

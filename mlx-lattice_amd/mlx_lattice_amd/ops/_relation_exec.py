@@ -319,7 +319,9 @@ def sparse_quantized_conv_features_from_relation(
         relation.output_csr.row_offsets, kv, reorder, tiles,
         relation.n_out_capacity, relation.n_kernels, weight.in_channels,
         weight.out_channels, weight.storage_in_channels, weight.group_size,
-        weight.bits, bias=bias, tile_order=order, relu=relu)
+        weight.bits, bias=bias, tile_order=order, relu=relu,
+        weight_fragments=(_quantized_fragments(weight)
+                          if order is not None else None))
 
 
 def sparse_pool_features_from_relation(feats: torch.Tensor,
@@ -400,6 +402,24 @@ def _weight_fragments(weight5d: torch.Tensor) -> torch.Tensor:
     fp16/bf16 weight (``ext.conv_weight_fragments``; empty when the shape
     takes the other matrix-core kernel), cached with the weight."""
     return _cached_weight(weight5d, 'fragments', ext.conv_weight_fragments)
+
+
+def _quantized_fragments(weight: QuantizedWeight) -> torch.Tensor:
+    """The streamed matrix-core conv's fragment-ordered packed copy of a
+    quantized weight (``ext.quantized_weight_fragments``: codes, scale and
+    bias per 16-byte piece, dequantised in the kernel; empty when the shape
+    takes the other matrix-core kernel), cached with the packed words and
+    rebuilt when they, the scales or the biases change."""
+    kind = ('quantized fragments', id(weight.scales), weight.scales._version,
+            id(weight.biases), weight.biases._version)
+
+    def make(words):
+        return ext.quantized_weight_fragments(
+            words, weight.scales, weight.biases, weight.in_channels,
+            weight.out_channels, weight.storage_in_channels,
+            weight.group_size, weight.bits)
+
+    return _cached_weight(weight.weight, kind, make)
 
 
 def _matrix_core_weight(weight: torch.Tensor) -> torch.Tensor:

@@ -221,7 +221,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("out_capacity"), py::arg("n_kernels"),
           py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"), py::arg("group_size"),
           py::arg("bits"), py::kw_only(), py::arg("bias") = py::none(), py::arg("tile_order") = py::none(),
-          py::arg("relu") = false);
+          py::arg("relu") = false, py::arg("weight_fragments") = py::none());
+    m.def("quantized_weight_fragments", &ln::quantized_weight_fragments, py::arg("weights"), py::arg("scales"),
+          py::arg("biases"), py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"),
+          py::arg("group_size"), py::arg("bits"),
+          "Fragment-ordered packed copy of a quantized weight for the streamed matrix-core conv (empty when the "
+          "shape does not take it).");
     m.def("conv_tile_order", &ln::conv_tile_order, py::arg("tile_masks"), py::arg("out_capacity"),
           "Longest-first order of the sorted view's 128-row tiles, for the matrix-core conv's tile_order.");
 

@@ -305,6 +305,50 @@ at::Tensor conv_weight_fragments(const at::Tensor& weights_in) {
     return frag;
 }
 
+at::Tensor quantized_weight_fragments(const at::Tensor& weights_in, const at::Tensor& scales_in,
+                                      const at::Tensor& biases_in, int in_channels, int out_channels,
+                                      int storage_in_channels, int group_size, int bits) {
+    if (weights_in.dim() != 3 || weights_in.scalar_type() != at::kUInt32) {
+        throw std::invalid_argument("packed weights must be a three-dimensional uint32 array.");
+    }
+    if (scales_in.dim() != 3 || biases_in.sizes() != scales_in.sizes() ||
+        biases_in.scalar_type() != scales_in.scalar_type()) {
+        throw std::invalid_argument("quantized scales and biases must have equal shapes and dtypes.");
+    }
+    if (bits != 4 && bits != 8) throw std::invalid_argument("quantized convolution bits must be 4 or 8.");
+    if (group_size != 32 && group_size != 64 && group_size != 128) {
+        throw std::invalid_argument("quantized convolution group_size must be 32, 64, or 128.");
+    }
+    if (in_channels <= 0 || out_channels <= 0 || storage_in_channels < in_channels ||
+        storage_in_channels % group_size != 0) {
+        throw std::invalid_argument("quantized convolution channel metadata is invalid.");
+    }
+    const int k = static_cast<int>(weights_in.size(0));
+    if (weights_in.size(1) != static_cast<int64_t>(storage_in_channels) * bits / 32 ||
+        weights_in.size(2) != out_channels || scales_in.size(0) != k ||
+        scales_in.size(1) != storage_in_channels / group_size || scales_in.size(2) != out_channels) {
+        throw std::invalid_argument("packed weight shape does not match quantized convolution metadata.");
+    }
+    require_device(weights_in, "weights");
+    require_device(scales_in, "scales");
+    require_device(biases_in, "biases");
+    int dtype = -1;
+    if (scales_in.scalar_type() == at::kHalf) dtype = LATTICE_F16;
+    if (scales_in.scalar_type() == at::kBFloat16) dtype = LATTICE_BF16;
+    const size_t bytes =
+        dtype < 0 ? 0 : lattice_hip_quantized_weight_fragments_bytes(dtype, k, in_channels, out_channels);
+    at::Tensor frag = at::empty({static_cast<int64_t>(bytes / 2)}, scales_in.options());
+    if (bytes == 0) return frag;
+    const at::Tensor weights = weights_in.contiguous();
+    const at::Tensor scales = scales_in.contiguous();
+    const at::Tensor biases = biases_in.contiguous();
+    check_status(lattice_hip_quantized_weight_fragments(
+        dtype, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(), k,
+        in_channels, out_channels, storage_in_channels, group_size, bits, frag.data_ptr(), bytes,
+        current_stream(weights)));
+    return frag;
+}
+
 at::Tensor conv_tile_order(const at::Tensor& tile_masks, int out_capacity) {
     require_i32_vector(tile_masks, "tile_masks must have shape (ceil(N_out / 64) * 4,) and int32 dtype.");
     if (out_capacity < 0 || tile_masks.size(0) != ((out_capacity + 63) / 64) * 4) {
@@ -327,7 +371,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
                                           int out_capacity, int n_kernels, int in_channels, int out_channels,
                                           int storage_in_channels, int group_size, int bits,
                                           const std::optional<at::Tensor>& bias,
-                                          const std::optional<at::Tensor>& tile_order, bool relu) {
+                                          const std::optional<at::Tensor>& tile_order, bool relu,
+                                          const std::optional<at::Tensor>& weight_fragments) {
     if (out_capacity < 0 || n_kernels <= 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
     }
@@ -402,6 +447,31 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
     if (has_plan) ws = schedule_workspace(tile_order, out_capacity, feats, &ws_bytes);
     at::Tensor bias_keep;
     const void* b = bias_ptr(bias, feats, out_channels, &bias_keep);
+    const int dtype = dtype_code(feats, "quantized sparse convolution");
+    const size_t frag_bytes = dtype == LATTICE_F32 ? 0
+                                                   : lattice_hip_quantized_weight_fragments_bytes(
+                                                         dtype, n_kernels, in_channels, out_channels);
+    const bool small_table = (feats.size(0) + 1) * static_cast<int64_t>(in_channels) * 2 <= (int64_t{1} << 32);
+    if (has_plan && frag_bytes > 0 && small_table) {
+        // Streamed route: the packed weight in fragment order (the caller's
+        // cached copy, or made now), dequantised in registers.
+        at::Tensor frag;
+        if (weight_fragments.has_value() && weight_fragments->numel() > 0) {
+            frag = *weight_fragments;
+            if (!frag.is_contiguous() || static_cast<size_t>(frag.numel()) * frag.element_size() < frag_bytes) {
+                throw std::invalid_argument("weight_fragments must be the quantized_weight_fragments of this weight.");
+            }
+            require_device(frag, "weight_fragments");
+        } else {
+            frag = quantized_weight_fragments(weights, scales, biases, in_channels, out_channels,
+                                              storage_in_channels, group_size, bits);
+        }
+        check_status(lattice_hip_sparse_quantized_conv_features_sorted_fragments(
+            dtype, feats.data_ptr(), static_cast<int>(feats.size(0)), in_channels, frag.data_ptr(), bits, n_kernels,
+            out_channels, ci32(kv), ci32(tiles), ci32(order), out_capacity, out.data_ptr(), b,
+            relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, ws.data_ptr(), ws_bytes, current_stream(feats)));
+        return out;
+    }
     check_status(lattice_hip_sparse_quantized_conv_features(
         dtype_code(feats, "quantized sparse convolution"), feats.data_ptr(), static_cast<int>(feats.size(0)),
         in_channels, reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(),

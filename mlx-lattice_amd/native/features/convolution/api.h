@@ -56,7 +56,17 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           int storage_in_channels, int group_size, int bits,
                                           const std::optional<at::Tensor>& bias = std::nullopt,
                                           const std::optional<at::Tensor>& tile_order = std::nullopt,
-                                          bool relu = false);
+                                          bool relu = false,
+                                          const std::optional<at::Tensor>& weight_fragments = std::nullopt);
+
+// The fragment-ordered packed copy of a quantized weight that the streamed
+// matrix-core conv reads (lattice_hip_quantized_weight_fragments: codes,
+// scale and bias of each lane's 8 input channels in one 16-byte piece),
+// kept with the weight and passed back as `weight_fragments`; an empty
+// tensor when the shape does not take that route.
+at::Tensor quantized_weight_fragments(const at::Tensor& weights, const at::Tensor& scales,
+                                      const at::Tensor& biases, int in_channels, int out_channels,
+                                      int storage_in_channels, int group_size, int bits);
 
 // Longest-first order of the 128-row tiles of a sorted view
 // (lattice_hip_conv_tile_order), kept with the view and passed back as
