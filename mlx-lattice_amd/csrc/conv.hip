@@ -1552,35 +1552,43 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
-    // Each lane holds 4 consecutive output channels of one row per (rb,
-    // cb): 8-byte stores straight from registers to out[reorder_rows[row]].
-    // Rows with no edges store zeros (plus bias).
-    T* const obase = out + half * S::C_OUT + col0 + lg * 4;
+    // The finished tile goes through LDS (the A ring is free once every
+    // wave's copies have landed) so that it leaves as 16-byte stores of
+    // whole output rows to out[reorder_rows[row]].  Rows with no edges store
+    // zeros (plus bias).
+    constexpr int LDW = S::C_OUT + 8;  // halves per staged row: rows 16 bytes apart in the banks
+    static_assert(S::ROWS * LDW <= 3 * S::ABUF, "the staged tile fits the A ring");
+    __syncthreads();
+    T* const stage = lds;
     uint2 bias4[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
         bias4[cb] = epi.bias != nullptr
                         ? *reinterpret_cast<const uint2*>(epi.bias + half * S::C_OUT + col0 + cb * 16 + lg * 4)
                         : uint2{0u, 0u};
-    int orow[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        const int sr = min(row0 + wr * S::WROWS + rb * 16 + lr, rows - 1);
-        orow[rb] = reorder_rows != nullptr ? reorder_rows[sr] : sr;
-    }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const int sr = row0 + wr * S::WROWS + rb * 16 + lr;
+        const int r = wr * S::WROWS + rb * 16 + lr;
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
             const T* bq = reinterpret_cast<const T*>(&bias4[cb]);
             T v[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = epi.finish(acc[rb][cb][q], static_cast<float>(bq[q]));
-            if (sr < rows) {
-                *reinterpret_cast<uint2*>(obase + static_cast<long long>(orow[rb]) * out_ld + cb * 16) =
-                    *reinterpret_cast<const uint2*>(v);
-            }
+            *reinterpret_cast<uint2*>(stage + r * LDW + col0 + cb * 16 + lg * 4) = *reinterpret_cast<const uint2*>(v);
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = S::C_OUT / 8;  // 16-byte pieces per row
+    T* const ohalf = out + half * S::C_OUT;
+    for (int i = threadIdx.x; i < S::ROWS * CPR; i += S::THREADS) {
+        const int r = i / CPR;
+        const int piece = i % CPR;
+        const int sr = row0 + r;
+        if (sr < rows) {
+            const int orow = reorder_rows != nullptr ? reorder_rows[sr] : sr;
+            *reinterpret_cast<uint4*>(ohalf + static_cast<long long>(orow) * out_ld + piece * 8) =
+                *reinterpret_cast<const uint4*>(stage + r * LDW + piece * 8);
         }
     }
 }
