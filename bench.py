@@ -40,7 +40,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # (profiles/config3_kernel_traffic.md), valid for the kernel source whose
 # SHA-256 prefix is given: when csrc/conv.hip changes, the bench reports
 # traffic as null until the counters are measured again.
-CONV_TRAFFIC = {'bytes': 1.2040e9, 'conv_hip_sha256': 'ebaa45f1b4770227'}
+CONV_TRAFFIC = {'bytes': 1.2080e9, 'conv_hip_sha256': '8ac64cab3f820b55'}
 
 
 def parse_args():
