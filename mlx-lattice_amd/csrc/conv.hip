@@ -1170,12 +1170,25 @@ __device__ inline void static_for_range(F& f, int lo, int hi) {
 }
 
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+
+// Vector-memory ops a streamed stage j issues: the row indices of a trip
+// when stage j + li starts one (trips of nch stages), then its B loads and
+// A copies (nbd).  stream_wait_a: the ops issued after the copies of
+// stage p + 1 - la, which the wait at the end of stage p lets through.
+constexpr int stream_ops(int j, int li, int nch, int nbd) {
+    return (((j + li) % nch + nch) % nch == 0 ? 1 : 0) + nbd;
+}
+constexpr int stream_wait_a(int p, int la, int li, int nch, int nbd) {
+    int w = 0;
+    for (int j = p + 2 - la; j <= p; ++j) w += stream_ops(j, li, nch, nbd);
+    return w;
+}
 constexpr int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
 
 // Tile of the streamed kernel: C_OUT output channels per block (a column
 // half when C_out = 256), its 4 waves in WR row groups x 4 / WR column
 // groups of 32 columns.
-template <int C_OUT_, int WR_>
+template <int C_OUT_, int WR_, int LA_ = 2, int OCC_ = 3>
 struct StreamShape {
     static constexpr int C_OUT = C_OUT_;
     static constexpr int WAVES = 4;
@@ -1191,9 +1204,15 @@ struct StreamShape {
     static constexpr int ST = CHUNK / 32;     // 32-channel MFMA steps per stage
     static constexpr int GATHER = ROWS * (CHUNK / 8) / THREADS;  // row-line copies per thread and stage
     static constexpr int ABUF = ROWS * CHUNK;  // halves of one A buffer
-    static constexpr int OCC = 3;              // blocks per CU (3 x 48 KB of LDS)
+    static constexpr int OCC = OCC_;           // blocks per CU
+    // A copies lead by LA stages (a ring of LA + 1 buffers).  LA = 2 at
+    // three blocks per CU measured fastest: LA = 3 or 4 at two blocks per
+    // CU (a third more copies in flight per CU) ran config 3 at 0.200 /
+    // 0.204 against 0.188 ms, and C_out = 64 at LA = 1 with four blocks
+    // per CU at 0.055 against 0.053 ms.
+    static constexpr int LA = LA_;
     static constexpr int LB = 2;               // B loads lead by LB stages
-    static constexpr int LI = 3;               // row-index loads lead by LI stages
+    static constexpr int LI = LA_ + 1;         // row-index loads lead by LI stages
     static constexpr int READ_AHEAD = 2;       // 16-row fragment reads in flight
     static_assert(WCOLS == 32 && WROWS % 16 == 0 && GATHER == 4, "stream tile shape");
 };
@@ -1332,7 +1351,7 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
     constexpr int NB = CB * ST;  // B loads per stage
     constexpr int ND = G;        // LDS copies per stage
     constexpr int ABYTES = S::ABUF * static_cast<int>(sizeof(T));
-    __shared__ __align__(16) T lds[3 * S::ABUF];
+    __shared__ __align__(16) T lds[(S::LA + 1) * S::ABUF];
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1380,7 +1399,7 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
             wfrag, static_cast<unsigned>(static_cast<long long>(kernel_count) * c_in * c_out_total * sizeof(T)));
         const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<unsigned long long>(lds));
 
-        constexpr int LA = 2, LB = S::LB, LI = S::LI;
+        constexpr int LA = S::LA, LB = S::LB, LI = S::LI;
         static_assert(LI - LA == 1, "row indices arrive one stage before their copies");
         // Row indices are loaded once per trip (an offset's NCH stages share
         // them): one dword per lane, lane j < 32 holding copy row j of the
@@ -1471,14 +1490,17 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
             constexpr int NI = has_idx(p) ? 1 : 0;
             constexpr int NT = NI + NB + ND;
             constexpr int W_B = ND + ops(p - 1);  // B(s), before stage s issues (LB = 2)
-            constexpr int W_A = NT;                // A(s + 1), at the end of stage s (LA = 2)
+            // A(s + 1), at the end of stage s: the copies of stage s + 1 - LA
+            // came last in it, then every op of stages s + 2 - LA .. s
+            constexpr int W_A = stream_wait_a(p, LA, LI, NCH, NB + ND);
+            static_assert(W_A < 64, "waits fit the counter");
             static_assert(LB == 2, "W_B counts one stage between a B load and its use");
             V (&bcur)[CB][ST] = b[p % NBS];
             V (&bfill)[CB][ST] = b[(p + LB) % NBS];
             const int k = kr[p / NCH];
             const int k_i = kr[(p + LI) / NCH];
             const int k_b = kr[(p + LB) / NCH];
-            const int abuf_fill = buf == 0 ? 2 : buf - 1;  // (s + 2) % 3
+            const int abuf_fill = buf == 0 ? LA : buf - 1;  // (s + LA) % (LA + 1)
             if constexpr ((p + LA) % NCH == 0) {
                 int& ra = raw[((p + LA) / NCH) % NRS];
                 wait_vm_1<W_IDX>(ra);
@@ -1536,7 +1558,7 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
             // A(s + 1) has landed for this wave; the barrier makes it so for
             // every wave and frees buffer `buf` for the copy of A(s + 3).
             asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(W_A) : "memory");
-            buf = buf == 2 ? 0 : buf + 1;
+            buf = buf == LA ? 0 : buf + 1;
         };
         auto block = [&](int t0) {
             auto guarded = [&](auto P) {
@@ -1557,7 +1579,7 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
     // whole output rows to out[reorder_rows[row]].  Rows with no edges store
     // zeros (plus bias).
     constexpr int LDW = S::C_OUT + 8;  // halves per staged row: rows 16 bytes apart in the banks
-    static_assert(S::ROWS * LDW <= 3 * S::ABUF, "the staged tile fits the A ring");
+    static_assert(S::ROWS * LDW <= (S::LA + 1) * S::ABUF, "the staged tile fits the A ring");
     __syncthreads();
     T* const stage = lds;
     uint2 bias4[CB];
