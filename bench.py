@@ -40,7 +40,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # (profiles/config3_kernel_traffic.md), valid for the kernel source whose
 # SHA-256 prefix is given: when csrc/conv.hip changes, the bench reports
 # traffic as null until the counters are measured again.
-CONV_TRAFFIC = {'bytes': 1.2080e9, 'conv_hip_sha256': '8ac64cab3f820b55'}
+CONV_TRAFFIC = {'bytes': 1.2082e9, 'conv_hip_sha256': '4726573ea2b0a7f7'}
 
 
 def parse_args():
@@ -791,7 +791,7 @@ def main() -> int:
                                'profiles/config3_kernel_traffic.md'
                                if traffic is not None else
                                f'not measured for conv.hip {conv_sha}'),
-            'kernel': 'conv_igemm_stream<f16, StreamShape<128, 1>, 2>',
+            'kernel': 'conv_igemm_stream<f16, StreamShape<128, 1>, 2, 0>',
         },
     }
     if args.phase == 'config3':
