@@ -364,6 +364,68 @@ def test_quantized_csr_route_matches_oracle(bits):
     del rng
 
 
+@pytest.mark.parametrize('dtype,bits,c_in,c_out', [
+    (torch.float16, 4, 64, 128),
+    (torch.float16, 8, 128, 128),
+    (torch.float16, 8, 256, 64),     # four 64-channel chunks per offset
+    (torch.float16, 4, 96, 64),      # a 32-channel last chunk
+    (torch.bfloat16, 4, 64, 64),
+    (torch.bfloat16, 8, 128, 256),   # two column halves
+])
+def test_quantized_streamed_route(dtype, bits, c_in, c_out):
+    """The quantized conv on the streamed matrix-core kernel (packed
+    fragments dequantised in registers) against the fp64 sum over the
+    dequantised weight, fp16/bf16 features, int4/int8, and through the C ABI
+    entry of the route itself (no silent fallback)."""
+    import ctypes
+
+    from mlx_lattice_amd import dequantize_weight, quantize_weight
+    from mlx_lattice_amd._native import ext
+
+    coords, rng = _shell(20000, 128, 61 + bits + c_in + c_out)
+    n = len(coords)
+    feats = rng.standard_normal((n, c_in)).astype(np.float32)
+    w = torch.as_tensor((rng.standard_normal((c_out, 3, 3, 3, c_in))
+                         * np.sqrt(2.0 / (27 * c_in))).astype(np.float32)).to(DEV, dtype)
+    q = quantize_weight(w, group_size=32, bits=bits)
+    f = torch.as_tensor(feats).to(DEV, dtype)
+    print(f'quantized streamed {dtype} int{bits} {c_in}->{c_out}', flush=True)
+    c = torch.as_tensor(coords, dtype=torch.int32).to(DEV)
+    active = torch.tensor([n], dtype=torch.int32, device=DEV)
+    rel = ext.build_submanifold_kernel_relation_with_view(c, active, [3, 3, 3],
+                                                          [1, 1, 1])
+    reorder, _, kv, tiles = ext.build_sorted_implicit_gemm_view(rel[10], rel[11])
+    frag = ext.quantized_weight_fragments(q.weight, q.scales, q.biases, q.in_channels,
+                                          q.out_channels, q.storage_in_channels,
+                                          q.group_size, q.bits)
+    assert frag.numel() > 0
+    lib = ctypes.CDLL(str(ROOT_LIB))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    lib.lattice_hip_conv_workspace_bytes.restype = ctypes.c_size_t
+    entry = lib.lattice_hip_sparse_quantized_conv_features_sorted_fragments
+    entry.argtypes = [I, P, I, I, P, I, I, I, P, P, P, I, P, P, I, P, ctypes.c_size_t, P]
+    lib.lattice_hip_last_error.restype = ctypes.c_char_p
+    wsb = lib.lattice_hip_conv_workspace_bytes(n)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    out = torch.empty((n, c_out), dtype=dtype, device=DEV)
+    code = 1 if dtype == torch.float16 else 2
+    rc = entry(code, f.data_ptr(), n, c_in, frag.data_ptr(), bits, 27, c_out,
+               kv.data_ptr(), tiles.data_ptr(), reorder.data_ptr(), n, out.data_ptr(),
+               None, 0, ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.lattice_hip_last_error()
+    torch.cuda.synchronize()
+    fin = to_np(f.float())
+    _, ref = _reference(coords, fin, to_np(dequantize_weight(q).float()),
+                        dict(kernel_size=3))
+    tol = (RTOL_F16, ATOL_F16) if dtype == torch.float16 else (2e-2, 3e-2)
+    _close(to_np(out.float()), ref, *tol, f'streamed int{bits} {dtype} {c_in}->{c_out}')
+    # the operator path takes the same route
+    x = _tensor(coords, feats).astype(dtype)
+    ops, _ = _imports()
+    ops_out = ops.subm_conv3d(x, q, kernel_size=3)
+    _close(to_np(ops_out.feats.float()), ref, *tol, 'operator path')
+
+
 def test_config4_int4_fused_200k():
     from mlx_lattice_amd import dequantize_weight, quantize_weight
     from mlx_lattice_amd.synthetic import config_rng, kaiming_weight, sphere_shell_cloud
