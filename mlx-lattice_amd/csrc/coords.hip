@@ -113,7 +113,9 @@ clear_blocks(BlockBucket* buckets, long long quarters, Prologue p) {
 }
 
 // Inserts the active rows into the block table.  Every int32 coordinate
-// has a key: packed when it fits, wide otherwise.
+// has a key: packed when it fits, wide otherwise.  kExact = false stores
+// the rows plainly (see BlockTable::insert).
+template <bool kExact>
 __global__ void __launch_bounds__(kThreads)
 insert_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
               const int32_t* __restrict__ active_rows) {
@@ -123,7 +125,7 @@ insert_blocks(BlockTable table, const int32_t* __restrict__ coords, int rows,
         TableKey block_key;
         int octant;
         block_of(c.x, c.y, c.z, c.w, &block_key, &octant);
-        table.insert(block_key, octant, i);
+        table.insert<kExact>(block_key, octant, i);
     }
 }
 
@@ -355,6 +357,14 @@ struct QueryArgs {
     // offset) finds an earlier row with the same coordinate; else null.
     int32_t* repeat_status;
     int center;
+    // 3x3x3 submanifold over a table whose voxel slots were stored plainly:
+    // an active row whose self lookup finds a larger row (a repeated
+    // coordinate whose store came last) puts its own row back with an
+    // atomic max, and the repeat flag makes the query run again
+    // (rerun_if: the status word; the launch returns at once when its
+    // LATTICE_STATUS_REPEATED_COORD bit is clear).
+    bool fix_rows;
+    const int32_t* rerun_if;
 };
 
 // Flags a repeated coordinate seen by any lane of the wave (one atomic).
@@ -531,6 +541,7 @@ __device__ inline int query_rows_k3(const QueryArgs& a, long long row0, int lane
             }
     uint32_t mask = 0;
     int degree = 0;
+    uint32_t self_raw = 0;
 #pragma unroll
     for (int dx = 0; dx < 3; ++dx)
 #pragma unroll
@@ -541,6 +552,7 @@ __device__ inline int query_rows_k3(const QueryArgs& a, long long row0, int lane
                 const uint32_t y1 = py ? wx[dx][dy][dz + 1] : wx[dx][dy + 1][dz + 1];
                 const uint32_t raw = pz ? y0 : y1;
                 const int k = dx * 9 + dy * 3 + dz;
+                if (k == kK3 / 2) self_raw = raw;
                 const int32_t v = raw == 0 ? -1 : kRowBias - static_cast<int32_t>(raw);
                 stage[lane * K + k] = v;
                 if (raw != 0) {
@@ -548,6 +560,15 @@ __device__ inline int query_rows_k3(const QueryArgs& a, long long row0, int lane
                     ++degree;
                 }
             }
+    if (a.fix_rows && active && self_raw != 0 && kRowBias - static_cast<int32_t>(self_raw) > row) {
+        // the own voxel sits in window block (1 - x&1, 1 - y&1, 1 - z&1), octant (x&1, y&1, z&1)
+        const int j_own = (px ? 0 : 4) + (py ? 0 : 2) + (pz ? 0 : 1);
+        uint32_t own_slot = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) own_slot = j == j_own ? slot[j] : own_slot;
+        atomicMax(&a.table.buckets[own_slot].rows[(px ? 4 : 0) + (py ? 2 : 0) + (pz ? 1 : 0)],
+                  kRowBias - static_cast<int32_t>(row));
+    }
     if (row_ok) a.row_masks[row] = static_cast<int32_t>(mask);
     return row_ok ? degree : 0;
 }
@@ -560,23 +581,30 @@ __device__ inline void store_map_rows_k3(const QueryArgs& a, long long row0, int
 }
 
 __global__ void __launch_bounds__(kWave) query_map_k3(QueryArgs a) {
+    if (a.rerun_if != nullptr && (*a.rerun_if & LATTICE_STATUS_REPEATED_COORD) == 0) return;
     __shared__ int32_t stage[kQueryRows * kK3];
     const int lane = lane_id();
-    const long long row0 = static_cast<long long>(blockIdx.x) * kQueryRows;
-    const int degree = query_rows_k3(a, row0, lane, stage);
-    if (a.degrees != nullptr && row0 + lane < a.out_capacity) a.degrees[row0 + lane] = degree;
-    __syncthreads();
-    if (a.repeat_status != nullptr) {
-        const long long r = row0 + lane;
-        const int n_active = min(max(*a.out_active, 0), a.out_capacity);
-        flag_repeats(a.repeat_status, r < n_active && stage[lane * kK3 + kK3 / 2] != r);
-    }
-    store_map_rows_k3(a, row0, lane, stage);
-    if (a.block_totals != nullptr) {
-        int sum = degree;
+    const long long chunks = (static_cast<long long>(a.out_capacity) + kQueryRows - 1) / kQueryRows;
+    // one 64-row chunk per block, or several when the grid is capped (the
+    // conditional second pass)
+    for (long long chunk = blockIdx.x; chunk < chunks; chunk += gridDim.x) {
+        const long long row0 = chunk * kQueryRows;
+        const int degree = query_rows_k3(a, row0, lane, stage);
+        if (a.degrees != nullptr && row0 + lane < a.out_capacity) a.degrees[row0 + lane] = degree;
+        __syncthreads();
+        if (a.repeat_status != nullptr) {
+            const long long r = row0 + lane;
+            const int n_active = min(max(*a.out_active, 0), a.out_capacity);
+            flag_repeats(a.repeat_status, r < n_active && stage[lane * kK3 + kK3 / 2] != r);
+        }
+        store_map_rows_k3(a, row0, lane, stage);
+        if (a.block_totals != nullptr) {
+            int sum = degree;
 #pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-        if (lane == 0) a.block_totals[blockIdx.x] = sum;
+            for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+            if (lane == 0) a.block_totals[chunk] = sum;
+        }
+        __syncthreads();
     }
 }
 
@@ -820,7 +848,7 @@ size_t block_table_bytes(int rows) {
 // (an earlier relation build over them): only the prologue runs.
 int build_block_table(const int32_t* coords, int rows, const int32_t* active_rows,
                       const Prologue& prologue, Workspace& ws, hipStream_t stream, BlockTable* table,
-                      bool ready = false) {
+                      bool ready = false, bool exact_rows = true) {
     const int cap = block_capacity(rows);
     table->buckets = ws.take<BlockBucket>(cap);
     table->mask = static_cast<uint32_t>(cap - 1);
@@ -835,7 +863,13 @@ int build_block_table(const int32_t* coords, int rows, const int32_t* active_row
                    stream>>>(table->buckets, quarters, prologue);
     LATTICE_LAUNCH_CHECK();
     if (rows > 0 && !ready) {
-        insert_blocks<<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows, active_rows);
+        if (exact_rows) {
+            insert_blocks<true><<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows,
+                                                                                      active_rows);
+        } else {
+            insert_blocks<false><<<grid_for(rows, kThreads, 4096), kThreads, 0, stream>>>(*table, coords, rows,
+                                                                                       active_rows);
+        }
         LATTICE_LAUNCH_CHECK();
     }
     return LATTICE_OK;
@@ -958,6 +992,15 @@ int finish_relation(QueryArgs q, int in_capacity, const lattice_relation_outputs
         q.block_totals = totals;
         int rc = launch_query(q, stream);
         if (rc != LATTICE_OK) return rc;
+        if (q.fix_rows) {
+            // the same query again once a repeated coordinate has restored its
+            // first row; a capped grid that returns at once otherwise
+            QueryArgs again = q;
+            again.fix_rows = false;
+            again.rerun_if = q.repeat_status;
+            query_map_k3<<<static_cast<unsigned>(std::min(blocks, 1024)), kWave, 0, stream>>>(again);
+            LATTICE_LAUNCH_CHECK();
+        }
         scan_block_totals<<<1, kBlockScanThreads, 0, stream>>>(totals, blocks, offsets, out->counts);
         LATTICE_LAUNCH_CHECK();
         rc = launch_emit(q.out_in_map, out_capacity, K, offsets, out, stream);
@@ -1089,8 +1132,12 @@ extern "C" int lattice_hip_build_kernel_relation_with_table(
         prologue.copy_rows = rows;
         prologue.copy_dst = out->out_coords;
     }
+    // The 3x3x3 submanifold query restores first rows itself, so its table
+    // takes plain stores (one device atomic per row instead of two).
+    const bool unit_k3_subm = identity && kernel_size[0] == 3 && kernel_size[1] == 3 && kernel_size[2] == 3 &&
+                              dilation[0] == 1 && dilation[1] == 1 && dilation[2] == 1;
     BlockTable table;
-    rc = build_block_table(coords, rows, active_rows, prologue, tws, stream, &table, table_ready);
+    rc = build_block_table(coords, rows, active_rows, prologue, tws, stream, &table, table_ready, !unit_k3_subm);
     if (rc != LATTICE_OK) return rc;
 
     QueryArgs q{};
@@ -1111,6 +1158,7 @@ extern "C" int lattice_hip_build_kernel_relation_with_table(
         const int cz = kernel_size[2] % 2 ? kernel_size[2] / 2 : 0;
         q.repeat_status = out->status;
         q.center = (cx * kernel_size[1] + cy) * kernel_size[2] + cz;
+        q.fix_rows = unit_k3_subm && !table_ready;
     } else if (kernel_size[0] == 2 && kernel_size[1] == 2 && kernel_size[2] == 2 && stride[0] == 2 &&
                stride[1] == 2 && stride[2] == 2 && padding[0] == 0 && padding[1] == 0 && padding[2] == 0 &&
                dilation[0] == 1 && dilation[1] == 1 && dilation[2] == 1) {

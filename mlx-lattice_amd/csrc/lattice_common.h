@@ -324,6 +324,12 @@ struct BlockTable {
     BlockSource src;  // the input coordinates the table was built from
     int32_t* status = nullptr;  // overflow flag word, or null
 
+    // kExact: the voxel's slot keeps the smallest row (an atomic max on the
+    // biased row).  Otherwise a plain store: the slot then holds one of the
+    // rows with the voxel's coordinate (the smallest unless a coordinate
+    // repeats), and the caller restores the smallest afterwards
+    // (query_rows_k3 does so from each row's self lookup).
+    template <bool kExact = true>
     __device__ inline void insert(const TableKey& block_key, int octant, int32_t row) const {
         uint32_t slot = static_cast<uint32_t>(block_key.hash) & mask;
         const unsigned long long mine =
@@ -336,7 +342,11 @@ struct BlockTable {
                              (block_key.wide ? same_tag(k, block_key) && src.key_of(claim_row(k)) == block_key.full
                                              : k == block_key.word);
             if (hit) {
-                atomicMax(&buckets[slot].rows[octant], kRowBias - row);
+                if constexpr (kExact) {
+                    atomicMax(&buckets[slot].rows[octant], kRowBias - row);
+                } else {
+                    buckets[slot].rows[octant] = kRowBias - row;
+                }
                 return;
             }
             slot = (slot + 1) & mask;
