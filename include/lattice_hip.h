@@ -424,9 +424,13 @@ int lattice_hip_sparse_conv_features_sorted_fragments(
  * 128 KiB per GPU (kept until the process ends), so the call allocates
  * nothing and takes no workspace.  out_capacity must not exceed
  * LATTICE_NOALLOC_CONV_MAX_ROWS (LATTICE_ERROR_INVALID_ARGUMENT otherwise).
- * The calling thread's current device must be the stream's.  Calls that
- * overlap on one GPU share the array and race; serialise them (one stream,
- * or events).  Results are bit-identical to the entry above. */
+ * The calling thread's current device must be the stream's.  Calls on one
+ * GPU share the array: outside graph capture each call's stream waits for
+ * the previous call's launches (an event the library records, whatever the
+ * stream), so calls on different streams run one after another; launches
+ * captured into a graph are not ordered, and replays that overlap another
+ * use of the array on that GPU race.  Results are bit-identical to the
+ * entry above. */
 #define LATTICE_NOALLOC_CONV_MAX_ROWS 2097088
 int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     int dtype, const void* feats, int n_in, int c_in, const void* weights,

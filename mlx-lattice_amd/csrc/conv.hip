@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -2293,8 +2294,16 @@ extern "C" int lattice_hip_sparse_quantized_conv_features_sorted_fragments(
 // address on each device is taken once, with the device current, through
 // hipGetSymbolAddress; in host code the array's own name is only a
 // host-side stand-in and is never passed to a kernel.  schedule_tiles
-// writes every entry a launch reads, so nothing needs clearing.  Calls that
-// overlap on one GPU share the array and race.
+// writes every entry a launch reads, so nothing needs clearing.
+//
+// Calls on one GPU share the array.  Outside graph capture they are put in
+// submission order: each call's stream first waits for the event recorded
+// after the previous call on that device (whatever its stream), and records
+// it again after its own launches, under a per-device host mutex; the event
+// is created once per device at the first call.  A call made while its
+// stream is being captured neither waits nor records (an event recorded
+// outside the capture cannot be waited on inside it), so replays of a
+// captured graph that overlap another caller's use of the device race.
 
 namespace lattice {
 namespace {
@@ -2304,9 +2313,17 @@ static __device__ __align__(256) int32_t scratch[kMaxScheduledTiles];
 constexpr int kMaxScratchDevices = 64;
 std::atomic<int32_t*> g_scratch_ptr[kMaxScratchDevices];
 
+// Per-device order of the calls that use the scratch.
+struct ScratchOrder {
+    std::mutex lock;
+    hipEvent_t last_use = nullptr;  // recorded after the latest call's launches
+    bool recorded = false;
+};
+ScratchOrder g_scratch_order[kMaxScratchDevices];
+
 // The scratch of the current device, which must be the stream's device
 // (hipGetSymbolAddress answers for the current device).
-int scratch_on_current_device(hipStream_t stream, int32_t** ptr) {
+int scratch_on_current_device(hipStream_t stream, int32_t** ptr, int* device_out) {
     int device = 0;
     LATTICE_HIP_TRY(hipGetDevice(&device));
     if (stream != nullptr) {
@@ -2322,6 +2339,7 @@ int scratch_on_current_device(hipStream_t stream, int32_t** ptr) {
         g_scratch_ptr[device].store(p, std::memory_order_release);
     }
     *ptr = p;
+    *device_out = device;
     return LATTICE_OK;
 }
 
@@ -2339,11 +2357,28 @@ extern "C" int lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
     static_assert(static_cast<size_t>(LATTICE_NOALLOC_CONV_MAX_ROWS) / 64 + 1 <= kMaxScheduledTiles,
                   "the scratch holds the schedule of the largest allowed launch");
     int32_t* schedule = nullptr;
-    const int rc = scratch_on_current_device(as_stream(stream_ptr), &schedule);
+    int device = 0;
+    const hipStream_t stream = as_stream(stream_ptr);
+    int rc = scratch_on_current_device(stream, &schedule, &device);
     if (rc != LATTICE_OK) return rc;
-    return lattice_hip_sparse_conv_features_sorted_implicit_gemm(
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    LATTICE_HIP_TRY(hipStreamIsCapturing(stream, &capture));
+    const bool ordered = capture == hipStreamCaptureStatusNone;
+    ScratchOrder& order = g_scratch_order[device];
+    std::lock_guard<std::mutex> guard(order.lock);
+    if (ordered) {
+        if (order.last_use == nullptr)
+            LATTICE_HIP_TRY(hipEventCreateWithFlags(&order.last_use, hipEventDisableTiming));
+        if (order.recorded) LATTICE_HIP_TRY(hipStreamWaitEvent(stream, order.last_use, 0));
+    }
+    rc = lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         dtype, feats, n_in, c_in, weights, weight_layout, kernel_count, c_out, sorted_kv_out_in_map, tile_masks,
         reorder_rows, out_capacity, out, bias, epilogue, schedule, sizeof(scratch), stream_ptr);
+    if (rc == LATTICE_OK && ordered) {
+        LATTICE_HIP_TRY(hipEventRecord(order.last_use, stream));
+        order.recorded = true;
+    }
+    return rc;
 }
 
 extern "C" int lattice_hip_sparse_quantized_conv_features(

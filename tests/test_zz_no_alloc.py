@@ -5,7 +5,8 @@ through the C ABI, against the entry point it mirrors
 workspace).  Both run the same kernels; only where the tile schedule lives
 differs, so the outputs must agree bit for bit.  Two calls in a row, the
 second on a smaller cloud (the scratch keeps the first call's schedule and
-must not leak into the second)."""
+must not leak into the second).  Calls on two streams of one GPU share
+the scratch and are put in submission order by the entry point."""
 
 from __future__ import annotations
 
@@ -36,7 +37,9 @@ def _lib():
     return lib
 
 
-def _case(lib, n, grid, seed, c_in, c_out, epilogue=0):
+def _prepare(lib, n, grid, seed, c_in, c_out, epilogue=0):
+    """A cloud, its sorted view and the workspace entry's output `ref`;
+    returns (args, ref, got, bias, epilogue, keep) for the no-alloc call."""
     from mlx_lattice_amd._native import ext
     from mlx_lattice_amd.synthetic import sphere_shell_cloud
 
@@ -64,12 +67,28 @@ def _case(lib, n, grid, seed, c_in, c_out, epilogue=0):
     assert lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm(
         *args, ref.data_ptr(), bias.data_ptr(), epilogue, ws.data_ptr(), wsb,
         stream) == 0
+    torch.cuda.synchronize()
+    return args, ref, got, bias, epilogue, (c, active, rel, kv, tiles, reorder, feats, w, ws)
+
+
+def _noalloc(lib, prepared, stream):
+    args, _, got, bias, epilogue, _ = prepared
     rc = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
         *args, got.data_ptr(), bias.data_ptr(), epilogue, stream)
     assert rc == 0, lib.lattice_hip_last_error()
-    torch.cuda.synchronize()
+
+
+def _check(prepared):
+    _, ref, got, _, _, _ = prepared
     assert not torch.isnan(got).any()
     assert torch.equal(got, ref)
+
+
+def _case(lib, n, grid, seed, c_in, c_out, epilogue=0):
+    prepared = _prepare(lib, n, grid, seed, c_in, c_out, epilogue)
+    _noalloc(lib, prepared, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    _check(prepared)
 
 
 def test_noalloc_conv_matches_workspace_entry():
@@ -78,6 +97,24 @@ def test_noalloc_conv_matches_workspace_entry():
     _case(lib, 9000, 96, 6, 32, 64)        # second call, smaller
     _case(lib, 20000, 128, 7, 64, 256)     # two launches share one schedule
     _case(lib, 12000, 128, 8, 64, 128, 1)  # with the fused ReLU
+
+
+def test_noalloc_conv_orders_calls_on_two_streams():
+    # A large call on one stream and, queued right behind it with no
+    # synchronisation between the streams, a smaller one on another: the
+    # second call's schedule would overwrite the first's in the shared
+    # scratch while the first conv still reads it, unless the entry point
+    # orders them.
+    lib = _lib()
+    big = _prepare(lib, 300000, 400, 9, 128, 128)
+    small = _prepare(lib, 9000, 128, 10, 32, 64)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    print('no-alloc conv on two streams', flush=True)
+    _noalloc(lib, big, s1.cuda_stream)
+    _noalloc(lib, small, s2.cuda_stream)
+    torch.cuda.synchronize()
+    _check(big)
+    _check(small)
 
 
 def test_noalloc_conv_rejects_oversized_launches():
