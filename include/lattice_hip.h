@@ -360,6 +360,33 @@ int lattice_hip_sparse_conv_features(
     const int32_t* row_offsets, int out_capacity, void* out, const void* bias,
     int epilogue, void* stream);
 
+/* The same sum (cpu/algorithms.cpp:180-302; quantized weights as in
+ * cpu/quantized.cpp:64-141) for few input channels, over the relation's
+ * dense map out_in_map[row * K + k] (input row or -1; the implicit-GEMM
+ * view of relation_views_detail.h:122-169) instead of the CSR: a row's K
+ * offsets x c_in channels form one contraction on the matrix cores (fp32
+ * accumulate; the sum's order differs from the CSR route's, its value
+ * does not beyond fp32 rounding).  float16/bfloat16 features with c_in 4
+ * or 8 and rows aligned to their size, c_out 16 or 32, K * c_in <= 256
+ * (lattice_hip_conv_dense_map_supported); rows >= counts[1] hold the bias
+ * alone; bias and epilogue as above.  The quantized entry takes the packed
+ * weights, scales and biases of lattice_hip_sparse_quantized_conv_features
+ * and dequantises them once per block (w = q * scale + bias,
+ * rounded once to the feature dtype). */
+int lattice_hip_conv_dense_map_supported(int dtype, int c_in, int c_out,
+                                         int kernel_count);
+int lattice_hip_sparse_conv_features_dense_map(
+    int dtype, const void* feats, int n_in, int c_in, const void* weights,
+    int weight_layout, int kernel_count, int c_out, const int32_t* out_in_map,
+    const int32_t* counts, int out_capacity, void* out, const void* bias,
+    int epilogue, void* stream);
+int lattice_hip_sparse_quantized_conv_features_dense_map(
+    int dtype, const void* feats, int n_in, int c_in, const uint32_t* weights,
+    const void* scales, const void* biases, int kernel_count, int c_out,
+    int storage_c_in, int group_size, int bits, const int32_t* out_in_map,
+    const int32_t* counts, int out_capacity, void* out, const void* bias,
+    int epilogue, void* stream);
+
 /* Implicit-GEMM conv over the sorted view (the reference's sorted plan):
  * row i of the mask-sorted order gathers feats[sorted_kv_out_in_map[k, i]]
  * (-1 = no contribution) for every kernel offset k and writes its result to

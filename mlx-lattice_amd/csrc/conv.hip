@@ -1616,6 +1616,135 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
     }
 }
 
+// ------------------------------------------------- dense-map small C_in --
+//
+// Convolutions with few input channels (C_in 4 or 8: the stem of an
+// encoder) over the relation's dense map out_in_map[row][k]: a row's
+// neighbourhood, K offsets x C_in channels, is one contraction of K * C_in
+// values (padded to a multiple of 32) against the weight flattened the same
+// way, so the whole conv is a GEMM whose A rows are gathered from the map.
+// A wave takes 16 rows at a time: lane (lr, lg) gathers, for each 32-wide
+// step j, the flat positions j * 32 + lg * 8 .. + 7 of row lr (8 / C_in
+// offsets of C_in channels, one 8- or 16-byte row load each); the weight's
+// B fragments for every step (CO / 16 column blocks) are built once per
+// block in LDS and held in registers (quantized weights dequantised there:
+// w = q * scale + bias in fp32, rounded once to T).  A wave walks 16-row
+// blocks grid-stride, loading the next block's map entries while the
+// current one computes.  The MFMAs accumulate in fp32; the
+// store applies the bias and ReLU as the other routes do.  Map entries of
+// -1 or out of range, and rows at or past the relation's active output
+// count, contribute nothing (rows past it store the bias alone).
+template <typename T, int CI, int CO, bool QUANT, int KS_MAX>
+__global__ void __launch_bounds__(256)
+conv_dense_map(const T* __restrict__ feats, int n_in, const T* __restrict__ fweights, WeightIndex widx,
+               const uint32_t* __restrict__ qweights, const T* __restrict__ scales, const T* __restrict__ qbiases,
+               QuantIndex q, int K, const int32_t* __restrict__ out_in_map, const int32_t* __restrict__ counts,
+               int out_capacity, T* __restrict__ out, Epilogue<T> epi) {
+    using V = typename MfmaOps<T>::vec;
+    constexpr int CB = CO / 16;
+    // KS_MAX: bound on the 32-wide steps (K * CI <= 32 * KS_MAX)
+    constexpr int OPL = 8 / CI;  // offsets per lane and step
+    constexpr int NFRAG = KS_MAX * CB;
+    static_assert(CI == 4 || CI == 8, "8- or 16-byte feature rows");
+    __shared__ __align__(16) T wlds[NFRAG * 64 * 8];
+    const int KS = (K * CI + 31) / 32;
+    const int lane = lane_id();
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    // B fragments, built once per block into LDS: fragment (j, cb), lane
+    // (lr, lg) holds W[co = cb*16 + lr] at flat positions j*32 + lg*8 .. + 7
+    // (flat = k * CI + ci; zero past K), in the order of the MFMA operand.
+    for (int slot = threadIdx.x; slot < NFRAG * 64; slot += blockDim.x) {
+        const int f = slot / 64, l = slot % 64;
+        const int j = f / CB, cb = f % CB;
+        const int co = cb * 16 + (l & 15);
+        V v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int flat = j * 32 + (l >> 4) * 8 + e;
+            const int k = flat / CI;
+            const int ci = flat % CI;
+            float w = 0.0f;
+            if (k < K) {
+                w = QUANT ? dequant(qweights, scales, qbiases, q, k, ci, co) : Elem<T>::load(fweights, widx(k, ci, co));
+            }
+            v[e] = static_cast<T>(w);
+        }
+        *reinterpret_cast<V*>(wlds + slot * 8) = v;
+    }
+    __syncthreads();
+    V bfrag[KS_MAX][CB];
+#pragma unroll
+    for (int j = 0; j < KS_MAX; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) bfrag[j][cb] = *reinterpret_cast<const V*>(wlds + ((j * CB + cb) * 64 + lane) * 8);
+
+    const int n_out = min(max(counts[1], 0), out_capacity);
+    const int waves = static_cast<int>(gridDim.x) * (blockDim.x / kWave);
+    const int wave_id = static_cast<int>(blockIdx.x) * (blockDim.x / kWave) + static_cast<int>(threadIdx.x) / kWave;
+    const int blocks16 = (out_capacity + 15) / 16;
+    // map entries of 16-row block b16 for this lane (-1 = none)
+    auto load_map = [&](int b16, int (&m)[KS_MAX][OPL]) {
+        const int row = b16 * 16 + lr;
+        const bool active = row < n_out;
+#pragma unroll
+        for (int j = 0; j < KS_MAX; ++j)
+#pragma unroll
+            for (int t = 0; t < OPL; ++t) {
+                const int k = (j * 32 + lg * 8) / CI + t;
+                m[j][t] = active && j < KS && k < K ? out_in_map[static_cast<long long>(row) * K + k] : -1;
+            }
+    };
+    int mnext[KS_MAX][OPL];
+    if (wave_id < blocks16) load_map(wave_id, mnext);
+    for (int b16 = wave_id; b16 < blocks16; b16 += waves) {
+        const int row = b16 * 16 + lr;
+        int m[KS_MAX][OPL];
+#pragma unroll
+        for (int j = 0; j < KS_MAX; ++j)
+#pragma unroll
+            for (int t = 0; t < OPL; ++t) m[j][t] = mnext[j][t] >= 0 && mnext[j][t] < n_in ? mnext[j][t] : -1;
+        V a[KS_MAX];
+#pragma unroll
+        for (int j = 0; j < KS_MAX; ++j) {
+            if constexpr (CI == 4) {
+                uint2 w2[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    w2[t] = m[j][t] >= 0 ? *reinterpret_cast<const uint2*>(feats + static_cast<long long>(m[j][t]) * 4)
+                                         : uint2{0u, 0u};
+                a[j] = __builtin_bit_cast(V, uint4{w2[0].x, w2[0].y, w2[1].x, w2[1].y});
+            } else {
+                a[j] = m[j][0] >= 0 ? *reinterpret_cast<const V*>(feats + static_cast<long long>(m[j][0]) * 8)
+                                    : __builtin_bit_cast(V, uint4{0u, 0u, 0u, 0u});
+            }
+        }
+        // the next block's map entries load while this block computes
+        if (b16 + waves < blocks16) load_map(b16 + waves, mnext);
+        float4_t acc[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KS_MAX; ++j) {
+            if (j < KS) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[cb] = MfmaOps<T>::mfma(bfrag[j][cb], a[j], acc[cb]);
+            }
+        }
+        // lane (lr, lg): row lr, columns cb*16 + lg*4 .. + 3
+        if (row < out_capacity) {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                T v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = epi.apply(acc[cb][i], cb * 16 + lg * 4 + i);
+                *reinterpret_cast<uint2*>(out + static_cast<long long>(row) * CO + cb * 16 + lg * 4) =
+                    *reinterpret_cast<const uint2*>(v);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------- direct expansion ----
 //
 // Conv over a direct generative / transposed relation (output row
@@ -2490,4 +2619,118 @@ extern "C" int lattice_hip_sparse_conv_features_expand(int dtype, const void* fe
     return launch_expand<__bf16>(static_cast<const __bf16*>(feats), n_in, active_rows, c_in,
                                  static_cast<const __bf16*>(weights), kernel_count, c_out,
                                  static_cast<__bf16*>(out), epilogue_of<__bf16>(bias, epilogue), stream);
+}
+
+// ------------------------------------------------- dense-map small C_in --
+
+namespace lattice {
+namespace {
+
+bool dense_map_shape_ok(int dtype, int c_in, int c_out, int kernel_count) {
+    return (dtype == LATTICE_F16 || dtype == LATTICE_BF16) && (c_in == 4 || c_in == 8) &&
+           (c_out == 16 || c_out == 32) && kernel_count > 0 && kernel_count * c_in <= 256;
+}
+
+template <typename T, bool QUANT>
+int launch_dense_map(const void* feats, int n_in, int c_in, const void* fweights, WeightIndex widx,
+                     const uint32_t* qweights, const void* scales, const void* qbiases, QuantIndex q, int K,
+                     const int32_t* out_in_map, const int32_t* counts, int out_capacity, void* out,
+                     const void* bias, int epilogue, hipStream_t stream) {
+    const long long waves = (static_cast<long long>(out_capacity) + 15) / 16;
+    const unsigned grid = static_cast<unsigned>(std::max<long long>(1, std::min<long long>((waves + 3) / 4, 2048)));
+    const T* f = static_cast<const T*>(feats);
+    const Epilogue<T> epi = epilogue_of<T>(bias, epilogue);
+#define LATTICE_DENSE_MAP(CI, CO, KS)                                                                            \
+    conv_dense_map<T, CI, CO, QUANT, KS><<<grid, 256, 0, stream>>>(                                             \
+        f, n_in, static_cast<const T*>(fweights), widx, qweights, static_cast<const T*>(scales),              \
+        static_cast<const T*>(qbiases), q, K, out_in_map, counts, out_capacity, static_cast<T*>(out), epi)
+    const bool short_k = K * c_in <= 128;  // at most four 32-wide steps (e.g. 27 offsets x 4 channels)
+    if (c_in == 4) {
+        if (q.c_out == 16) {
+            if (short_k) LATTICE_DENSE_MAP(4, 16, 4); else LATTICE_DENSE_MAP(4, 16, 8);
+        } else {
+            if (short_k) LATTICE_DENSE_MAP(4, 32, 4); else LATTICE_DENSE_MAP(4, 32, 8);
+        }
+    } else {
+        if (q.c_out == 16) {
+            if (short_k) LATTICE_DENSE_MAP(8, 16, 4); else LATTICE_DENSE_MAP(8, 16, 8);
+        } else {
+            if (short_k) LATTICE_DENSE_MAP(8, 32, 4); else LATTICE_DENSE_MAP(8, 32, 8);
+        }
+    }
+#undef LATTICE_DENSE_MAP
+    LATTICE_LAUNCH_CHECK();
+    return LATTICE_OK;
+}
+
+int dense_map_common_checks(int dtype, const void* feats, int n_in, int c_in, int c_out, int kernel_count,
+                            const int32_t* out_in_map, const int32_t* counts, int out_capacity, void* out,
+                            int epilogue) {
+    LATTICE_REQUIRE((epilogue & ~LATTICE_EPILOGUE_RELU) == 0, "unknown conv epilogue flags.");
+    LATTICE_REQUIRE(dense_map_shape_ok(dtype, c_in, c_out, kernel_count),
+                    "the dense-map conv takes float16/bfloat16 features with C_in 4 or 8, C_out 16 or 32 and "
+                    "K * C_in <= 256.");
+    LATTICE_REQUIRE(n_in >= 0 && out_capacity >= 0, "feats and out_capacity must be nonnegative.");
+    LATTICE_REQUIRE(out_capacity == 0 || (out_in_map && counts && out), "dense-map conv pointers must be non-null.");
+    LATTICE_REQUIRE(n_in == 0 || feats != nullptr, "feats must be non-null.");
+    LATTICE_REQUIRE(reinterpret_cast<uintptr_t>(feats) % (static_cast<size_t>(c_in) * 2) == 0,
+                    "the dense-map conv needs feature rows aligned to their size.");
+    return LATTICE_OK;
+}
+
+}  // namespace
+}  // namespace lattice
+
+extern "C" int lattice_hip_conv_dense_map_supported(int dtype, int c_in, int c_out, int kernel_count) {
+    return lattice::dense_map_shape_ok(dtype, c_in, c_out, kernel_count) ? 1 : 0;
+}
+
+extern "C" int lattice_hip_sparse_conv_features_dense_map(int dtype, const void* feats, int n_in, int c_in,
+                                                         const void* weights, int weight_layout, int kernel_count,
+                                                         int c_out, const int32_t* out_in_map,
+                                                         const int32_t* counts, int out_capacity, void* out,
+                                                         const void* bias, int epilogue, void* stream_ptr) {
+    int rc = dense_map_common_checks(dtype, feats, n_in, c_in, c_out, kernel_count, out_in_map, counts,
+                                     out_capacity, out, epilogue);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(weight_layout == LATTICE_WEIGHT_KERNEL_MAJOR || weight_layout == LATTICE_WEIGHT_DENSE_5D,
+                    "unknown weight layout.");
+    LATTICE_REQUIRE(weights != nullptr, "weights must be non-null.");
+    if (out_capacity == 0) return LATTICE_OK;
+    const WeightIndex widx{weight_layout, kernel_count, c_in, c_out};
+    const QuantIndex q{kernel_count, c_in, c_out, 0, 0, 0, 0};
+    if (dtype == LATTICE_F16)
+        return launch_dense_map<_Float16, false>(feats, n_in, c_in, weights, widx, nullptr, nullptr, nullptr, q,
+                                                 kernel_count, out_in_map, counts, out_capacity, out, bias, epilogue,
+                                                 as_stream(stream_ptr));
+    return launch_dense_map<__bf16, false>(feats, n_in, c_in, weights, widx, nullptr, nullptr, nullptr, q,
+                                           kernel_count, out_in_map, counts, out_capacity, out, bias, epilogue,
+                                           as_stream(stream_ptr));
+}
+
+extern "C" int lattice_hip_sparse_quantized_conv_features_dense_map(
+    int dtype, const void* feats, int n_in, int c_in, const uint32_t* weights, const void* scales,
+    const void* biases, int kernel_count, int c_out, int storage_c_in, int group_size, int bits,
+    const int32_t* out_in_map, const int32_t* counts, int out_capacity, void* out, const void* bias, int epilogue,
+    void* stream_ptr) {
+    int rc = dense_map_common_checks(dtype, feats, n_in, c_in, c_out, kernel_count, out_in_map, counts,
+                                     out_capacity, out, epilogue);
+    if (rc != LATTICE_OK) return rc;
+    LATTICE_REQUIRE(bits == 4 || bits == 8, "quantized convolution bits must be 4 or 8.");
+    LATTICE_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+                    "quantized convolution group_size must be 32, 64, or 128.");
+    LATTICE_REQUIRE(storage_c_in >= c_in && storage_c_in % group_size == 0,
+                    "quantized convolution channel metadata is invalid.");
+    LATTICE_REQUIRE(weights && scales && biases, "quantized conv pointers must be non-null.");
+    if (out_capacity == 0) return LATTICE_OK;
+    const QuantIndex q{kernel_count, c_in, c_out, storage_c_in * bits / 32, storage_c_in / group_size, group_size,
+                       bits};
+    const WeightIndex none{};
+    if (dtype == LATTICE_F16)
+        return launch_dense_map<_Float16, true>(feats, n_in, c_in, nullptr, none, weights, scales, biases, q,
+                                                kernel_count, out_in_map, counts, out_capacity, out, bias, epilogue,
+                                                as_stream(stream_ptr));
+    return launch_dense_map<__bf16, true>(feats, n_in, c_in, nullptr, none, weights, scales, biases, q, kernel_count,
+                                          out_in_map, counts, out_capacity, out, bias, epilogue,
+                                          as_stream(stream_ptr));
 }

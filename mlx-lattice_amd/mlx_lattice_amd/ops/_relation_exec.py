@@ -49,6 +49,22 @@ def _matrix_core_eligible(dtype: torch.dtype, c_in: int, c_out: int,
             and n_in * c_in * 2 < 2 ** 31)
 
 
+def _small_dense_map(dtype: torch.dtype, c_in: int, c_out: int,
+                     relation: KernelRelation) -> torch.Tensor | None:
+    """The relation's dense map for the dense-map conv of few input
+    channels (C_in 4 or 8, C_out 16 or 32, fp16/bf16), when the relation
+    already holds it: the native CSR entry then contracts a row's whole
+    neighbourhood on the matrix cores instead of walking its edges."""
+    view = relation.implicit_gemm
+    if (view is None or dtype not in (torch.float16, torch.bfloat16)
+            or c_in not in (4, 8) or c_out not in (16, 32)
+            or relation.n_kernels is None or relation.n_kernels * c_in > 256
+            or view.out_in_map.dtype != torch.int32
+            or not relation.dense_map_exact):
+        return None
+    return view.out_in_map
+
+
 _EXPAND_CHANNELS = (32, 64, 128, 256)
 
 
@@ -255,10 +271,13 @@ def _conv_features(feats: torch.Tensor, weight: torch.Tensor,
         return sparse_conv_features_sorted_from_relation(feats, weight,
                                                          relation, bias=bias,
                                                          relu=relu)
+    dense = (_small_dense_map(feats.dtype, int(feats.shape[1]), c_out,
+                              relation) if feats.ndim == 2 else None)
     return ext.sparse_conv_features_csr(
         feats, weight, relation.edges.in_rows, relation.edges.kernel_ids,
         relation.counts, relation.output_csr.row_offsets,
-        relation.n_out_capacity, relation.n_kernels, bias=bias, relu=relu)
+        relation.n_out_capacity, relation.n_kernels, bias=bias, relu=relu,
+        out_in_map=dense)
 
 
 def sparse_conv_features_sorted_from_relation(feats: torch.Tensor,
@@ -304,6 +323,7 @@ def sparse_quantized_conv_features_from_relation(
     device = feats.device
     kv = reorder = tiles = _empty_i32(device)
     order = None
+    dense = None
     if _matrix_core_eligible(feats.dtype, weight.in_channels,
                              weight.out_channels, relation,
                              int(feats.shape[0])):
@@ -312,6 +332,9 @@ def sparse_quantized_conv_features_from_relation(
         reorder = view.reorder_rows
         tiles = view.tile_masks
         order = view.tile_order()
+    else:
+        dense = _small_dense_map(feats.dtype, weight.in_channels,
+                                 weight.out_channels, relation)
     return ext.sparse_quantized_conv_features(
         feats, weight.weight, weight.scales, weight.biases,
         relation.edges.in_rows, relation.edges.out_rows,
@@ -321,7 +344,8 @@ def sparse_quantized_conv_features_from_relation(
         weight.out_channels, weight.storage_in_channels, weight.group_size,
         weight.bits, bias=bias, tile_order=order, relu=relu,
         weight_fragments=(_quantized_fragments(weight)
-                          if order is not None else None))
+                          if order is not None else None),
+        out_in_map=dense)
 
 
 def sparse_pool_features_from_relation(feats: torch.Tensor,

@@ -188,7 +188,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("sparse_conv_features_csr", &ln::sparse_conv_features_csr, py::arg("feats"), py::arg("weights"),
           py::arg("in_rows"), py::arg("kernel_ids"), py::arg("counts"), py::arg("row_offsets"),
           py::arg("out_capacity"), py::arg("n_kernels"), py::kw_only(), py::arg("bias") = py::none(),
-          py::arg("relu") = false);
+          py::arg("relu") = false, py::arg("out_in_map") = py::none());
     m.def(
         "sparse_conv_features_sorted_implicit_gemm",
         [](const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& sorted_out_in_map,
@@ -221,7 +221,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("reorder_rows"), py::arg("tile_masks"), py::arg("out_capacity"), py::arg("n_kernels"),
           py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"), py::arg("group_size"),
           py::arg("bits"), py::kw_only(), py::arg("bias") = py::none(), py::arg("tile_order") = py::none(),
-          py::arg("relu") = false, py::arg("weight_fragments") = py::none());
+          py::arg("relu") = false, py::arg("weight_fragments") = py::none(), py::arg("out_in_map") = py::none());
     m.def("quantized_weight_fragments", &ln::quantized_weight_fragments, py::arg("weights"), py::arg("scales"),
           py::arg("biases"), py::arg("in_channels"), py::arg("out_channels"), py::arg("storage_in_channels"),
           py::arg("group_size"), py::arg("bits"),

@@ -64,6 +64,23 @@ void validate_weights(const at::Tensor& feats, const at::Tensor& weights, int n_
 
 int64_t out_channels_of(const at::Tensor& weights) { return weights.dim() == 3 ? weights.size(2) : weights.size(0); }
 
+// The relation's dense map when the caller passed one and the dense-map
+// conv takes the shape (few input channels); an undefined tensor otherwise.
+at::Tensor dense_map_for(const std::optional<at::Tensor>& out_in_map, int dtype, const at::Tensor& feats, int c_in,
+                         int c_out, int n_kernels, int out_capacity) {
+    if (!out_in_map.has_value() || !out_in_map->defined() || out_in_map->numel() == 0) return {};
+    if (lattice_hip_conv_dense_map_supported(dtype, c_in, c_out, n_kernels) == 0) return {};
+    if (reinterpret_cast<uintptr_t>(feats.data_ptr()) % (static_cast<size_t>(c_in) * feats.element_size()) != 0) {
+        return {};
+    }
+    const at::Tensor& m = *out_in_map;
+    if (m.dim() != 2 || m.size(0) != out_capacity || m.size(1) != n_kernels || m.scalar_type() != at::kInt) {
+        throw std::invalid_argument("out_in_map must have shape (out_capacity, n_kernels) and int32 dtype.");
+    }
+    require_device(m, "out_in_map");
+    return m.contiguous();
+}
+
 }  // namespace
 
 at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& weights_in, const at::Tensor& in_rows,
@@ -129,7 +146,8 @@ at::Tensor sparse_conv_features(const at::Tensor& feats_in, const at::Tensor& we
 at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor& weights_in, const at::Tensor& in_rows,
                                     const at::Tensor& kernel_ids, const at::Tensor& counts,
                                     const at::Tensor& row_offsets, int out_capacity, int n_kernels,
-                                    const std::optional<at::Tensor>& bias, bool relu) {
+                                    const std::optional<at::Tensor>& bias, bool relu,
+                                    const std::optional<at::Tensor>& out_in_map) {
     const char* op = "sparse_conv_features";
     if (out_capacity < 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
@@ -154,6 +172,15 @@ at::Tensor sparse_conv_features_csr(const at::Tensor& feats_in, const at::Tensor
     const int layout = weights.dim() == 3 ? LATTICE_WEIGHT_KERNEL_MAJOR : LATTICE_WEIGHT_DENSE_5D;
     at::Tensor bias_keep;
     const void* b = bias_ptr(bias, feats, c_out, &bias_keep);
+    const at::Tensor map = dense_map_for(out_in_map, dtype_code(feats, op), feats, static_cast<int>(feats.size(1)),
+                                         static_cast<int>(c_out), n_kernels, out_capacity);
+    if (map.defined()) {
+        check_status(lattice_hip_sparse_conv_features_dense_map(
+            dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
+            weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(map), ci32(counts), out_capacity,
+            out.data_ptr(), b, relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, current_stream(feats)));
+        return out;
+    }
     check_status(lattice_hip_sparse_conv_features(
         dtype_code(feats, op), feats.data_ptr(), static_cast<int>(feats.size(0)), static_cast<int>(feats.size(1)),
         weights.data_ptr(), layout, n_kernels, static_cast<int>(c_out), ci32(in_rows), ci32(kernel_ids),
@@ -372,7 +399,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
                                           int storage_in_channels, int group_size, int bits,
                                           const std::optional<at::Tensor>& bias,
                                           const std::optional<at::Tensor>& tile_order, bool relu,
-                                          const std::optional<at::Tensor>& weight_fragments) {
+                                          const std::optional<at::Tensor>& weight_fragments,
+                                          const std::optional<at::Tensor>& out_in_map) {
     if (out_capacity < 0 || n_kernels <= 0) {
         throw std::invalid_argument("out_capacity must be nonnegative and n_kernels must be positive.");
     }
@@ -451,6 +479,16 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats_in, const at::
     const size_t frag_bytes = dtype == LATTICE_F32 ? 0
                                                    : lattice_hip_quantized_weight_fragments_bytes(
                                                          dtype, n_kernels, in_channels, out_channels);
+    const at::Tensor map =
+        dense_map_for(out_in_map, dtype, feats, in_channels, out_channels, n_kernels, out_capacity);
+    if (map.defined()) {
+        check_status(lattice_hip_sparse_quantized_conv_features_dense_map(
+            dtype, feats.data_ptr(), static_cast<int>(feats.size(0)), in_channels,
+            reinterpret_cast<const uint32_t*>(weights.data_ptr()), scales.data_ptr(), biases.data_ptr(), n_kernels,
+            out_channels, storage_in_channels, group_size, bits, ci32(map), ci32(counts), out_capacity,
+            out.data_ptr(), b, relu ? LATTICE_EPILOGUE_RELU : LATTICE_EPILOGUE_NONE, current_stream(feats)));
+        return out;
+    }
     const bool small_table = (feats.size(0) + 1) * static_cast<int64_t>(in_channels) * 2 <= (int64_t{1} << 32);
     if (has_plan && frag_bytes > 0 && small_table) {
         // Streamed route: the packed weight in fragment order (the caller's

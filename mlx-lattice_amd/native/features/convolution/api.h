@@ -18,11 +18,14 @@ at::Tensor sparse_conv_features(const at::Tensor& feats, const at::Tensor& weigh
                                 const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false);
 
 // The CSR conv without the grouped plan views the reference signature
-// carries for its gradient (the forward reads only the output CSR).
+// carries for its gradient (the forward reads only the output CSR).  With
+// the relation's dense map (out_in_map, (out_capacity, n_kernels)) and a
+// shape the dense-map conv takes (C_in 4 or 8), it runs that instead.
 at::Tensor sparse_conv_features_csr(const at::Tensor& feats, const at::Tensor& weights, const at::Tensor& in_rows,
                                     const at::Tensor& kernel_ids, const at::Tensor& counts,
                                     const at::Tensor& row_offsets, int out_capacity, int n_kernels,
-                                    const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false);
+                                    const std::optional<at::Tensor>& bias = std::nullopt, bool relu = false,
+                                    const std::optional<at::Tensor>& out_in_map = std::nullopt);
 
 // Dense expansion conv over a direct generative / transposed relation:
 // (rows * K, C_out), output row in * K + k = feats[in] @ W[k].
@@ -57,7 +60,8 @@ at::Tensor sparse_quantized_conv_features(const at::Tensor& feats, const at::Ten
                                           const std::optional<at::Tensor>& bias = std::nullopt,
                                           const std::optional<at::Tensor>& tile_order = std::nullopt,
                                           bool relu = false,
-                                          const std::optional<at::Tensor>& weight_fragments = std::nullopt);
+                                          const std::optional<at::Tensor>& weight_fragments = std::nullopt,
+                                          const std::optional<at::Tensor>& out_in_map = std::nullopt);
 
 // The fragment-ordered packed copy of a quantized weight that the streamed
 // matrix-core conv reads (lattice_hip_quantized_weight_fragments: codes,
