@@ -30,6 +30,7 @@
 #include "lattice_common.h"
 #include "scan.h"
 
+
 namespace lattice {
 namespace {
 
@@ -2637,7 +2638,11 @@ int launch_dense_map(const void* feats, int n_in, int c_in, const void* fweights
                      const int32_t* out_in_map, const int32_t* counts, int out_capacity, void* out,
                      const void* bias, int epilogue, hipStream_t stream) {
     const long long waves = (static_cast<long long>(out_capacity) + 15) / 16;
-    const unsigned grid = static_cast<unsigned>(std::max<long long>(1, std::min<long long>((waves + 3) / 4, 2048)));
+    // Blocks: each builds the weight's fragments once, then its waves walk
+    // 16-row blocks grid-stride.  1,024 blocks (four per CU) measured
+    // fastest on the config-5 stem: 40 us, against 44 / 46 / 51 / 65 us at
+    // 2,048 / 512 / 4,096 / 8,192.
+    const unsigned grid = static_cast<unsigned>(std::max<long long>(1, std::min<long long>((waves + 3) / 4, 1024)));
     const T* f = static_cast<const T*>(feats);
     const Epilogue<T> epi = epilogue_of<T>(bias, epilogue);
 #define LATTICE_DENSE_MAP(CI, CO, KS)                                                                            \
