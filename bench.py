@@ -40,7 +40,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # (profiles/config3_kernel_traffic.md), valid for the kernel source whose
 # SHA-256 prefix is given: when csrc/conv.hip changes, the bench reports
 # traffic as null until the counters are measured again.
-CONV_TRAFFIC = {'bytes': 1.2077e9, 'conv_hip_sha256': '136750eb7a7b6dcf'}
+CONV_TRAFFIC = {'bytes': 1.2071e9, 'conv_hip_sha256': '2c9f8380e54c88b3'}
 
 
 def parse_args():
