@@ -444,23 +444,53 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
 // dW[k] = sum of the partial tiles of offset k's blocks (XCD by XCD, then
 // turn by turn), one rounding, written in the weight's layout.  Blocks
 // (x, k): offset k's share is worked out once per thread, then the block
-// strides over the offset's C_in x C_out entries.
+// strides over the offset's C_in x C_out entries four at a time (16-byte
+// loads of the partials; each entry keeps its own summation order).
+constexpr int kReduceBatch = 16;  // partial loads in flight per thread
+
 template <typename T>
 __global__ void __launch_bounds__(256)
 weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict__ koff, int slots,
                    GradWeightIndex widx, T* __restrict__ grad) {
     const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
+    const long long mat4 = mat / 4;  // c_out is a multiple of 8 on this route
     const int k = blockIdx.y;
     int first = 0, count = 0;
     if (koff[widx.K] > koff[0]) wg_share(koff, widx.K, slots, k, &first, &count);
-    for (long long within = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; within < mat;
-         within += static_cast<long long>(gridDim.x) * blockDim.x) {
-        float acc = 0.0f;
-        for (int x = 0; x < kXcds; ++x)
-            for (int j = 0; j < count; ++j) acc += partial[(x * slots + first + j) * mat + within];
-        const int co = static_cast<int>(within % widx.c_out);
-        const int ci = static_cast<int>(within / widx.c_out);
-        grad[widx(k, ci, co)] = static_cast<T>(acc);
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    for (long long w4 = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; w4 < mat4;
+         w4 += static_cast<long long>(gridDim.x) * blockDim.x) {
+        // partial i of the (x, j) order: x = i / count, j = i % count; kReduceBatch
+        // loads are issued before their adds, which run in that order
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int n = kXcds * count;
+        for (int i0 = 0; i0 < n; i0 += kReduceBatch) {
+            float4 v[kReduceBatch];
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u) {
+                const int i = i0 + u;
+                const int x = count > 0 ? i / count : 0;
+                const int j = i - x * count;
+                v[u] = i < n ? p4[(x * slots + first + j) * mat4 + w4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u) {
+                if (i0 + u < n) {
+                    acc.x += v[u].x;
+                    acc.y += v[u].y;
+                    acc.z += v[u].z;
+                    acc.w += v[u].w;
+                }
+            }
+        }
+        const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long within = w4 * 4 + i;
+            const int co = static_cast<int>(within % widx.c_out);
+            const int ci = static_cast<int>(within / widx.c_out);
+            grad[widx(k, ci, co)] = static_cast<T>(a[i]);
+        }
     }
 }
 
@@ -569,7 +599,7 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
 #undef LATTICE_WG_LAUNCH
             LATTICE_LAUNCH_CHECK();
             const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
-            const dim3 rgrid(grid_for(mat, 256, 256), static_cast<unsigned>(widx.K));
+            const dim3 rgrid(grid_for(mat / 4, 256, 256), static_cast<unsigned>(widx.K));
             weight_grad_reduce<T><<<rgrid, 256, 0, stream>>>(partial, koff, slots, widx, static_cast<T*>(grad));
             LATTICE_LAUNCH_CHECK();
             return LATTICE_OK;
