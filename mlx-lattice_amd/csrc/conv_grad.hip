@@ -428,17 +428,15 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
         __syncthreads();
     }
     // D[m][n]: lane holds rows 4*(lane/16) + q, column lane%16 of each block.
-    float* out = partial + static_cast<long long>(x * slots + slot) * c_in * c_out;
+    // The partial tile is stored as the lanes hold it (fragment order, one
+    // 16-byte store per lane and block: whole 1 KB runs per wave); the
+    // reduction maps each 4-float piece back to its (ci, co).
+    float4_t* out = reinterpret_cast<float4_t*>(partial) +
+                    (static_cast<long long>(x * slots + slot) * tiles + tile) * (TCI * TCO / 4);
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int ci = ci0 + (TCI / 2) * wm + 16 * m + 4 * g + q;
-                const int co = co0 + (TCO / 2) * wn + 16 * n + lr;
-                if (ci < c_in && co < c_out) out[static_cast<long long>(ci) * c_out + co] = acc[m][n][q];
-            }
+        for (int n = 0; n < NB; ++n) out[((wave * MB + m) * NB + n) * 64 + lane] = acc[m][n];
 }
 
 // dW[k] = sum of the partial tiles of offset k's blocks (XCD by XCD, then
@@ -448,20 +446,29 @@ weight_grad_mfma(const T* __restrict__ feats, int n_in, int c_in, const T* __res
 // loads of the partials; each entry keeps its own summation order).
 constexpr int kReduceBatch = 16;  // partial loads in flight per thread
 
+// dW[k] = sum of the partial tiles of offset k's blocks (XCD by XCD, then
+// turn by turn), one rounding, written in the weight's layout.  Blocks
+// (x, k): offset k's share is worked out once per thread, then the block
+// strides over the partial matrix's 4-float pieces (fragment order of
+// weight_grad_mfma: piece (tile, wave, m, n, lane) holds ci = ci0 +
+// (TCI/2)*(wave&1) + 16m + 4(lane/16) + q, q < 4, and co = co0 +
+// (TCO/2)*(wave>>1) + 16n + lane%16); each entry keeps its own summation
+// order.
 template <typename T>
 __global__ void __launch_bounds__(256)
 weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict__ koff, int slots,
-                   GradWeightIndex widx, T* __restrict__ grad) {
-    const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
-    const long long mat4 = mat / 4;  // c_out is a multiple of 8 on this route
+                   GradWeightIndex widx, int tci, int tco, int tiles, int tiles_co, T* __restrict__ grad) {
+    const long long pieces = static_cast<long long>(tiles) * tci * tco / 4;  // per partial matrix
+    const int mb = tci / 32, nb = tco / 32;
     const int k = blockIdx.y;
     int first = 0, count = 0;
     if (koff[widx.K] > koff[0]) wg_share(koff, widx.K, slots, k, &first, &count);
     const float4* p4 = reinterpret_cast<const float4*>(partial);
-    for (long long w4 = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; w4 < mat4;
+    for (long long w4 = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; w4 < pieces;
          w4 += static_cast<long long>(gridDim.x) * blockDim.x) {
-        // partial i of the (x, j) order: x = i / count, j = i % count; kReduceBatch
-        // loads are issued before their adds, which run in that order
+        // partial i of the (x, j) order: x = i / count, j = i % count;
+        // kReduceBatch loads are issued before their adds, which run in that
+        // order
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const int n = kXcds * count;
         for (int i0 = 0; i0 < n; i0 += kReduceBatch) {
@@ -471,7 +478,7 @@ weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict_
                 const int i = i0 + u;
                 const int x = count > 0 ? i / count : 0;
                 const int j = i - x * count;
-                v[u] = i < n ? p4[(x * slots + first + j) * mat4 + w4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                v[u] = i < n ? p4[(x * slots + first + j) * pieces + w4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
 #pragma unroll
             for (int u = 0; u < kReduceBatch; ++u) {
@@ -483,13 +490,21 @@ weight_grad_reduce(const float* __restrict__ partial, const int32_t* __restrict_
                 }
             }
         }
+        const long long per_tile = static_cast<long long>(tci) * tco / 4;
+        const int tile = static_cast<int>(w4 / per_tile);
+        long long r = w4 - tile * per_tile;
+        const int lane = static_cast<int>(r % 64);
+        r /= 64;
+        const int nn = static_cast<int>(r % nb);
+        r /= nb;
+        const int mm = static_cast<int>(r % mb);
+        const int wave = static_cast<int>(r / mb);
+        const int ci = (tile / tiles_co) * tci + (tci / 2) * (wave & 1) + 16 * mm + 4 * (lane >> 4);
+        const int co = (tile % tiles_co) * tco + (tco / 2) * (wave >> 1) + 16 * nn + (lane & 15);
         const float a[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const long long within = w4 * 4 + i;
-            const int co = static_cast<int>(within % widx.c_out);
-            const int ci = static_cast<int>(within / widx.c_out);
-            grad[widx(k, ci, co)] = static_cast<T>(a[i]);
+        for (int q = 0; q < 4; ++q) {
+            if (ci + q < widx.c_in && co < widx.c_out) grad[widx(k, ci + q, co)] = static_cast<T>(a[q]);
         }
     }
 }
@@ -544,9 +559,27 @@ int weight_grad_slots(int edge_capacity, int kernel_count) {
     return static_cast<int>(std::max<long long>(kernel_count, std::min<long long>(kWgMaxSlots, want)));
 }
 
-// One fp32 partial tile per block.
+// Channel tiles of the matrix-core weight gradient: 128-channel tiles where
+// the channels fill them, so one gather of an edge's rows serves every
+// channel pair of the tile.
+struct WgTiles {
+    int tci, tco, tiles_ci, tiles_co;
+    int tiles() const { return tiles_ci * tiles_co; }
+};
+WgTiles wg_tiles(int c_in, int c_out) {
+    WgTiles t;
+    t.tci = c_in > 64 ? 128 : 64;
+    t.tco = c_out > 64 ? 128 : 64;
+    t.tiles_ci = (c_in + t.tci - 1) / t.tci;
+    t.tiles_co = (c_out + t.tco - 1) / t.tco;
+    return t;
+}
+
+// One fp32 partial matrix (every channel tile, in fragment order) per block
+// slot.
 size_t weight_grad_partial_bytes(int edge_capacity, int kernel_count, int c_in, int c_out) {
-    return static_cast<size_t>(kXcds) * weight_grad_slots(edge_capacity, kernel_count) * c_in * c_out *
+    const WgTiles t = wg_tiles(c_in, c_out);
+    return static_cast<size_t>(kXcds) * weight_grad_slots(edge_capacity, kernel_count) * t.tiles() * t.tci * t.tco *
            sizeof(float);
 }
 
@@ -579,13 +612,8 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
             const size_t need = weight_grad_partial_bytes(edge_capacity, widx.K, widx.c_in, widx.c_out);
             LATTICE_REQUIRE(workspace_bytes >= need, "weight gradient workspace too small.");
             float* partial = static_cast<float*>(workspace);
-            // 128-channel tiles where the channels fill them: one gather of
-            // an edge's rows then serves every channel pair of the tile.
-            const int tci = widx.c_in > 64 ? 128 : 64;
-            const int tco = widx.c_out > 64 ? 128 : 64;
-            const int tiles_ci = (widx.c_in + tci - 1) / tci;
-            const int tiles_co = (widx.c_out + tco - 1) / tco;
-            const int tiles = tiles_ci * tiles_co;
+            const WgTiles wt = wg_tiles(widx.c_in, widx.c_out);
+            const int tci = wt.tci, tco = wt.tco, tiles_co = wt.tiles_co, tiles = wt.tiles();
             const unsigned grid = static_cast<unsigned>(kXcds) * slots * tiles;
 #define LATTICE_WG_LAUNCH(A, B)                                                                                 \
     weight_grad_mfma<T, A, B><<<grid, 256, 0, stream>>>(static_cast<const T*>(feats), n_in, widx.c_in,          \
@@ -598,9 +626,10 @@ int launch_weight_grad(int dtype, const void* feats, int n_in, const void* cot, 
             else LATTICE_WG_LAUNCH(64, 64);
 #undef LATTICE_WG_LAUNCH
             LATTICE_LAUNCH_CHECK();
-            const long long mat = static_cast<long long>(widx.c_in) * widx.c_out;
-            const dim3 rgrid(grid_for(mat / 4, 256, 256), static_cast<unsigned>(widx.K));
-            weight_grad_reduce<T><<<rgrid, 256, 0, stream>>>(partial, koff, slots, widx, static_cast<T*>(grad));
+            const long long pieces = static_cast<long long>(tiles) * tci * tco / 4;
+            const dim3 rgrid(grid_for(pieces, 256, 256), static_cast<unsigned>(widx.K));
+            weight_grad_reduce<T><<<rgrid, 256, 0, stream>>>(partial, koff, slots, widx, tci, tco, tiles, tiles_co,
+                                                             static_cast<T*>(grad));
             LATTICE_LAUNCH_CHECK();
             return LATTICE_OK;
         }
