@@ -60,6 +60,8 @@ def _small_dense_map(dtype: torch.dtype, c_in: int, c_out: int,
             or c_in not in (4, 8) or c_out not in (16, 32)
             or relation.n_kernels is None or relation.n_kernels * c_in > 256
             or view.out_in_map.dtype != torch.int32
+            or tuple(view.out_in_map.shape) != (relation.n_out_capacity,
+                                                relation.n_kernels)
             or not relation.dense_map_exact):
         return None
     return view.out_in_map
