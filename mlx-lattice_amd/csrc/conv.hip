@@ -31,6 +31,7 @@
 #include "scan.h"
 
 
+
 namespace lattice {
 namespace {
 
@@ -38,6 +39,10 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Cache-policy operand of the raw buffer stores that write conv outputs:
+// non-temporal (the output is streamed past the caches; it is not read
+// again by the kernel that writes it).
+constexpr int kNonTemporal = 2;
 
 // ------------------------------------------------------------ element IO --
 
@@ -1061,8 +1066,8 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
         const int sr = row0 + r;
         if (sr < rows) {
             const long long orow = reorder_rows != nullptr ? reorder_rows[sr] : sr;
-            *reinterpret_cast<V*>(out + orow * out_ld + wc * S::WAVE_COLS + piece * 8) =
-                *reinterpret_cast<const V*>(stage + r * S::EROW + (piece ^ (r % S::EPIECES)) * 8);
+__builtin_nontemporal_store(*reinterpret_cast<const V*>(stage + r * S::EROW + (piece ^ (r % S::EPIECES)) * 8),
+                                        reinterpret_cast<V*>(out + orow * out_ld + wc * S::WAVE_COLS + piece * 8));
         }
     }
 }
@@ -1111,6 +1116,7 @@ conv_igemm(const T* __restrict__ feats, int n_in, int c_in, BSource bsrc, const 
 // in the unrolled loop.
 
 typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
 
 // Buffer resource of `bytes` bytes at `base` (raw, no stride): loads past
 // the range return zeros.
@@ -1578,7 +1584,9 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
 
     // The finished tile goes through LDS (the A ring is free once every
     // wave's copies have landed) so that it leaves as 16-byte stores of
-    // whole output rows to out[reorder_rows[row]].  Rows with no edges store
+    // whole output rows to out[reorder_rows[row]], non-temporal (streamed
+    // past the caches: config 2's conv 24.4 -> 21.5 us, config 3's
+    // 188 -> 184 us).  Rows with no edges store
     // zeros (plus bias).
     constexpr int LDW = S::C_OUT + 8;  // halves per staged row: rows 16 bytes apart in the banks
     static_assert(S::ROWS * LDW <= (S::LA + 1) * S::ABUF, "the staged tile fits the A ring");
@@ -1611,8 +1619,9 @@ conv_igemm_stream(const T* __restrict__ feats, int n_in, int c_in, const T* __re
         const int sr = row0 + r;
         if (sr < rows) {
             const int orow = reorder_rows != nullptr ? reorder_rows[sr] : sr;
-            *reinterpret_cast<uint4*>(ohalf + static_cast<long long>(orow) * out_ld + piece * 8) =
-                *reinterpret_cast<const uint4*>(stage + r * LDW + piece * 8);
+            __builtin_nontemporal_store(
+                *reinterpret_cast<const u32x4v_t*>(stage + r * LDW + piece * 8),
+                reinterpret_cast<u32x4v_t*>(ohalf + static_cast<long long>(orow) * out_ld + piece * 8));
         }
     }
 }
@@ -1739,8 +1748,9 @@ conv_dense_map(const T* __restrict__ feats, int n_in, const T* __restrict__ fwei
                 T v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = epi.apply(acc[cb][i], cb * 16 + lg * 4 + i);
-                *reinterpret_cast<uint2*>(out + static_cast<long long>(row) * CO + cb * 16 + lg * 4) =
-                    *reinterpret_cast<const uint2*>(v);
+                __builtin_nontemporal_store(*reinterpret_cast<const u32x2v_t*>(v),
+                                            reinterpret_cast<u32x2v_t*>(out + static_cast<long long>(row) * CO +
+                                                                        cb * 16 + lg * 4));
             }
         }
     }
@@ -1893,7 +1903,8 @@ conv_expand(const T* __restrict__ feats, int n_in, const int32_t* __restrict__ a
                 const int p = lane + j * kWave;
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(u32x4_t, piece_v[j]), out_rsrc,
-                    static_cast<int>((((p / PIECES) * K + k) * C_OUT + (p % PIECES) * 8) * sizeof(T)), 0, 0);
+                    static_cast<int>((((p / PIECES) * K + k) * C_OUT + (p % PIECES) * 8) * sizeof(T)), 0,
+                    kNonTemporal);
             }
         }
         __syncthreads();  // W[:, k+1, :] in LDS; the stage is free again
