@@ -28,6 +28,7 @@
 #include <climits>
 
 #include "lattice_common.h"
+
 #include "scan.h"
 #include "sort.h"
 
@@ -1353,7 +1354,9 @@ gather_sorted(const int32_t* __restrict__ out_in_map, const int32_t* __restrict_
     for (int i = threadIdx.x; i < n * K; i += kThreads) {
         const int k = i / n;
         const int r = i - k * n;
-        kv_map[static_cast<long long>(k) * rows + row0 + r] = tile[r * 33 + k];
+        // non-temporal: the k-major map is read by the conv launches, not by
+        // this kernel (sorted view of 400k rows 90 -> 87 us)
+        __builtin_nontemporal_store(tile[r * 33 + k], kv_map + static_cast<long long>(k) * rows + row0 + r);
     }
 }
 
