@@ -117,6 +117,35 @@ def test_noalloc_conv_orders_calls_on_two_streams():
     _check(small)
 
 
+def test_noalloc_conv_under_graph_capture():
+    # The entry's launches recorded into a graph (no allocation, no event
+    # while capturing), replayed three times with eager work and a
+    # synchronisation between replays; every replay equals the workspace
+    # entry's output.
+    lib = _lib()
+    prepared = _prepare(lib, 40000, 160, 12, 64, 128, 1)
+    args, ref, got, bias, epilogue, _ = prepared
+    print('no-alloc conv under graph capture', flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # warm-up on the capture stream
+        _noalloc(lib, prepared, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
+            *args, got.data_ptr(), bias.data_ptr(), epilogue,
+            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.lattice_hip_last_error()
+    for _ in range(3):
+        got.fill_(float('nan'))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(prepared)
+
+
 def test_noalloc_conv_rejects_oversized_launches():
     lib = _lib()
     rc = lib.lattice_hip_sparse_conv_features_sorted_implicit_gemm_noalloc(
